@@ -1,0 +1,282 @@
+#!/usr/bin/env python3
+"""Benchmark: achieved HBM GB/s of the fused data-parallel kernels on one GPU.
+
+Headline workload: FusedBatchNormV3 forward +
+FusedBatchNormGradV3, NHWC, is_training, epsilon 1.001e-5, at the four
+ResNet-50 stage shapes [256,56,56,256], [256,28,28,512], [256,14,14,1024],
+[256,7,7,2048], each in float16 and bfloat16 (float32 scale/offset/stats).
+One step = fwd + grad for all 8 (dtype, shape) pairs.  Inputs are synthetic
+(x, dy ~ N(0,1); scale ~ U(0.5,1.5); offset ~ N(0,0.1)), resident in HBM
+before the timed region.
+
+value = algorithmic bytes per step (fwd 2*s*E + grad 3*s*E per pair) x steps
+        / wall time of the timed region (HIP events around K steps).
+roofline: the dominant kernel (tfma_bn_grad_apply: reads x, dy, writes dx,
+        3*s*E bytes per launch) timed with HIP events recorded on its
+        stream around each of its launches inside the timed region.
+cpu_baseline: the TF-CPU restatement (oracle/, C + OpenMP) on one float16
+        fwd+grad pass over the four shapes, on the host's cores.
+components: the other north-star kernels (Adam, grouped Adam, elementwise
+        chains) at their config shapes, timed the same way.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PEAK_GBPS = 8000.0  # MI355X HBM3E
+SHAPES = [(256, 56, 56, 256), (256, 28, 28, 512), (256, 14, 14, 1024), (256, 7, 7, 2048)]
+EPS = 1.001e-5
+
+
+def resnet50_shapes():
+    """torchvision ResNet-50 parameter shapes: 53 bias-free convs, 53 BN
+    gamma/beta pairs, fc weight and bias (161 tensors, 25,557,032 params)."""
+    shapes = []
+
+    def conv_bn(cin, cout, k):
+        shapes.append((cout, cin, k, k))
+        shapes.append((cout,))
+        shapes.append((cout,))
+
+    conv_bn(3, 64, 7)
+    cin = 64
+    for width, blocks in ((64, 3), (128, 4), (256, 6), (512, 3)):
+        for b in range(blocks):
+            conv_bn(cin, width, 1)
+            conv_bn(width, width, 3)
+            conv_bn(width, width * 4, 1)
+            if b == 0:
+                conv_bn(cin, width * 4, 1)
+            cin = width * 4
+    shapes.append((1000, 2048))
+    shapes.append((1000,))
+    return shapes
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-components", action="store_true",
+                   help="skip the Adam / elementwise component lines")
+    p.add_argument("--trace", default="tfma_bn_grad_apply",
+                   help="kernel timed for the roofline object")
+    return p.parse_args()
+
+
+def _events(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def bn_workload(torch, ops, dev):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    calls, pairs = [], []
+    for dt in (torch.float16, torch.bfloat16):
+        for shape in SHAPES:
+            c = shape[-1]
+            x = torch.randn(shape, generator=gen, device=dev).to(dt)
+            dy = torch.randn(shape, generator=gen, device=dev).to(dt)
+            scale = torch.rand(c, generator=gen, device=dev) + 0.5
+            offset = 0.1 * torch.randn(c, generator=gen, device=dev)
+            empty = torch.empty(0, device=dev)
+            ws = torch.empty(ops.fused_batch_norm_workspace_bytes(x), dtype=torch.uint8,
+                             device=dev)
+            fwd = ops.bind(ops.FusedBatchNormV3, x, scale, offset, empty, empty, epsilon=EPS,
+                           data_format="NHWC", is_training=True, workspace=ws)
+            r = fwd.result
+            grad = ops.bind(ops.FusedBatchNormGradV3, dy, x, scale, r.reserve_space_1,
+                            r.reserve_space_2, r.reserve_space_3, epsilon=EPS,
+                            data_format="NHWC", is_training=True, workspace=ws)
+            calls += [fwd, grad]
+            pairs.append((dt, shape, x.numel(), x.element_size()))
+    return calls, pairs
+
+
+def time_calls(torch, calls, steps, warmup):
+    for _ in range(warmup):
+        for c in calls:
+            c()
+    torch.cuda.synchronize()
+    t0, t1 = _events(torch)
+    t0.record()
+    for _ in range(steps):
+        for c in calls:
+            c()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps  # ms per step
+
+
+def components(torch, ops, dev):
+    """Adam (cfg3), grouped Adam (cfg3b), elementwise chains (cfg4)."""
+    out = {}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    reps, warm = 20, 3
+
+    def rate(calls, nbytes, reps_=reps):
+        ms = time_calls(torch, calls, reps_, warm)
+        gbps = nbytes / (ms / 1e3) / 1e9
+        return {"ms": round(ms, 4), "GB/s": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1)}
+
+    n = 25_600_000
+    var = 0.02 * torch.randn(n, generator=gen, device=dev)
+    m = torch.zeros(n, device=dev)
+    v = torch.zeros(n, device=dev)
+    g = 1e-3 * torch.randn(n, generator=gen, device=dev)
+    adam = ops.bind(ops.ResourceApplyAdam, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7, g)
+    out["adam_f32_25.6M"] = rate([adam], 28 * n)
+
+    shapes = resnet50_shapes()
+    tv = [0.02 * torch.randn(s, generator=gen, device=dev) for s in shapes]
+    tm = [torch.zeros(s, device=dev) for s in shapes]
+    tvv = [torch.zeros(s, device=dev) for s in shapes]
+    tg = [1e-3 * torch.randn(s, generator=gen, device=dev) for s in shapes]
+    total = sum(t.numel() for t in tv)
+    grouped = ops.bind(ops.MusaGroupedResourceApplyAdam, tv, tm, tvv, tg, 0.9, 0.999, 1e-3, 0.9,
+                       0.999, 1e-7)
+    out["grouped_adam_f32_resnet50_161"] = rate([grouped], 28 * total)
+    del var, m, v, g, tv, tm, tvv, tg
+
+    for dt, name in ((torch.float32, "f32"), (torch.float16, "f16")):
+        s = torch.tensor([], dtype=dt).element_size()
+        x = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
+        b = torch.randn(4096, generator=gen, device=dev).to(dt)
+        E = x.numel()
+        out[f"bias_add_relu_{name}_8192x4096"] = rate([ops.bind(ops.MusaBiasAddRelu, x, b)],
+                                                      2 * s * E + s * 4096)
+        out[f"add_v2_relu_{name}_8192x4096"] = rate([ops.bind(ops.MusaAddV2Relu, x, b)],
+                                                    2 * s * E + s * 4096)
+        a_full = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
+        b_full = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
+        out[f"mul_add_full_{name}_8192x4096"] = rate(
+            [ops.bind(ops.MusaShiftedAffineMap, x, a_full, b_full)], 4 * s * E)
+        out[f"mul_add_row_{name}_8192x4096"] = rate(
+            [ops.bind(ops.MusaShiftedAffineMap, x, b, b)], 2 * s * E + 2 * s * 4096)
+        xo = torch.randn(8191, 4095, generator=gen, device=dev).to(dt)
+        bo = torch.randn(4095, generator=gen, device=dev).to(dt)
+        out[f"bias_add_relu_{name}_8191x4095"] = rate([ops.bind(ops.MusaBiasAddRelu, xo, bo)],
+                                                      2 * s * xo.numel() + s * 4095)
+        del x, b, a_full, b_full, xo, bo
+    torch.cuda.synchronize()
+    return out
+
+
+def cpu_baseline(torch, dev):
+    """TF-CPU restatement (oracle, C + OpenMP) on one float16 fwd+grad pass
+    over the four cfg2 shapes.  Inputs are drawn on the GPU and copied to
+    host memory before timing."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import oracle
+    threads = min(16, os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    total_bytes, secs = 0, 0.0
+    for shape in SHAPES:
+        c = shape[-1]
+        x = torch.randn(shape, generator=gen, device=dev).half().cpu().numpy()
+        dy = torch.randn(shape, generator=gen, device=dev).half().cpu().numpy()
+        scale = np.random.default_rng(0).uniform(0.5, 1.5, c).astype(np.float32)
+        offset = np.zeros(c, np.float32)
+        t = time.perf_counter()
+        _, _, _, sm, sv = oracle.bn_fwd(x, scale, offset, epsilon=EPS, dtype="float16")
+        oracle.bn_grad(dy, x, scale, sm, sv, epsilon=EPS, dtype="float16")
+        secs += time.perf_counter() - t
+        total_bytes += 10 * x.size
+        del x, dy
+    gbps = total_bytes / secs / 1e9
+    return {"value": round(gbps, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "seconds": round(secs, 2),
+            "sample": "one float16 FusedBatchNormV3+GradV3 pass over the 4 cfg2 shapes "
+                      f"({total_bytes // 10} elements; algorithmic bytes / wall time)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU runs are "
+              "not part of this build.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    sys.path.insert(0, ROOT)
+    import tensorflow_musa_extension_amd as tfma
+    ops = tfma.raw_ops
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+
+    calls, pairs = bn_workload(torch, ops, dev)
+    bytes_per_step = sum(5 * s * e for _, _, e, s in pairs)
+    kernel_bytes_per_step = sum(3 * s * e for _, _, e, s in pairs)  # grad apply
+
+    for _ in range(args.warmup):
+        for c in calls:
+            c()
+    torch.cuda.synchronize()
+    ops.trace_enable(args.trace)
+    t0, t1 = _events(torch)
+    t0.record()
+    for _ in range(args.steps):
+        for c in calls:
+            c()
+    t1.record()
+    torch.cuda.synchronize()
+    traced_ms, launches = ops.trace_read()
+    ops.trace_enable(None)
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+    value = bytes_per_step / (ms_per_step / 1e3) / 1e9
+
+    achieved = kernel_bytes_per_step * args.steps / (traced_ms / 1e3) / 1e9 if traced_ms else None
+    roofline = {
+        "kernel": args.trace,
+        "bound": "hbm",
+        "achieved": round(achieved, 1) if achieved else None,
+        "peak": PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_GBPS, 4) if achieved else None,
+        "traffic": None,
+        "launches": launches,
+        "avg_launch_us": round(1e3 * traced_ms / launches, 2) if launches else None,
+        "algorithmic_bytes_per_step": kernel_bytes_per_step,
+    }
+    result = {
+        "metric": "achieved HBM GB/s (% of peak) for FusedBN fwd+grad, fused Adam, eltwise",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "pct_of_peak": round(100 * value / PEAK_GBPS, 2),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 compute on f16/bf16 data",
+        "data": "synthetic",
+        "config": {
+            "workload": "cfg2: FusedBatchNormV3 fwd + FusedBatchNormGradV3, NHWC, "
+                        "is_training, eps=1.001e-5, f16 and bf16 x/dy, f32 stats, shapes "
+                        + ", ".join("x".join(map(str, s)) for s in SHAPES),
+            "bytes_per_step": bytes_per_step,
+            "parallelism": "single GPU",
+        },
+        "roofline": roofline,
+    }
+    if not args.no_components:
+        result["components"] = components(torch, ops, dev)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(torch, dev)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,250 @@
+/*
+ * tfma.h — C ABI of the MI355X (gfx950) fused data-parallel kernel library.
+ *
+ * This is the drop-in boundary for the hot path of
+ * MooreThreads/tensorflow_musa_extension: FusedBatchNormV3 /
+ * FusedBatchNormGradV3, ResourceApplyAdam and a multi-tensor (grouped) Adam,
+ * and the elementwise chains BiasAdd+Relu, AddV2+Relu and Mul+Add.
+ *
+ * Each entry point is what a TensorFlow PluggableDevice kernel's compute
+ * callback (registered through TF_NewKernelBuilder in TF_InitKernel) would
+ * call after it has resolved its inputs, allocated its outputs and fetched
+ * its stream: plain pointers, shapes and dtypes, a hipStream_t passed as
+ * void*, and a status object that mirrors TF_Status.  Nothing here uses
+ * torch or TensorFlow types.
+ *
+ * Conventions
+ *  - Codes in TFMA_Code have the numeric values of TF_Code
+ *    (tensorflow/c/tf_status.h); dtypes in TFMA_DataType have the numeric
+ *    values of TF_DataType (tensorflow/c/tf_datatype.h).
+ *  - Every entry point returns the status code and also stores it, with a
+ *    message, in *status.  No entry point throws or aborts.
+ *  - Work is enqueued on `stream` and the call returns without waiting for
+ *    the device (no host synchronisation), as the reference's ops do on the
+ *    TF-provided stream.
+ *  - Outputs are allocated by the caller with the shapes the op's shape
+ *    function gives (TF's allocate_output); the library checks them and
+ *    reports INVALID_ARGUMENT on a mismatch.
+ *  - Scratch memory comes from the caller (the `workspace` arguments, sized
+ *    by the *WorkspaceBytes queries), as TF kernels take it from
+ *    allocate_temp.
+ */
+#ifndef TFMA_H_
+#define TFMA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TFMA_MAX_DIMS 8
+
+/* Same numeric values as TF_Code. */
+typedef enum TFMA_Code {
+  TFMA_OK = 0,
+  TFMA_CANCELLED = 1,
+  TFMA_UNKNOWN = 2,
+  TFMA_INVALID_ARGUMENT = 3,
+  TFMA_NOT_FOUND = 5,
+  TFMA_RESOURCE_EXHAUSTED = 8,
+  TFMA_FAILED_PRECONDITION = 9,
+  TFMA_OUT_OF_RANGE = 11,
+  TFMA_UNIMPLEMENTED = 12,
+  TFMA_INTERNAL = 13,
+  TFMA_UNAVAILABLE = 14
+} TFMA_Code;
+
+/* Same numeric values as TF_DataType. */
+typedef enum TFMA_DataType {
+  TFMA_FLOAT = 1,
+  TFMA_DOUBLE = 2,
+  TFMA_INT32 = 3,
+  TFMA_INT64 = 9,
+  TFMA_BFLOAT16 = 14,
+  TFMA_HALF = 19
+} TFMA_DataType;
+
+/* A dense, row-major tensor: device memory unless an entry point says the
+ * argument is host memory (TF's HostMemory inputs). */
+typedef struct TFMA_Tensor {
+  void* data;
+  int32_t dtype;  /* TFMA_DataType */
+  int32_t ndims;  /* 0 .. TFMA_MAX_DIMS */
+  int64_t dims[TFMA_MAX_DIMS];
+} TFMA_Tensor;
+
+/* Mirrors TF_Status: a code and a NUL-terminated message. */
+typedef struct TFMA_Status {
+  int32_t code;
+  char message[500];
+} TFMA_Status;
+
+/* ---------------------------------------------------------------------------
+ * Library / device
+ * ------------------------------------------------------------------------- */
+
+/* Version string of the library, e.g. "tfma 0.1 gfx950". */
+const char* TFMA_Version(void);
+
+/* Number of visible HIP devices; 0 (and TFMA_OK) when no driver or device is
+ * present.  Replaces plugin_get_device_count
+ * (reference: musa_ext/mu/musa_se_plugin.cc:855-880), including its
+ * "no driver -> zero devices, OK" behaviour. */
+int TFMA_GetDeviceCount(int* count, TFMA_Status* status);
+
+/* ---------------------------------------------------------------------------
+ * FusedBatchNormV3 / FusedBatchNormGradV3
+ * Replaces MusaFusedBatchNormOp<T>::Compute and
+ * MusaFusedBatchNormGradOp<T>::Compute
+ * (reference: musa_ext/kernels/nn/musa_fused_batchnorm_op.cc:42-182, 206-295;
+ * registrations :303-325) together with the BN helper kernels
+ * (musa_ext/kernels/nn/musa_fused_batchnorm_kernel.mu:16-56).
+ *
+ * x/y/y_backprop/x_backprop: rank-4 T tensors, T in {FLOAT, HALF, BFLOAT16};
+ * data_format "NHWC" or "NCHW".  scale, offset, mean, variance and every
+ * statistics output: rank-1 FLOAT tensors of length C (U = float).
+ * reserve_space_3: 0-d FLOAT scalar, written with 0 (reference :59-62,
+ * :100-104).  reserve_space_4/5 of the grad: FLOAT tensors of any length
+ * (the reference allocates [C], :220-223), filled with zeros.
+ * ------------------------------------------------------------------------- */
+
+/* Scratch bytes FusedBatchNormV3 / FusedBatchNormGradV3 need for this x. */
+int TFMA_FusedBatchNormWorkspaceBytes(const TFMA_Tensor* x,
+                                      const char* data_format,
+                                      size_t* bytes, TFMA_Status* status);
+
+int TFMA_FusedBatchNormV3(void* stream, const TFMA_Tensor* x,
+                          const TFMA_Tensor* scale, const TFMA_Tensor* offset,
+                          const TFMA_Tensor* mean, const TFMA_Tensor* variance,
+                          float epsilon, float exponential_avg_factor,
+                          const char* data_format, int is_training,
+                          TFMA_Tensor* y, TFMA_Tensor* batch_mean,
+                          TFMA_Tensor* batch_variance,
+                          TFMA_Tensor* reserve_space_1,
+                          TFMA_Tensor* reserve_space_2,
+                          TFMA_Tensor* reserve_space_3, void* workspace,
+                          size_t workspace_bytes, TFMA_Status* status);
+
+int TFMA_FusedBatchNormGradV3(
+    void* stream, const TFMA_Tensor* y_backprop, const TFMA_Tensor* x,
+    const TFMA_Tensor* scale, const TFMA_Tensor* reserve_space_1,
+    const TFMA_Tensor* reserve_space_2, const TFMA_Tensor* reserve_space_3,
+    float epsilon, const char* data_format, int is_training,
+    TFMA_Tensor* x_backprop, TFMA_Tensor* scale_backprop,
+    TFMA_Tensor* offset_backprop, TFMA_Tensor* reserve_space_4,
+    TFMA_Tensor* reserve_space_5, void* workspace, size_t workspace_bytes,
+    TFMA_Status* status);
+
+/* ---------------------------------------------------------------------------
+ * ResourceApplyAdam
+ * Replaces MusaResourceApplyAdamOp<T>::Compute
+ * (reference: musa_ext/kernels/training/musa_applyadam_op.cc:130-416,
+ * registration :645-682) and its fp32 kernel
+ * (musa_ext/kernels/training/musa_apply_sparse_adam_kernel.mu:140-169).
+ *
+ * var, m, v: the variables' device tensors, updated in place; grad: device
+ * tensor; all the same shape and dtype T in {FLOAT, HALF, BFLOAT16, DOUBLE}.
+ * beta1_power .. epsilon: 0-d HOST tensors of dtype T (HostMemory inputs).
+ * A NULL var/m/v data pointer with a non-empty shape is an uninitialised
+ * variable (FAILED_PRECONDITION).  use_locking serialises calls that touch
+ * the same var/m/v memory through this library (locks taken in address
+ * order, reference :138-156).
+ * ------------------------------------------------------------------------- */
+int TFMA_ResourceApplyAdam(void* stream, TFMA_Tensor* var, TFMA_Tensor* m,
+                           TFMA_Tensor* v, const TFMA_Tensor* beta1_power,
+                           const TFMA_Tensor* beta2_power,
+                           const TFMA_Tensor* lr, const TFMA_Tensor* beta1,
+                           const TFMA_Tensor* beta2,
+                           const TFMA_Tensor* epsilon, const TFMA_Tensor* grad,
+                           int use_locking, int use_nesterov,
+                           TFMA_Status* status);
+
+/* Multi-tensor Adam: N independent ResourceApplyAdam updates with shared
+ * host scalars in one launch; each element's result is bit-identical to
+ * TFMA_ResourceApplyAdam on that tensor.  No reference op exists; it follows
+ * the reference's grouped optimizer op
+ * MusaGroupedResourceApplyGradientDescentMixed
+ * (reference: musa_ext/kernels/training/musa_applygradientdescent_op.cc:
+ * 305-448, kernel musa_applygradientdescent_kernel.mu:31-105) with inputs
+ * vars/ms/vs/grads: N tensors each.  The per-launch tensor table lives in
+ * `workspace` (TFMA_GroupedApplyAdamWorkspaceBytes); the library uploads it
+ * on the stream, so the workspace must stay allocated until the launch has
+ * run. */
+int TFMA_GroupedApplyAdamWorkspaceBytes(int n, const TFMA_Tensor* vars,
+                                        size_t* bytes, TFMA_Status* status);
+
+int TFMA_GroupedResourceApplyAdam(
+    void* stream, int n, TFMA_Tensor* vars, TFMA_Tensor* ms, TFMA_Tensor* vs,
+    const TFMA_Tensor* grads, const TFMA_Tensor* beta1_power,
+    const TFMA_Tensor* beta2_power, const TFMA_Tensor* lr,
+    const TFMA_Tensor* beta1, const TFMA_Tensor* beta2,
+    const TFMA_Tensor* epsilon, int use_locking, int use_nesterov,
+    void* workspace, size_t workspace_bytes, TFMA_Status* status);
+
+/* ---------------------------------------------------------------------------
+ * Elementwise ops and fused chains, T in {FLOAT, HALF, BFLOAT16}.
+ * Stock ops replace MusaBiasAddOp (musa_ext/kernels/nn/musa_biasadd_op.cc:
+ * 10-82), MusaReluOp (musa_ext/kernels/nn/musa_relu_op.cc:10-60),
+ * MusaAddOp (musa_ext/kernels/math/musa_add_op.cc:379-470) and
+ * MusaMultiplyOp (musa_ext/kernels/math/musa_multiply_op.cc:248-324).
+ * Binary ops follow TF broadcasting (BCast); `z`/`output` must have the
+ * broadcast shape.
+ * ------------------------------------------------------------------------- */
+int TFMA_BiasAdd(void* stream, const TFMA_Tensor* value,
+                 const TFMA_Tensor* bias, const char* data_format,
+                 TFMA_Tensor* output, TFMA_Status* status);
+int TFMA_Relu(void* stream, const TFMA_Tensor* features,
+              TFMA_Tensor* activations, TFMA_Status* status);
+int TFMA_AddV2(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* y,
+               TFMA_Tensor* z, TFMA_Status* status);
+int TFMA_Mul(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* y,
+             TFMA_Tensor* z, TFMA_Status* status);
+
+/* Fused Relu(BiasAdd(value, bias)).  No live reference op: the reference
+ * runs BiasAdd then Relu (musa_biasadd_op.cc:10-70, musa_relu_op.cc:10-62);
+ * its only fused kernel, BiasAddReluKernel
+ * (musa_ext/kernels/fusion/musa_linear_relu_kernel.mu:41-91), has no
+ * caller.  Result is bitwise equal to the unfused pair. */
+int TFMA_MusaBiasAddRelu(void* stream, const TFMA_Tensor* value,
+                         const TFMA_Tensor* bias, const char* data_format,
+                         TFMA_Tensor* output, TFMA_Status* status);
+
+/* Fused Relu(AddV2(x, y)) with TF broadcasting.  No reference op: the
+ * reference runs MusaAddOp then MusaReluOp (musa_add_op.cc:388-459).
+ * Bitwise equal to the unfused pair. */
+int TFMA_MusaAddV2Relu(void* stream, const TFMA_Tensor* x,
+                       const TFMA_Tensor* y, TFMA_Tensor* z,
+                       TFMA_Status* status);
+
+/* Fused Mul+Add: output = data_left * mask + sliced_var_right, each input
+ * broadcast to the output (rank <= 8), rounded after the multiply and after
+ * the add as the unfused Mul -> AddV2 pair is.  Same op name, inputs and
+ * broadcast shape rule as MusaShiftedAffineMap
+ * (musa_ext/kernels/fusion/musa_shifted_affine_map_op.cc:108-262). */
+int TFMA_MusaShiftedAffineMap(void* stream, const TFMA_Tensor* data_left,
+                              const TFMA_Tensor* mask,
+                              const TFMA_Tensor* sliced_var_right,
+                              TFMA_Tensor* output, TFMA_Status* status);
+
+/* ---------------------------------------------------------------------------
+ * Kernel timing.  No reference counterpart (the reference removed its kernel
+ * timing macros and points to external profilers).  When a kernel whose name
+ * contains `name_substr` is launched by this library, HIP events are
+ * recorded on the launch stream right before and after it; TFMA_TraceRead
+ * returns the summed event time and the launch count.  TFMA_TraceEnable(NULL)
+ * switches tracing off.  Not thread-safe against concurrent launches.
+ * ------------------------------------------------------------------------- */
+int TFMA_TraceEnable(const char* name_substr, TFMA_Status* status);
+int TFMA_TraceRead(double* total_ms, int64_t* launches, TFMA_Status* status);
+
+/* Name of the last kernel this library launched on the calling thread (for
+ * tests that check which path an op took). */
+const char* TFMA_LastKernelName(void);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* TFMA_H_ */

@@ -1,0 +1,392 @@
+/*
+ * tfcpu_oracle.c - CPU restatement of TensorFlow's CPU kernels for the hot
+ * path (FusedBatchNormV3 / FusedBatchNormGradV3, ResourceApplyAdam, and the
+ * elementwise ops behind BiasAdd+Relu, AddV2+Relu, Mul+Add).
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP
+ * library and the CPU baseline ("port") that bench.py times; nothing in the
+ * product links, loads or calls it.
+ *
+ * The reference (MooreThreads/tensorflow_musa_extension) defers this
+ * arithmetic to closed muDNN kernels and judges it against TF's CPU kernels
+ * (test/musa_test_utils.py:82-111), so the oracle restates TF-CPU semantics,
+ * with the conventions the reference documents:
+ *   - BN statistics, Bessel factor and reserve-space meaning:
+ *     musa_ext/kernels/nn/musa_fused_batchnorm_op.cc:13-15, 60-62, 141-170,
+ *     265-277 (grad takes population variance + epsilon).
+ *   - Adam inputs / alpha / dtypes: musa_ext/kernels/training/
+ *     musa_applyadam_op.cc:158-186, 224-246, 645-682 (alpha is computed the
+ *     TF-CPU way, in T, not in double as the reference does).
+ *   - BiasAdd channel dimension: musa_ext/kernels/nn/musa_biasadd_op.cc:31-52.
+ *   - Broadcasting: musa_ext/kernels/math/musa_add_op.cc:194-220, 397-403;
+ *     musa_ext/kernels/fusion/musa_shifted_affine_map_op.cc:108-165.
+ * Summation order is the one deliberate difference from TF: BN sums are
+ * accumulated in double (TF sums in float in Eigen's tree order), so the
+ * oracle is closer to the exact value than TF; the rest rounds exactly where
+ * TF does.  Build with -ffp-contract=off (see Makefile).
+ *
+ * dtype codes are TF_DataType values: 1 float, 2 double, 14 bfloat16, 19 half.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+enum { DT_FLOAT = 1, DT_DOUBLE = 2, DT_BFLOAT16 = 14, DT_HALF = 19 };
+
+/* ------------------------------------------------------------------------ */
+/* half / bfloat16 <-> float, round to nearest even                          */
+/* ------------------------------------------------------------------------ */
+static inline uint32_t fbits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float bitsf(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+uint16_t oracle_f32_to_f16(float f) {
+  uint32_t x = fbits(f);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  int32_t exp = (int32_t)((x >> 23) & 0xff);
+  uint32_t man = x & 0x7fffffu;
+  if (exp == 0xff) return (uint16_t)(sign | 0x7c00u | (man ? (0x200u | (man >> 13)) : 0u));
+  int32_t e = exp - 112; /* rebias 127 -> 15 */
+  if (e >= 0x1f) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    if (e < -10) return (uint16_t)sign;
+    man |= 0x800000u;
+    uint32_t sh = (uint32_t)(14 - e);
+    uint32_t q = man >> sh, r = man & ((1u << sh) - 1u), hw = 1u << (sh - 1u);
+    if (r > hw || (r == hw && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+  }
+  uint32_t q = ((uint32_t)e << 10) | (man >> 13), r = man & 0x1fffu;
+  if (r > 0x1000u || (r == 0x1000u && (q & 1u))) q++;
+  return (uint16_t)(sign | q);
+}
+
+float oracle_f16_to_f32(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1fu, man = h & 0x3ffu;
+  if (exp == 0) {
+    float v = (float)man * 5.9604644775390625e-8f; /* 2^-24 */
+    return sign ? -v : v;
+  }
+  if (exp == 0x1f) return bitsf(sign | 0x7f800000u | (man << 13));
+  return bitsf(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+uint16_t oracle_f32_to_bf16(float f) {
+  uint32_t u = fbits(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u & 0x80000000u) ? 0xffc0u : 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float oracle_bf16_to_f32(uint16_t h) { return bitsf((uint32_t)h << 16); }
+
+static inline float ld(int dt, const void* p, int64_t i) {
+  switch (dt) {
+    case DT_FLOAT: return ((const float*)p)[i];
+    case DT_HALF: return oracle_f16_to_f32(((const uint16_t*)p)[i]);
+    case DT_BFLOAT16: return oracle_bf16_to_f32(((const uint16_t*)p)[i]);
+  }
+  return 0.f;
+}
+static inline void st(int dt, void* p, int64_t i, float v) {
+  switch (dt) {
+    case DT_FLOAT: ((float*)p)[i] = v; break;
+    case DT_HALF: ((uint16_t*)p)[i] = oracle_f32_to_f16(v); break;
+    case DT_BFLOAT16: ((uint16_t*)p)[i] = oracle_f32_to_bf16(v); break;
+  }
+}
+/* round a float to T and back */
+static inline float rnd(int dt, float v) {
+  switch (dt) {
+    case DT_HALF: return oracle_f16_to_f32(oracle_f32_to_f16(v));
+    case DT_BFLOAT16: return oracle_bf16_to_f32(oracle_f32_to_bf16(v));
+  }
+  return v;
+}
+
+static int g_threads = 1;
+void oracle_set_threads(int n) { g_threads = n > 0 ? n : 1; }
+int oracle_get_threads(void) { return g_threads; }
+
+/* element (image n, channel c, spatial s) of an NHWC or NCHW tensor */
+static inline int64_t bn_index(int nhwc, int64_t n, int64_t c, int64_t s, int64_t C, int64_t S) {
+  return nhwc ? (n * S + s) * C + c : (n * C + c) * S + s;
+}
+
+/* Per-channel double sums of f(x[, dy]) over all N*S positions, parallel
+ * over images with per-thread accumulators combined in thread order. */
+typedef struct {
+  int dt, nhwc;
+  const void* x;
+  const void* dy;
+  int64_t N, C, S;
+  const float* center; /* per-channel value subtracted from x (float op) */
+  const float* k;      /* grad: per-channel rsqrt, for sum(dy * (xc*k)) */
+} bn_sum_args;
+
+/* mode 0: s1 = sum x
+ * mode 1: s1 = sum (xc)^2 where xc = x - center (float)
+ * mode 2: s1 = sum dy, s2 = sum (dy*xc) (float product), s3 = sum dy*(xc*k) */
+static void bn_sums(const bn_sum_args* a, int mode, double* s1, double* s2, double* s3) {
+  const int64_t C = a->C;
+  int nt = g_threads;
+  if (nt > a->N) nt = (int)(a->N > 0 ? a->N : 1);
+  double* acc = (double*)calloc((size_t)nt * 3 * (size_t)C, sizeof(double));
+#ifdef _OPENMP
+#pragma omp parallel num_threads(nt)
+#endif
+  {
+#ifdef _OPENMP
+    int t = omp_get_thread_num();
+#else
+    int t = 0;
+#endif
+    double* p1 = acc + (size_t)t * 3 * C;
+    double* p2 = p1 + C;
+    double* p3 = p2 + C;
+    int64_t nb = a->N * t / nt, ne = a->N * (t + 1) / nt;
+    for (int64_t n = nb; n < ne; ++n) {
+      for (int64_t s = 0; s < a->S; ++s) {
+        for (int64_t c = 0; c < C; ++c) {
+          int64_t i = bn_index(a->nhwc, n, c, s, C, a->S);
+          float xv = ld(a->dt, a->x, i);
+          if (mode == 0) {
+            p1[c] += xv;
+          } else if (mode == 1) {
+            float xc = xv - a->center[c];
+            p1[c] += (double)xc * (double)xc;
+          } else {
+            float d = ld(a->dt, a->dy, i);
+            float xc = xv - a->center[c];
+            p1[c] += d;
+            p2[c] += (double)(d * xc);
+            p3[c] += (double)(d * (xc * a->k[c]));
+          }
+        }
+      }
+    }
+  }
+  for (int64_t c = 0; c < C; ++c) {
+    double a1 = 0, a2 = 0, a3 = 0;
+    for (int t = 0; t < nt; ++t) {
+      a1 += acc[(size_t)t * 3 * C + c];
+      a2 += acc[(size_t)t * 3 * C + C + c];
+      a3 += acc[(size_t)t * 3 * C + 2 * C + c];
+    }
+    if (s1) s1[c] = a1;
+    if (s2) s2[c] = a2;
+    if (s3) s3[c] = a3;
+  }
+  free(acc);
+}
+
+/* FusedBatchNormV3 forward (TF CPU FusedBatchNorm<CPUDevice, T, float>). */
+void oracle_bn_fwd(int dt, int nhwc, const void* x, int64_t N, int64_t C, int64_t S,
+                   const float* scale, const float* offset, const float* mean_in,
+                   const float* var_in, float eps, float f, int is_training, void* y,
+                   float* batch_mean, float* batch_var, float* saved_mean, float* saved_var) {
+  const int64_t n = N * S;
+  float* mean = (float*)malloc(sizeof(float) * (size_t)(C > 0 ? C : 1));
+  float* var = (float*)malloc(sizeof(float) * (size_t)(C > 0 ? C : 1));
+  float* scaling = (float*)malloc(sizeof(float) * (size_t)(C > 0 ? C : 1));
+  if (is_training) {
+    if (n == 0) {
+      for (int64_t c = 0; c < C; ++c) {
+        batch_mean[c] = NAN; batch_var[c] = NAN; saved_mean[c] = 0.f; saved_var[c] = 0.f;
+      }
+      free(mean); free(var); free(scaling);
+      return;
+    }
+    double* s = (double*)malloc(sizeof(double) * (size_t)C);
+    bn_sum_args a = {dt, nhwc, x, NULL, N, C, S, NULL, NULL};
+    bn_sums(&a, 0, s, NULL, NULL);
+    for (int64_t c = 0; c < C; ++c) mean[c] = (float)(s[c] / (double)n);
+    a.center = mean;
+    bn_sums(&a, 1, s, NULL, NULL);
+    for (int64_t c = 0; c < C; ++c) var[c] = (float)(s[c] / (double)n);
+    free(s);
+    const float adj = (float)n / (float)(n > 1 ? n - 1 : 1);
+    for (int64_t c = 0; c < C; ++c) {
+      saved_mean[c] = mean[c];
+      saved_var[c] = var[c];
+      if (f == 1.0f) {
+        batch_mean[c] = mean[c];
+        batch_var[c] = var[c] * adj;
+      } else {
+        const float omf = 1.0f - f;
+        batch_mean[c] = mean_in[c] * omf + mean[c] * f;
+        batch_var[c] = var_in[c] * omf + (var[c] * adj) * f;
+      }
+    }
+  } else {
+    for (int64_t c = 0; c < C; ++c) {
+      mean[c] = mean_in[c];
+      var[c] = var_in[c];
+      batch_mean[c] = mean_in[c];
+      batch_var[c] = var_in[c];
+      saved_mean[c] = mean_in[c];
+      saved_var[c] = var_in[c];
+    }
+  }
+  for (int64_t c = 0; c < C; ++c) scaling[c] = (1.0f / sqrtf(var[c] + eps)) * scale[c];
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+#endif
+  for (int64_t nn = 0; nn < N; ++nn)
+    for (int64_t s = 0; s < S; ++s)
+      for (int64_t c = 0; c < C; ++c) {
+        int64_t i = bn_index(nhwc, nn, c, s, C, S);
+        float xc = ld(dt, x, i) - mean[c];
+        st(dt, y, i, xc * scaling[c] + offset[c]);
+      }
+  free(mean); free(var); free(scaling);
+}
+
+/* FusedBatchNormGradV3 (TF CPU FusedBatchNormGrad<CPUDevice, T, float>);
+ * mean/var are reserve_space_1/2 (population variance). */
+void oracle_bn_grad(int dt, int nhwc, const void* dy, const void* x, int64_t N, int64_t C,
+                    int64_t S, const float* scale, const float* mean, const float* var,
+                    float eps, int is_training, void* dx, float* scale_bp, float* offset_bp) {
+  const int64_t n = N * S;
+  if (C == 0) return;
+  if (n == 0) {
+    for (int64_t c = 0; c < C; ++c) { scale_bp[c] = 0.f; offset_bp[c] = 0.f; }
+    return;
+  }
+  float* k = (float*)malloc(sizeof(float) * (size_t)C);
+  float* coef1 = (float*)malloc(sizeof(float) * (size_t)C);
+  float* coef2 = (float*)malloc(sizeof(float) * (size_t)C);
+  float* mdy = (float*)malloc(sizeof(float) * (size_t)C);
+  double* s1 = (double*)malloc(sizeof(double) * (size_t)C);
+  double* s2 = (double*)malloc(sizeof(double) * (size_t)C);
+  double* s3 = (double*)malloc(sizeof(double) * (size_t)C);
+  for (int64_t c = 0; c < C; ++c) k[c] = 1.0f / sqrtf(var[c] + eps);
+  bn_sum_args a = {dt, nhwc, x, dy, N, C, S, mean, k};
+  bn_sums(&a, 2, s1, s2, s3);
+  for (int64_t c = 0; c < C; ++c) {
+    offset_bp[c] = (float)s1[c];
+    scale_bp[c] = (float)s3[c];
+    coef1[c] = scale[c] * k[c];
+    if (is_training) {
+      mdy[c] = (float)(s1[c] / (double)n);
+      coef2[c] = (k[c] * k[c]) * (float)(s2[c] / (double)n);
+    } else {
+      mdy[c] = 0.f;
+      coef2[c] = 0.f;
+    }
+  }
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+#endif
+  for (int64_t nn = 0; nn < N; ++nn)
+    for (int64_t s = 0; s < S; ++s)
+      for (int64_t c = 0; c < C; ++c) {
+        int64_t i = bn_index(nhwc, nn, c, s, C, S);
+        float xc = ld(dt, x, i) - mean[c];
+        float d = ld(dt, dy, i);
+        float r = is_training ? coef1[c] * ((d - mdy[c]) - xc * coef2[c]) : d * coef1[c];
+        st(dt, dx, i, r);
+      }
+  free(k); free(coef1); free(coef2); free(mdy); free(s1); free(s2); free(s3);
+}
+
+/* ResourceApplyAdam (TF CPU ApplyAdamNonCuda): in place on var/m/v; the
+ * scalars are given as doubles holding T values exactly. */
+void oracle_adam(int dt, void* var, void* m, void* v, const void* grad, int64_t n, double b1p_,
+                 double b2p_, double lr_, double b1_, double b2_, double eps_, int nesterov) {
+  if (dt == DT_DOUBLE) {
+    double* X = (double*)var; double* M = (double*)m; double* V = (double*)v;
+    const double* G = (const double*)grad;
+    const double alpha = lr_ * sqrt(1.0 - b2p_) / (1.0 - b1p_);
+    const double omb1 = 1.0 - b1_, omb2 = 1.0 - b2_;
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+#endif
+    for (int64_t i = 0; i < n; ++i) {
+      double g = G[i];
+      M[i] += (g - M[i]) * omb1;
+      V[i] += (g * g - V[i]) * omb2;
+      if (nesterov)
+        X[i] -= ((g * omb1 + b1_ * M[i]) * alpha) / (sqrt(V[i]) + eps_);
+      else
+        X[i] -= (M[i] * alpha) / (sqrt(V[i]) + eps_);
+    }
+    return;
+  }
+  const float b1p = (float)b1p_, b2p = (float)b2p_, lr = (float)lr_;
+  const float b1 = (float)b1_, b2 = (float)b2_, eps = (float)eps_;
+  /* alpha = lr * sqrt(1 - beta2_power) / (1 - beta1_power), in T */
+  const float alpha = rnd(dt, rnd(dt, lr * rnd(dt, sqrtf(rnd(dt, 1.0f - b2p)))) /
+                                  rnd(dt, 1.0f - b1p));
+  const float omb1 = rnd(dt, 1.0f - b1), omb2 = rnd(dt, 1.0f - b2);
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+#endif
+  for (int64_t i = 0; i < n; ++i) {
+    const float g = ld(dt, grad, i);
+    float mm = ld(dt, m, i), vv = ld(dt, v, i), xx = ld(dt, var, i);
+    mm = rnd(dt, mm + rnd(dt, rnd(dt, g - mm) * omb1));
+    vv = rnd(dt, vv + rnd(dt, rnd(dt, rnd(dt, g * g) - vv) * omb2));
+    float num;
+    if (nesterov)
+      num = rnd(dt, rnd(dt, rnd(dt, g * omb1) + rnd(dt, b1 * mm)) * alpha);
+    else
+      num = rnd(dt, mm * alpha);
+    const float den = rnd(dt, rnd(dt, sqrtf(vv)) + eps);
+    xx = rnd(dt, xx - rnd(dt, num / den));
+    st(dt, m, i, mm);
+    st(dt, v, i, vv);
+    st(dt, var, i, xx);
+  }
+}
+
+/* Elementwise ops with TF broadcasting.  op: 0 add, 1 add+relu, 2 mul,
+ * 3 mul+add (in0*in1 rounded, + in2), 4 relu.  Each input i has rank
+ * in_ndims[i] <= 8 and dims in_dims[8*i ...]; out has rank out_ndims. */
+void oracle_eltwise(int dt, int op, int nin, const void* const* ins, const int64_t* in_dims,
+                    const int* in_ndims, int out_ndims, const int64_t* out_dims, void* out) {
+  int64_t strides[3][8];
+  int64_t total = 1;
+  for (int d = 0; d < out_ndims; ++d) total *= out_dims[d];
+  for (int k = 0; k < nin; ++k) {
+    int64_t s = 1;
+    for (int d = out_ndims - 1; d >= 0; --d) {
+      int it = in_ndims[k] - out_ndims + d;
+      int64_t td = it >= 0 ? in_dims[8 * k + it] : 1;
+      strides[k][d] = (td == out_dims[d]) ? s : 0;
+      s *= td;
+    }
+  }
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+#endif
+  for (int64_t i = 0; i < total; ++i) {
+    int64_t off[3] = {0, 0, 0};
+    int64_t rem = i;
+    for (int d = out_ndims - 1; d >= 0; --d) {
+      int64_t coord = rem % out_dims[d];
+      rem /= out_dims[d];
+      for (int k = 0; k < nin; ++k) off[k] += coord * strides[k][d];
+    }
+    float a = ld(dt, ins[0], off[0]);
+    float r;
+    switch (op) {
+      case 0: r = a + ld(dt, ins[1], off[1]); break;
+      case 1: r = rnd(dt, a + ld(dt, ins[1], off[1])); r = r < 0.f ? 0.f : r; break;
+      case 2: r = a * ld(dt, ins[1], off[1]); break;
+      case 3: r = rnd(dt, a * ld(dt, ins[1], off[1])) + ld(dt, ins[2], off[2]); break;
+      default: r = a < 0.f ? 0.f : a; break;
+    }
+    if (op == 4 && !(a < 0.f)) {
+      /* keep the input bits (Relu(-0) = -0, NaN stays NaN) */
+      if (dt == DT_FLOAT) ((float*)out)[i] = ((const float*)ins[0])[off[0]];
+      else ((uint16_t*)out)[i] = ((const uint16_t*)ins[0])[off[0]];
+    } else {
+      st(dt, out, i, r);
+    }
+  }
+}

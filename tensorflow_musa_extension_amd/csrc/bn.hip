@@ -1,0 +1,660 @@
+// FusedBatchNormV3 / FusedBatchNormGradV3 kernels for gfx950.
+//
+// Semantics (TF CPU kernels, which the reference's op reproduces; reference
+// conventions at musa_ext/kernels/nn/musa_fused_batchnorm_op.cc:13-15,
+// 60-62, 141-170, 265-277):
+//   forward, training, per channel c over the n = N*H*W elements:
+//     mean = sum(x)/n, var = sum((x-mean)^2)/n  (population variance)
+//     y = (x - mean) * (rsqrt(var + eps) * scale) + offset
+//     batch_mean = mean, batch_variance = var * n/(n-1)  (Bessel)
+//       (blended with the running values when exponential_avg_factor != 1)
+//     reserve_space_1 = mean, reserve_space_2 = var, reserve_space_3 = 0
+//   grad, training (reserve_space_1/2 = mean / population variance):
+//     k = rsqrt(var + eps), xc = x - mean
+//     offset_backprop = sum(dy), scale_backprop = k * sum(dy * xc)
+//     dx = scale*k * ((dy - sum(dy)/n) - xc * (k*k * sum(dy*xc)/n))
+//
+// Structure: three kernels per op.
+//   1. reduce:   each workgroup owns a row range x channel tile and writes
+//                one float2 partial per channel (shifted sums for the
+//                forward, sum(dy) / sum(dy*xc) for the grad).  16-byte loads,
+//                8 loads in flight per thread, lanes mapped to channel
+//                vectors so a wave reads whole 512-byte row segments.
+//   2. finalize: per channel, a double-precision sum over the partials;
+//                writes the statistics outputs and 4 per-channel
+//                coefficients.
+//   3. apply:    y (or dx) from x (and dy) and the coefficients.  Row ranges
+//                are walked in the reverse of the reduce order, so the
+//                lines the reduce touched last - still in the 256 MB
+//                Infinity Cache - are re-read first.
+// The forward statistics use sums of (x - K) with K = the channel's first
+// element, which keeps sum((x-K)^2) - sum(x-K)^2/n free of cancellation
+// when |mean| >> std; partials add exactly like plain sums because every
+// workgroup uses the same K.
+#include "device_util.h"
+#include "tfma_internal.h"
+
+namespace tfma {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 8;
+constexpr int kFinCh = 64;      // channels per finalize workgroup
+constexpr int kFinSlices = 16;  // partial slices per finalize workgroup
+
+struct Plan {
+  bool nhwc;
+  int vec;          // elements per thread access
+  int64_t cv;       // channel vectors per row (NHWC) / vectors per plane (NCHW)
+  int tx_shift;     // log2(threads along channels) (NHWC)
+  int ct;           // channel tiles (NHWC) / channels (NCHW)
+  int64_t rows_per_g;
+  int64_t groups;   // G: row groups (NHWC) / image groups (NCHW)
+};
+
+int pow2_ceil_log2(int64_t v) {
+  int s = 0;
+  while ((int64_t(1) << s) < v) ++s;
+  return s;
+}
+
+int target_wgs() {
+  static int t = [] {
+    const char* e = getenv("TFMA_BN_TARGET_WGS");
+    int v = e ? atoi(e) : 0;
+    return v > 0 ? v : 1024;
+  }();
+  return t;
+}
+
+int vec_of(DType t) { return t == DType::kF32 ? 4 : 8; }
+int elem_bytes(DType t) { return t == DType::kF32 ? 4 : 2; }
+
+Plan make_plan(DType t, const BnGeometry& g, bool aligned) {
+  Plan p;
+  p.nhwc = g.nhwc;
+  const int kv = vec_of(t);
+  if (g.nhwc) {
+    p.vec = (aligned && g.c % kv == 0) ? kv : 1;
+    p.cv = g.c / p.vec;
+    int s = pow2_ceil_log2(p.cv);
+    if (s > 5) s = 5;  // at most 32 lanes along channels
+    p.tx_shift = s;
+    const int tx = 1 << s;
+    const int ry = kThreads / tx;
+    p.ct = static_cast<int>((p.cv + tx - 1) / tx);
+    int64_t gt = target_wgs() / p.ct;
+    if (gt < 1) gt = 1;
+    int64_t rpg = (g.rows + gt - 1) / gt;
+    const int64_t min_rows = static_cast<int64_t>(ry) * kUnroll;
+    if (rpg < min_rows) rpg = min_rows;
+    rpg = (rpg + ry - 1) / ry * ry;
+    p.rows_per_g = rpg;
+    p.groups = (g.rows + rpg - 1) / rpg;
+    if (p.groups < 1) p.groups = 1;
+  } else {
+    const int64_t plane = g.h * g.w;
+    p.vec = (aligned && plane % kv == 0) ? kv : 1;
+    p.cv = plane / p.vec;
+    p.tx_shift = 0;
+    p.ct = static_cast<int>(g.c);
+    int64_t gt = target_wgs() / g.c;
+    if (gt < 1) gt = 1;
+    // Images per group: enough vectors per workgroup to keep it busy.
+    int64_t ipg = (g.n + gt - 1) / gt;
+    const int64_t min_imgs = (kThreads * 4 + p.cv - 1) / p.cv;
+    if (ipg < min_imgs) ipg = min_imgs;
+    if (ipg > g.n) ipg = g.n;
+    if (ipg < 1) ipg = 1;
+    p.rows_per_g = ipg;
+    p.groups = (g.n + ipg - 1) / ipg;
+    if (p.groups < 1) p.groups = 1;
+  }
+  return p;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+size_t partial_bytes(const Plan& p, const BnGeometry& g) {
+  return align256(static_cast<size_t>(p.groups) * g.c * sizeof(float2));
+}
+size_t coef_bytes(const BnGeometry& g) {
+  return align256(static_cast<size_t>(g.c) * sizeof(float4));
+}
+
+// ---------------------------------------------------------------------------
+// 1. Reduce.
+// ---------------------------------------------------------------------------
+// kGrad = false: s1 += x - K, s2 += (x - K)^2, K = first element of channel.
+// kGrad = true:  s1 += dy,    s2 += dy * (x - mean).
+template <class Tr, int VEC, bool kGrad>
+__device__ inline void accum(const typename Tr::S (&xv)[VEC],
+                             const typename Tr::S (&dv)[VEC],
+                             const float (&k)[VEC], float (&s1)[VEC],
+                             float (&s2)[VEC]) {
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    const float xc = Tr::ld(xv[j]) - k[j];
+    if constexpr (kGrad) {
+      const float d = Tr::ld(dv[j]);
+      s1[j] += d;
+      s2[j] += d * xc;
+    } else {
+      s1[j] += xc;
+      s2[j] += xc * xc;
+    }
+  }
+}
+
+template <class Tr, int VEC, bool kGrad>
+__global__ __launch_bounds__(kThreads) void bn_nhwc_reduce_kernel(
+    const typename Tr::S* __restrict__ x, const typename Tr::S* __restrict__ dy,
+    const float* __restrict__ mean_in, int64_t rows, int c, int64_t cv,
+    int tx_shift, int64_t rows_per_g, float2* __restrict__ partial) {
+  using S = typename Tr::S;
+  extern __shared__ float2 red[];  // [ry][tx*VEC]
+  const int tx = threadIdx.x & ((1 << tx_shift) - 1);
+  const int ty = threadIdx.x >> tx_shift;
+  const int ry = kThreads >> tx_shift;
+  const int width = (1 << tx_shift) * VEC;
+  const int64_t cvi = static_cast<int64_t>(blockIdx.y) * (1 << tx_shift) + tx;
+  const int64_t g = blockIdx.x;
+  const int64_t r0 = g * rows_per_g;
+  int64_t r1 = r0 + rows_per_g;
+  if (r1 > rows) r1 = rows;
+  float s1[VEC], s2[VEC], k[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) { s1[j] = 0.f; s2[j] = 0.f; }
+  if (cvi < cv) {
+    const int64_t c0 = cvi * VEC;
+    if constexpr (kGrad) {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) k[j] = mean_in[c0 + j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) k[j] = Tr::ld(x[c0 + j]);
+    }
+    const S* __restrict__ px = x + c0;
+    const S* __restrict__ pd = kGrad ? dy + c0 : nullptr;
+    int64_t r = r0 + ty;
+    for (; r + (kUnroll - 1) * ry < r1; r += kUnroll * ry) {
+      S xv[kUnroll][VEC], dv[kUnroll][VEC];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        vload<S, VEC>(px + (r + u * ry) * c, xv[u]);
+        if constexpr (kGrad) vload<S, VEC>(pd + (r + u * ry) * c, dv[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) accum<Tr, VEC, kGrad>(xv[u], dv[u], k, s1, s2);
+    }
+    for (; r < r1; r += ry) {
+      S xv[VEC], dv[VEC];
+      vload<S, VEC>(px + r * c, xv);
+      if constexpr (kGrad) vload<S, VEC>(pd + r * c, dv);
+      accum<Tr, VEC, kGrad>(xv, dv, k, s1, s2);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) red[ty * width + tx * VEC + j] = make_float2(s1[j], s2[j]);
+  __syncthreads();
+  const int64_t cbase = static_cast<int64_t>(blockIdx.y) * width;
+  for (int cl = threadIdx.x; cl < width; cl += kThreads) {
+    if (cbase + cl >= c) break;
+    float a = 0.f, b = 0.f;
+    for (int t = 0; t < ry; ++t) {
+      const float2 v = red[t * width + cl];
+      a += v.x;
+      b += v.y;
+    }
+    partial[g * c + cbase + cl] = make_float2(a, b);
+  }
+}
+
+// NCHW: workgroup (g, ch) reduces images [g*ipg, ...) of channel ch.
+template <class Tr, int VEC, bool kGrad>
+__global__ __launch_bounds__(kThreads) void bn_nchw_reduce_kernel(
+    const typename Tr::S* __restrict__ x, const typename Tr::S* __restrict__ dy,
+    const float* __restrict__ mean_in, int64_t nimg, int c, int64_t plane,
+    int64_t pv, int64_t ipg, FastDiv div_pv, float2* __restrict__ partial) {
+  using S = typename Tr::S;
+  __shared__ float2 red[kThreads];
+  const int ch = blockIdx.y;
+  const int64_t g = blockIdx.x;
+  const int64_t n0 = g * ipg;
+  int64_t n1 = n0 + ipg;
+  if (n1 > nimg) n1 = nimg;
+  float kk = kGrad ? mean_in[ch] : Tr::ld(x[static_cast<int64_t>(ch) * plane]);
+  float k[VEC], s1[VEC], s2[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) { k[j] = kk; s1[j] = 0.f; s2[j] = 0.f; }
+  const uint32_t count = static_cast<uint32_t>((n1 - n0) * pv);
+  for (uint32_t e = threadIdx.x; e < count; e += kThreads) {
+    uint32_t q, r;
+    div_pv.divmod(e, q, r);
+    const int64_t off = ((n0 + q) * c + ch) * plane + static_cast<int64_t>(r) * VEC;
+    S xv[VEC], dv[VEC];
+    vload<S, VEC>(x + off, xv);
+    if constexpr (kGrad) vload<S, VEC>(dy + off, dv);
+    accum<Tr, VEC, kGrad>(xv, dv, k, s1, s2);
+  }
+  float a = 0.f, b = 0.f;
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) { a += s1[j]; b += s2[j]; }
+  red[threadIdx.x] = make_float2(a, b);
+  __syncthreads();
+  for (int s = kThreads / 2; s > 0; s >>= 1) {
+    if (threadIdx.x < s) {
+      red[threadIdx.x].x += red[threadIdx.x + s].x;
+      red[threadIdx.x].y += red[threadIdx.x + s].y;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) partial[g * c + ch] = red[0];
+}
+
+// ---------------------------------------------------------------------------
+// 2. Finalize: per channel, double sums over the G partials.
+// ---------------------------------------------------------------------------
+struct FinArgs {
+  int64_t groups;
+  int c;
+  int64_t n;          // elements per channel
+  const void* x;      // forward shift source (first element of each channel)
+  int64_t k_stride;   // element stride between channels' first elements
+  const float* scale;
+  const float* offset;
+  const float* mean_in;
+  const float* var_in;
+  float eps;
+  float f;            // exponential_avg_factor
+  float* batch_mean;
+  float* batch_var;
+  float* saved_mean;
+  float* saved_var;
+  float* reserve3;
+  // grad
+  float* scale_bp;
+  float* offset_bp;
+  float* reserve4;
+  int64_t reserve4_n;
+  float* reserve5;
+  int64_t reserve5_n;
+  bool is_training;
+};
+
+template <class Tr, bool kGrad>
+__global__ __launch_bounds__(kFinCh* kFinSlices) void bn_finalize_kernel(
+    const float2* __restrict__ partial, FinArgs a, float4* __restrict__ coef) {
+  __shared__ double2 red[kFinSlices][kFinCh];
+  const int lane = threadIdx.x % kFinCh;
+  const int slice = threadIdx.x / kFinCh;
+  const int ch = blockIdx.x * kFinCh + lane;
+  double s1 = 0.0, s2 = 0.0;
+  if (ch < a.c) {
+    for (int64_t g = slice; g < a.groups; g += kFinSlices) {
+      const float2 v = partial[g * a.c + ch];
+      s1 += v.x;
+      s2 += v.y;
+    }
+  }
+  red[slice][lane] = make_double2(s1, s2);
+  __syncthreads();
+  if (slice == 0 && ch < a.c) {
+    for (int s = 1; s < kFinSlices; ++s) {
+      s1 += red[s][lane].x;
+      s2 += red[s][lane].y;
+    }
+    const double n = static_cast<double>(a.n);
+    if constexpr (!kGrad) {
+      const float kshift =
+          Tr::ld(static_cast<const typename Tr::S*>(a.x)[ch * a.k_stride]);
+      const double mean = static_cast<double>(kshift) + s1 / n;
+      double m2 = s2 - s1 * s1 / n;
+      if (m2 < 0.0) m2 = 0.0;
+      const float mean_f = static_cast<float>(mean);
+      const float var_f = static_cast<float>(m2 / n);
+      const float nf = static_cast<float>(a.n);
+      const float nm1 = static_cast<float>(a.n > 1 ? a.n - 1 : 1);
+      const float adj = nf / nm1;
+      a.saved_mean[ch] = mean_f;
+      a.saved_var[ch] = var_f;
+      if (a.f == 1.0f) {
+        a.batch_mean[ch] = mean_f;
+        a.batch_var[ch] = var_f * adj;
+      } else {
+        const float omf = 1.0f - a.f;
+        a.batch_mean[ch] = a.mean_in[ch] * omf + mean_f * a.f;
+        a.batch_var[ch] = a.var_in[ch] * omf + (var_f * adj) * a.f;
+      }
+      const float inv = __fdiv_rn(1.0f, __fsqrt_rn(var_f + a.eps));
+      coef[ch] = make_float4(mean_f, inv * a.scale[ch], a.offset[ch], 0.f);
+    } else {
+      const float mu = a.mean_in[ch];
+      const float k = __fdiv_rn(1.0f, __fsqrt_rn(a.var_in[ch] + a.eps));
+      a.offset_bp[ch] = static_cast<float>(s1);
+      a.scale_bp[ch] = static_cast<float>(s2 * static_cast<double>(k));
+      if (a.is_training) {
+        const float mean_dy = static_cast<float>(s1 / n);
+        const float mean_dyxc = static_cast<float>(s2 / n);
+        coef[ch] = make_float4(mu, a.scale[ch] * k, mean_dy, (k * k) * mean_dyxc);
+      } else {
+        coef[ch] = make_float4(mu, a.scale[ch] * k, 0.f, 0.f);
+      }
+    }
+  }
+  // Zero-filled side outputs.
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t gstride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  if constexpr (!kGrad) {
+    if (gtid == 0 && a.reserve3) a.reserve3[0] = 0.f;
+  } else {
+    for (int64_t i = gtid; i < a.reserve4_n; i += gstride) a.reserve4[i] = 0.f;
+    for (int64_t i = gtid; i < a.reserve5_n; i += gstride) a.reserve5[i] = 0.f;
+  }
+}
+
+// Inference-mode forward coefficients from the running statistics.
+__global__ void bn_infer_coef_kernel(FinArgs a, float4* __restrict__ coef) {
+  const int ch = blockIdx.x * blockDim.x + threadIdx.x;
+  if (ch == 0 && a.reserve3) a.reserve3[0] = 0.f;
+  if (ch >= a.c) return;
+  const float mu = a.mean_in[ch];
+  const float var = a.var_in[ch];
+  const float inv = __fdiv_rn(1.0f, __fsqrt_rn(var + a.eps));
+  a.batch_mean[ch] = mu;
+  a.batch_var[ch] = var;
+  a.saved_mean[ch] = mu;
+  a.saved_var[ch] = var;
+  coef[ch] = make_float4(mu, inv * a.scale[ch], a.offset[ch], 0.f);
+}
+
+// ---------------------------------------------------------------------------
+// 3. Apply.
+// ---------------------------------------------------------------------------
+template <class Tr, bool kGrad>
+__device__ inline typename Tr::S apply_one(typename Tr::S xs, typename Tr::S ds,
+                                           float4 cf) {
+  const float xc = Tr::ld(xs) - cf.x;
+  if constexpr (kGrad) {
+    const float t = Tr::ld(ds) - cf.z;
+    return Tr::st(cf.y * (t - xc * cf.w));
+  } else {
+    return Tr::st(xc * cf.y + cf.z);
+  }
+}
+
+template <class Tr, int VEC, bool kGrad>
+__global__ __launch_bounds__(kThreads) void bn_nhwc_apply_kernel(
+    const typename Tr::S* __restrict__ x, const typename Tr::S* __restrict__ dy,
+    typename Tr::S* __restrict__ out, const float4* __restrict__ coef,
+    int64_t rows, int c, int64_t cv, int tx_shift, int64_t rows_per_g,
+    int64_t groups) {
+  using S = typename Tr::S;
+  const int tx = threadIdx.x & ((1 << tx_shift) - 1);
+  const int ty = threadIdx.x >> tx_shift;
+  const int ry = kThreads >> tx_shift;
+  const int64_t cvi = static_cast<int64_t>(blockIdx.y) * (1 << tx_shift) + tx;
+  if (cvi >= cv) return;
+  const int64_t g = groups - 1 - blockIdx.x;  // reverse of the reduce order
+  const int64_t r0 = g * rows_per_g;
+  int64_t r1 = r0 + rows_per_g;
+  if (r1 > rows) r1 = rows;
+  const int64_t c0 = cvi * VEC;
+  float4 cf[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) cf[j] = coef[c0 + j];
+  if (r0 + ty >= r1) return;
+  const int64_t nr = (r1 - r0 - ty + ry - 1) / ry;  // rows of this thread
+  const S* __restrict__ px = x + c0;
+  const S* __restrict__ pd = kGrad ? dy + c0 : nullptr;
+  S* __restrict__ po = out + c0;
+  // Walk this thread's rows last-to-first.
+  int64_t k = nr - 1;
+  for (; k >= kUnroll - 1; k -= kUnroll) {
+    S xv[kUnroll][VEC], dv[kUnroll][VEC];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t r = r0 + ty + (k - u) * ry;
+      vload<S, VEC>(px + r * c, xv[u]);
+      if constexpr (kGrad) vload<S, VEC>(pd + r * c, dv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t r = r0 + ty + (k - u) * ry;
+      S ov[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j)
+        ov[j] = apply_one<Tr, kGrad>(xv[u][j], kGrad ? dv[u][j] : xv[u][j], cf[j]);
+      vstore<S, VEC>(po + r * c, ov);
+    }
+  }
+  for (; k >= 0; --k) {
+    const int64_t r = r0 + ty + k * ry;
+    S xv[VEC], dv[VEC], ov[VEC];
+    vload<S, VEC>(px + r * c, xv);
+    if constexpr (kGrad) vload<S, VEC>(pd + r * c, dv);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j)
+      ov[j] = apply_one<Tr, kGrad>(xv[j], kGrad ? dv[j] : xv[j], cf[j]);
+    vstore<S, VEC>(po + r * c, ov);
+  }
+}
+
+// NCHW apply: flat over vectors (plane % VEC == 0 keeps a vector inside one
+// (image, channel) plane); channel = (i / plane) % C.  Reverse order.
+template <class Tr, int VEC, bool kGrad>
+__global__ __launch_bounds__(kThreads) void bn_nchw_apply_kernel(
+    const typename Tr::S* __restrict__ x, const typename Tr::S* __restrict__ dy,
+    typename Tr::S* __restrict__ out, const float4* __restrict__ coef,
+    int64_t nvec, int64_t pv, int c) {
+  using S = typename Tr::S;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t i = nvec - 1 - (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x);
+       i >= 0; i -= stride) {
+    const int ch = static_cast<int>((i / pv) % c);
+    const float4 cf = coef[ch];
+    S xv[VEC], dv[VEC], ov[VEC];
+    vload<S, VEC>(x + i * VEC, xv);
+    if constexpr (kGrad) vload<S, VEC>(dy + i * VEC, dv);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j)
+      ov[j] = apply_one<Tr, kGrad>(xv[j], kGrad ? dv[j] : xv[j], cf);
+    vstore<S, VEC>(out + i * VEC, ov);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host drivers.
+// ---------------------------------------------------------------------------
+template <class Tr, int VEC, bool kGrad>
+hipError_t launch_reduce(const Plan& p, const BnGeometry& g, const void* x,
+                         const void* dy, const float* mean_in, float2* partial,
+                         hipStream_t stream) {
+  using S = typename Tr::S;
+  if (p.nhwc) {
+    const size_t smem = static_cast<size_t>(kThreads) * VEC * sizeof(float2);
+    LaunchScope scope(stream, kGrad ? "tfma_bn_grad_reduce" : "tfma_bn_fwd_reduce");
+    hipLaunchKernelGGL((bn_nhwc_reduce_kernel<Tr, VEC, kGrad>),
+                       dim3(p.groups, p.ct), dim3(kThreads), smem, stream,
+                       static_cast<const S*>(x), static_cast<const S*>(dy),
+                       mean_in, g.rows, static_cast<int>(g.c), p.cv, p.tx_shift,
+                       p.rows_per_g, partial);
+  } else {
+    LaunchScope scope(stream, kGrad ? "tfma_bn_grad_reduce_nchw" : "tfma_bn_fwd_reduce_nchw");
+    hipLaunchKernelGGL((bn_nchw_reduce_kernel<Tr, VEC, kGrad>),
+                       dim3(p.groups, g.c), dim3(kThreads), 0, stream,
+                       static_cast<const S*>(x), static_cast<const S*>(dy),
+                       mean_in, g.n, static_cast<int>(g.c), g.h * g.w, p.cv,
+                       p.rows_per_g, FastDiv(static_cast<uint32_t>(p.cv)),
+                       partial);
+  }
+  return hipGetLastError();
+}
+
+template <class Tr, int VEC, bool kGrad>
+hipError_t launch_apply(const Plan& p, const BnGeometry& g, const void* x,
+                        const void* dy, void* out, const float4* coef,
+                        hipStream_t stream) {
+  using S = typename Tr::S;
+  if (p.nhwc) {
+    LaunchScope scope(stream, kGrad ? "tfma_bn_grad_apply" : "tfma_bn_fwd_apply");
+    hipLaunchKernelGGL((bn_nhwc_apply_kernel<Tr, VEC, kGrad>),
+                       dim3(p.groups, p.ct), dim3(kThreads), 0, stream,
+                       static_cast<const S*>(x), static_cast<const S*>(dy),
+                       static_cast<S*>(out), coef, g.rows, static_cast<int>(g.c),
+                       p.cv, p.tx_shift, p.rows_per_g, p.groups);
+  } else {
+    const int64_t nvec = g.n * g.c * p.cv;
+    int64_t blocks = (nvec + kThreads * 4 - 1) / (kThreads * 4);
+    const int64_t maxb = static_cast<int64_t>(DeviceCUs()) * 16;
+    if (blocks > maxb) blocks = maxb;
+    if (blocks < 1) blocks = 1;
+    LaunchScope scope(stream, kGrad ? "tfma_bn_grad_apply_nchw" : "tfma_bn_fwd_apply_nchw");
+    hipLaunchKernelGGL((bn_nchw_apply_kernel<Tr, VEC, kGrad>), dim3(blocks),
+                       dim3(kThreads), 0, stream, static_cast<const S*>(x),
+                       static_cast<const S*>(dy), static_cast<S*>(out), coef,
+                       nvec, p.cv, static_cast<int>(g.c));
+  }
+  return hipGetLastError();
+}
+
+template <class Tr, bool kGrad>
+hipError_t launch_finalize(const Plan& p, const FinArgs& fa,
+                           const float2* partial, float4* coef,
+                           hipStream_t stream) {
+  const int blocks = (fa.c + kFinCh - 1) / kFinCh;
+  LaunchScope scope(stream, kGrad ? "tfma_bn_grad_finalize" : "tfma_bn_fwd_finalize");
+  hipLaunchKernelGGL((bn_finalize_kernel<Tr, kGrad>), dim3(blocks),
+                     dim3(kFinCh * kFinSlices), 0, stream, partial, fa, coef);
+  (void)p;
+  return hipGetLastError();
+}
+
+bool ptr_aligned(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+}
+
+template <class Tr>
+hipError_t forward_t(const BnGeometry& g, const BnFwdArgs& a, void* ws,
+                     size_t ws_bytes, hipStream_t stream) {
+  const bool aligned = ptr_aligned(a.x) && ptr_aligned(a.y);
+  const Plan p = make_plan(Tr::kVec == 4 ? DType::kF32 : DType::kF16, g, aligned);
+  const size_t pb = partial_bytes(p, g);
+  if (ws_bytes < pb + coef_bytes(g)) return hipErrorInvalidValue;
+  float2* partial = static_cast<float2*>(ws);
+  float4* coef = reinterpret_cast<float4*>(static_cast<char*>(ws) + pb);
+  FinArgs fa{};
+  fa.groups = p.groups;
+  fa.c = static_cast<int>(g.c);
+  fa.n = g.rows;
+  fa.x = a.x;
+  fa.k_stride = g.nhwc ? 1 : g.h * g.w;
+  fa.scale = a.scale;
+  fa.offset = a.offset;
+  fa.mean_in = a.mean_in;
+  fa.var_in = a.var_in;
+  fa.eps = a.epsilon;
+  fa.f = a.exp_avg_factor;
+  fa.batch_mean = a.batch_mean;
+  fa.batch_var = a.batch_var;
+  fa.saved_mean = a.saved_mean;
+  fa.saved_var = a.saved_var;
+  fa.reserve3 = a.reserve3;
+  fa.is_training = a.is_training;
+  hipError_t e;
+  if (a.is_training) {
+    e = p.vec == 1 ? launch_reduce<Tr, 1, false>(p, g, a.x, nullptr, nullptr, partial, stream)
+                   : launch_reduce<Tr, Tr::kVec, false>(p, g, a.x, nullptr, nullptr, partial, stream);
+    if (e != hipSuccess) return e;
+    e = launch_finalize<Tr, false>(p, fa, partial, coef, stream);
+  } else {
+    LaunchScope scope(stream, "tfma_bn_infer_coef");
+    hipLaunchKernelGGL(bn_infer_coef_kernel, dim3((g.c + 255) / 256), dim3(256),
+                       0, stream, fa, coef);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
+  return p.vec == 1 ? launch_apply<Tr, 1, false>(p, g, a.x, nullptr, a.y, coef, stream)
+                    : launch_apply<Tr, Tr::kVec, false>(p, g, a.x, nullptr, a.y, coef, stream);
+}
+
+template <class Tr>
+hipError_t grad_t(const BnGeometry& g, const BnGradArgs& a, void* ws,
+                  size_t ws_bytes, hipStream_t stream) {
+  const bool aligned = ptr_aligned(a.x) && ptr_aligned(a.dy) && ptr_aligned(a.dx);
+  const Plan p = make_plan(Tr::kVec == 4 ? DType::kF32 : DType::kF16, g, aligned);
+  const size_t pb = partial_bytes(p, g);
+  if (ws_bytes < pb + coef_bytes(g)) return hipErrorInvalidValue;
+  float2* partial = static_cast<float2*>(ws);
+  float4* coef = reinterpret_cast<float4*>(static_cast<char*>(ws) + pb);
+  FinArgs fa{};
+  fa.groups = p.groups;
+  fa.c = static_cast<int>(g.c);
+  fa.n = g.rows;
+  fa.scale = a.scale;
+  fa.mean_in = a.saved_mean;
+  fa.var_in = a.saved_var;
+  fa.eps = a.epsilon;
+  fa.scale_bp = a.scale_backprop;
+  fa.offset_bp = a.offset_backprop;
+  fa.reserve4 = a.reserve4;
+  fa.reserve4_n = a.reserve4 ? a.reserve4_n : 0;
+  fa.reserve5 = a.reserve5;
+  fa.reserve5_n = a.reserve5 ? a.reserve5_n : 0;
+  fa.is_training = a.is_training;
+  hipError_t e =
+      p.vec == 1 ? launch_reduce<Tr, 1, true>(p, g, a.x, a.dy, a.saved_mean, partial, stream)
+                 : launch_reduce<Tr, Tr::kVec, true>(p, g, a.x, a.dy, a.saved_mean, partial, stream);
+  if (e != hipSuccess) return e;
+  e = launch_finalize<Tr, true>(p, fa, partial, coef, stream);
+  if (e != hipSuccess) return e;
+  return p.vec == 1 ? launch_apply<Tr, 1, true>(p, g, a.x, a.dy, a.dx, coef, stream)
+                    : launch_apply<Tr, Tr::kVec, true>(p, g, a.x, a.dy, a.dx, coef, stream);
+}
+
+__global__ void fill_f32_kernel(float* __restrict__ p, int64_t n, float v) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    p[i] = v;
+}
+
+}  // namespace
+
+hipError_t LaunchFillF32(float* p, int64_t n, float value, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 1024) blocks = 1024;
+  LaunchScope scope(stream, "tfma_fill_f32");
+  hipLaunchKernelGGL(fill_f32_kernel, dim3(blocks), dim3(256), 0, stream, p, n, value);
+  return hipGetLastError();
+}
+
+size_t BnWorkspaceBytes(DType t, const BnGeometry& g) {
+  // The plan depends on pointer alignment; size for the larger of the two.
+  const Plan pv = make_plan(t, g, true);
+  const Plan ps = make_plan(t, g, false);
+  size_t a = partial_bytes(pv, g), b = partial_bytes(ps, g);
+  return (a > b ? a : b) + coef_bytes(g);
+}
+
+hipError_t LaunchBnForward(DType t, const BnGeometry& g, const BnFwdArgs& a,
+                           void* ws, size_t ws_bytes, hipStream_t stream) {
+  switch (t) {
+    case DType::kF32: return forward_t<TF32>(g, a, ws, ws_bytes, stream);
+    case DType::kF16: return forward_t<TF16>(g, a, ws, ws_bytes, stream);
+    case DType::kBF16: return forward_t<TBF16>(g, a, ws, ws_bytes, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t LaunchBnGrad(DType t, const BnGeometry& g, const BnGradArgs& a,
+                        void* ws, size_t ws_bytes, hipStream_t stream) {
+  switch (t) {
+    case DType::kF32: return grad_t<TF32>(g, a, ws, ws_bytes, stream);
+    case DType::kF16: return grad_t<TF16>(g, a, ws, ws_bytes, stream);
+    case DType::kBF16: return grad_t<TBF16>(g, a, ws, ws_bytes, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace tfma

@@ -1,0 +1,338 @@
+// Elementwise kernels for gfx950: BiasAdd, Relu, AddV2, Mul and the fused
+// chains Relu(BiasAdd), Relu(AddV2) and Mul+Add (MusaShiftedAffineMap).
+//
+// Numerics follow TensorFlow's CPU kernels: each TF op computes in float and
+// rounds to T once, so a fused chain rounds after every op it replaces
+// (Mul+Add rounds the product before the add; compiled with
+// -ffp-contract=off so it never becomes a fused multiply-add).  Relu keeps
+// the input bits unless x < 0, so Relu(-0) = -0 and Relu(NaN) = NaN as with
+// Eigen's max.
+//
+// Memory: the value input and the output are streamed with 16-byte vector
+// accesses over the flat index; a broadcast operand is read as a 16-byte
+// vector when its period is a multiple of the vector width (row vectors such
+// as a BiasAdd bias over the last dimension), as one value per vector when
+// its inner extent is (NCHW bias), and gathered per element otherwise (odd
+// shapes such as [8191, 4095]).  Broadcast operands are tiny and stay in
+// L1/L2, so HBM traffic is the compulsory stream of the full-size tensors.
+#include "device_util.h"
+#include "tfma_internal.h"
+
+namespace tfma {
+namespace {
+
+constexpr int kThreads = 256;
+
+enum Kind : int { kFullK = 0, kScalarK = 1, kRowK = 2, kChanK = 3, kGatherK = 4 };
+
+struct Operand {
+  const void* p;
+  int kind;
+  uint32_t period;
+  FastDiv div_inner;
+  FastDiv div_period;
+};
+
+template <typename S>
+__device__ inline S gather_one(const Operand& o, uint32_t i) {
+  const S* p = static_cast<const S*>(o.p);
+  const uint32_t q = o.div_inner.div(i);
+  const uint32_t idx = q - o.div_period.div(q) * o.period;
+  return p[idx];
+}
+
+template <typename S, int V>
+__device__ inline void fetch(const Operand& o, uint32_t i0, S (&out)[V]) {
+  const S* p = static_cast<const S*>(o.p);
+  switch (o.kind) {
+    case kFullK:
+      vload<S, V>(p + i0, out);
+      break;
+    case kScalarK: {
+      const S s = p[0];
+#pragma unroll
+      for (int j = 0; j < V; ++j) out[j] = s;
+      break;
+    }
+    case kRowK: {
+      const uint32_t idx = i0 - o.div_period.div(i0) * o.period;
+      vload<S, V>(p + idx, out);
+      break;
+    }
+    case kChanK: {
+      const S s = gather_one<S>(o, i0);
+#pragma unroll
+      for (int j = 0; j < V; ++j) out[j] = s;
+      break;
+    }
+    default:
+#pragma unroll
+      for (int j = 0; j < V; ++j) out[j] = gather_one<S>(o, i0 + j);
+      break;
+  }
+}
+
+template <class Tr, EwOp OP>
+__device__ inline typename Tr::S ew_apply(typename Tr::S a, typename Tr::S b,
+                                          typename Tr::S c) {
+  using C = typename Tr::C;
+  const C x = Tr::ld(a);
+  if constexpr (OP == EwOp::kAdd) {
+    return Tr::st(x + Tr::ld(b));
+  } else if constexpr (OP == EwOp::kAddRelu) {
+    const typename Tr::S r = Tr::st(x + Tr::ld(b));
+    return Tr::ld(r) < C(0) ? Tr::st(C(0)) : r;
+  } else if constexpr (OP == EwOp::kMul) {
+    return Tr::st(x * Tr::ld(b));
+  } else if constexpr (OP == EwOp::kMulAdd) {
+    const C t = Tr::rnd(x * Tr::ld(b));
+    return Tr::st(t + Tr::ld(c));
+  } else {  // kRelu
+    return x < C(0) ? Tr::st(C(0)) : a;
+  }
+}
+
+template <EwOp OP>
+constexpr int arity() {
+  return OP == EwOp::kRelu ? 1 : (OP == EwOp::kMulAdd ? 3 : 2);
+}
+
+// Flat kernel over n < 2^31 elements; `a` is always full-size.
+template <class Tr, EwOp OP, int V, int UNROLL>
+__global__ __launch_bounds__(kThreads) void ew_flat_kernel(
+    const typename Tr::S* __restrict__ a, Operand b, Operand c,
+    typename Tr::S* __restrict__ out, uint32_t n) {
+  using S = typename Tr::S;
+  constexpr int kArity = arity<OP>();
+  const uint32_t nv = n / V;
+  const uint32_t stride = gridDim.x * kThreads;
+  const uint32_t tid = blockIdx.x * kThreads + threadIdx.x;
+  uint32_t i = tid;
+  for (; i + (UNROLL - 1) * stride < nv; i += UNROLL * stride) {
+    S av[UNROLL][V], bv[UNROLL][V], cv[UNROLL][V];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const uint32_t i0 = (i + u * stride) * V;
+      vload<S, V>(a + i0, av[u]);
+      if constexpr (kArity >= 2) fetch<S, V>(b, i0, bv[u]);
+      if constexpr (kArity >= 3) fetch<S, V>(c, i0, cv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      S ov[V];
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        ov[j] = ew_apply<Tr, OP>(av[u][j], kArity >= 2 ? bv[u][j] : S(0),
+                                 kArity >= 3 ? cv[u][j] : S(0));
+      vstore<S, V>(out + (i + u * stride) * V, ov);
+    }
+  }
+  for (; i < nv; i += stride) {
+    const uint32_t i0 = i * V;
+    S av[V], bv[V], cv[V], ov[V];
+    vload<S, V>(a + i0, av);
+    if constexpr (kArity >= 2) fetch<S, V>(b, i0, bv);
+    if constexpr (kArity >= 3) fetch<S, V>(c, i0, cv);
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+      ov[j] = ew_apply<Tr, OP>(av[j], kArity >= 2 ? bv[j] : S(0),
+                               kArity >= 3 ? cv[j] : S(0));
+    vstore<S, V>(out + i0, ov);
+  }
+  const uint32_t tail = n - nv * V;
+  if (tid < tail) {
+    const uint32_t k = nv * V + tid;
+    const S bs = kArity >= 2 ? gather_one<S>(b, k) : S(0);
+    const S cs = kArity >= 3 ? gather_one<S>(c, k) : S(0);
+    out[k] = ew_apply<Tr, OP>(a[k], bs, cs);
+  }
+}
+
+// General broadcast: per element coordinate decomposition (64-bit).
+template <class Tr, EwOp OP>
+__global__ __launch_bounds__(kThreads) void ew_strided_kernel(
+    const typename Tr::S* __restrict__ a, const typename Tr::S* __restrict__ b,
+    const typename Tr::S* __restrict__ c, StridedShape sh,
+    typename Tr::S* __restrict__ out, int64_t n) {
+  using S = typename Tr::S;
+  constexpr int kArity = arity<OP>();
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+       i < n; i += stride) {
+    int64_t rem = i, oa = 0, ob = 0, oc = 0;
+    for (int d = sh.ndims - 1; d >= 0; --d) {
+      const int64_t coord = rem % sh.dims[d];
+      rem /= sh.dims[d];
+      oa += coord * sh.stride_a[d];
+      ob += coord * sh.stride_b[d];
+      oc += coord * sh.stride_c[d];
+    }
+    out[i] = ew_apply<Tr, OP>(a[oa], kArity >= 2 ? b[ob] : S(0),
+                              kArity >= 3 ? c[oc] : S(0));
+  }
+}
+
+const char* op_kernel_name(EwOp op) {
+  switch (op) {
+    case EwOp::kAdd: return "tfma_ew_add";
+    case EwOp::kAddRelu: return "tfma_ew_add_relu";
+    case EwOp::kMul: return "tfma_ew_mul";
+    case EwOp::kMulAdd: return "tfma_ew_mul_add";
+    case EwOp::kRelu: return "tfma_ew_relu";
+  }
+  return "tfma_ew";
+}
+
+int64_t grid_for(int64_t units, int unroll) {
+  int64_t blocks = (units + kThreads * unroll - 1) / (kThreads * unroll);
+  const int64_t max_blocks = static_cast<int64_t>(DeviceCUs()) * 16;
+  if (blocks > max_blocks) blocks = max_blocks;
+  if (blocks < 1) blocks = 1;
+  return blocks;
+}
+
+// Classify an operand for vector width V.
+Operand make_operand(const BcastOperand& o, int elem_bytes, int V,
+                     bool* vec_ok) {
+  Operand r;
+  r.p = o.data;
+  r.period = 1;
+  const bool aligned = (reinterpret_cast<uintptr_t>(o.data) & 15) == 0;
+  switch (o.mode) {
+    case BcastMode::kFull:
+      r.kind = kFullK;
+      r.div_inner = FastDiv(1);
+      r.div_period = FastDiv(0x7fffffffu);  // i < 2^31: idx = i
+      r.period = 0x7fffffffu;
+      if (!aligned) *vec_ok = false;
+      break;
+    case BcastMode::kScalar:
+      r.kind = kScalarK;
+      r.div_inner = FastDiv(1);
+      r.div_period = FastDiv(1);
+      r.period = 1;
+      break;
+    case BcastMode::kPeriodic:
+      r.div_inner = FastDiv(static_cast<uint32_t>(o.inner));
+      r.div_period = FastDiv(static_cast<uint32_t>(o.period));
+      r.period = static_cast<uint32_t>(o.period);
+      if (o.inner == 1 && o.period % V == 0 && aligned) {
+        r.kind = kRowK;
+      } else if (o.inner % V == 0) {
+        r.kind = kChanK;
+      } else {
+        r.kind = kGatherK;
+      }
+      break;
+  }
+  (void)elem_bytes;
+  return r;
+}
+
+template <class Tr, EwOp OP>
+hipError_t launch_ew(int64_t n, const BcastOperand& a, const BcastOperand& b,
+                     const BcastOperand& c, void* out, hipStream_t stream) {
+  using S = typename Tr::S;
+  constexpr int V = Tr::kVec;
+  bool vec_ok = ((reinterpret_cast<uintptr_t>(a.data) |
+                  reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  constexpr int kArity = arity<OP>();
+  Operand ob = kArity >= 2 ? make_operand(b, sizeof(S), V, &vec_ok)
+                           : make_operand(a, sizeof(S), V, &vec_ok);
+  Operand oc = kArity >= 3 ? make_operand(c, sizeof(S), V, &vec_ok)
+                           : make_operand(a, sizeof(S), V, &vec_ok);
+  const uint32_t n32 = static_cast<uint32_t>(n);
+  LaunchScope scope(stream, op_kernel_name(OP));
+  if (vec_ok) {
+    constexpr int U = 2;
+    hipLaunchKernelGGL((ew_flat_kernel<Tr, OP, V, U>), dim3(grid_for(n / V, U)),
+                       dim3(kThreads), 0, stream, static_cast<const S*>(a.data),
+                       ob, oc, static_cast<S*>(out), n32);
+  } else {
+    // Re-classify for V = 1 (rows and channels become per-element gathers).
+    bool dummy = true;
+    ob = kArity >= 2 ? make_operand(b, sizeof(S), 1, &dummy)
+                     : make_operand(a, sizeof(S), 1, &dummy);
+    oc = kArity >= 3 ? make_operand(c, sizeof(S), 1, &dummy)
+                     : make_operand(a, sizeof(S), 1, &dummy);
+    constexpr int U = 4;
+    hipLaunchKernelGGL((ew_flat_kernel<Tr, OP, 1, U>), dim3(grid_for(n, U)),
+                       dim3(kThreads), 0, stream, static_cast<const S*>(a.data),
+                       ob, oc, static_cast<S*>(out), n32);
+  }
+  return hipGetLastError();
+}
+
+template <class Tr, EwOp OP>
+hipError_t launch_ew_strided(int64_t n, const void* a, const void* b,
+                             const void* c, const StridedShape& sh, void* out,
+                             hipStream_t stream) {
+  using S = typename Tr::S;
+  LaunchScope scope(stream, "tfma_ew_strided");
+  hipLaunchKernelGGL((ew_strided_kernel<Tr, OP>), dim3(grid_for(n, 4)),
+                     dim3(kThreads), 0, stream, static_cast<const S*>(a),
+                     static_cast<const S*>(b), static_cast<const S*>(c), sh,
+                     static_cast<S*>(out), n);
+  return hipGetLastError();
+}
+
+template <class Tr>
+hipError_t dispatch_op(EwOp op, int64_t n, const BcastOperand& a,
+                       const BcastOperand& b, const BcastOperand& c, void* out,
+                       hipStream_t stream) {
+  switch (op) {
+    case EwOp::kAdd: return launch_ew<Tr, EwOp::kAdd>(n, a, b, c, out, stream);
+    case EwOp::kAddRelu: return launch_ew<Tr, EwOp::kAddRelu>(n, a, b, c, out, stream);
+    case EwOp::kMul: return launch_ew<Tr, EwOp::kMul>(n, a, b, c, out, stream);
+    case EwOp::kMulAdd: return launch_ew<Tr, EwOp::kMulAdd>(n, a, b, c, out, stream);
+    case EwOp::kRelu: return launch_ew<Tr, EwOp::kRelu>(n, a, b, c, out, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <class Tr>
+hipError_t dispatch_strided(EwOp op, int64_t n, const void* a, const void* b,
+                            const void* c, const StridedShape& sh, void* out,
+                            hipStream_t stream) {
+  switch (op) {
+    case EwOp::kAdd: return launch_ew_strided<Tr, EwOp::kAdd>(n, a, b, c, sh, out, stream);
+    case EwOp::kAddRelu: return launch_ew_strided<Tr, EwOp::kAddRelu>(n, a, b, c, sh, out, stream);
+    case EwOp::kMul: return launch_ew_strided<Tr, EwOp::kMul>(n, a, b, c, sh, out, stream);
+    case EwOp::kMulAdd: return launch_ew_strided<Tr, EwOp::kMulAdd>(n, a, b, c, sh, out, stream);
+    case EwOp::kRelu: return launch_ew_strided<Tr, EwOp::kRelu>(n, a, b, c, sh, out, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t LaunchElementwise(DType t, EwOp op, int64_t n,
+                             const BcastOperand& a, const BcastOperand& b,
+                             const BcastOperand& c, void* out,
+                             hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  if (n >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  switch (t) {
+    case DType::kF32: return dispatch_op<TF32>(op, n, a, b, c, out, stream);
+    case DType::kF16: return dispatch_op<TF16>(op, n, a, b, c, out, stream);
+    case DType::kBF16: return dispatch_op<TBF16>(op, n, a, b, c, out, stream);
+    case DType::kF64: return dispatch_op<TF64>(op, n, a, b, c, out, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t LaunchElementwiseStrided(DType t, EwOp op, int64_t n,
+                                    const void* a, const void* b,
+                                    const void* c, const StridedShape& shape,
+                                    void* out, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  switch (t) {
+    case DType::kF32: return dispatch_strided<TF32>(op, n, a, b, c, shape, out, stream);
+    case DType::kF16: return dispatch_strided<TF16>(op, n, a, b, c, shape, out, stream);
+    case DType::kBF16: return dispatch_strided<TBF16>(op, n, a, b, c, shape, out, stream);
+    case DType::kF64: return dispatch_strided<TF64>(op, n, a, b, c, shape, out, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace tfma

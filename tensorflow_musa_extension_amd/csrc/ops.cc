@@ -1,0 +1,991 @@
+// Op layer of the C ABI: argument validation, TF shape rules, host scalar
+// arithmetic and dispatch to the gfx950 kernels.  Each TFMA_* entry point
+// mirrors the Compute() of the reference op it replaces (cited per entry
+// point in include/tfma.h); error codes and messages follow the reference
+// where it defines them and TensorFlow's CPU kernels otherwise.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "device_util.h"
+#include "tfma_internal.h"
+
+namespace tfma {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Status helpers.
+// ---------------------------------------------------------------------------
+int set_status(TFMA_Status* st, int code, const char* fmt, ...) {
+  if (st) {
+    st->code = code;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(st->message, sizeof(st->message), fmt, ap);
+    va_end(ap);
+  }
+  return code;
+}
+int ok(TFMA_Status* st) {
+  if (st) {
+    st->code = TFMA_OK;
+    st->message[0] = '\0';
+  }
+  return TFMA_OK;
+}
+int hip_status(TFMA_Status* st, hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok(st);
+  return set_status(st, TFMA_INTERNAL, "%s launch failed: %s", what,
+                    hipGetErrorString(e));
+}
+
+std::string shape_str(const TFMA_Tensor* t) {
+  std::string s = "[";
+  for (int i = 0; i < t->ndims; ++i) {
+    if (i) s += ",";
+    s += std::to_string(t->dims[i]);
+  }
+  return s + "]";
+}
+
+int64_t num_elements(const TFMA_Tensor* t) {
+  int64_t n = 1;
+  for (int i = 0; i < t->ndims; ++i) n *= t->dims[i];
+  return n;
+}
+
+bool same_shape(const TFMA_Tensor* a, const TFMA_Tensor* b) {
+  if (a->ndims != b->ndims) return false;
+  for (int i = 0; i < a->ndims; ++i)
+    if (a->dims[i] != b->dims[i]) return false;
+  return true;
+}
+
+bool valid_tensor(const TFMA_Tensor* t) {
+  if (!t || t->ndims < 0 || t->ndims > TFMA_MAX_DIMS) return false;
+  for (int i = 0; i < t->ndims; ++i)
+    if (t->dims[i] < 0) return false;
+  return true;
+}
+
+const char* dtype_name(int dt) {
+  switch (dt) {
+    case TFMA_FLOAT: return "float";
+    case TFMA_DOUBLE: return "double";
+    case TFMA_HALF: return "half";
+    case TFMA_BFLOAT16: return "bfloat16";
+    case TFMA_INT32: return "int32";
+    case TFMA_INT64: return "int64";
+  }
+  return "unknown";
+}
+
+bool to_dtype(int dt, DType* out) {
+  switch (dt) {
+    case TFMA_FLOAT: *out = DType::kF32; return true;
+    case TFMA_HALF: *out = DType::kF16; return true;
+    case TFMA_BFLOAT16: *out = DType::kBF16; return true;
+    case TFMA_DOUBLE: *out = DType::kF64; return true;
+  }
+  return false;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------------------
+// Host half / bfloat16 rounding for the Adam scalars (TF computes alpha and
+// 1 - beta in T).
+// ---------------------------------------------------------------------------
+uint16_t host_f32_to_f16(float f) {
+  const uint32_t x = f32_bits(f);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t mant = x & 0x7fffffu;
+  const int exp = static_cast<int>((x >> 23) & 0xffu);
+  if (exp == 255) return static_cast<uint16_t>(sign | 0x7c00u | (mant ? 0x200u | (mant >> 13) : 0u));
+  const int e = exp - 127 + 15;
+  if (e >= 31) return static_cast<uint16_t>(sign | 0x7c00u);
+  if (e <= 0) {
+    if (e < -10) return static_cast<uint16_t>(sign);
+    mant |= 0x800000u;
+    const int shift = 14 - e;
+    uint32_t h = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (h & 1u))) ++h;
+    return static_cast<uint16_t>(sign | h);
+  }
+  uint32_t h = (static_cast<uint32_t>(e) << 10) | (mant >> 13);
+  const uint32_t rem = mant & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+  return static_cast<uint16_t>(sign | h);
+}
+
+float host_f16_to_f32(uint16_t h) {
+  const uint32_t sign = static_cast<uint32_t>(h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1fu;
+  const uint32_t mant = h & 0x3ffu;
+  if (exp == 0) {
+    const float v = static_cast<float>(mant) * (1.0f / 16777216.0f);
+    return sign ? -v : v;
+  }
+  if (exp == 31) return bits_f32(sign | 0x7f800000u | (mant << 13));
+  return bits_f32(sign | ((exp + 112u) << 23) | (mant << 13));
+}
+
+// Reads a 0-d host scalar of dtype t as a double (exact for every T).
+double read_scalar(const TFMA_Tensor* s, DType t) {
+  switch (t) {
+    case DType::kF32: return *static_cast<const float*>(s->data);
+    case DType::kF64: return *static_cast<const double*>(s->data);
+    case DType::kF16: return host_f16_to_f32(*static_cast<const uint16_t*>(s->data));
+    case DType::kBF16: return bf16_to_f32(*static_cast<const uint16_t*>(s->data));
+  }
+  return 0.0;
+}
+
+// Rounds a float to T's precision (float, half or bfloat16).
+float round_to(DType t, float v) {
+  switch (t) {
+    case DType::kF16: return host_f16_to_f32(host_f32_to_f16(v));
+    case DType::kBF16: return bf16_to_f32(f32_to_bf16(v));
+    default: return v;
+  }
+}
+
+// alpha = lr * sqrt(1 - beta2_power) / (1 - beta1_power), each operation in
+// T, as TF's CPU ApplyAdam computes it.
+AdamScalars adam_scalars(DType t, double b1p, double b2p, double lr,
+                         double b1, double b2, double eps) {
+  AdamScalars s;
+  if (t == DType::kF64) {
+    s.alpha = lr * sqrt(1.0 - b2p) / (1.0 - b1p);
+    s.one_minus_beta1 = 1.0 - b1;
+    s.one_minus_beta2 = 1.0 - b2;
+  } else {
+    const float fb1p = static_cast<float>(b1p), fb2p = static_cast<float>(b2p);
+    const float flr = static_cast<float>(lr);
+    const float fb1 = static_cast<float>(b1), fb2 = static_cast<float>(b2);
+    volatile float r1 = round_to(t, 1.0f - fb2p);
+    volatile float r2 = round_to(t, sqrtf(r1));
+    volatile float r3 = round_to(t, flr * r2);
+    volatile float r4 = round_to(t, 1.0f - fb1p);
+    s.alpha = round_to(t, r3 / r4);
+    s.one_minus_beta1 = round_to(t, 1.0f - fb1);
+    s.one_minus_beta2 = round_to(t, 1.0f - fb2);
+  }
+  s.beta1 = b1;
+  s.beta2 = b2;
+  s.epsilon = eps;
+  return s;
+}
+
+// ---------------------------------------------------------------------------
+// Variable locks: a striped table keyed by the variable's memory; a call
+// takes the stripes of var/m/v in ascending order (the reference sorts its
+// var/m/v mutexes the same way, musa_applyadam_op.cc:138-156).
+// ---------------------------------------------------------------------------
+constexpr int kLockStripes = 256;
+std::mutex& stripe(int i) {
+  static std::mutex* table = new std::mutex[kLockStripes];
+  return table[i];
+}
+int stripe_of(const void* p) {
+  const uintptr_t u = reinterpret_cast<uintptr_t>(p);
+  return static_cast<int>((u >> 8) * 2654435761u % kLockStripes);
+}
+
+class VarLocks {
+ public:
+  void add(const void* p) { ids_.push_back(stripe_of(p)); }
+  void lock() {
+    std::sort(ids_.begin(), ids_.end());
+    ids_.erase(std::unique(ids_.begin(), ids_.end()), ids_.end());
+    for (int i : ids_) stripe(i).lock();
+    locked_ = true;
+  }
+  ~VarLocks() {
+    if (!locked_) return;
+    for (auto it = ids_.rbegin(); it != ids_.rend(); ++it) stripe(*it).unlock();
+  }
+
+ private:
+  std::vector<int> ids_;
+  bool locked_ = false;
+};
+
+// ---------------------------------------------------------------------------
+// Pinned staging ring for small host->device uploads (grouped Adam tables).
+// A slot is reused only after the event recorded behind its copy completes.
+// ---------------------------------------------------------------------------
+class PinnedRing {
+ public:
+  static constexpr size_t kSlotBytes = 64 * 1024;
+  static constexpr int kSlots = 16;
+
+  // Copies `bytes` from `src` to device `dst` on `stream`.
+  hipError_t upload(void* dst, const void* src, size_t bytes,
+                    hipStream_t stream) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (bytes > kSlotBytes) {
+      // Large table: synchronous copy (rare; > 1300 tensors).
+      hipError_t e = hipStreamSynchronize(stream);
+      if (e != hipSuccess) return e;
+      return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
+    }
+    hipError_t e = ensure();
+    if (e != hipSuccess) return e;
+    const int s = next_;
+    next_ = (next_ + 1) % kSlots;
+    if (used_[s]) {
+      e = hipEventSynchronize(events_[s]);
+      if (e != hipSuccess) return e;
+    }
+    char* slot = static_cast<char*>(host_) + s * kSlotBytes;
+    memcpy(slot, src, bytes);
+    e = hipMemcpyAsync(dst, slot, bytes, hipMemcpyHostToDevice, stream);
+    if (e != hipSuccess) return e;
+    e = hipEventRecord(events_[s], stream);
+    used_[s] = true;
+    return e;
+  }
+
+ private:
+  hipError_t ensure() {
+    if (host_) return hipSuccess;
+    hipError_t e = hipHostMalloc(&host_, kSlotBytes * kSlots, hipHostMallocDefault);
+    if (e != hipSuccess) {
+      host_ = nullptr;
+      return e;
+    }
+    for (int i = 0; i < kSlots; ++i) {
+      e = hipEventCreateWithFlags(&events_[i], hipEventDisableTiming);
+      if (e != hipSuccess) return e;
+      used_[i] = false;
+    }
+    return hipSuccess;
+  }
+  std::mutex mu_;
+  void* host_ = nullptr;
+  hipEvent_t events_[kSlots];
+  bool used_[kSlots];
+  int next_ = 0;
+};
+
+PinnedRing& pinned_ring() {
+  static PinnedRing* r = new PinnedRing();
+  return *r;
+}
+
+// ---------------------------------------------------------------------------
+// Broadcasting (TF BCast rules, right-aligned).
+// ---------------------------------------------------------------------------
+bool broadcast_shape(const TFMA_Tensor* a, const TFMA_Tensor* b, int* nd,
+                     int64_t* dims) {
+  const int n = std::max(a->ndims, b->ndims);
+  for (int i = 0; i < n; ++i) {
+    const int ia = a->ndims - n + i, ib = b->ndims - n + i;
+    const int64_t da = ia >= 0 ? a->dims[ia] : 1;
+    const int64_t db = ib >= 0 ? b->dims[ib] : 1;
+    if (da == db || db == 1) {
+      dims[i] = da;
+    } else if (da == 1) {
+      dims[i] = db;
+    } else {
+      return false;
+    }
+  }
+  *nd = n;
+  return true;
+}
+
+// Describes operand t broadcast to out (rank nd, dims od): returns false if
+// it needs the general strided path.
+bool classify(const TFMA_Tensor* t, int nd, const int64_t* od,
+              BcastOperand* o) {
+  o->data = t->data;
+  // Output dims of size 1 are neutral.  The operand's non-broadcast
+  // ("active") dims must form one run, with only broadcast dims outside it.
+  int lo = -1, last = -1;
+  bool gap = false, any_bcast = false;
+  for (int d = 0; d < nd; ++d) {
+    const int it = t->ndims - nd + d;
+    const int64_t td = it >= 0 ? t->dims[it] : 1;
+    if (od[d] == 1) continue;
+    if (td == od[d]) {
+      if (lo < 0) lo = d;
+      else if (gap) return false;
+      last = d;
+    } else {
+      any_bcast = true;
+      if (lo >= 0) gap = true;
+    }
+  }
+  o->inner = 1;
+  o->period = 1;
+  if (lo < 0) {
+    o->mode = BcastMode::kScalar;
+    return true;
+  }
+  if (!any_bcast) {
+    o->mode = BcastMode::kFull;
+    return true;
+  }
+  int64_t period = 1, inner = 1;
+  for (int d = lo; d <= last; ++d) period *= od[d];
+  for (int d = last + 1; d < nd; ++d) inner *= od[d];
+  o->mode = BcastMode::kPeriodic;
+  o->inner = inner;
+  o->period = period;
+  return true;
+}
+
+void strides_for(const TFMA_Tensor* t, int nd, const int64_t* od,
+                 int64_t* st) {
+  int64_t s = 1;
+  for (int d = nd - 1; d >= 0; --d) {
+    const int it = t->ndims - nd + d;
+    const int64_t td = it >= 0 ? t->dims[it] : 1;
+    st[d] = (td == od[d] && td != 1) ? s : 0;
+    s *= td;
+  }
+}
+
+// Runs op over up to three inputs broadcast to `out`.  `a_name` etc. are
+// for messages; commutative says whether inputs 0 and 1 may be swapped.
+int run_elementwise(void* stream, EwOp op, const char* op_name,
+                    const TFMA_Tensor* const* ins, int n_in, TFMA_Tensor* out,
+                    bool commutative01, TFMA_Status* st) {
+  for (int i = 0; i < n_in; ++i)
+    if (!valid_tensor(ins[i]))
+      return set_status(st, TFMA_INVALID_ARGUMENT, "%s: invalid input %d", op_name, i);
+  if (!valid_tensor(out))
+    return set_status(st, TFMA_INVALID_ARGUMENT, "%s: invalid output", op_name);
+  const int dt = ins[0]->dtype;
+  DType t;
+  if (!to_dtype(dt, &t))
+    return set_status(st, TFMA_UNIMPLEMENTED, "%s: dtype %s is not supported",
+                      op_name, dtype_name(dt));
+  for (int i = 1; i < n_in; ++i)
+    if (ins[i]->dtype != dt)
+      return set_status(st, TFMA_INVALID_ARGUMENT,
+                        "%s: input %d has dtype %s, expected %s", op_name, i,
+                        dtype_name(ins[i]->dtype), dtype_name(dt));
+  if (out->dtype != dt)
+    return set_status(st, TFMA_INVALID_ARGUMENT, "%s: output dtype %s, expected %s",
+                      op_name, dtype_name(out->dtype), dtype_name(dt));
+  // Broadcast shape over all inputs.
+  TFMA_Tensor acc = *ins[0];
+  for (int i = 1; i < n_in; ++i) {
+    TFMA_Tensor next = acc;
+    if (!broadcast_shape(&acc, ins[i], &next.ndims, next.dims))
+      return set_status(st, TFMA_INVALID_ARGUMENT, "Incompatible shapes for %s: %s and %s",
+                        op_name, shape_str(&acc).c_str(), shape_str(ins[i]).c_str());
+    acc = next;
+  }
+  if (!same_shape(&acc, out))
+    return set_status(st, TFMA_INVALID_ARGUMENT,
+                      "%s: output shape %s does not match broadcast shape %s",
+                      op_name, shape_str(out).c_str(), shape_str(&acc).c_str());
+  const int64_t n = num_elements(out);
+  if (n == 0) return ok(st);
+  for (int i = 0; i < n_in; ++i)
+    if (!ins[i]->data) return set_status(st, TFMA_INVALID_ARGUMENT, "%s: null input %d", op_name, i);
+  if (!out->data) return set_status(st, TFMA_INVALID_ARGUMENT, "%s: null output", op_name);
+
+  const int nd = out->ndims;
+  const TFMA_Tensor* ord[3] = {ins[0], n_in > 1 ? ins[1] : ins[0], n_in > 2 ? ins[2] : ins[0]};
+  BcastOperand o[3];
+  bool fast = n < (int64_t(1) << 31);
+  for (int i = 0; i < n_in && fast; ++i) fast = classify(ord[i], nd, out->dims, &o[i]);
+  if (fast && o[0].mode != BcastMode::kFull && commutative01 && n_in > 1 &&
+      o[1].mode == BcastMode::kFull) {
+    std::swap(ord[0], ord[1]);
+    std::swap(o[0], o[1]);
+  }
+  if (fast && o[0].mode != BcastMode::kFull) fast = false;
+  hipError_t e;
+  if (fast) {
+    if (n_in < 2) o[1] = o[0];
+    if (n_in < 3) o[2] = o[0];
+    e = LaunchElementwise(t, op, n, o[0], o[1], o[2], out->data, as_stream(stream));
+  } else {
+    StridedShape sh{};
+    sh.ndims = nd;
+    for (int d = 0; d < nd; ++d) sh.dims[d] = out->dims[d];
+    strides_for(ord[0], nd, out->dims, sh.stride_a);
+    strides_for(ord[1], nd, out->dims, sh.stride_b);
+    strides_for(ord[2], nd, out->dims, sh.stride_c);
+    e = LaunchElementwiseStrided(t, op, n, ord[0]->data, ord[1]->data,
+                                 ord[2]->data, sh, out->data, as_stream(stream));
+  }
+  return hip_status(st, e, op_name);
+}
+
+int bias_add_impl(void* stream, const TFMA_Tensor* value, const TFMA_Tensor* bias,
+                  const char* data_format, TFMA_Tensor* output, bool relu,
+                  TFMA_Status* st) {
+  const char* name = relu ? "MusaBiasAddRelu" : "BiasAdd";
+  if (!valid_tensor(value) || !valid_tensor(bias) || !valid_tensor(output))
+    return set_status(st, TFMA_INVALID_ARGUMENT, "%s: invalid tensor", name);
+  const std::string fmt = data_format ? data_format : "NHWC";
+  if (fmt != "NHWC" && fmt != "NCHW")
+    return set_status(st, TFMA_INVALID_ARGUMENT, "Invalid data format");
+  if (value->ndims < 2)
+    return set_status(st, TFMA_INVALID_ARGUMENT, "Input tensor must be at least 2D: %s",
+                      shape_str(value).c_str());
+  if (bias->ndims != 1)
+    return set_status(st, TFMA_INVALID_ARGUMENT, "Biases must be 1D: %s",
+                      shape_str(bias).c_str());
+  DType t;
+  if (!to_dtype(value->dtype, &t))
+    return set_status(st, TFMA_UNIMPLEMENTED, "%s: dtype %s is not supported", name,
+                      dtype_name(value->dtype));
+  if (bias->dtype != value->dtype || output->dtype != value->dtype)
+    return set_status(st, TFMA_INVALID_ARGUMENT, "%s: bias/output dtype must match value", name);
+  if (!same_shape(value, output))
+    return set_status(st, TFMA_INVALID_ARGUMENT, "%s: output shape %s != input shape %s",
+                      name, shape_str(output).c_str(), shape_str(value).c_str());
+  const int64_t n = num_elements(value);
+  if (n == 0 || num_elements(bias) == 0) return ok(st);
+  const int channel_dim = fmt == "NCHW" ? 1 : value->ndims - 1;
+  if (bias->dims[0] != value->dims[channel_dim])
+    return set_status(st, TFMA_INVALID_ARGUMENT, "Dimension mismatch in BiasAdd");
+  int64_t inner = 1;
+  for (int d = channel_dim + 1; d < value->ndims; ++d) inner *= value->dims[d];
+  if (!value->data || !bias->data || !output->data)
+    return set_status(st, TFMA_INVALID_ARGUMENT, "%s: null data pointer", name);
+  hipError_t e;
+  if (n < (int64_t(1) << 31)) {
+    BcastOperand a{value->data, BcastMode::kFull, 1, 1};
+    BcastOperand b{bias->data, BcastMode::kPeriodic, inner, bias->dims[0]};
+    e = LaunchElementwise(t, relu ? EwOp::kAddRelu : EwOp::kAdd, n, a, b, a,
+                          output->data, as_stream(stream));
+  } else {
+    StridedShape sh{};
+    sh.ndims = value->ndims;
+    int64_t s = 1;
+    for (int d = value->ndims - 1; d >= 0; --d) {
+      sh.dims[d] = value->dims[d];
+      sh.stride_a[d] = s;
+      sh.stride_b[d] = d == channel_dim ? 1 : 0;
+      sh.stride_c[d] = 0;
+      s *= value->dims[d];
+    }
+    e = LaunchElementwiseStrided(t, relu ? EwOp::kAddRelu : EwOp::kAdd, n,
+                                 value->data, bias->data, value->data, sh,
+                                 output->data, as_stream(stream));
+  }
+  return hip_status(st, e, name);
+}
+
+// ---------------------------------------------------------------------------
+// Fused batch norm helpers.
+// ---------------------------------------------------------------------------
+bool parse_bn_format(const char* f, bool* nhwc) {
+  const std::string s = f ? f : "NHWC";
+  if (s == "NHWC" || s == "NDHWC") { *nhwc = true; return true; }
+  if (s == "NCHW" || s == "NCDHW") { *nhwc = false; return true; }
+  return false;
+}
+
+BnGeometry bn_geometry(const TFMA_Tensor* x, bool nhwc) {
+  BnGeometry g;
+  g.nhwc = nhwc;
+  g.n = x->dims[0];
+  if (nhwc) {
+    g.c = x->dims[x->ndims - 1];
+    g.h = 1;
+    for (int d = 1; d < x->ndims - 1; ++d) g.h *= x->dims[d];
+  } else {
+    g.c = x->dims[1];
+    g.h = 1;
+    for (int d = 2; d < x->ndims; ++d) g.h *= x->dims[d];
+  }
+  g.w = 1;
+  g.rows = g.n * g.h * g.w;
+  return g;
+}
+
+bool is_vec_f32(const TFMA_Tensor* t) {
+  return valid_tensor(t) && t->ndims == 1 && t->dtype == TFMA_FLOAT;
+}
+
+}  // namespace
+
+int DeviceCUs() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Fill a float buffer on the stream (empty-input statistics).
+hipError_t LaunchFillF32(float* p, int64_t n, float value, hipStream_t stream);
+
+}  // namespace tfma
+
+using namespace tfma;
+
+// ===========================================================================
+// Exported C ABI.
+// ===========================================================================
+extern "C" {
+
+const char* TFMA_Version(void) { return "tfma 0.1 gfx950"; }
+
+int TFMA_GetDeviceCount(int* count, TFMA_Status* status) {
+  if (!count) return set_status(status, TFMA_INVALID_ARGUMENT, "count is null");
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+  *count = n;
+  return ok(status);
+}
+
+int TFMA_FusedBatchNormWorkspaceBytes(const TFMA_Tensor* x, const char* data_format,
+                                      size_t* bytes, TFMA_Status* status) {
+  if (!bytes || !valid_tensor(x))
+    return set_status(status, TFMA_INVALID_ARGUMENT, "invalid arguments");
+  bool nhwc;
+  if (!parse_bn_format(data_format, &nhwc))
+    return set_status(status, TFMA_INVALID_ARGUMENT, "Invalid data format");
+  if (x->ndims != 4 && x->ndims != 5)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "input must be 4 or 5-dimensional%s",
+                      shape_str(x).c_str());
+  DType t;
+  if (!to_dtype(x->dtype, &t) || t == DType::kF64)
+    return set_status(status, TFMA_UNIMPLEMENTED, "FusedBatchNorm: dtype %s is not supported",
+                      dtype_name(x->dtype));
+  const BnGeometry g = bn_geometry(x, nhwc);
+  *bytes = g.c > 0 ? BnWorkspaceBytes(t, g) : 0;
+  return ok(status);
+}
+
+int TFMA_FusedBatchNormV3(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* scale,
+                          const TFMA_Tensor* offset, const TFMA_Tensor* mean,
+                          const TFMA_Tensor* variance, float epsilon,
+                          float exponential_avg_factor, const char* data_format,
+                          int is_training, TFMA_Tensor* y, TFMA_Tensor* batch_mean,
+                          TFMA_Tensor* batch_variance, TFMA_Tensor* reserve_space_1,
+                          TFMA_Tensor* reserve_space_2, TFMA_Tensor* reserve_space_3,
+                          void* workspace, size_t workspace_bytes, TFMA_Status* status) {
+  bool nhwc;
+  if (!parse_bn_format(data_format, &nhwc))
+    return set_status(status, TFMA_INVALID_ARGUMENT, "Invalid data format");
+  if (!valid_tensor(x) || !valid_tensor(scale) || !valid_tensor(offset) || !valid_tensor(y))
+    return set_status(status, TFMA_INVALID_ARGUMENT, "FusedBatchNormV3: invalid tensor");
+  if (x->ndims != 4 && x->ndims != 5)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "input must be 4 or 5-dimensional%s",
+                      shape_str(x).c_str());
+  if (scale->ndims != 1)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "scale must be 1-dimensional%s",
+                      shape_str(scale).c_str());
+  if (offset->ndims != 1)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "offset must be 1-dimensional%s",
+                      shape_str(offset).c_str());
+  DType t;
+  if (!to_dtype(x->dtype, &t) || t == DType::kF64)
+    return set_status(status, TFMA_UNIMPLEMENTED, "FusedBatchNormV3: dtype %s is not supported",
+                      dtype_name(x->dtype));
+  if (y->dtype != x->dtype || !same_shape(x, y))
+    return set_status(status, TFMA_INVALID_ARGUMENT, "FusedBatchNormV3: y must match x (%s %s)",
+                      dtype_name(x->dtype), shape_str(x).c_str());
+  if (scale->dtype != TFMA_FLOAT || offset->dtype != TFMA_FLOAT)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "FusedBatchNormV3: scale/offset must be float");
+  const BnGeometry g = bn_geometry(x, nhwc);
+  const int64_t c = g.c;
+  if (num_elements(scale) != c)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "scale must have the same number of elements as the channels of x, got %lld and %lld",
+                      (long long)num_elements(scale), (long long)c);
+  if (num_elements(offset) != c)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "offset must have the same number of elements as the channels of x, got %lld and %lld",
+                      (long long)num_elements(offset), (long long)c);
+  const bool need_running = !is_training || exponential_avg_factor != 1.0f;
+  if (need_running) {
+    const char* prefix = is_training ? "When exponential_avg_factor != 1" : "When is_training=false";
+    if (!valid_tensor(mean) || num_elements(mean) != c || mean->dtype != TFMA_FLOAT)
+      return set_status(status, TFMA_INVALID_ARGUMENT,
+                        "%s, mean must have the same number of elements as the channels of x, got %lld and %lld",
+                        prefix, (long long)(valid_tensor(mean) ? num_elements(mean) : 0), (long long)c);
+    if (!valid_tensor(variance) || num_elements(variance) != c || variance->dtype != TFMA_FLOAT)
+      return set_status(status, TFMA_INVALID_ARGUMENT,
+                        "%s, variance must have the same number of elements as the channels of x, got %lld and %lld",
+                        prefix, (long long)(valid_tensor(variance) ? num_elements(variance) : 0), (long long)c);
+  }
+  TFMA_Tensor* stats[4] = {batch_mean, batch_variance, reserve_space_1, reserve_space_2};
+  const char* stat_names[4] = {"batch_mean", "batch_variance", "reserve_space_1", "reserve_space_2"};
+  for (int i = 0; i < 4; ++i)
+    if (!is_vec_f32(stats[i]) || num_elements(stats[i]) != c)
+      return set_status(status, TFMA_INVALID_ARGUMENT, "%s must be a float vector of length %lld",
+                        stat_names[i], (long long)c);
+  if (reserve_space_3 && (!valid_tensor(reserve_space_3) || reserve_space_3->ndims != 0 ||
+                          reserve_space_3->dtype != TFMA_FLOAT))
+    return set_status(status, TFMA_INVALID_ARGUMENT, "reserve_space_3 must be a float scalar");
+  float* r3 = reserve_space_3 ? static_cast<float*>(reserve_space_3->data) : nullptr;
+  hipStream_t s = as_stream(stream);
+  if (c == 0) return ok(status);
+  if (num_elements(x) == 0) {
+    // Empty batch: statistics are NaN (TF's SetNanFunctor), saved stats 0.
+    const float nan = bits_f32(0x7fc00000u);
+    hipError_t e = LaunchFillF32(static_cast<float*>(batch_mean->data), c, nan, s);
+    if (e == hipSuccess) e = LaunchFillF32(static_cast<float*>(batch_variance->data), c, nan, s);
+    if (e == hipSuccess) e = LaunchFillF32(static_cast<float*>(reserve_space_1->data), c, 0.f, s);
+    if (e == hipSuccess) e = LaunchFillF32(static_cast<float*>(reserve_space_2->data), c, 0.f, s);
+    if (e == hipSuccess && r3) e = LaunchFillF32(r3, 1, 0.f, s);
+    return hip_status(status, e, "FusedBatchNormV3");
+  }
+  if (!x->data || !y->data || !scale->data || !offset->data)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "FusedBatchNormV3: null data pointer");
+  const size_t need = BnWorkspaceBytes(t, g);
+  if (!workspace || workspace_bytes < need)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "FusedBatchNormV3: workspace of %zu bytes required, got %zu", need,
+                      workspace ? workspace_bytes : size_t(0));
+  BnFwdArgs a{};
+  a.x = x->data;
+  a.scale = static_cast<const float*>(scale->data);
+  a.offset = static_cast<const float*>(offset->data);
+  a.mean_in = need_running ? static_cast<const float*>(mean->data) : nullptr;
+  a.var_in = need_running ? static_cast<const float*>(variance->data) : nullptr;
+  a.epsilon = epsilon;
+  a.exp_avg_factor = exponential_avg_factor;
+  a.is_training = is_training != 0;
+  a.y = y->data;
+  a.batch_mean = static_cast<float*>(batch_mean->data);
+  a.batch_var = static_cast<float*>(batch_variance->data);
+  a.saved_mean = static_cast<float*>(reserve_space_1->data);
+  a.saved_var = static_cast<float*>(reserve_space_2->data);
+  a.reserve3 = r3;
+  return hip_status(status, LaunchBnForward(t, g, a, workspace, workspace_bytes, s),
+                    "FusedBatchNormV3");
+}
+
+int TFMA_FusedBatchNormGradV3(void* stream, const TFMA_Tensor* y_backprop, const TFMA_Tensor* x,
+                              const TFMA_Tensor* scale, const TFMA_Tensor* reserve_space_1,
+                              const TFMA_Tensor* reserve_space_2,
+                              const TFMA_Tensor* reserve_space_3, float epsilon,
+                              const char* data_format, int is_training, TFMA_Tensor* x_backprop,
+                              TFMA_Tensor* scale_backprop, TFMA_Tensor* offset_backprop,
+                              TFMA_Tensor* reserve_space_4, TFMA_Tensor* reserve_space_5,
+                              void* workspace, size_t workspace_bytes, TFMA_Status* status) {
+  (void)reserve_space_3;
+  bool nhwc;
+  if (!parse_bn_format(data_format, &nhwc))
+    return set_status(status, TFMA_INVALID_ARGUMENT, "Invalid data format");
+  if (!valid_tensor(y_backprop) || !valid_tensor(x) || !valid_tensor(scale) ||
+      !valid_tensor(reserve_space_1) || !valid_tensor(reserve_space_2) ||
+      !valid_tensor(x_backprop))
+    return set_status(status, TFMA_INVALID_ARGUMENT, "FusedBatchNormGradV3: invalid tensor");
+  if (y_backprop->ndims != 4 && y_backprop->ndims != 5)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "input must be 4 or 5-dimensional%s",
+                      shape_str(y_backprop).c_str());
+  if (x->ndims != 4 && x->ndims != 5)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "input must be 4 or 5-dimensional%s",
+                      shape_str(x).c_str());
+  if (scale->ndims != 1)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "scale must be 1-dimensional%s",
+                      shape_str(scale).c_str());
+  if (reserve_space_1->ndims != 1)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "saved mean must be 1-dimensional%s",
+                      shape_str(reserve_space_1).c_str());
+  if (reserve_space_2->ndims != 1)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "saved variance must be 1-dimensional%s",
+                      shape_str(reserve_space_2).c_str());
+  if (!same_shape(x, y_backprop))
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "x and y_backprop must have same shape, but x has shape %s and y_backprop has shape %s",
+                      shape_str(x).c_str(), shape_str(y_backprop).c_str());
+  DType t;
+  if (!to_dtype(x->dtype, &t) || t == DType::kF64)
+    return set_status(status, TFMA_UNIMPLEMENTED, "FusedBatchNormGradV3: dtype %s is not supported",
+                      dtype_name(x->dtype));
+  if (y_backprop->dtype != x->dtype || x_backprop->dtype != x->dtype || !same_shape(x, x_backprop))
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "FusedBatchNormGradV3: y_backprop and x_backprop must match x");
+  if (scale->dtype != TFMA_FLOAT || reserve_space_1->dtype != TFMA_FLOAT ||
+      reserve_space_2->dtype != TFMA_FLOAT)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "FusedBatchNormGradV3: scale and reserve spaces must be float");
+  const BnGeometry g = bn_geometry(x, nhwc);
+  const int64_t c = g.c;
+  if (num_elements(scale) != c)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "scale must have the same number of elements as the channels of x, got %lld and %lld",
+                      (long long)num_elements(scale), (long long)c);
+  if (num_elements(reserve_space_1) != c)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "reserve_space_1 must have the same number of elements as the channels of x, got %lld and %lld",
+                      (long long)num_elements(reserve_space_1), (long long)c);
+  if (num_elements(reserve_space_2) != c)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "reserve_space_2 must have the same number of elements as the channels of x, got %lld and %lld",
+                      (long long)num_elements(reserve_space_2), (long long)c);
+  if (!is_vec_f32(scale_backprop) || num_elements(scale_backprop) != c ||
+      !is_vec_f32(offset_backprop) || num_elements(offset_backprop) != c)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "scale_backprop/offset_backprop must be float vectors of length %lld", (long long)c);
+  for (TFMA_Tensor* r : {reserve_space_4, reserve_space_5})
+    if (r && (!valid_tensor(r) || r->dtype != TFMA_FLOAT))
+      return set_status(status, TFMA_INVALID_ARGUMENT, "reserve_space_4/5 must be float");
+  hipStream_t s = as_stream(stream);
+  float* r4 = reserve_space_4 ? static_cast<float*>(reserve_space_4->data) : nullptr;
+  float* r5 = reserve_space_5 ? static_cast<float*>(reserve_space_5->data) : nullptr;
+  const int64_t n4 = reserve_space_4 ? num_elements(reserve_space_4) : 0;
+  const int64_t n5 = reserve_space_5 ? num_elements(reserve_space_5) : 0;
+  if (c == 0) return ok(status);
+  if (num_elements(x) == 0) {
+    hipError_t e = LaunchFillF32(static_cast<float*>(scale_backprop->data), c, 0.f, s);
+    if (e == hipSuccess) e = LaunchFillF32(static_cast<float*>(offset_backprop->data), c, 0.f, s);
+    if (e == hipSuccess && n4) e = LaunchFillF32(r4, n4, 0.f, s);
+    if (e == hipSuccess && n5) e = LaunchFillF32(r5, n5, 0.f, s);
+    return hip_status(status, e, "FusedBatchNormGradV3");
+  }
+  if (!x->data || !y_backprop->data || !x_backprop->data || !scale->data ||
+      !reserve_space_1->data || !reserve_space_2->data)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "FusedBatchNormGradV3: null data pointer");
+  const size_t need = BnWorkspaceBytes(t, g);
+  if (!workspace || workspace_bytes < need)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "FusedBatchNormGradV3: workspace of %zu bytes required, got %zu", need,
+                      workspace ? workspace_bytes : size_t(0));
+  BnGradArgs a{};
+  a.dy = y_backprop->data;
+  a.x = x->data;
+  a.scale = static_cast<const float*>(scale->data);
+  a.saved_mean = static_cast<const float*>(reserve_space_1->data);
+  a.saved_var = static_cast<const float*>(reserve_space_2->data);
+  a.epsilon = epsilon;
+  a.is_training = is_training != 0;
+  a.dx = x_backprop->data;
+  a.scale_backprop = static_cast<float*>(scale_backprop->data);
+  a.offset_backprop = static_cast<float*>(offset_backprop->data);
+  a.reserve4 = r4;
+  a.reserve4_n = n4;
+  a.reserve5 = r5;
+  a.reserve5_n = n5;
+  return hip_status(status, LaunchBnGrad(t, g, a, workspace, workspace_bytes, s),
+                    "FusedBatchNormGradV3");
+}
+
+// ---------------------------------------------------------------------------
+// Adam
+// ---------------------------------------------------------------------------
+namespace {
+
+int check_adam_scalars(const TFMA_Tensor* const* sc, int dt, AdamScalars* out, DType t,
+                       TFMA_Status* st) {
+  static const char* names[6] = {"beta1_power", "beta2_power", "lr", "beta1", "beta2", "epsilon"};
+  double v[6];
+  for (int i = 0; i < 6; ++i) {
+    if (!valid_tensor(sc[i]) || !sc[i]->data)
+      return set_status(st, TFMA_INVALID_ARGUMENT, "%s is missing", names[i]);
+    if (sc[i]->ndims != 0)
+      return set_status(st, TFMA_INVALID_ARGUMENT, "%s is not a scalar: %s", names[i],
+                        shape_str(sc[i]).c_str());
+    if (sc[i]->dtype != dt)
+      return set_status(st, TFMA_INVALID_ARGUMENT, "%s has dtype %s, expected %s", names[i],
+                        dtype_name(sc[i]->dtype), dtype_name(dt));
+    v[i] = read_scalar(sc[i], t);
+  }
+  *out = adam_scalars(t, v[0], v[1], v[2], v[3], v[4], v[5]);
+  return TFMA_OK;
+}
+
+int check_adam_triple(const TFMA_Tensor* var, const TFMA_Tensor* m, const TFMA_Tensor* v,
+                      const TFMA_Tensor* grad, int* dt, TFMA_Status* st) {
+  if (!valid_tensor(var) || !valid_tensor(m) || !valid_tensor(v) || !valid_tensor(grad))
+    return set_status(st, TFMA_INVALID_ARGUMENT, "ResourceApplyAdam: invalid tensor");
+  if ((!var->data && num_elements(var) > 0) || (!m->data && num_elements(m) > 0) ||
+      (!v->data && num_elements(v) > 0))
+    return set_status(st, TFMA_FAILED_PRECONDITION, "Adam variables (var/m/v) not initialized.");
+  if (!same_shape(var, m))
+    return set_status(st, TFMA_INVALID_ARGUMENT, "var and m must have the same shape. var: %s m: %s",
+                      shape_str(var).c_str(), shape_str(m).c_str());
+  if (!same_shape(var, v))
+    return set_status(st, TFMA_INVALID_ARGUMENT, "var and v must have the same shape. var: %s v: %s",
+                      shape_str(var).c_str(), shape_str(v).c_str());
+  if (!same_shape(var, grad))
+    return set_status(st, TFMA_INVALID_ARGUMENT,
+                      "var and grad must have the same shape. var: %s grad: %s",
+                      shape_str(var).c_str(), shape_str(grad).c_str());
+  if (m->dtype != var->dtype || v->dtype != var->dtype || grad->dtype != var->dtype)
+    return set_status(st, TFMA_INVALID_ARGUMENT,
+                      "ResourceApplyAdam: var, m, v and grad must have the same dtype");
+  if (!grad->data && num_elements(grad) > 0)
+    return set_status(st, TFMA_INVALID_ARGUMENT, "ResourceApplyAdam: grad data is null");
+  *dt = var->dtype;
+  return TFMA_OK;
+}
+
+}  // namespace
+
+int TFMA_ResourceApplyAdam(void* stream, TFMA_Tensor* var, TFMA_Tensor* m, TFMA_Tensor* v,
+                           const TFMA_Tensor* beta1_power, const TFMA_Tensor* beta2_power,
+                           const TFMA_Tensor* lr, const TFMA_Tensor* beta1,
+                           const TFMA_Tensor* beta2, const TFMA_Tensor* epsilon,
+                           const TFMA_Tensor* grad, int use_locking, int use_nesterov,
+                           TFMA_Status* status) {
+  int dt = 0;
+  if (check_adam_triple(var, m, v, grad, &dt, status) != TFMA_OK) return status->code;
+  DType t;
+  if (!to_dtype(dt, &t))
+    return set_status(status, TFMA_UNIMPLEMENTED, "ResourceApplyAdam: dtype %s is not supported",
+                      dtype_name(dt));
+  const TFMA_Tensor* sc[6] = {beta1_power, beta2_power, lr, beta1, beta2, epsilon};
+  AdamScalars s;
+  if (check_adam_scalars(sc, dt, &s, t, status) != TFMA_OK) return status->code;
+  VarLocks locks;
+  if (use_locking) {
+    locks.add(var->data);
+    locks.add(m->data);
+    locks.add(v->data);
+    locks.lock();
+  }
+  const int64_t n = num_elements(var);
+  if (n == 0) return ok(status);
+  return hip_status(status,
+                    LaunchApplyAdam(t, var->data, m->data, v->data, grad->data, n, s,
+                                    use_nesterov != 0, as_stream(stream)),
+                    "ResourceApplyAdam");
+}
+
+int TFMA_GroupedApplyAdamWorkspaceBytes(int n, const TFMA_Tensor* vars, size_t* bytes,
+                                        TFMA_Status* status) {
+  (void)vars;
+  if (n < 1 || !bytes)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "N must be >= 1");
+  *bytes = (static_cast<size_t>(n) * sizeof(AdamTensorEntry) + 255) & ~size_t(255);
+  return ok(status);
+}
+
+int TFMA_GroupedResourceApplyAdam(void* stream, int n, TFMA_Tensor* vars, TFMA_Tensor* ms,
+                                  TFMA_Tensor* vs, const TFMA_Tensor* grads,
+                                  const TFMA_Tensor* beta1_power, const TFMA_Tensor* beta2_power,
+                                  const TFMA_Tensor* lr, const TFMA_Tensor* beta1,
+                                  const TFMA_Tensor* beta2, const TFMA_Tensor* epsilon,
+                                  int use_locking, int use_nesterov, void* workspace,
+                                  size_t workspace_bytes, TFMA_Status* status) {
+  if (n < 1 || !vars || !ms || !vs || !grads)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "N must be >= 1");
+  int dt0 = 0;
+  std::vector<AdamTensorEntry> table;
+  table.reserve(n);
+  int64_t chunks = 0;
+  for (int i = 0; i < n; ++i) {
+    int dt = 0;
+    if (check_adam_triple(&vars[i], &ms[i], &vs[i], &grads[i], &dt, status) != TFMA_OK) {
+      std::string msg = status->message;
+      return set_status(status, status->code, "tensor %d: %s", i, msg.c_str());
+    }
+    if (i == 0) dt0 = dt;
+    if (dt != dt0)
+      return set_status(status, TFMA_INVALID_ARGUMENT,
+                        "tensor %d has dtype %s, expected %s", i, dtype_name(dt), dtype_name(dt0));
+    const int64_t ne = num_elements(&vars[i]);
+    if (ne == 0) continue;
+    AdamTensorEntry e;
+    e.var = vars[i].data;
+    e.m = ms[i].data;
+    e.v = vs[i].data;
+    e.grad = grads[i].data;
+    e.n = ne;
+    e.first_chunk = chunks;
+    chunks += (ne + kGroupedAdamChunk - 1) / kGroupedAdamChunk;
+    table.push_back(e);
+  }
+  DType t;
+  if (!to_dtype(dt0, &t))
+    return set_status(status, TFMA_UNIMPLEMENTED,
+                      "MusaGroupedResourceApplyAdam: dtype %s is not supported", dtype_name(dt0));
+  const TFMA_Tensor* sc[6] = {beta1_power, beta2_power, lr, beta1, beta2, epsilon};
+  AdamScalars s;
+  if (check_adam_scalars(sc, dt0, &s, t, status) != TFMA_OK) return status->code;
+  size_t need = 0;
+  TFMA_GroupedApplyAdamWorkspaceBytes(n, vars, &need, nullptr);
+  if (!workspace || workspace_bytes < need)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "MusaGroupedResourceApplyAdam: workspace of %zu bytes required, got %zu",
+                      need, workspace ? workspace_bytes : size_t(0));
+  VarLocks locks;
+  if (use_locking) {
+    for (int i = 0; i < n; ++i) {
+      locks.add(vars[i].data);
+      locks.add(ms[i].data);
+      locks.add(vs[i].data);
+    }
+    locks.lock();
+  }
+  if (table.empty()) return ok(status);
+  hipStream_t strm = as_stream(stream);
+  hipError_t e = pinned_ring().upload(workspace, table.data(),
+                                      table.size() * sizeof(AdamTensorEntry), strm);
+  if (e != hipSuccess) return hip_status(status, e, "MusaGroupedResourceApplyAdam table upload");
+  e = LaunchGroupedApplyAdam(t, static_cast<const AdamTensorEntry*>(workspace),
+                             static_cast<int>(table.size()), chunks, s, use_nesterov != 0,
+                             strm);
+  return hip_status(status, e, "MusaGroupedResourceApplyAdam");
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise
+// ---------------------------------------------------------------------------
+int TFMA_BiasAdd(void* stream, const TFMA_Tensor* value, const TFMA_Tensor* bias,
+                 const char* data_format, TFMA_Tensor* output, TFMA_Status* status) {
+  return bias_add_impl(stream, value, bias, data_format, output, false, status);
+}
+
+int TFMA_MusaBiasAddRelu(void* stream, const TFMA_Tensor* value, const TFMA_Tensor* bias,
+                         const char* data_format, TFMA_Tensor* output, TFMA_Status* status) {
+  return bias_add_impl(stream, value, bias, data_format, output, true, status);
+}
+
+int TFMA_Relu(void* stream, const TFMA_Tensor* features, TFMA_Tensor* activations,
+              TFMA_Status* status) {
+  const TFMA_Tensor* ins[1] = {features};
+  return run_elementwise(stream, EwOp::kRelu, "Relu", ins, 1, activations, false, status);
+}
+
+int TFMA_AddV2(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* y, TFMA_Tensor* z,
+               TFMA_Status* status) {
+  const TFMA_Tensor* ins[2] = {x, y};
+  return run_elementwise(stream, EwOp::kAdd, "Add", ins, 2, z, true, status);
+}
+
+int TFMA_Mul(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* y, TFMA_Tensor* z,
+             TFMA_Status* status) {
+  const TFMA_Tensor* ins[2] = {x, y};
+  return run_elementwise(stream, EwOp::kMul, "Mul", ins, 2, z, true, status);
+}
+
+int TFMA_MusaAddV2Relu(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* y,
+                       TFMA_Tensor* z, TFMA_Status* status) {
+  const TFMA_Tensor* ins[2] = {x, y};
+  return run_elementwise(stream, EwOp::kAddRelu, "MusaAddV2Relu", ins, 2, z, true, status);
+}
+
+int TFMA_MusaShiftedAffineMap(void* stream, const TFMA_Tensor* data_left,
+                              const TFMA_Tensor* mask, const TFMA_Tensor* sliced_var_right,
+                              TFMA_Tensor* output, TFMA_Status* status) {
+  const TFMA_Tensor* ins[3] = {data_left, mask, sliced_var_right};
+  return run_elementwise(stream, EwOp::kMulAdd, "MusaShiftedAffineMap", ins, 3, output, true,
+                         status);
+}
+
+}  // extern "C"

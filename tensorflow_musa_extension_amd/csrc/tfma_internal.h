@@ -1,0 +1,156 @@
+// Internal host-side declarations shared by the op layer and the kernel
+// launchers.  Launchers return hipError_t; the op layer turns every failure
+// into a TFMA_Status.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "tfma.h"
+
+namespace tfma {
+
+enum class DType { kF32, kF16, kBF16, kF64 };
+
+// ---------------------------------------------------------------------------
+// Kernel launch tracing (TFMA_TraceEnable / TFMA_TraceRead).
+// ---------------------------------------------------------------------------
+void TraceBefore(hipStream_t stream, const char* kernel_name);
+void TraceAfter(hipStream_t stream);
+void SetLastKernel(const char* kernel_name);
+
+// Brackets one kernel launch: records the kernel name and, when tracing is
+// on for this name, HIP events around the launch.
+struct LaunchScope {
+  hipStream_t stream;
+  LaunchScope(hipStream_t s, const char* name) : stream(s) {
+    SetLastKernel(name);
+    TraceBefore(s, name);
+  }
+  ~LaunchScope() { TraceAfter(stream); }
+};
+
+// Number of compute units of the current device (cached per device).
+int DeviceCUs();
+
+// ---------------------------------------------------------------------------
+// Adam
+// ---------------------------------------------------------------------------
+// Host scalars, already in the compute type of T (float for f32/f16/bf16,
+// double for f64), with alpha computed the way TF's CPU kernel does.
+struct AdamScalars {
+  double alpha, beta1, beta2, epsilon, one_minus_beta1, one_minus_beta2;
+};
+
+hipError_t LaunchApplyAdam(DType t, void* var, void* m, void* v,
+                           const void* grad, int64_t n, const AdamScalars& s,
+                           bool nesterov, hipStream_t stream);
+
+// One entry of the grouped-Adam tensor table (device memory).
+struct AdamTensorEntry {
+  void* var;
+  void* m;
+  void* v;
+  const void* grad;
+  int64_t n;
+  int64_t first_chunk;  // prefix sum of chunks over the preceding tensors
+};
+constexpr int64_t kGroupedAdamChunk = 8192;  // elements per workgroup chunk
+
+hipError_t LaunchGroupedApplyAdam(DType t, const AdamTensorEntry* dev_table,
+                                  int n_tensors, int64_t total_chunks,
+                                  const AdamScalars& s, bool nesterov,
+                                  hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// Elementwise
+// ---------------------------------------------------------------------------
+enum class EwOp { kAdd, kAddRelu, kMul, kMulAdd, kRelu };
+
+// How an input of an elementwise kernel maps a flat output index i to its
+// own flat index: kFull: i; kScalar: 0; kPeriodic: (i / inner) % period.
+enum class BcastMode { kFull, kScalar, kPeriodic };
+struct BcastOperand {
+  const void* data;
+  BcastMode mode;
+  int64_t inner;
+  int64_t period;
+};
+
+// out[i] = op(a[i], b[i], c[i]) for i < n.  Operands past the op's arity are
+// ignored.  a is the "value" input; all operands have dtype t.
+hipError_t LaunchElementwise(DType t, EwOp op, int64_t n,
+                             const BcastOperand& a, const BcastOperand& b,
+                             const BcastOperand& c, void* out,
+                             hipStream_t stream);
+
+// General strided broadcast fallback (rank <= 8): strides are in elements,
+// 0 on broadcast dimensions.
+struct StridedShape {
+  int ndims;
+  int64_t dims[TFMA_MAX_DIMS];
+  int64_t stride_a[TFMA_MAX_DIMS];
+  int64_t stride_b[TFMA_MAX_DIMS];
+  int64_t stride_c[TFMA_MAX_DIMS];
+};
+hipError_t LaunchElementwiseStrided(DType t, EwOp op, int64_t n,
+                                    const void* a, const void* b,
+                                    const void* c, const StridedShape& shape,
+                                    void* out, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// Fused batch norm
+// ---------------------------------------------------------------------------
+struct BnGeometry {
+  bool nhwc;
+  int64_t n, c, h, w;  // logical NCHW sizes
+  int64_t rows;        // elements per channel = n*h*w
+};
+
+// Scratch bytes needed by the BN kernels for this geometry and dtype.
+size_t BnWorkspaceBytes(DType t, const BnGeometry& g);
+
+struct BnFwdArgs {
+  const void* x;
+  const float* scale;
+  const float* offset;
+  const float* mean_in;  // running mean (exponential average / inference)
+  const float* var_in;   // running variance
+  float epsilon;
+  float exp_avg_factor;
+  bool is_training;
+  void* y;
+  float* batch_mean;
+  float* batch_var;
+  float* saved_mean;
+  float* saved_var;
+  float* reserve3;  // 0-d scalar, may be null
+};
+hipError_t LaunchBnForward(DType t, const BnGeometry& g, const BnFwdArgs& a,
+                           void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
+
+struct BnGradArgs {
+  const void* dy;
+  const void* x;
+  const float* scale;
+  const float* saved_mean;
+  const float* saved_var;
+  float epsilon;
+  bool is_training;
+  void* dx;
+  float* scale_backprop;
+  float* offset_backprop;
+  float* reserve4;
+  int64_t reserve4_n;
+  float* reserve5;
+  int64_t reserve5_n;
+};
+hipError_t LaunchBnGrad(DType t, const BnGeometry& g, const BnGradArgs& a,
+                        void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+}  // namespace tfma

@@ -1,0 +1,127 @@
+// Kernel launch tracing: HIP events recorded on the launch stream around
+// every launch whose kernel name contains a chosen substring.  Used by the
+// benchmark to time one kernel inside a timed region on the stream the
+// kernel runs on.
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "tfma_internal.h"
+
+namespace tfma {
+namespace {
+
+struct Pending {
+  hipEvent_t start;
+  hipEvent_t end;
+};
+
+struct TraceState {
+  std::mutex mu;
+  bool enabled = false;
+  std::string substr;
+  std::vector<Pending> pending;
+  std::vector<hipEvent_t> pool;
+  double total_ms = 0.0;
+  int64_t launches = 0;
+};
+
+TraceState& state() {
+  static TraceState* s = new TraceState();
+  return *s;
+}
+
+thread_local bool t_open = false;
+thread_local Pending t_cur;
+thread_local const char* t_last_kernel = "";
+
+hipEvent_t take_event(TraceState& s) {
+  if (!s.pool.empty()) {
+    hipEvent_t e = s.pool.back();
+    s.pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Folds completed pending pairs into the totals (caller holds the mutex).
+void drain(TraceState& s) {
+  for (auto& p : s.pending) {
+    float ms = 0.f;
+    if (hipEventSynchronize(p.end) == hipSuccess &&
+        hipEventElapsedTime(&ms, p.start, p.end) == hipSuccess) {
+      s.total_ms += ms;
+      s.launches += 1;
+    }
+    s.pool.push_back(p.start);
+    s.pool.push_back(p.end);
+  }
+  s.pending.clear();
+}
+
+}  // namespace
+
+void SetLastKernel(const char* kernel_name) { t_last_kernel = kernel_name; }
+
+void TraceBefore(hipStream_t stream, const char* kernel_name) {
+  TraceState& s = state();
+  if (!s.enabled) return;  // racy read is fine: tracing is set up before use
+  std::lock_guard<std::mutex> lk(s.mu);
+  if (!s.enabled || strstr(kernel_name, s.substr.c_str()) == nullptr) return;
+  Pending p{take_event(s), take_event(s)};
+  if (!p.start || !p.end) return;
+  if (hipEventRecord(p.start, stream) != hipSuccess) return;
+  t_cur = p;
+  t_open = true;
+}
+
+void TraceAfter(hipStream_t stream) {
+  if (!t_open) return;
+  t_open = false;
+  TraceState& s = state();
+  std::lock_guard<std::mutex> lk(s.mu);
+  if (hipEventRecord(t_cur.end, stream) != hipSuccess) return;
+  s.pending.push_back(t_cur);
+  if (s.pending.size() > 4096) drain(s);
+}
+
+}  // namespace tfma
+
+extern "C" {
+
+int TFMA_TraceEnable(const char* name_substr, TFMA_Status* status) {
+  tfma::TraceState& s = tfma::state();
+  std::lock_guard<std::mutex> lk(s.mu);
+  tfma::drain(s);
+  s.total_ms = 0.0;
+  s.launches = 0;
+  s.enabled = name_substr != nullptr;
+  s.substr = name_substr ? name_substr : "";
+  if (status) {
+    status->code = TFMA_OK;
+    status->message[0] = '\0';
+  }
+  return TFMA_OK;
+}
+
+int TFMA_TraceRead(double* total_ms, int64_t* launches, TFMA_Status* status) {
+  tfma::TraceState& s = tfma::state();
+  std::lock_guard<std::mutex> lk(s.mu);
+  tfma::drain(s);
+  if (total_ms) *total_ms = s.total_ms;
+  if (launches) *launches = s.launches;
+  if (status) {
+    status->code = TFMA_OK;
+    status->message[0] = '\0';
+  }
+  return TFMA_OK;
+}
+
+const char* TFMA_LastKernelName(void) { return tfma::t_last_kernel; }
+
+}  // extern "C"

@@ -1,0 +1,221 @@
+"""CPU tests of the C ABI: the library loads, exports every entry point that
+include/tfma.h declares, and its host-side validation returns TF's codes and
+the reference's messages without touching a device (the pointers below are
+never dereferenced: each call fails validation first)."""
+import ctypes
+import os
+import re
+import threading
+
+import pytest
+
+from tensorflow_musa_extension_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FAKE = 0x1000  # a non-null device address that validation never touches
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "tfma.h")).read()
+    return sorted(set(re.findall(r"\b(TFMA_[A-Za-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_device_count():
+    lib = _lib.load()
+    assert lib.TFMA_Version().decode().startswith("tfma")
+    n = ctypes.c_int(-1)
+    st = _lib.TFMA_Status()
+    assert lib.TFMA_GetDeviceCount(ctypes.byref(n), ctypes.byref(st)) == _lib.OK
+    assert n.value >= 0  # 0 on a host without a GPU driver, as the plugin reports
+
+
+def T(shape, dtype=_lib.DT_FLOAT, ptr=FAKE):
+    return _lib.make_tensor(ptr, dtype, shape)
+
+
+def call(name, *args):
+    st = _lib.TFMA_Status()
+    code = getattr(_lib.load(), name)(*args, ctypes.byref(st))
+    assert code == st.code
+    return code, st.message.decode()
+
+
+def ref(t):
+    return ctypes.byref(t) if t is not None else None
+
+
+def bn_fwd(x, scale, offset, mean, var, factor=1.0, fmt=b"NHWC", training=1, c=None):
+    c = c if c is not None else scale.dims[0]
+    outs = [T((c,)) for _ in range(4)] + [T(())]
+    y = T(tuple(x.dims[:x.ndims]), x.dtype)
+    return call("TFMA_FusedBatchNormV3", None, ref(x), ref(scale), ref(offset), ref(mean),
+                ref(var), 1e-3, factor, fmt, training, ref(y), *[ref(o) for o in outs],
+                ctypes.c_void_p(FAKE), 1 << 30)
+
+
+def test_bn_validation():
+    x = T((2, 3, 3, 4))
+    ok4 = T((4,))
+    e = T((0,), ptr=None)
+    code, msg = bn_fwd(x, T((5,)), ok4, e, e, c=4)
+    assert code == _lib.INVALID_ARGUMENT and "scale must have the same number" in msg
+    code, msg = bn_fwd(x, ok4, T((3,)), e, e)
+    assert code == _lib.INVALID_ARGUMENT and "offset must have the same number" in msg
+    code, msg = bn_fwd(x, ok4, ok4, e, e, training=0)
+    assert code == _lib.INVALID_ARGUMENT and msg.startswith("When is_training=false, mean")
+    code, msg = bn_fwd(x, ok4, ok4, e, e, factor=0.5)
+    assert msg.startswith("When exponential_avg_factor != 1, mean")
+    code, msg = bn_fwd(T((2, 3, 4)), ok4, ok4, e, e)
+    assert code == _lib.INVALID_ARGUMENT and "4 or 5-dimensional" in msg
+    code, msg = bn_fwd(x, ok4, ok4, e, e, fmt=b"NHCW")
+    assert code == _lib.INVALID_ARGUMENT and msg == "Invalid data format"
+    code, msg = bn_fwd(T((2, 3, 3, 4), _lib.DT_INT32), ok4, ok4, e, e)
+    assert code == _lib.UNIMPLEMENTED
+    # NCHW: channels are dim 1.
+    code, msg = bn_fwd(T((2, 4, 3, 3)), T((3,)), T((3,)), e, e, fmt=b"NCHW", c=3)
+    assert "scale must have the same number of elements as the channels of x, got 3 and 4" in msg
+
+
+def test_bn_workspace_query():
+    st = _lib.TFMA_Status()
+    nbytes = ctypes.c_size_t(0)
+    x = T((256, 56, 56, 256), _lib.DT_HALF)
+    assert _lib.load().TFMA_FusedBatchNormWorkspaceBytes(ctypes.byref(x), b"NHWC",
+                                                         ctypes.byref(nbytes),
+                                                         ctypes.byref(st)) == _lib.OK
+    # Partials + coefficients stay a small fraction of x (411 MB).
+    assert 256 * 16 <= nbytes.value < 16 << 20
+
+
+def test_bn_grad_validation():
+    x = T((2, 3, 3, 4))
+    c4 = T((4,))
+    outs = [T((2, 3, 3, 4)), T((4,)), T((4,)), T((4,)), T((4,))]
+    code, msg = call("TFMA_FusedBatchNormGradV3", None, ref(T((2, 3, 3, 5))), ref(x), ref(c4),
+                     ref(c4), ref(c4), ref(T(())), 1e-3, b"NHWC", 1, *[ref(o) for o in outs],
+                     ctypes.c_void_p(FAKE), 1 << 30)
+    assert code == _lib.INVALID_ARGUMENT
+    assert msg.startswith("x and y_backprop must have same shape, but x has shape [2,3,3,4]")
+    code, msg = call("TFMA_FusedBatchNormGradV3", None, ref(x), ref(x), ref(c4), ref(T((3,))),
+                     ref(c4), ref(T(())), 1e-3, b"NHWC", 1, *[ref(o) for o in outs],
+                     ctypes.c_void_p(FAKE), 1 << 30)
+    assert "reserve_space_1 must have the same number of elements" in msg
+
+
+def scalars(dtype=_lib.DT_FLOAT, values=(0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7)):
+    bufs = [(ctypes.c_float * 1)(v) for v in values]
+    descs = [_lib.make_tensor(ctypes.addressof(b), dtype, ()) for b in bufs]
+    return bufs, descs
+
+
+def adam(var, m, v, grad, descs, locking=0):
+    return call("TFMA_ResourceApplyAdam", None, ref(var), ref(m), ref(v),
+                *[ref(d) for d in descs], ref(grad), locking, 0)
+
+
+def test_adam_validation():
+    bufs, descs = scalars()
+    a, b = T((4, 3)), T((4, 2))
+    code, msg = adam(a, b, a, a, descs)
+    assert code == _lib.INVALID_ARGUMENT
+    assert msg == "var and m must have the same shape. var: [4,3] m: [4,2]"
+    code, msg = adam(a, a, b, a, descs)
+    assert msg == "var and v must have the same shape. var: [4,3] v: [4,2]"
+    code, msg = adam(a, a, a, b, descs)
+    assert msg == "var and grad must have the same shape. var: [4,3] grad: [4,2]"
+    code, msg = adam(T((4, 3), ptr=None), a, a, a, descs)
+    assert code == _lib.FAILED_PRECONDITION and msg == "Adam variables (var/m/v) not initialized."
+    bad = list(descs)
+    bad[2] = _lib.make_tensor(ctypes.addressof(bufs[2]), _lib.DT_FLOAT, (1,))
+    code, msg = adam(a, a, a, a, bad)
+    assert code == _lib.INVALID_ARGUMENT and msg == "lr is not a scalar: [1]"
+    code, msg = adam(T((4, 3), _lib.DT_INT32), T((4, 3), _lib.DT_INT32),
+                     T((4, 3), _lib.DT_INT32), T((4, 3), _lib.DT_INT32), descs)
+    assert code == _lib.UNIMPLEMENTED
+
+
+def test_adam_locking_is_deadlock_free():
+    """Concurrent use_locking calls over overlapping var/m/v sets in every
+    order complete (locks are taken in address order).  Empty tensors make
+    each call return after locking, before any device work."""
+    bufs, descs = scalars()
+    ptrs = [0x10000 * (i + 1) for i in range(3)]
+    orders = [(0, 1, 2), (2, 1, 0), (1, 0, 2), (2, 0, 1)]
+    errors = []
+
+    def worker(order):
+        try:
+            for _ in range(2000):
+                ts = [T((0,), ptr=ptrs[k]) for k in order]
+                code, _ = adam(ts[0], ts[1], ts[2], T((0,)), descs, locking=1)
+                assert code == _lib.OK
+        except Exception as e:  # pragma: no cover
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(o,)) for o in orders]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in threads), "deadlock"
+    assert not errors
+
+
+def test_grouped_adam_validation():
+    bufs, descs = scalars()
+    n = 2
+    arr = lambda shapes: (_lib.TFMA_Tensor * n)(*[T(s) for s in shapes])
+    vs = arr([(4,), (5,)])
+    ms = arr([(4,), (6,)])
+    code, msg = call("TFMA_GroupedResourceApplyAdam", None, n, vs, ms, arr([(4,), (5,)]),
+                     arr([(4,), (5,)]), *[ref(d) for d in descs], 0, 0,
+                     ctypes.c_void_p(FAKE), 4096)
+    assert code == _lib.INVALID_ARGUMENT
+    assert msg == "tensor 1: var and m must have the same shape. var: [5] m: [6]"
+    code, msg = call("TFMA_GroupedResourceApplyAdam", None, n, vs, arr([(4,), (5,)]),
+                     arr([(4,), (5,)]), arr([(4,), (5,)]), *[ref(d) for d in descs], 0, 0,
+                     None, 0)
+    assert code == _lib.INVALID_ARGUMENT and "workspace" in msg
+
+
+def test_elementwise_validation():
+    x = T((4, 5))
+    code, msg = call("TFMA_BiasAdd", None, ref(x), ref(T((4,))), b"NHWC", ref(T((4, 5))))
+    assert code == _lib.INVALID_ARGUMENT and msg == "Dimension mismatch in BiasAdd"
+    code, msg = call("TFMA_BiasAdd", None, ref(T((5,))), ref(T((5,))), b"NHWC", ref(T((5,))))
+    assert msg == "Input tensor must be at least 2D: [5]"
+    code, msg = call("TFMA_BiasAdd", None, ref(x), ref(T((1, 5))), b"NHWC", ref(T((4, 5))))
+    assert msg == "Biases must be 1D: [1,5]"
+    code, msg = call("TFMA_AddV2", None, ref(x), ref(T((3,))), ref(T((4, 5))))
+    assert code == _lib.INVALID_ARGUMENT and msg == "Incompatible shapes for Add: [4,5] and [3]"
+    code, msg = call("TFMA_Mul", None, ref(x), ref(T((4, 1))), ref(T((4, 4))))
+    assert "does not match broadcast shape [4,5]" in msg
+    code, msg = call("TFMA_MusaShiftedAffineMap", None, ref(x), ref(T((5,))),
+                     ref(T((2, 1, 5))), ref(T((4, 5))))
+    assert "does not match broadcast shape [2,4,5]" in msg
+    code, msg = call("TFMA_AddV2", None, ref(x), ref(T((4, 5), _lib.DT_HALF)), ref(T((4, 5))))
+    assert code == _lib.INVALID_ARGUMENT and "dtype" in msg
+    # Empty outputs succeed without device work.
+    code, _ = call("TFMA_Relu", None, ref(T((0, 5))), ref(T((0, 5))))
+    assert code == _lib.OK
+
+
+def test_trace_api_without_device():
+    st = _lib.TFMA_Status()
+    lib = _lib.load()
+    assert lib.TFMA_TraceEnable(b"tfma_bn", ctypes.byref(st)) == _lib.OK
+    ms = ctypes.c_double(-1)
+    n = ctypes.c_int64(-1)
+    assert lib.TFMA_TraceRead(ctypes.byref(ms), ctypes.byref(n), ctypes.byref(st)) == _lib.OK
+    assert ms.value == 0 and n.value == 0
+    assert lib.TFMA_TraceEnable(None, ctypes.byref(st)) == _lib.OK

@@ -1,0 +1,241 @@
+"""FusedBatchNormV3 / FusedBatchNormGradV3 on the GPU vs the TF-CPU oracle.
+
+Tolerances (written per check): float32 outputs and all float32 statistics
+1e-5, float16/bfloat16 activations 1e-2, each as max|got-ref| / max|ref| over
+the output (the reference's own tests use np.allclose with rtol=atol=1e-4 at
+[2,2,2,4], test/ops/fused_batchnorm_op_test.py:25-55).
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import tensorflow_musa_extension_amd as tfma
+from oracle import oracle
+from tests.helpers import assert_close, gen, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+ops = tfma.raw_ops
+
+ACT_TOL = {"float32": 1e-5, "float16": 1e-2, "bfloat16": 1e-2}
+STAT_TOL = 1e-5
+
+
+def _inputs(rng, shape, dtype, data_format, loc=0.0):
+    c = shape[-1] if data_format == "NHWC" else shape[1]
+    x = gen(rng, shape, dtype, loc=loc)
+    scale = rng.uniform(0.5, 1.5, c).astype(np.float32)
+    offset = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    dy = gen(rng, shape, dtype)
+    return x, scale, offset, dy
+
+
+def _run_fwd_grad(dev, x, scale, offset, dy, dtype, data_format, eps, poison=True,
+                  mean=None, var=None, factor=1.0, is_training=True):
+    f = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    tx = to_dev(x, dtype, dev)
+    c = scale.shape[0]
+    f32 = dict(dtype=torch.float32, device=dev)
+    out = ops.FusedBatchNormV3Result(
+        torch.empty_like(tx), torch.empty(c, **f32), torch.empty(c, **f32),
+        torch.empty(c, **f32), torch.empty(c, **f32), torch.empty((), **f32))
+    if poison:  # every output must be overwritten
+        for o in out:
+            o.fill_(float("nan"))
+    tm = f(mean) if mean is not None else torch.empty(0, **f32)
+    tv = f(var) if var is not None else torch.empty(0, **f32)
+    fwd = ops.FusedBatchNormV3(tx, f(scale), f(offset), tm, tv, epsilon=eps,
+                               exponential_avg_factor=factor, data_format=data_format,
+                               is_training=is_training, out=out)
+    tdy = to_dev(dy, dtype, dev)
+    gout = ops.FusedBatchNormGradV3Result(
+        torch.empty_like(tx), torch.empty(c, **f32), torch.empty(c, **f32),
+        torch.empty(c, **f32), torch.empty(c, **f32))
+    if poison:
+        for o in gout:
+            o.fill_(float("nan"))
+    grad = ops.FusedBatchNormGradV3(tdy, tx, f(scale), fwd.reserve_space_1,
+                                    fwd.reserve_space_2, fwd.reserve_space_3, epsilon=eps,
+                                    data_format=data_format, is_training=is_training, out=gout)
+    torch.cuda.synchronize()
+    return fwd, grad
+
+
+CASES = [
+    # (shape, dtype, data_format)
+    ((2, 2, 2, 4), "float32", "NHWC"),       # reference test shape
+    ((2, 4, 5, 3), "float32", "NHWC"),       # C % 4 != 0: scalar path
+    ((4, 7, 9, 64), "float32", "NHWC"),
+    ((32, 56, 56, 64), "float32", "NHWC"),   # cfg1
+    ((8, 14, 14, 256), "float16", "NHWC"),
+    ((8, 14, 14, 256), "bfloat16", "NHWC"),
+    ((3, 5, 5, 2048), "float16", "NHWC"),
+    ((16, 7, 7, 33), "float16", "NHWC"),     # odd C: scalar path
+    ((5, 3, 3, 520), "bfloat16", "NHWC"),    # C % 256 != 0: partial channel tile
+    ((2, 3, 5, 5), "float32", "NCHW"),
+    ((4, 16, 7, 7), "float16", "NCHW"),
+    ((2, 8, 28, 28), "bfloat16", "NCHW"),
+    ((3, 6, 8, 8), "float32", "NCHW"),
+]
+
+
+@pytest.mark.parametrize("shape,dtype,data_format", CASES)
+def test_fwd_grad_matches_oracle(dev, shape, dtype, data_format):
+    rng = np.random.default_rng(zlib.crc32(repr((shape, dtype, data_format)).encode()))
+    eps = 1e-3
+    x, scale, offset, dy = _inputs(rng, shape, dtype, data_format)
+    fwd, grad = _run_fwd_grad(dev, x, scale, offset, dy, dtype, data_format, eps)
+    ry, rbm, rbv, rsm, rsv = oracle.bn_fwd(x, scale, offset, epsilon=eps,
+                                          data_format=data_format, dtype=dtype)
+    assert_close(to_np(fwd.y, dtype), ry, dtype, ACT_TOL[dtype], "y")
+    for name, got, ref in (("batch_mean", fwd.batch_mean, rbm),
+                           ("batch_variance", fwd.batch_variance, rbv),
+                           ("reserve_space_1", fwd.reserve_space_1, rsm),
+                           ("reserve_space_2", fwd.reserve_space_2, rsv)):
+        assert_close(got.cpu().numpy(), ref, "float32", STAT_TOL, name)
+    assert float(fwd.reserve_space_3.cpu()) == 0.0
+    # Grad consumes the forward's reserve spaces, as in a training step.
+    rdx, rsb, rob = oracle.bn_grad(dy, x, scale, fwd.reserve_space_1.cpu().numpy(),
+                                   fwd.reserve_space_2.cpu().numpy(), epsilon=eps,
+                                   data_format=data_format, dtype=dtype)
+    assert_close(to_np(grad.x_backprop, dtype), rdx, dtype, ACT_TOL[dtype], "x_backprop")
+    assert_close(grad.scale_backprop.cpu().numpy(), rsb, "float32", STAT_TOL, "scale_backprop")
+    assert_close(grad.offset_backprop.cpu().numpy(), rob, "float32", STAT_TOL, "offset_backprop")
+    assert torch.all(grad.reserve_space_4 == 0) and torch.all(grad.reserve_space_5 == 0)
+
+
+def test_large_mean_statistics(dev):
+    """|mean| >> std: the shifted sums must not cancel (variance to 1e-5)."""
+    rng = np.random.default_rng(7)
+    shape = (16, 28, 28, 64)
+    x, scale, offset, dy = _inputs(rng, shape, "float32", "NHWC", loc=1000.0)
+    fwd, _ = _run_fwd_grad(dev, x, scale, offset, dy, "float32", "NHWC", 1e-3)
+    _, rbm, rbv, rsm, rsv = oracle.bn_fwd(x, scale, offset, epsilon=1e-3)
+    assert_close(fwd.reserve_space_1.cpu().numpy(), rsm, "float32", STAT_TOL, "mean")
+    assert_close(fwd.reserve_space_2.cpu().numpy(), rsv, "float32", 1e-5, "variance")
+
+
+def test_exponential_avg_factor_and_inference(dev):
+    rng = np.random.default_rng(11)
+    shape = (4, 6, 6, 32)
+    x, scale, offset, dy = _inputs(rng, shape, "float32", "NHWC")
+    run_mean = rng.standard_normal(32).astype(np.float32)
+    run_var = rng.uniform(0.5, 2.0, 32).astype(np.float32)
+    fwd, _ = _run_fwd_grad(dev, x, scale, offset, dy, "float32", "NHWC", 1e-3,
+                           mean=run_mean, var=run_var, factor=0.3)
+    ry, rbm, rbv, rsm, rsv = oracle.bn_fwd(x, scale, offset, run_mean, run_var, epsilon=1e-3,
+                                          exponential_avg_factor=0.3)
+    assert_close(fwd.batch_mean.cpu().numpy(), rbm, "float32", STAT_TOL, "blended mean")
+    assert_close(fwd.batch_variance.cpu().numpy(), rbv, "float32", STAT_TOL, "blended var")
+    assert_close(to_np(fwd.y, "float32"), ry, "float32", 1e-5, "y")
+    # Inference: y from the running statistics; grad with is_training=False.
+    fwd, grad = _run_fwd_grad(dev, x, scale, offset, dy, "float32", "NHWC", 1e-3,
+                              mean=run_mean, var=run_var, is_training=False)
+    ry, rbm, rbv, _, _ = oracle.bn_fwd(x, scale, offset, run_mean, run_var, epsilon=1e-3,
+                                      is_training=False)
+    assert_close(to_np(fwd.y, "float32"), ry, "float32", 1e-5, "inference y")
+    np.testing.assert_array_equal(fwd.batch_mean.cpu().numpy(), run_mean)
+    rdx, rsb, rob = oracle.bn_grad(dy, x, scale, run_mean, run_var, epsilon=1e-3,
+                                   is_training=False)
+    assert_close(to_np(grad.x_backprop, "float32"), rdx, "float32", 1e-5, "inference dx")
+    assert_close(grad.scale_backprop.cpu().numpy(), rsb, "float32", STAT_TOL, "inference dscale")
+
+
+def test_empty_batch(dev):
+    f32 = dict(dtype=torch.float32, device=dev)
+    x = torch.empty((0, 4, 4, 8), **f32)
+    scale = torch.ones(8, **f32)
+    offset = torch.zeros(8, **f32)
+    e = torch.empty(0, **f32)
+    fwd = ops.FusedBatchNormV3(x, scale, offset, e, e)
+    torch.cuda.synchronize()
+    assert fwd.y.shape == x.shape
+    assert torch.isnan(fwd.batch_mean).all() and torch.isnan(fwd.batch_variance).all()
+    grad = ops.FusedBatchNormGradV3(x, x, scale, fwd.reserve_space_1, fwd.reserve_space_2,
+                                    fwd.reserve_space_3)
+    torch.cuda.synchronize()
+    assert torch.all(grad.scale_backprop == 0) and torch.all(grad.offset_backprop == 0)
+
+
+def test_constant_channel(dev):
+    """sigma^2 = 0: y = offset exactly, batch_variance = 0."""
+    f32 = dict(dtype=torch.float32, device=dev)
+    x = torch.full((4, 5, 5, 16), 3.25, **f32)
+    scale = torch.linspace(0.5, 1.5, 16, **f32)
+    offset = torch.linspace(-1, 1, 16, **f32)
+    e = torch.empty(0, **f32)
+    fwd = ops.FusedBatchNormV3(x, scale, offset, e, e, epsilon=1e-3)
+    torch.cuda.synchronize()
+    assert torch.equal(fwd.y, offset.expand_as(fwd.y))
+    assert torch.all(fwd.batch_variance == 0)
+    assert torch.all(fwd.batch_mean == 3.25)
+
+
+@pytest.mark.parametrize("shape", [(256, 7, 7, 2048), (256, 14, 14, 1024)])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_cfg2_full_size(dev, shape, dtype):
+    """BASELINE cfg2 shapes at full size against the oracle (eps=1.001e-5)."""
+    rng = np.random.default_rng(0)
+    eps = 1.001e-5
+    x, scale, offset, dy = _inputs(rng, shape, dtype, "NHWC")
+    fwd, grad = _run_fwd_grad(dev, x, scale, offset, dy, dtype, "NHWC", eps, poison=False)
+    ry, rbm, rbv, rsm, rsv = oracle.bn_fwd(x, scale, offset, epsilon=eps, dtype=dtype)
+    rdx, rsb, rob = oracle.bn_grad(dy, x, scale, fwd.reserve_space_1.cpu().numpy(),
+                                   fwd.reserve_space_2.cpu().numpy(), epsilon=eps,
+                                   dtype=dtype)
+    assert_close(to_np(fwd.y, dtype), ry, dtype, 1e-2, "y")
+    assert_close(fwd.batch_mean.cpu().numpy(), rbm, "float32", STAT_TOL, "batch_mean")
+    assert_close(fwd.batch_variance.cpu().numpy(), rbv, "float32", STAT_TOL, "batch_variance")
+    assert_close(to_np(grad.x_backprop, dtype), rdx, dtype, 1e-2, "x_backprop")
+    assert_close(grad.scale_backprop.cpu().numpy(), rsb, "float32", STAT_TOL, "scale_backprop")
+    assert_close(grad.offset_backprop.cpu().numpy(), rob, "float32", STAT_TOL, "offset_backprop")
+
+
+def test_largest_shape_invariants(dev):
+    """[256,56,56,256] f16 (cfg2's largest): size-independent properties.
+    Per channel: mean(y) = offset and var(y) = scale^2 var/(var+eps) (both
+    measured in float64 on the device); the grad's dx sums to 0."""
+    torch.manual_seed(0)
+    shape = (256, 56, 56, 256)
+    x = torch.randn(shape, device=dev).half()
+    dy = torch.randn(shape, device=dev).half()
+    scale = torch.rand(256, device=dev) + 0.5
+    offset = 0.1 * torch.randn(256, device=dev)
+    e = torch.empty(0, device=dev)
+    eps = 1.001e-5
+    fwd = ops.FusedBatchNormV3(x, scale, offset, e, e, epsilon=eps)
+    xd = x.double().reshape(-1, 256)
+    mean_ref = xd.mean(0)
+    var_ref = xd.var(0, unbiased=False)
+    assert torch.allclose(fwd.reserve_space_1.double(), mean_ref, rtol=0, atol=1e-5)
+    assert torch.allclose(fwd.reserve_space_2.double(), var_ref, rtol=1e-5, atol=0)
+    yd = fwd.y.double().reshape(-1, 256)
+    assert torch.allclose(yd.mean(0), offset.double(), atol=2e-3)
+    want_var = scale.double() ** 2 * var_ref / (var_ref + eps)
+    assert torch.allclose(yd.var(0, unbiased=False), want_var, rtol=2e-3)
+    grad = ops.FusedBatchNormGradV3(dy, x, scale, fwd.reserve_space_1, fwd.reserve_space_2,
+                                    fwd.reserve_space_3, epsilon=eps)
+    dyd = dy.double().reshape(-1, 256)
+    assert torch.allclose(grad.offset_backprop.double(), dyd.sum(0), rtol=1e-5, atol=1e-2)
+    dxd = grad.x_backprop.double().reshape(-1, 256)
+    # sum(dx) = 0 up to the f16 rounding of each dx: |dx| ~ 1 rounds with
+    # error std ~2e-4, so the sum over n = 802816 has std ~0.2 (max over 256
+    # channels ~0.6); a wrong mean term would give |sum| ~ n * 1e-3 = 800.
+    assert float(dxd.sum(0).abs().max()) < 1.5
+    torch.cuda.synchronize()
+
+
+def test_shape_errors(dev):
+    f32 = dict(dtype=torch.float32, device=dev)
+    x = torch.zeros((2, 3, 3, 4), **f32)
+    e = torch.empty(0, **f32)
+    with pytest.raises(tfma.InvalidArgumentError, match="scale must have the same number"):
+        ops.FusedBatchNormV3(x, torch.ones(5, **f32), torch.zeros(4, **f32), e, e)
+    with pytest.raises(tfma.InvalidArgumentError, match="When is_training=false, mean"):
+        ops.FusedBatchNormV3(x, torch.ones(4, **f32), torch.zeros(4, **f32), e, e,
+                             is_training=False)
+    with pytest.raises(tfma.InvalidArgumentError, match="x and y_backprop must have same shape"):
+        ops.FusedBatchNormGradV3(torch.zeros((2, 3, 3, 5), **f32), x, torch.ones(4, **f32),
+                                 torch.zeros(4, **f32), torch.ones(4, **f32),
+                                 torch.zeros((), **f32))

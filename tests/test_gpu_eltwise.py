@@ -1,0 +1,120 @@
+"""Elementwise ops and fused chains on the GPU vs the TF-CPU oracle.  Bar:
+bitwise equality (each fused chain rounds exactly where the unfused TF ops
+do)."""
+import numpy as np
+import pytest
+import torch
+
+import tensorflow_musa_extension_amd as tfma
+from oracle import oracle
+from tests.helpers import assert_bitwise, gen, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+ops = tfma.raw_ops
+DTYPES = ["float32", "float16", "bfloat16"]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(8192, 4096), (8191, 4095), (3, 5), (1, 1), (7, 9, 33)])
+@pytest.mark.parametrize("relu", [False, True])
+def test_bias_add_nhwc(dev, dtype, shape, relu):
+    rng = np.random.default_rng(1)
+    x = gen(rng, shape, dtype)
+    b = gen(rng, shape[-1:], dtype)
+    fn = ops.MusaBiasAddRelu if relu else ops.BiasAdd
+    out = fn(to_dev(x, dtype, dev), to_dev(b, dtype, dev))
+    torch.cuda.synchronize()
+    assert_bitwise(to_np(out, dtype), oracle.bias_add(x, b, relu=relu, dtype=dtype), "bias_add")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(4, 16, 7, 7), (2, 3, 5, 8), (2, 5, 3)])
+def test_bias_add_relu_nchw(dev, dtype, shape):
+    rng = np.random.default_rng(2)
+    x = gen(rng, shape, dtype)
+    b = gen(rng, shape[1:2], dtype)
+    out = ops.MusaBiasAddRelu(to_dev(x, dtype, dev), to_dev(b, dtype, dev), data_format="NCHW")
+    torch.cuda.synchronize()
+    ref = oracle.bias_add(x, b, data_format="NCHW", relu=True, dtype=dtype)
+    assert_bitwise(to_np(out, dtype), ref, "bias_add_relu nchw")
+
+
+BCAST = [
+    ((8192, 4096), (4096,)),        # cfg4 row broadcast
+    ((8191, 4095), (4095,)),        # odd tail
+    ((8192, 4096), (8192, 4096)),   # full
+    ((4096,), (8192, 4096)),        # broadcast operand first
+    ((64, 33), ()),                 # scalar
+    ((64, 33), (64, 1)),            # column broadcast (inner > 1)
+    ((4, 1, 5), (1, 3, 1)),         # neither operand full: strided path
+    ((2, 3, 4, 8), (3, 1, 8)),      # two broadcast runs: strided path
+    ((0, 4), (4,)),                 # empty
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("xs,ys", BCAST)
+@pytest.mark.parametrize("op", ["add", "add_relu", "mul"])
+def test_binary_broadcast(dev, dtype, xs, ys, op):
+    rng = np.random.default_rng(3)
+    x = gen(rng, xs, dtype)
+    y = gen(rng, ys, dtype)
+    fn = {"add": ops.AddV2, "add_relu": ops.MusaAddV2Relu, "mul": ops.Mul}[op]
+    out = fn(to_dev(x, dtype, dev), to_dev(y, dtype, dev))
+    torch.cuda.synchronize()
+    assert_bitwise(to_np(out, dtype), oracle.eltwise(op, [x, y], dtype), op)
+
+
+MULADD = [
+    ((8192, 4096), (8192, 4096), (8192, 4096)),   # a, b full
+    ((8192, 4096), (4096,), (4096,)),             # a, b row broadcast
+    ((8191, 4095), (8191, 4095), (8191, 4095)),
+    ((8191, 4095), (4095,), (4095,)),
+    ((5, 7), (5, 7), ()),
+    ((5, 1, 7), (1, 3, 1), (3, 7)),               # strided path
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("xs,as_,bs", MULADD)
+def test_mul_add(dev, dtype, xs, as_, bs):
+    rng = np.random.default_rng(4)
+    x, a, b = gen(rng, xs, dtype), gen(rng, as_, dtype), gen(rng, bs, dtype)
+    out = ops.MusaShiftedAffineMap(to_dev(x, dtype, dev), to_dev(a, dtype, dev),
+                                   to_dev(b, dtype, dev))
+    torch.cuda.synchronize()
+    assert_bitwise(to_np(out, dtype), oracle.eltwise("mul_add", [x, a, b], dtype), "mul_add")
+
+
+def test_relu_known_answers(dev):
+    """The reference's Relu literal (test/ops/relu_op_test.py:45-96) plus
+    -0 and NaN, which keep their bits as with Eigen's max."""
+    x = torch.tensor([-2.0, -1.0, 0.0, 1.0, 2.0, -0.0, float("nan"), float("-inf")], device=dev)
+    y = ops.Relu(x).cpu()
+    want = torch.tensor([0.0, 0.0, 0.0, 1.0, 2.0, -0.0, float("nan"), 0.0])
+    assert torch.equal(y[:6], want[:6])
+    assert torch.signbit(y[5]) and torch.isnan(y[6]) and y[7] == 0
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_relu_large(dev, dtype):
+    rng = np.random.default_rng(5)
+    x = gen(rng, (4097, 1031), dtype)
+    out = ops.Relu(to_dev(x, dtype, dev))
+    torch.cuda.synchronize()
+    assert_bitwise(to_np(out, dtype), oracle.eltwise("relu", [x], dtype), "relu")
+
+
+def test_vector_path_is_taken(dev):
+    x = torch.randn(8192, 4096, device=dev)
+    b = torch.randn(4096, device=dev)
+    ops.MusaBiasAddRelu(x, b)
+    assert ops.last_kernel_name() == "tfma_ew_add_relu"
+
+
+def test_errors(dev):
+    x = torch.zeros(4, 5, device=dev)
+    with pytest.raises(tfma.InvalidArgumentError, match="Dimension mismatch in BiasAdd"):
+        ops.BiasAdd(x, torch.zeros(4, device=dev))
+    with pytest.raises(tfma.InvalidArgumentError, match="Incompatible shapes for Add"):
+        ops.AddV2(x, torch.zeros(3, device=dev))
