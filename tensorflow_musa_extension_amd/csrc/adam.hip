@@ -29,9 +29,9 @@ struct AdamP {
   C alpha, beta1, eps, omb1, omb2;
 };
 
-__device__ inline float dsqrt(float x) { return __fsqrt_rn(x); }
-__device__ inline double dsqrt(double x) { return __dsqrt_rn(x); }
-__device__ inline float ddiv(float a, float b) { return __fdiv_rn(a, b); }
+__device__ inline float dsqrt(float x) { return __builtin_sqrtf(x); }
+__device__ inline double dsqrt(double x) { return __builtin_sqrt(x); }
+__device__ inline float ddiv(float a, float b) { return a / b; }
 __device__ inline double ddiv(double a, double b) { return a / b; }
 
 template <class Tr, bool kNesterov>

@@ -326,11 +326,11 @@ __global__ __launch_bounds__(kFinCh* kFinSlices) void bn_finalize_kernel(
         a.batch_mean[ch] = a.mean_in[ch] * omf + mean_f * a.f;
         a.batch_var[ch] = a.var_in[ch] * omf + (var_f * adj) * a.f;
       }
-      const float inv = __fdiv_rn(1.0f, __fsqrt_rn(var_f + a.eps));
+      const float inv = 1.0f / __builtin_sqrtf(var_f + a.eps);
       coef[ch] = make_float4(mean_f, inv * a.scale[ch], a.offset[ch], 0.f);
     } else {
       const float mu = a.mean_in[ch];
-      const float k = __fdiv_rn(1.0f, __fsqrt_rn(a.var_in[ch] + a.eps));
+      const float k = 1.0f / __builtin_sqrtf(a.var_in[ch] + a.eps);
       a.offset_bp[ch] = static_cast<float>(s1);
       a.scale_bp[ch] = static_cast<float>(s2 * static_cast<double>(k));
       if (a.is_training) {
@@ -360,7 +360,7 @@ __global__ void bn_infer_coef_kernel(FinArgs a, float4* __restrict__ coef) {
   if (ch >= a.c) return;
   const float mu = a.mean_in[ch];
   const float var = a.var_in[ch];
-  const float inv = __fdiv_rn(1.0f, __fsqrt_rn(var + a.eps));
+  const float inv = 1.0f / __builtin_sqrtf(var + a.eps);
   a.batch_mean[ch] = mu;
   a.batch_var[ch] = var;
   a.saved_mean[ch] = mu;

@@ -128,7 +128,11 @@ def test_grouped_repeated_calls_reuse_staging(dev):
     ts = []
     for k in range(n_calls):
         n = 1000 + 37 * k
-        ts.append([to_dev(gen(rng, n, "float32", scale=0.02), "float32", dev) for _ in range(4)])
+        var = gen(rng, n, "float32", scale=0.02)
+        m = gen(rng, n, "float32", scale=1e-4)
+        v = np.abs(gen(rng, n, "float32", scale=1e-4))  # second moment >= 0
+        g = gen(rng, n, "float32", scale=1e-3)
+        ts.append([to_dev(a, "float32", dev) for a in (var, m, v, g)])
     refs = [[to_np(t, "float32").copy() for t in group] for group in ts]
     for group in ts:
         var, m, v, g = group
@@ -140,6 +144,8 @@ def test_grouped_repeated_calls_reuse_staging(dev):
                     _t_scalar(LR, "float32"), _t_scalar(B1, "float32"),
                     _t_scalar(B2, "float32"), _t_scalar(EPS, "float32"))
         assert_bitwise(to_np(group[0], "float32"), rv, "var")
+        assert_bitwise(to_np(group[1], "float32"), rm, "m")
+        assert_bitwise(to_np(group[2], "float32"), rw, "v")
 
 
 def test_adam_errors(dev):

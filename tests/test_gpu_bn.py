@@ -219,10 +219,12 @@ def test_largest_shape_invariants(dev):
     dyd = dy.double().reshape(-1, 256)
     assert torch.allclose(grad.offset_backprop.double(), dyd.sum(0), rtol=1e-5, atol=1e-2)
     dxd = grad.x_backprop.double().reshape(-1, 256)
-    # sum(dx) = 0 up to the f16 rounding of each dx: |dx| ~ 1 rounds with
-    # error std ~2e-4, so the sum over n = 802816 has std ~0.2 (max over 256
-    # channels ~0.6); a wrong mean term would give |sum| ~ n * 1e-3 = 800.
-    assert float(dxd.sum(0).abs().max()) < 1.5
+    # sum(dx) = 0 up to the f16 rounding of each dx (|dx| up to ~4, rounding
+    # error std up to ~6e-4): over n = 802816 rows the sum has std ~0.5 and
+    # a max over 256 channels below ~2; a wrong mean term would give
+    # |sum| ~ n * 1e-3 = 800.
+    worst = float(dxd.sum(0).abs().max())
+    assert worst < 5.0, worst
     torch.cuda.synchronize()
 
 

@@ -1,0 +1,389 @@
+"""Pins for the CPU oracle (oracle/tfcpu_oracle.c).
+
+Each check is independent of the oracle's code: library routines (numpy's
+IEEE float32/float16 arithmetic, torch's bfloat16 rounding, torch's float64
+batch_norm and its autograd, torch.optim.Adam), closed forms in float64,
+invariants, finite differences, and the reference's own known answers.
+Each is chosen so that a plausible mistake (a dropped term, a wrong sign,
+Bessel applied to the wrong output, a transposed layout, a missing rounding
+step) fails it.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+
+rng_global = np.random.default_rng(1234)
+
+
+# ---------------------------------------------------------------------------
+# Rounding helpers
+# ---------------------------------------------------------------------------
+def _edge_f32():
+    vals = [0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0, 1e6, -1e6, 6.1e-5, 6e-8,
+            5.96e-8, 2.98e-8, 2.9802322e-08, 1e-10, np.inf, -np.inf, 3.0e38]
+    # every half-way point between consecutive float16 values in [1, 2) and in
+    # the subnormal range
+    h = np.arange(0x3C00, 0x4000, dtype=np.uint16).view(np.float16).astype(np.float32)
+    mids = ((h[:-1].astype(np.float64) + h[1:]) / 2).astype(np.float32)
+    s = np.arange(1, 0x400, dtype=np.uint16).view(np.float16).astype(np.float64)
+    smids = ((s[:-1] + s[1:]) / 2).astype(np.float32)
+    return np.concatenate([np.array(vals, np.float32), mids, smids])
+
+
+def test_f16_rounding_matches_numpy():
+    lib = oracle.load()
+    x = np.concatenate([
+        _edge_f32(),
+        (rng_global.standard_normal(20000) * 10.0 ** rng_global.integers(-9, 5, 20000)
+         ).astype(np.float32)])
+    got = np.array([lib.oracle_f32_to_f16(float(v)) for v in x], np.uint16)
+    want = x.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(got, want)
+    back = np.array([lib.oracle_f16_to_f32(int(b)) for b in want], np.float32)
+    np.testing.assert_array_equal(back, want.view(np.float16).astype(np.float32))
+
+
+def test_bf16_rounding_matches_torch():
+    lib = oracle.load()
+    x = np.concatenate([_edge_f32(), (rng_global.standard_normal(20000) * 10.0 **
+                                      rng_global.integers(-30, 30, 20000)).astype(np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = np.array([lib.oracle_f32_to_bf16(float(v)) for v in x], np.uint16)
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(oracle.f32_to_bf16_bits(x), want)
+    np.testing.assert_array_equal(oracle.bf16_bits_to_f32(want),
+                                  torch.from_numpy(want.view(np.int16)).view(torch.bfloat16)
+                                  .float().numpy())
+
+
+# ---------------------------------------------------------------------------
+# FusedBatchNormV3
+# ---------------------------------------------------------------------------
+def _bn_case(shape, dtype="float32", seed=0, loc=0.0):
+    rng = np.random.default_rng(seed)
+    x = oracle.to_storage(loc + rng.standard_normal(shape), dtype)
+    c = shape[-1]
+    scale = rng.uniform(0.5, 1.5, c).astype(np.float32)
+    offset = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    return x, scale, offset
+
+
+def _torch_bn_f64(x_nhwc, scale, offset, eps):
+    """torch.nn.functional.batch_norm in float64 (training statistics)."""
+    x = torch.from_numpy(np.asarray(x_nhwc, np.float64)).permute(0, 3, 1, 2).contiguous()
+    x.requires_grad_(True)
+    w = torch.from_numpy(scale.astype(np.float64)).requires_grad_(True)
+    b = torch.from_numpy(offset.astype(np.float64)).requires_grad_(True)
+    y = torch.nn.functional.batch_norm(x, None, None, w, b, training=True, eps=eps)
+    return x, w, b, y
+
+
+@pytest.mark.parametrize("shape", [(2, 2, 2, 4), (2, 4, 5, 3), (4, 7, 9, 64), (32, 9, 9, 16)])
+def test_bn_fwd_vs_torch_f64(shape):
+    eps = 1e-3
+    x, scale, offset = _bn_case(shape)
+    y, bm, bv, sm, sv = oracle.bn_fwd(x, scale, offset, epsilon=eps)
+    xt, _, _, yt = _torch_bn_f64(x, scale, offset, eps)
+    y_ref = yt.detach().permute(0, 2, 3, 1).numpy()
+    xd = x.astype(np.float64).reshape(-1, shape[-1])
+    tol = lambda a, b: np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30)
+    assert tol(y, y_ref) < 1e-6
+    assert tol(sm, xd.mean(0)) < 1e-6
+    assert tol(sv, xd.var(0, ddof=0)) < 1e-6          # reserve_space_2: population
+    assert tol(bv, xd.var(0, ddof=1)) < 1e-6          # batch_variance: Bessel
+    np.testing.assert_array_equal(bm, sm)
+
+
+def test_bn_reference_shape_brute_force():
+    """[2,2,2,4] (test/ops/fused_batchnorm_op_test.py:26) by explicit loops."""
+    eps = 1e-3
+    x, scale, offset = _bn_case((2, 2, 2, 4), seed=3)
+    y, bm, bv, sm, sv = oracle.bn_fwd(x, scale, offset, epsilon=eps)
+    for c in range(4):
+        vals = [float(x[n, h, w, c]) for n in range(2) for h in range(2) for w in range(2)]
+        mu = sum(vals) / 8
+        var = sum((v - mu) ** 2 for v in vals) / 8
+        assert abs(sm[c] - mu) <= 1e-6 and abs(sv[c] - var) <= 1e-6 * max(var, 1)
+        assert abs(bv[c] - var * 8 / 7) <= 1e-6 * max(var, 1)
+        for n in range(2):
+            for h in range(2):
+                for w in range(2):
+                    want = (float(x[n, h, w, c]) - mu) / np.sqrt(var + eps) * scale[c] + offset[c]
+                    assert abs(y[n, h, w, c] - want) <= 1e-5
+
+
+def test_bn_invariants_and_layouts():
+    eps = 1e-3
+    x, scale, offset = _bn_case((8, 6, 6, 12), seed=5)
+    y, bm, bv, sm, sv = oracle.bn_fwd(x, scale, offset, epsilon=eps)
+    yd = y.astype(np.float64).reshape(-1, 12)
+    np.testing.assert_allclose(yd.mean(0), offset, atol=1e-6)
+    var = x.astype(np.float64).reshape(-1, 12).var(0)
+    np.testing.assert_allclose(yd.var(0), scale.astype(np.float64) ** 2 * var / (var + eps),
+                               rtol=1e-5)
+    # NCHW is the same computation on the transposed tensor.
+    xn = np.ascontiguousarray(x.transpose(0, 3, 1, 2))
+    yn, bmn, bvn, smn, svn = oracle.bn_fwd(xn, scale, offset, epsilon=eps, data_format="NCHW")
+    np.testing.assert_allclose(yn.transpose(0, 2, 3, 1), y, rtol=0, atol=1e-6)
+    np.testing.assert_allclose(svn, sv, rtol=1e-6)
+
+
+def test_bn_special_cases():
+    # One element per channel: variance 0, Bessel guard divides by 1.
+    x = np.array([[[[1.5, -2.0, 3.0]]]], np.float32)
+    y, bm, bv, sm, sv = oracle.bn_fwd(x, np.ones(3, np.float32), np.array([0.5, 0, -1], np.float32),
+                                      epsilon=1e-3)
+    np.testing.assert_array_equal(bv, 0.0)
+    np.testing.assert_array_equal(y.ravel(), [0.5, 0, -1])
+    # Exponential average factor blends the running statistics (float64 check).
+    xx, scale, offset = _bn_case((4, 3, 3, 5), seed=9)
+    rm = np.linspace(-1, 1, 5).astype(np.float32)
+    rv = np.linspace(0.5, 2, 5).astype(np.float32)
+    _, bm, bv, sm, sv = oracle.bn_fwd(xx, scale, offset, rm, rv, epsilon=1e-3,
+                                      exponential_avg_factor=0.25)
+    xd = xx.astype(np.float64).reshape(-1, 5)
+    np.testing.assert_allclose(bm, 0.75 * rm + 0.25 * xd.mean(0), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(bv, 0.75 * rv + 0.25 * xd.var(0, ddof=1), rtol=1e-6)
+    np.testing.assert_allclose(sv, xd.var(0), rtol=1e-6)
+    # Inference: y from the given statistics.
+    y, bm, bv, _, _ = oracle.bn_fwd(xx, scale, offset, rm, rv, epsilon=1e-3, is_training=False)
+    want = (xd - rm) / np.sqrt(rv.astype(np.float64) + 1e-3) * scale + offset
+    np.testing.assert_allclose(y.reshape(-1, 5), want, atol=1e-5)
+    np.testing.assert_array_equal(bm, rm)
+    # Empty batch: NaN statistics.
+    _, bm, bv, _, _ = oracle.bn_fwd(np.zeros((0, 2, 2, 3), np.float32), np.ones(3, np.float32),
+                                    np.zeros(3, np.float32))
+    assert np.isnan(bm).all() and np.isnan(bv).all()
+
+
+def test_bn_large_mean_is_accurate():
+    x, scale, offset = _bn_case((16, 8, 8, 8), seed=2, loc=1000.0)
+    _, _, _, sm, sv = oracle.bn_fwd(x, scale, offset, epsilon=1e-3)
+    xd = x.astype(np.float64).reshape(-1, 8)
+    np.testing.assert_allclose(sv, xd.var(0), rtol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_bn_low_precision_activations(dtype):
+    x, scale, offset = _bn_case((8, 5, 5, 16), dtype=dtype, seed=4)
+    y, _, _, sm, sv = oracle.bn_fwd(x, scale, offset, epsilon=1e-3, dtype=dtype)
+    xf = oracle.to_f32(x, dtype).astype(np.float64)
+    _, _, _, yt = _torch_bn_f64(xf, scale, offset, 1e-3)
+    y_ref = yt.detach().permute(0, 2, 3, 1).numpy()
+    err = np.max(np.abs(oracle.to_f32(y, dtype) - y_ref)) / np.max(np.abs(y_ref))
+    assert err < (2 ** -8 if dtype == "float16" else 2 ** -7)
+
+
+# ---------------------------------------------------------------------------
+# FusedBatchNormGradV3
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape", [(2, 2, 2, 4), (4, 5, 5, 8), (16, 3, 3, 32)])
+def test_bn_grad_vs_torch_autograd_f64(shape):
+    eps = 1e-3
+    x, scale, offset = _bn_case(shape, seed=11)
+    dy = np.random.default_rng(12).standard_normal(shape).astype(np.float32)
+    _, _, _, sm, sv = oracle.bn_fwd(x, scale, offset, epsilon=eps)
+    dx, dscale, doffset = oracle.bn_grad(dy, x, scale, sm, sv, epsilon=eps)
+    xt, w, b, yt = _torch_bn_f64(x, scale, offset, eps)
+    yt.backward(torch.from_numpy(dy.astype(np.float64)).permute(0, 3, 1, 2))
+    rel = lambda a, b: np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30)
+    assert rel(dx, xt.grad.permute(0, 2, 3, 1).numpy()) < 2e-6
+    assert rel(dscale, w.grad.numpy()) < 2e-6
+    assert rel(doffset, b.grad.numpy()) < 2e-6
+    # Invariants per channel: sum(dx) = 0, and with xc = x - mean,
+    # S = sum(dy*xc), k = rsqrt(var+eps): sum(dx*xc) = scale*k*S*eps/(var+eps)
+    # (zero only when eps = 0, since sum(xc^2) = n*var).
+    c = shape[-1]
+    xc = (x.astype(np.float64) - sm).reshape(-1, c)
+    dxd = dx.astype(np.float64).reshape(-1, c)
+    S = (dy.astype(np.float64).reshape(-1, c) * xc).sum(0)
+    var = sv.astype(np.float64)
+    k = 1 / np.sqrt(var + eps)
+    tol = 1e-5 * np.abs(dxd).max() * xc.shape[0]
+    assert np.max(np.abs(dxd.sum(0))) < tol
+    want = scale * k * S * eps / (var + eps)
+    assert np.max(np.abs((dxd * xc).sum(0) - want)) < tol * np.abs(xc).max()
+
+
+def test_bn_grad_finite_differences():
+    """L = sum(y * dy): dL/dx by central differences in float64 vs the
+    oracle's dx on a tiny input."""
+    eps = 1e-3
+    x, scale, offset = _bn_case((2, 2, 3, 3), seed=21)
+    dy = np.random.default_rng(22).standard_normal(x.shape)
+
+    def loss(xv):
+        xd = xv.reshape(-1, 3)
+        mu, var = xd.mean(0), xd.var(0)
+        y = (xd - mu) / np.sqrt(var + eps) * scale + offset
+        return float(np.sum(y * dy.reshape(-1, 3)))
+
+    xd = x.astype(np.float64)
+    fd = np.zeros_like(xd)
+    h = 1e-6
+    for i in np.ndindex(xd.shape):
+        p, m = xd.copy(), xd.copy()
+        p[i] += h
+        m[i] -= h
+        fd[i] = (loss(p) - loss(m)) / (2 * h)
+    _, _, _, sm, sv = oracle.bn_fwd(x, scale, offset, epsilon=eps)
+    dx, _, _ = oracle.bn_grad(dy.astype(np.float32), x, scale, sm, sv, epsilon=eps)
+    np.testing.assert_allclose(dx, fd, atol=1e-4 * np.max(np.abs(fd)))
+
+
+def test_bn_grad_inference_mode():
+    eps = 1e-3
+    x, scale, offset = _bn_case((3, 4, 4, 6), seed=31)
+    dy = np.random.default_rng(32).standard_normal(x.shape).astype(np.float32)
+    mean = np.linspace(-0.5, 0.5, 6).astype(np.float32)
+    var = np.linspace(0.5, 1.5, 6).astype(np.float32)
+    dx, ds, do = oracle.bn_grad(dy, x, scale, mean, var, epsilon=eps, is_training=False)
+    k = 1 / np.sqrt(var.astype(np.float64) + eps)
+    np.testing.assert_allclose(dx, dy * scale * k, rtol=1e-6)
+    xd = x.astype(np.float64)
+    np.testing.assert_allclose(ds, (dy * (xd - mean) * k).reshape(-1, 6).sum(0), rtol=1e-5)
+    np.testing.assert_allclose(do, dy.astype(np.float64).reshape(-1, 6).sum(0), rtol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# ResourceApplyAdam
+# ---------------------------------------------------------------------------
+def test_adam_matches_torch_adam_f64_without_epsilon():
+    """With epsilon -> 0, TF's update var -= alpha*m/(sqrt(v)+eps) equals
+    torch.optim.Adam's bias-corrected update (eps = 0) exactly in real
+    arithmetic; ten float32 steps stay within float32 rounding of it."""
+    rng = np.random.default_rng(40)
+    n = 5000
+    var0 = (0.02 * rng.standard_normal(n)).astype(np.float32)
+    grads = [(1e-3 * rng.standard_normal(n)).astype(np.float32) for _ in range(10)]
+    var, m, v = var0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    p = torch.nn.Parameter(torch.from_numpy(var0.astype(np.float64)))
+    opt = torch.optim.Adam([p], lr=1e-3, betas=(0.9, 0.999), eps=0.0)
+    b1p = b2p = np.float32(1)
+    for g in grads:
+        b1p, b2p = np.float32(b1p * np.float32(0.9)), np.float32(b2p * np.float32(0.999))
+        oracle.adam(var, m, v, g, b1p, b2p, np.float32(1e-3), np.float32(0.9),
+                    np.float32(0.999), 1e-30)
+        p.grad = torch.from_numpy(g.astype(np.float64))
+        opt.step()
+    upd = var.astype(np.float64) - var0
+    upd_ref = p.detach().numpy() - var0
+    assert np.max(np.abs(upd - upd_ref)) / np.max(np.abs(upd_ref)) < 1e-5
+
+
+def test_adam_first_step_closed_form():
+    rng = np.random.default_rng(41)
+    n = 4096
+    g = (1e-3 * rng.standard_normal(n)).astype(np.float32)
+    g[:4] = 0.0
+    var0 = (0.02 * rng.standard_normal(n)).astype(np.float32)
+    for nesterov in (False, True):
+        var, m, v = var0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+        b1, b2, lr, eps = 0.9, 0.999, 1e-3, 1e-7
+        oracle.adam(var, m, v, g, np.float32(b1), np.float32(b2), np.float32(lr), np.float32(b1),
+                    np.float32(b2), np.float32(eps), use_nesterov=nesterov)
+        gd = g.astype(np.float64)
+        f = lambda a: np.float64(np.float32(a))
+        m1 = gd * (1 - f(b1))
+        v1 = gd * gd * (1 - f(b2))
+        alpha = f(lr) * np.sqrt(1 - f(b2)) / (1 - f(b1))
+        num = (gd * (1 - f(b1)) + f(b1) * m1) if nesterov else m1
+        var1 = var0 - alpha * num / (np.sqrt(v1) + f(eps))
+        np.testing.assert_allclose(m, m1, rtol=2e-7, atol=0)
+        np.testing.assert_allclose(v, v1, rtol=5e-7, atol=0)
+        # var1 = var0 - upd with |upd| ~ lr: float32 rounds upd to ~1e-7 of
+        # itself, so the bound is relative to the update, not to var.
+        upd = np.max(np.abs(var1 - var0))
+        np.testing.assert_allclose(var, var1, rtol=0, atol=2e-6 * upd)
+        # g = 0 with m = v = 0: the variable is untouched.
+        np.testing.assert_array_equal(var[:4], var0[:4])
+
+
+@pytest.mark.parametrize("dtype,tol", [("float16", 2e-3), ("bfloat16", 1.6e-2),
+                                       ("float64", 1e-12)])
+def test_adam_other_dtypes_vs_f64(dtype, tol):
+    rng = np.random.default_rng(42)
+    n = 3000
+    var0 = 0.02 * rng.standard_normal(n)
+    # |g| in [0.5, 1): g*g*(1-beta2) stays a normal float16.
+    g0 = rng.choice([-1.0, 1.0], n) * rng.uniform(0.5, 1.0, n)
+    var = oracle.to_storage(var0, dtype)
+    m = oracle.to_storage(np.zeros(n), dtype)
+    v = oracle.to_storage(np.zeros(n), dtype)
+    g = oracle.to_storage(g0, dtype)
+    vd = oracle.to_f32(var, dtype).astype(np.float64) if dtype != "float64" else var.copy()
+    gd = oracle.to_f32(g, dtype).astype(np.float64) if dtype != "float64" else g.copy()
+    oracle.adam(var, m, v, g, 0.875, 0.9990234375, 0.0009765625, 0.875, 0.9990234375,
+                0.0, dtype=dtype)
+    m1 = gd * 0.125
+    v1 = gd * gd * 0.0009765625
+    alpha = 0.0009765625 * np.sqrt(1 - 0.9990234375) / 0.125
+    want = vd - alpha * m1 / np.sqrt(v1)
+    got = oracle.to_f32(var, dtype).astype(np.float64) if dtype != "float64" else var
+    mg = oracle.to_f32(m, dtype).astype(np.float64) if dtype != "float64" else m
+    assert np.max(np.abs(mg - m1)) <= tol * np.max(np.abs(m1))
+    assert np.max(np.abs((got - vd) - (want - vd))) <= tol * 8 * np.max(np.abs(want - vd))
+
+
+# ---------------------------------------------------------------------------
+# Elementwise
+# ---------------------------------------------------------------------------
+def test_relu_reference_known_answers():
+    """test/ops/relu_op_test.py:45-96 literal [-2,-1,0,1,2]."""
+    x = np.array([-2.0, -1.0, 0.0, 1.0, 2.0], np.float32)
+    np.testing.assert_array_equal(oracle.eltwise("relu", [x]), [0, 0, 0, 1, 2])
+    z = oracle.eltwise("relu", [np.array([-0.0, np.nan, -np.inf], np.float32)])
+    assert np.signbit(z[0]) and np.isnan(z[1]) and z[2] == 0
+
+
+@pytest.mark.parametrize("xs,ys", [((64, 33), (33,)), ((64, 33), (64, 1)), ((4, 1, 5), (3, 1)),
+                                   ((7,), ()), ((2, 3, 4), (2, 3, 4))])
+def test_eltwise_f32_matches_numpy(xs, ys):
+    rng = np.random.default_rng(50)
+    x = rng.standard_normal(xs).astype(np.float32)
+    y = rng.standard_normal(ys).astype(np.float32)
+    np.testing.assert_array_equal(oracle.eltwise("add", [x, y]), x + y)
+    np.testing.assert_array_equal(oracle.eltwise("mul", [x, y]), x * y)
+    np.testing.assert_array_equal(oracle.eltwise("add_relu", [x, y]), np.maximum(x + y, 0))
+    b = rng.standard_normal(ys).astype(np.float32)
+    np.testing.assert_array_equal(oracle.eltwise("mul_add", [x, y, b]), (x * y) + b)
+
+
+def test_eltwise_f16_matches_numpy_half_arithmetic():
+    rng = np.random.default_rng(51)
+    x = rng.standard_normal((128, 77)).astype(np.float16)
+    y = rng.standard_normal(77).astype(np.float16)
+    b = rng.standard_normal((128, 77)).astype(np.float16)
+    np.testing.assert_array_equal(oracle.eltwise("add", [x, y], "float16"), x + y)
+    np.testing.assert_array_equal(oracle.eltwise("mul_add", [x, y, b], "float16"), (x * y) + b)
+    np.testing.assert_array_equal(oracle.eltwise("add_relu", [x, y], "float16"),
+                                  np.maximum(x + y, np.float16(0)))
+
+
+def test_eltwise_bf16_matches_torch_bf16_arithmetic():
+    rng = np.random.default_rng(52)
+    xt = torch.from_numpy(rng.standard_normal((96, 40)).astype(np.float32)).bfloat16()
+    yt = torch.from_numpy(rng.standard_normal(40).astype(np.float32)).bfloat16()
+    bt = torch.from_numpy(rng.standard_normal((96, 40)).astype(np.float32)).bfloat16()
+    bits = lambda t: t.view(torch.int16).numpy().view(np.uint16)
+    x, y, b = bits(xt), bits(yt), bits(bt)
+    np.testing.assert_array_equal(oracle.eltwise("add", [x, y], "bfloat16"), bits(xt + yt))
+    np.testing.assert_array_equal(oracle.eltwise("mul_add", [x, y, b], "bfloat16"),
+                                  bits((xt * yt) + bt))
+    np.testing.assert_array_equal(oracle.eltwise("add_relu", [x, y], "bfloat16"),
+                                  bits(torch.relu(xt + yt)))
+
+
+def test_bias_add_nchw_channel_dim():
+    """NCHW bias runs along dim 1 (musa_biasadd_op.cc:31-52)."""
+    x = np.zeros((2, 3, 2, 2), np.float32)
+    b = np.array([1, 2, 3], np.float32)
+    out = oracle.bias_add(x, b, data_format="NCHW")
+    for c in range(3):
+        assert np.all(out[:, c] == b[c])
+    out = oracle.bias_add(np.zeros((2, 2, 3), np.float32), b)
+    assert np.all(out[..., 2] == 3)
