@@ -11,13 +11,14 @@ before the timed region.
 
 value = algorithmic bytes per step (fwd 2*s*E + grad 3*s*E per pair) x steps
         / wall time of the timed region (HIP events around K steps).
-roofline: the dominant kernel (tfma_bn_grad_apply: reads x, dy, writes dx,
+roofline: the dominant kernel (tfma_bn_grad_fused: reads x, dy, writes dx,
         3*s*E bytes per launch) timed with HIP events recorded on its
         stream around each of its launches inside the timed region.
 cpu_baseline: the TF-CPU restatement (oracle/, C + OpenMP) on one float16
         fwd+grad pass over the four shapes, on the host's cores.
 components: the other north-star kernels (Adam, grouped Adam, elementwise
-        chains) at their config shapes, timed the same way.
+        chains) at their config shapes, each rep timed with HIP events after
+        a 1 GiB read that evicts the Infinity Cache.
 """
 import argparse
 import json
@@ -64,7 +65,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-components", action="store_true",
                    help="skip the Adam / elementwise component lines")
-    p.add_argument("--trace", default="tfma_bn_grad_apply",
+    p.add_argument("--trace", default="tfma_bn_grad_fused",
                    help="kernel timed for the roofline object")
     return p.parse_args()
 
@@ -76,7 +77,7 @@ def _events(torch):
 def bn_workload(torch, ops, dev):
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
-    calls, pairs = [], []
+    fwds, grads, pairs = [], [], []
     for dt in (torch.float16, torch.bfloat16):
         for shape in SHAPES:
             c = shape[-1]
@@ -93,24 +94,42 @@ def bn_workload(torch, ops, dev):
             grad = ops.bind(ops.FusedBatchNormGradV3, dy, x, scale, r.reserve_space_1,
                             r.reserve_space_2, r.reserve_space_3, epsilon=EPS,
                             data_format="NHWC", is_training=True, workspace=ws)
-            calls += [fwd, grad]
+            fwds.append(fwd)
+            grads.append(grad)
             pairs.append((dt, shape, x.numel(), x.element_size()))
-    return calls, pairs
+    # A training step runs every forward, then the grads in reverse order, so
+    # a grad never finds its x still cache-warm from its own forward.
+    return fwds + grads[::-1], pairs
 
 
-def time_calls(torch, calls, steps, warmup):
+def time_calls(torch, calls, steps, warmup, flush=None):
+    """ms per pass over `calls`.  With `flush` (a large device buffer), each
+    pass is timed on its own after reading the buffer, so the 256 MB
+    Infinity Cache holds none of the op's data (the BASELINE.md protocol)."""
     for _ in range(warmup):
         for c in calls:
             c()
     torch.cuda.synchronize()
-    t0, t1 = _events(torch)
-    t0.record()
+    if flush is None:
+        t0, t1 = _events(torch)
+        t0.record()
+        for _ in range(steps):
+            for c in calls:
+                c()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / steps
+    pairs = []
     for _ in range(steps):
+        flush.sum()
+        t0, t1 = _events(torch)
+        t0.record()
         for c in calls:
             c()
-    t1.record()
+        t1.record()
+        pairs.append((t0, t1))
     torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps  # ms per step
+    return sum(a.elapsed_time(b) for a, b in pairs) / steps
 
 
 def components(torch, ops, dev):
@@ -119,9 +138,10 @@ def components(torch, ops, dev):
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
     reps, warm = 20, 3
+    flush = torch.ones(1 << 28, device=dev)  # 1 GiB, read between reps
 
     def rate(calls, nbytes, reps_=reps):
-        ms = time_calls(torch, calls, reps_, warm)
+        ms = time_calls(torch, calls, reps_, warm, flush=flush)
         gbps = nbytes / (ms / 1e3) / 1e9
         return {"ms": round(ms, 4), "GB/s": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1)}
 
@@ -165,6 +185,7 @@ def components(torch, ops, dev):
                                                       2 * s * xo.numel() + s * 4095)
         del x, b, a_full, b_full, xo, bo
     torch.cuda.synchronize()
+    del flush
     return out
 
 

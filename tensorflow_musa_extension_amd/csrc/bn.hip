@@ -31,6 +31,8 @@
 // element, which keeps sum((x-K)^2) - sum(x-K)^2/n free of cancellation
 // when |mean| >> std; partials add exactly like plain sums because every
 // workgroup uses the same K.
+#include <hip/hip_cooperative_groups.h>
+
 #include "device_util.h"
 #include "tfma_internal.h"
 
@@ -39,8 +41,8 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kUnroll = 8;
-constexpr int kFinCh = 64;      // channels per finalize workgroup
-constexpr int kFinSlices = 16;  // partial slices per finalize workgroup
+constexpr int kFinCh = 8;          // channels per finalize workgroup
+constexpr int kFinThreads = 256;   // 32 partial slices x 8 channels
 
 struct Plan {
   bool nhwc;
@@ -282,67 +284,55 @@ struct FinArgs {
   bool is_training;
 };
 
+// Final statistics and apply coefficients of channel ch from the double
+// sums s1, s2 over all of the channel's elements; writes the op's per-channel
+// outputs and coef[ch] = {mean, a, b, c2} for apply_one().
 template <class Tr, bool kGrad>
-__global__ __launch_bounds__(kFinCh* kFinSlices) void bn_finalize_kernel(
-    const float2* __restrict__ partial, FinArgs a, float4* __restrict__ coef) {
-  __shared__ double2 red[kFinSlices][kFinCh];
-  const int lane = threadIdx.x % kFinCh;
-  const int slice = threadIdx.x / kFinCh;
-  const int ch = blockIdx.x * kFinCh + lane;
-  double s1 = 0.0, s2 = 0.0;
-  if (ch < a.c) {
-    for (int64_t g = slice; g < a.groups; g += kFinSlices) {
-      const float2 v = partial[g * a.c + ch];
-      s1 += v.x;
-      s2 += v.y;
-    }
-  }
-  red[slice][lane] = make_double2(s1, s2);
-  __syncthreads();
-  if (slice == 0 && ch < a.c) {
-    for (int s = 1; s < kFinSlices; ++s) {
-      s1 += red[s][lane].x;
-      s2 += red[s][lane].y;
-    }
-    const double n = static_cast<double>(a.n);
-    if constexpr (!kGrad) {
-      const float kshift =
-          Tr::ld(static_cast<const typename Tr::S*>(a.x)[ch * a.k_stride]);
-      const double mean = static_cast<double>(kshift) + s1 / n;
-      double m2 = s2 - s1 * s1 / n;
-      if (m2 < 0.0) m2 = 0.0;
-      const float mean_f = static_cast<float>(mean);
-      const float var_f = static_cast<float>(m2 / n);
-      const float nf = static_cast<float>(a.n);
-      const float nm1 = static_cast<float>(a.n > 1 ? a.n - 1 : 1);
-      const float adj = nf / nm1;
-      a.saved_mean[ch] = mean_f;
-      a.saved_var[ch] = var_f;
-      if (a.f == 1.0f) {
-        a.batch_mean[ch] = mean_f;
-        a.batch_var[ch] = var_f * adj;
-      } else {
-        const float omf = 1.0f - a.f;
-        a.batch_mean[ch] = a.mean_in[ch] * omf + mean_f * a.f;
-        a.batch_var[ch] = a.var_in[ch] * omf + (var_f * adj) * a.f;
-      }
-      const float inv = 1.0f / __builtin_sqrtf(var_f + a.eps);
-      coef[ch] = make_float4(mean_f, inv * a.scale[ch], a.offset[ch], 0.f);
+__device__ inline void finish_channel(const FinArgs& a, int ch, double s1, double s2,
+                                      float4* __restrict__ coef) {
+  const double n = static_cast<double>(a.n);
+  if constexpr (!kGrad) {
+    const float kshift =
+        Tr::ld(static_cast<const typename Tr::S*>(a.x)[ch * a.k_stride]);
+    const double mean = static_cast<double>(kshift) + s1 / n;
+    double m2 = s2 - s1 * s1 / n;
+    if (m2 < 0.0) m2 = 0.0;
+    const float mean_f = static_cast<float>(mean);
+    const float var_f = static_cast<float>(m2 / n);
+    const float nf = static_cast<float>(a.n);
+    const float nm1 = static_cast<float>(a.n > 1 ? a.n - 1 : 1);
+    const float adj = nf / nm1;
+    a.saved_mean[ch] = mean_f;
+    a.saved_var[ch] = var_f;
+    if (a.f == 1.0f) {
+      a.batch_mean[ch] = mean_f;
+      a.batch_var[ch] = var_f * adj;
     } else {
-      const float mu = a.mean_in[ch];
-      const float k = 1.0f / __builtin_sqrtf(a.var_in[ch] + a.eps);
-      a.offset_bp[ch] = static_cast<float>(s1);
-      a.scale_bp[ch] = static_cast<float>(s2 * static_cast<double>(k));
-      if (a.is_training) {
-        const float mean_dy = static_cast<float>(s1 / n);
-        const float mean_dyxc = static_cast<float>(s2 / n);
-        coef[ch] = make_float4(mu, a.scale[ch] * k, mean_dy, (k * k) * mean_dyxc);
-      } else {
-        coef[ch] = make_float4(mu, a.scale[ch] * k, 0.f, 0.f);
-      }
+      const float omf = 1.0f - a.f;
+      a.batch_mean[ch] = a.mean_in[ch] * omf + mean_f * a.f;
+      a.batch_var[ch] = a.var_in[ch] * omf + (var_f * adj) * a.f;
+    }
+    const float inv = 1.0f / __builtin_sqrtf(var_f + a.eps);
+    coef[ch] = make_float4(mean_f, inv * a.scale[ch], a.offset[ch], 0.f);
+  } else {
+    const float mu = a.mean_in[ch];
+    const float k = 1.0f / __builtin_sqrtf(a.var_in[ch] + a.eps);
+    a.offset_bp[ch] = static_cast<float>(s1);
+    a.scale_bp[ch] = static_cast<float>(s2 * static_cast<double>(k));
+    if (a.is_training) {
+      const float mean_dy = static_cast<float>(s1 / n);
+      const float mean_dyxc = static_cast<float>(s2 / n);
+      coef[ch] = make_float4(mu, a.scale[ch] * k, mean_dy, (k * k) * mean_dyxc);
+    } else {
+      coef[ch] = make_float4(mu, a.scale[ch] * k, 0.f, 0.f);
     }
   }
-  // Zero-filled side outputs.
+}
+
+// Zero-filled side outputs (reserve_space_3 of the forward, reserve_space_4/5
+// of the grad), spread over the whole grid.
+template <bool kGrad>
+__device__ inline void zero_side_outputs(const FinArgs& a) {
   const int64_t gtid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t gstride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   if constexpr (!kGrad) {
@@ -351,6 +341,37 @@ __global__ __launch_bounds__(kFinCh* kFinSlices) void bn_finalize_kernel(
     for (int64_t i = gtid; i < a.reserve4_n; i += gstride) a.reserve4[i] = 0.f;
     for (int64_t i = gtid; i < a.reserve5_n; i += gstride) a.reserve5[i] = 0.f;
   }
+}
+
+// Split-path finalize: workgroup b owns kFinCh consecutive channels; its
+// threads stride over the G partial rows (kFinCh*8 contiguous bytes per row)
+// and combine in double through LDS.
+template <class Tr, bool kGrad>
+__global__ __launch_bounds__(kFinThreads) void bn_finalize_kernel(
+    const float2* __restrict__ partial, FinArgs a, float4* __restrict__ coef) {
+  constexpr int kSlices = kFinThreads / kFinCh;
+  __shared__ double2 red[kSlices][kFinCh];
+  const int lane = threadIdx.x % kFinCh;
+  const int slice = threadIdx.x / kFinCh;
+  const int ch = blockIdx.x * kFinCh + lane;
+  double s1 = 0.0, s2 = 0.0;
+  if (ch < a.c) {
+    for (int64_t g = slice; g < a.groups; g += kSlices) {
+      const float2 v = partial[g * a.c + ch];
+      s1 += v.x;
+      s2 += v.y;
+    }
+  }
+  red[slice][lane] = make_double2(s1, s2);
+  __syncthreads();
+  if (slice == 0 && ch < a.c) {
+    for (int s = 1; s < kSlices; ++s) {
+      s1 += red[s][lane].x;
+      s2 += red[s][lane].y;
+    }
+    finish_channel<Tr, kGrad>(a, ch, s1, s2, coef);
+  }
+  zero_side_outputs<kGrad>(a);
 }
 
 // Inference-mode forward coefficients from the running statistics.
@@ -464,6 +485,271 @@ __global__ __launch_bounds__(kThreads) void bn_nchw_apply_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// 4. Fused persistent kernel (NHWC, 16-byte vectors): one cooperative launch
+//    per op, one workgroup of 512 threads per CU.
+//    phase 1: statistics partials.  Each thread's rows are split three ways:
+//             its first KR row-vectors stay in VGPRs, the next KL in LDS
+//             (about 150 KB per workgroup), the rest are streamed;
+//    sync;    phase 2: per-channel finals, channels spread over workgroups;
+//    sync;    phase 3: outputs - streamed rows re-read last-to-first, then the
+//             LDS- and register-resident rows, which are not read again.
+//    On-chip residency is what removes the second read: on MI355X re-reads
+//    served by the Infinity Cache run at about the same rate as HBM reads.
+// ---------------------------------------------------------------------------
+constexpr int kFusedThreads = 512;
+constexpr int kStreamUnroll = 4;
+// Resident 16-byte vectors per thread and per input tensor: KR in VGPRs (the
+// largest counts that compile without spills - the 8-wide types carry twice
+// the per-channel state), KL in LDS (the LDS budget split over the inputs).
+template <class Tr> struct Resident {
+  static constexpr int kRegFwd = 40, kRegGrad = 16, kLdsFwd = 19, kLdsGrad = 9;
+};
+template <> struct Resident<TF16> {
+  static constexpr int kRegFwd = 16, kRegGrad = 8, kLdsFwd = 19, kLdsGrad = 9;
+};
+template <> struct Resident<TBF16> {
+  static constexpr int kRegFwd = 16, kRegGrad = 8, kLdsFwd = 19, kLdsGrad = 9;
+};
+
+struct FusedArgs {
+  const void* x;
+  const void* dy;
+  void* out;
+  int64_t rows;
+  int c;
+  int64_t cv;
+  int tx_shift;
+  int ct;
+  int64_t groups;
+  int64_t rows_per_g;
+  float2* partial;
+  float4* coef;
+  FinArgs fin;
+};
+
+__device__ inline double2 wave_sum(double a, double b) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    a += __shfl_xor(a, off, 64);
+    b += __shfl_xor(b, off, 64);
+  }
+  return make_double2(a, b);
+}
+
+template <class Tr, bool kGrad>
+__device__ inline void accum_words(const uint4& xw, const uint4& dw, const float (&k)[Tr::kVec],
+                                   float (&s1)[Tr::kVec], float (&s2)[Tr::kVec]) {
+  typename Tr::S xv[Tr::kVec], dv[Tr::kVec];
+  __builtin_memcpy(xv, &xw, 16);
+  if constexpr (kGrad) __builtin_memcpy(dv, &dw, 16);
+  accum<Tr, Tr::kVec, kGrad>(xv, dv, k, s1, s2);
+}
+
+template <class Tr, bool kGrad>
+__device__ inline uint4 apply_words(const uint4& xw, const uint4& dw,
+                                    const float4 (&cf)[Tr::kVec]) {
+  typename Tr::S xv[Tr::kVec], dv[Tr::kVec], ov[Tr::kVec];
+  __builtin_memcpy(xv, &xw, 16);
+  if constexpr (kGrad) __builtin_memcpy(dv, &dw, 16);
+#pragma unroll
+  for (int j = 0; j < Tr::kVec; ++j)
+    ov[j] = apply_one<Tr, kGrad>(xv[j], kGrad ? dv[j] : xv[j], cf[j]);
+  uint4 o;
+  __builtin_memcpy(&o, ov, 16);
+  return o;
+}
+
+__device__ inline uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ inline void st16(void* p, const uint4& v) { *reinterpret_cast<uint4*>(p) = v; }
+
+template <class Tr, bool kGrad, int KR, int KL>
+__global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs a) {
+  using S = typename Tr::S;
+  constexpr int VEC = Tr::kVec;
+  constexpr int kIn = kGrad ? 2 : 1;
+  extern __shared__ uint4 lds_rows[];  // [KL][kIn][kFusedThreads]
+  __shared__ float2 red[kFusedThreads];
+  __shared__ double2 dred[kFusedThreads / 64];
+  cooperative_groups::grid_group grid = cooperative_groups::this_grid();
+  const int tid = threadIdx.x;
+  const int tx = tid & ((1 << a.tx_shift) - 1);
+  const int ty = tid >> a.tx_shift;
+  const int ry = kFusedThreads >> a.tx_shift;
+  const int ct = blockIdx.x % a.ct;
+  const int64_t g = blockIdx.x / a.ct;
+  const int64_t cvi = static_cast<int64_t>(ct) * (1 << a.tx_shift) + tx;
+  const bool active = cvi < a.cv;
+  const int64_t r0 = g * a.rows_per_g;
+  int64_t r1 = r0 + a.rows_per_g;
+  if (r1 > a.rows) r1 = a.rows;
+  const int64_t nk = (active && r0 + ty < r1) ? (r1 - r0 - ty + ry - 1) / ry : 0;
+  const int64_t c0 = active ? cvi * VEC : 0;
+  const S* __restrict__ px = static_cast<const S*>(a.x) + c0;
+  const S* __restrict__ pd = kGrad ? static_cast<const S*>(a.dy) + c0 : nullptr;
+  S* __restrict__ po = static_cast<S*>(a.out) + c0;
+  const int64_t rstride = static_cast<int64_t>(ry) * a.c;  // elements between my rows
+  const int64_t base = (r0 + ty) * a.c;                     // my first row
+  auto xrow = [&](int64_t q) { return px + base + q * rstride; };
+  auto drow = [&](int64_t q) { return pd + base + q * rstride; };
+  auto lds = [&](int q2, int which) -> uint4& {
+    return lds_rows[(q2 * kIn + which) * kFusedThreads + tid];
+  };
+
+  // ---- phase 1: partial statistics --------------------------------------
+  float k[VEC], s1[VEC], s2[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    s1[j] = 0.f;
+    s2[j] = 0.f;
+    k[j] = 0.f;
+  }
+  if (active) {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) k[j] = kGrad ? a.fin.mean_in[c0 + j] : Tr::ld(px[j]);
+  }
+  uint4 xr[KR];
+  uint4 dr[kGrad ? KR : 1];
+#pragma unroll
+  for (int q = 0; q < KR; ++q) {
+    if (q < nk) {
+      xr[q] = ld16(xrow(q));
+      if constexpr (kGrad) dr[q] = ld16(drow(q));
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < KR; ++q)
+    if (q < nk) accum_words<Tr, kGrad>(xr[q], dr[kGrad ? q : 0], k, s1, s2);
+  // LDS-resident rows, kStreamUnroll loads in flight.
+#pragma unroll
+  for (int q2 = 0; q2 < KL; q2 += kStreamUnroll) {
+    uint4 xw[kStreamUnroll], dw[kStreamUnroll];
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u) {
+      if (q2 + u < KL && KR + q2 + u < nk) {
+        xw[u] = ld16(xrow(KR + q2 + u));
+        if constexpr (kGrad) dw[u] = ld16(drow(KR + q2 + u));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u) {
+      if (q2 + u < KL && KR + q2 + u < nk) {
+        lds(q2 + u, 0) = xw[u];
+        if constexpr (kGrad) lds(q2 + u, 1) = dw[u];
+        accum_words<Tr, kGrad>(xw[u], dw[u], k, s1, s2);
+      }
+    }
+  }
+  // Streamed rows.
+  int64_t q = KR + KL;
+  for (; q + kStreamUnroll <= nk; q += kStreamUnroll) {
+    uint4 xw[kStreamUnroll], dw[kStreamUnroll];
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u) {
+      xw[u] = ld16(xrow(q + u));
+      if constexpr (kGrad) dw[u] = ld16(drow(q + u));
+    }
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u) accum_words<Tr, kGrad>(xw[u], dw[u], k, s1, s2);
+  }
+  for (; q < nk; ++q) {
+    const uint4 xw = ld16(xrow(q));
+    uint4 dw = xw;
+    if constexpr (kGrad) dw = ld16(drow(q));
+    accum_words<Tr, kGrad>(xw, dw, k, s1, s2);
+  }
+  // Workgroup partial per channel: one channel slot of the vector at a time.
+  for (int j = 0; j < VEC; ++j) {
+    red[tid] = make_float2(s1[j], s2[j]);
+    __syncthreads();
+    if (tid < (1 << a.tx_shift)) {
+      const int64_t cv2 = static_cast<int64_t>(ct) * (1 << a.tx_shift) + tid;
+      if (cv2 < a.cv) {
+        float sa = 0.f, sb = 0.f;
+        for (int t = 0; t < ry; ++t) {
+          const float2 v = red[(t << a.tx_shift) + tid];
+          sa += v.x;
+          sb += v.y;
+        }
+        a.partial[g * a.c + cv2 * VEC + j] = make_float2(sa, sb);
+      }
+    }
+    __syncthreads();
+  }
+  grid.sync();
+
+  // ---- phase 2: per-channel finals ---------------------------------------
+  {
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    for (int ch = blockIdx.x; ch < a.c; ch += gridDim.x) {
+      double t1 = 0.0, t2 = 0.0;
+      for (int64_t gg = tid; gg < a.groups; gg += kFusedThreads) {
+        const float2 v = a.partial[gg * a.c + ch];
+        t1 += v.x;
+        t2 += v.y;
+      }
+      const double2 w = wave_sum(t1, t2);
+      if (lane == 0) dred[wave] = w;
+      __syncthreads();
+      if (tid == 0) {
+        double u1 = 0.0, u2 = 0.0;
+        for (int i = 0; i < kFusedThreads / 64; ++i) {
+          u1 += dred[i].x;
+          u2 += dred[i].y;
+        }
+        finish_channel<Tr, kGrad>(a.fin, ch, u1, u2, a.coef);
+      }
+      __syncthreads();
+    }
+    zero_side_outputs<kGrad>(a.fin);
+  }
+  grid.sync();
+
+  // ---- phase 3: outputs --------------------------------------------------
+  // Make the resident words opaque so only the packed words (not their
+  // phase-1 float conversions) stay live across the syncs.
+#pragma unroll
+  for (int r = 0; r < KR; ++r) {
+    asm volatile("" : "+v"(xr[r].x), "+v"(xr[r].y), "+v"(xr[r].z), "+v"(xr[r].w));
+    if constexpr (kGrad)
+      asm volatile("" : "+v"(dr[r].x), "+v"(dr[r].y), "+v"(dr[r].z), "+v"(dr[r].w));
+  }
+  float4 cf[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j)
+    cf[j] = active ? a.coef[c0 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+  q = nk - 1;
+  for (; q >= KR + KL + kStreamUnroll - 1; q -= kStreamUnroll) {
+    uint4 xw[kStreamUnroll], dw[kStreamUnroll];
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u) {
+      xw[u] = ld16(xrow(q - u));
+      if constexpr (kGrad) dw[u] = ld16(drow(q - u));
+    }
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u)
+      st16(po + base + (q - u) * rstride, apply_words<Tr, kGrad>(xw[u], dw[u], cf));
+  }
+  for (; q >= KR + KL; --q) {
+    const uint4 xw = ld16(xrow(q));
+    uint4 dw = xw;
+    if constexpr (kGrad) dw = ld16(drow(q));
+    st16(po + base + q * rstride, apply_words<Tr, kGrad>(xw, dw, cf));
+  }
+#pragma unroll
+  for (int q2 = 0; q2 < KL; ++q2) {
+    if (KR + q2 < nk) {
+      const uint4 xw = lds(q2, 0);
+      const uint4 dw = kGrad ? lds(q2, kGrad ? 1 : 0) : xw;
+      st16(po + base + (KR + q2) * rstride, apply_words<Tr, kGrad>(xw, dw, cf));
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < KR; ++r)
+    if (r < nk) st16(po + base + r * rstride, apply_words<Tr, kGrad>(xr[r], dr[kGrad ? r : 0], cf));
+}
+
+// ---------------------------------------------------------------------------
 // Host drivers.
 // ---------------------------------------------------------------------------
 template <class Tr, int VEC, bool kGrad>
@@ -524,10 +810,128 @@ hipError_t launch_finalize(const Plan& p, const FinArgs& fa,
                            hipStream_t stream) {
   const int blocks = (fa.c + kFinCh - 1) / kFinCh;
   LaunchScope scope(stream, kGrad ? "tfma_bn_grad_finalize" : "tfma_bn_fwd_finalize");
-  hipLaunchKernelGGL((bn_finalize_kernel<Tr, kGrad>), dim3(blocks),
-                     dim3(kFinCh * kFinSlices), 0, stream, partial, fa, coef);
+  hipLaunchKernelGGL((bn_finalize_kernel<Tr, kGrad>), dim3(blocks), dim3(kFinThreads), 0,
+                     stream, partial, fa, coef);
   (void)p;
   return hipGetLastError();
+}
+
+// ---- fused path host side --------------------------------------------------
+bool fused_enabled() {
+  static bool on = [] {
+    const char* e = getenv("TFMA_BN_FUSED");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+// Upper bound on fused workgroups (one or two per CU); sizes the partials.
+int64_t fused_group_bound() { return 2 * static_cast<int64_t>(DeviceCUs()); }
+
+template <class Tr, bool kGrad>
+constexpr int fused_kr() { return kGrad ? Resident<Tr>::kRegGrad : Resident<Tr>::kRegFwd; }
+template <class Tr, bool kGrad>
+constexpr int fused_kl() { return kGrad ? Resident<Tr>::kLdsGrad : Resident<Tr>::kLdsFwd; }
+
+template <class Tr, bool kGrad>
+const void* fused_kernel() {
+  return reinterpret_cast<const void*>(
+      &bn_fused_nhwc_kernel<Tr, kGrad, fused_kr<Tr, kGrad>(), fused_kl<Tr, kGrad>()>);
+}
+
+template <class Tr, bool kGrad>
+size_t fused_smem() {
+  return static_cast<size_t>(fused_kl<Tr, kGrad>()) * (kGrad ? 2 : 1) * kFusedThreads * 16;
+}
+
+// Co-resident workgroups per CU for the fused kernel (0 if it cannot run).
+template <class Tr, bool kGrad>
+int fused_blocks_per_cu() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int nb = 0;
+    hipError_t e = hipFuncSetAttribute(fused_kernel<Tr, kGrad>(),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(fused_smem<Tr, kGrad>()));
+    if (e == hipSuccess)
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fused_kernel<Tr, kGrad>(),
+                                                       kFusedThreads, fused_smem<Tr, kGrad>());
+    if (e != hipSuccess || nb < 1) nb = -1;
+    cached[dev] = nb > 2 ? 2 : nb;
+  }
+  return cached[dev];
+}
+
+struct FusedPlan {
+  int tx_shift;
+  int ct;
+  int64_t cv;
+  int64_t groups;
+  int64_t rows_per_g;
+  int blocks;
+};
+
+bool make_fused_plan(const BnGeometry& g, int vec, int blocks_per_cu, FusedPlan* fp) {
+  if (!g.nhwc || blocks_per_cu < 1 || g.c % vec != 0) return false;
+  fp->cv = g.c / vec;
+  int s = pow2_ceil_log2(fp->cv);
+  if (s > 5) s = 5;
+  fp->tx_shift = s;
+  const int tx = 1 << s;
+  fp->ct = static_cast<int>((fp->cv + tx - 1) / tx);
+  const int64_t max_blocks = static_cast<int64_t>(blocks_per_cu) * DeviceCUs();
+  int64_t groups = max_blocks / fp->ct;
+  if (groups < 1) return false;
+  const int ry = kFusedThreads / tx;
+  // Fewer groups when rows are scarce: every thread gets at least one row.
+  const int64_t max_groups = (g.rows + ry - 1) / ry;
+  if (groups > max_groups) groups = max_groups;
+  if (groups > fused_group_bound()) groups = fused_group_bound();
+  fp->rows_per_g = (g.rows + groups - 1) / groups;
+  fp->groups = (g.rows + fp->rows_per_g - 1) / fp->rows_per_g;
+  fp->blocks = static_cast<int>(fp->groups * fp->ct);
+  return true;
+}
+
+template <class Tr, bool kGrad>
+hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
+                        const void* dy, void* out, const FinArgs& fin, float2* partial,
+                        float4* coef, hipStream_t stream) {
+  FusedArgs fa;
+  fa.x = x;
+  fa.dy = dy;
+  fa.out = out;
+  fa.rows = g.rows;
+  fa.c = static_cast<int>(g.c);
+  fa.cv = fp.cv;
+  fa.tx_shift = fp.tx_shift;
+  fa.ct = fp.ct;
+  fa.groups = fp.groups;
+  fa.rows_per_g = fp.rows_per_g;
+  fa.partial = partial;
+  fa.coef = coef;
+  fa.fin = fin;
+  fa.fin.groups = fp.groups;
+  void* args[] = {&fa};
+  LaunchScope scope(stream, kGrad ? "tfma_bn_grad_fused" : "tfma_bn_fwd_fused");
+  hipError_t e = hipLaunchCooperativeKernel(fused_kernel<Tr, kGrad>(), dim3(fp.blocks),
+                                            dim3(kFusedThreads), args,
+                                            fused_smem<Tr, kGrad>(), stream);
+  if (e != hipSuccess) return e;
+  return hipGetLastError();
+}
+
+// Partial-sum region: large enough for the split plan (either alignment)
+// and for the fused plan's at most fused_group_bound() row groups.
+size_t partial_region_bytes(DType t, const BnGeometry& g) {
+  const Plan pv = make_plan(t, g, true);
+  const Plan ps = make_plan(t, g, false);
+  size_t r = partial_bytes(pv, g);
+  if (partial_bytes(ps, g) > r) r = partial_bytes(ps, g);
+  const size_t f = align256(static_cast<size_t>(fused_group_bound()) * g.c * sizeof(float2));
+  return r > f ? r : f;
 }
 
 bool ptr_aligned(const void* p) {
@@ -538,8 +942,9 @@ template <class Tr>
 hipError_t forward_t(const BnGeometry& g, const BnFwdArgs& a, void* ws,
                      size_t ws_bytes, hipStream_t stream) {
   const bool aligned = ptr_aligned(a.x) && ptr_aligned(a.y);
-  const Plan p = make_plan(Tr::kVec == 4 ? DType::kF32 : DType::kF16, g, aligned);
-  const size_t pb = partial_bytes(p, g);
+  const DType dt = Tr::kVec == 4 ? DType::kF32 : DType::kF16;
+  const Plan p = make_plan(dt, g, aligned);
+  const size_t pb = partial_region_bytes(dt, g);
   if (ws_bytes < pb + coef_bytes(g)) return hipErrorInvalidValue;
   float2* partial = static_cast<float2*>(ws);
   float4* coef = reinterpret_cast<float4*>(static_cast<char*>(ws) + pb);
@@ -562,6 +967,12 @@ hipError_t forward_t(const BnGeometry& g, const BnFwdArgs& a, void* ws,
   fa.reserve3 = a.reserve3;
   fa.is_training = a.is_training;
   hipError_t e;
+  FusedPlan fp;
+  if (a.is_training && p.vec > 1 && fused_enabled() &&
+      make_fused_plan(g, p.vec, fused_blocks_per_cu<Tr, false>(), &fp)) {
+    return launch_fused<Tr, false>(fp, g, a.x, nullptr, a.y, fa, partial, coef,
+                                                  stream);
+  }
   if (a.is_training) {
     e = p.vec == 1 ? launch_reduce<Tr, 1, false>(p, g, a.x, nullptr, nullptr, partial, stream)
                    : launch_reduce<Tr, Tr::kVec, false>(p, g, a.x, nullptr, nullptr, partial, stream);
@@ -582,8 +993,9 @@ template <class Tr>
 hipError_t grad_t(const BnGeometry& g, const BnGradArgs& a, void* ws,
                   size_t ws_bytes, hipStream_t stream) {
   const bool aligned = ptr_aligned(a.x) && ptr_aligned(a.dy) && ptr_aligned(a.dx);
-  const Plan p = make_plan(Tr::kVec == 4 ? DType::kF32 : DType::kF16, g, aligned);
-  const size_t pb = partial_bytes(p, g);
+  const DType dt = Tr::kVec == 4 ? DType::kF32 : DType::kF16;
+  const Plan p = make_plan(dt, g, aligned);
+  const size_t pb = partial_region_bytes(dt, g);
   if (ws_bytes < pb + coef_bytes(g)) return hipErrorInvalidValue;
   float2* partial = static_cast<float2*>(ws);
   float4* coef = reinterpret_cast<float4*>(static_cast<char*>(ws) + pb);
@@ -602,6 +1014,12 @@ hipError_t grad_t(const BnGeometry& g, const BnGradArgs& a, void* ws,
   fa.reserve5 = a.reserve5;
   fa.reserve5_n = a.reserve5 ? a.reserve5_n : 0;
   fa.is_training = a.is_training;
+  FusedPlan fp;
+  if (p.vec > 1 && fused_enabled() &&
+      make_fused_plan(g, p.vec, fused_blocks_per_cu<Tr, true>(), &fp)) {
+    return launch_fused<Tr, true>(fp, g, a.x, a.dy, a.dx, fa, partial, coef,
+                                                  stream);
+  }
   hipError_t e =
       p.vec == 1 ? launch_reduce<Tr, 1, true>(p, g, a.x, a.dy, a.saved_mean, partial, stream)
                  : launch_reduce<Tr, Tr::kVec, true>(p, g, a.x, a.dy, a.saved_mean, partial, stream);
@@ -630,11 +1048,7 @@ hipError_t LaunchFillF32(float* p, int64_t n, float value, hipStream_t stream) {
 }
 
 size_t BnWorkspaceBytes(DType t, const BnGeometry& g) {
-  // The plan depends on pointer alignment; size for the larger of the two.
-  const Plan pv = make_plan(t, g, true);
-  const Plan ps = make_plan(t, g, false);
-  size_t a = partial_bytes(pv, g), b = partial_bytes(ps, g);
-  return (a > b ? a : b) + coef_bytes(g);
+  return partial_region_bytes(t, g) + coef_bytes(g);
 }
 
 hipError_t LaunchBnForward(DType t, const BnGeometry& g, const BnFwdArgs& a,
