@@ -31,7 +31,7 @@
 // element, which keeps sum((x-K)^2) - sum(x-K)^2/n free of cancellation
 // when |mean| >> std; partials add exactly like plain sums because every
 // workgroup uses the same K.
-#include <hip/hip_cooperative_groups.h>
+#include <mutex>
 
 #include "device_util.h"
 #include "tfma_internal.h"
@@ -286,10 +286,9 @@ struct FinArgs {
 
 // Final statistics and apply coefficients of channel ch from the double
 // sums s1, s2 over all of the channel's elements; writes the op's per-channel
-// outputs and coef[ch] = {mean, a, b, c2} for apply_one().
+// outputs and returns the coefficients {mean, a, b, c2} for apply_one().
 template <class Tr, bool kGrad>
-__device__ inline void finish_channel(const FinArgs& a, int ch, double s1, double s2,
-                                      float4* __restrict__ coef) {
+__device__ inline float4 finish_channel(const FinArgs& a, int ch, double s1, double s2) {
   const double n = static_cast<double>(a.n);
   if constexpr (!kGrad) {
     const float kshift =
@@ -313,7 +312,7 @@ __device__ inline void finish_channel(const FinArgs& a, int ch, double s1, doubl
       a.batch_var[ch] = a.var_in[ch] * omf + (var_f * adj) * a.f;
     }
     const float inv = 1.0f / __builtin_sqrtf(var_f + a.eps);
-    coef[ch] = make_float4(mean_f, inv * a.scale[ch], a.offset[ch], 0.f);
+    return make_float4(mean_f, inv * a.scale[ch], a.offset[ch], 0.f);
   } else {
     const float mu = a.mean_in[ch];
     const float k = 1.0f / __builtin_sqrtf(a.var_in[ch] + a.eps);
@@ -322,9 +321,9 @@ __device__ inline void finish_channel(const FinArgs& a, int ch, double s1, doubl
     if (a.is_training) {
       const float mean_dy = static_cast<float>(s1 / n);
       const float mean_dyxc = static_cast<float>(s2 / n);
-      coef[ch] = make_float4(mu, a.scale[ch] * k, mean_dy, (k * k) * mean_dyxc);
+      return make_float4(mu, a.scale[ch] * k, mean_dy, (k * k) * mean_dyxc);
     } else {
-      coef[ch] = make_float4(mu, a.scale[ch] * k, 0.f, 0.f);
+      return make_float4(mu, a.scale[ch] * k, 0.f, 0.f);
     }
   }
 }
@@ -369,7 +368,7 @@ __global__ __launch_bounds__(kFinThreads) void bn_finalize_kernel(
       s1 += red[s][lane].x;
       s2 += red[s][lane].y;
     }
-    finish_channel<Tr, kGrad>(a, ch, s1, s2, coef);
+    coef[ch] = finish_channel<Tr, kGrad>(a, ch, s1, s2);
   }
   zero_side_outputs<kGrad>(a);
 }
@@ -485,30 +484,36 @@ __global__ __launch_bounds__(kThreads) void bn_nchw_apply_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// 4. Fused persistent kernel (NHWC, 16-byte vectors): one cooperative launch
-//    per op, one workgroup of 512 threads per CU.
+// 4. Fused persistent kernel (NHWC, 16-byte vectors): one launch per op, one
+//    workgroup of 512 threads per CU, all workgroups co-resident.
 //    phase 1: statistics partials.  Each thread's rows are split three ways:
 //             its first KR row-vectors stay in VGPRs, the next KL in LDS
 //             (about 150 KB per workgroup), the rest are streamed;
-//    sync;    phase 2: per-channel finals, channels spread over workgroups;
-//    sync;    phase 3: outputs - streamed rows re-read last-to-first, then the
+//    barrier; phase 2: per-channel finals, channels spread over workgroups;
+//    barrier; phase 3: outputs - streamed rows re-read last-to-first, then the
 //             LDS- and register-resident rows, which are not read again.
 //    On-chip residency is what removes the second read: on MI355X re-reads
 //    served by the Infinity Cache run at about the same rate as HBM reads.
+//    The grid barrier is a device-wide counter advanced with relaxed
+//    agent-scope atomics (a cooperative launch costs ~18 us and each of its
+//    grid syncs ~33 us on MI355X; this barrier ~3 us).  Values that cross
+//    workgroups (partials, coefficients) are written and read with
+//    agent-scope atomic stores/loads, which are coherent across the XCDs'
+//    L2s, and every thread waits for its stores before arriving.
 // ---------------------------------------------------------------------------
 constexpr int kFusedThreads = 512;
-constexpr int kStreamUnroll = 4;
+constexpr unsigned kSpinLimit = 1u << 24;  // ~0.5 s, then give up (flagged)
 // Resident 16-byte vectors per thread and per input tensor: KR in VGPRs (the
 // largest counts that compile without spills - the 8-wide types carry twice
 // the per-channel state), KL in LDS (the LDS budget split over the inputs).
 template <class Tr> struct Resident {
-  static constexpr int kRegFwd = 40, kRegGrad = 16, kLdsFwd = 19, kLdsGrad = 9;
+  static constexpr int kRegFwd = 28, kRegGrad = 10, kLdsFwd = 18, kLdsGrad = 9;
 };
 template <> struct Resident<TF16> {
-  static constexpr int kRegFwd = 16, kRegGrad = 8, kLdsFwd = 19, kLdsGrad = 9;
+  static constexpr int kRegFwd = 12, kRegGrad = 8, kLdsFwd = 18, kLdsGrad = 9;
 };
 template <> struct Resident<TBF16> {
-  static constexpr int kRegFwd = 16, kRegGrad = 8, kLdsFwd = 19, kLdsGrad = 9;
+  static constexpr int kRegFwd = 10, kRegGrad = 4, kLdsFwd = 18, kLdsGrad = 9;
 };
 
 struct FusedArgs {
@@ -524,6 +529,9 @@ struct FusedArgs {
   int64_t rows_per_g;
   float2* partial;
   float4* coef;
+  unsigned long long* barrier;  // device-wide arrival counter
+  unsigned long long base;      // its value when this launch starts
+  unsigned* timeout_flag;
   FinArgs fin;
 };
 
@@ -534,6 +542,34 @@ __device__ inline double2 wave_sum(double a, double b) {
     b += __shfl_xor(b, off, 64);
   }
   return make_double2(a, b);
+}
+
+// Coherent (agent-scope) 8-byte store/load for values shared across XCDs.
+__device__ inline void store_shared(void* p, uint64_t v) {
+  __hip_atomic_store(static_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint64_t load_shared(const void* p) {
+  return __hip_atomic_load(static_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until every workgroup of the grid has arrived `k` times (k = 1, 2).
+__device__ inline void grid_barrier(const FusedArgs& a, unsigned k) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // my shared stores are done
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __hip_atomic_fetch_add(a.barrier, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long target = a.base + static_cast<unsigned long long>(k) * gridDim.x;
+    unsigned spins = 0;
+    while (__hip_atomic_load(a.barrier, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(2);
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(a.timeout_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
 }
 
 template <class Tr, bool kGrad>
@@ -559,18 +595,21 @@ __device__ inline uint4 apply_words(const uint4& xw, const uint4& dw,
   return o;
 }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __device__ inline uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
-__device__ inline void st16(void* p, const uint4& v) { *reinterpret_cast<uint4*>(p) = v; }
+// Outputs are written once and not read again by the op: non-temporal.
+__device__ inline void st16(void* p, const uint4& v) {
+  __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(p));
+}
 
 template <class Tr, bool kGrad, int KR, int KL>
 __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs a) {
   using S = typename Tr::S;
   constexpr int VEC = Tr::kVec;
   constexpr int kIn = kGrad ? 2 : 1;
+  constexpr int U = kGrad ? 4 : 8;  // streamed vectors per tensor in flight
   extern __shared__ uint4 lds_rows[];  // [KL][kIn][kFusedThreads]
-  __shared__ float2 red[kFusedThreads];
-  __shared__ double2 dred[kFusedThreads / 64];
-  cooperative_groups::grid_group grid = cooperative_groups::this_grid();
+  __shared__ float2 red[(kFusedThreads / 64) * 32 * VEC];  // [wave][tx * VEC + j]
   const int tid = threadIdx.x;
   const int tx = tid & ((1 << a.tx_shift) - 1);
   const int ty = tid >> a.tx_shift;
@@ -607,8 +646,11 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
 #pragma unroll
     for (int j = 0; j < VEC; ++j) k[j] = kGrad ? a.fin.mean_in[c0 + j] : Tr::ld(px[j]);
   }
+  // Register- and LDS-resident rows: all loads issued before any is used.
   uint4 xr[KR];
   uint4 dr[kGrad ? KR : 1];
+  uint4 xl[KL];
+  uint4 dl[kGrad ? KL : 1];
 #pragma unroll
   for (int q = 0; q < KR; ++q) {
     if (q < nk) {
@@ -617,39 +659,34 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     }
   }
 #pragma unroll
-  for (int q = 0; q < KR; ++q)
-    if (q < nk) accum_words<Tr, kGrad>(xr[q], dr[kGrad ? q : 0], k, s1, s2);
-  // LDS-resident rows, kStreamUnroll loads in flight.
-#pragma unroll
-  for (int q2 = 0; q2 < KL; q2 += kStreamUnroll) {
-    uint4 xw[kStreamUnroll], dw[kStreamUnroll];
-#pragma unroll
-    for (int u = 0; u < kStreamUnroll; ++u) {
-      if (q2 + u < KL && KR + q2 + u < nk) {
-        xw[u] = ld16(xrow(KR + q2 + u));
-        if constexpr (kGrad) dw[u] = ld16(drow(KR + q2 + u));
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kStreamUnroll; ++u) {
-      if (q2 + u < KL && KR + q2 + u < nk) {
-        lds(q2 + u, 0) = xw[u];
-        if constexpr (kGrad) lds(q2 + u, 1) = dw[u];
-        accum_words<Tr, kGrad>(xw[u], dw[u], k, s1, s2);
-      }
+  for (int q = 0; q < KL; ++q) {
+    if (KR + q < nk) {
+      xl[q] = ld16(xrow(KR + q));
+      if constexpr (kGrad) dl[q] = ld16(drow(KR + q));
     }
   }
-  // Streamed rows.
-  int64_t q = KR + KL;
-  for (; q + kStreamUnroll <= nk; q += kStreamUnroll) {
-    uint4 xw[kStreamUnroll], dw[kStreamUnroll];
 #pragma unroll
-    for (int u = 0; u < kStreamUnroll; ++u) {
+  for (int q = 0; q < KR; ++q)
+    if (q < nk) accum_words<Tr, kGrad>(xr[q], dr[kGrad ? q : 0], k, s1, s2);
+#pragma unroll
+  for (int q = 0; q < KL; ++q) {
+    if (KR + q < nk) {
+      lds(q, 0) = xl[q];
+      if constexpr (kGrad) lds(q, kGrad ? 1 : 0) = dl[kGrad ? q : 0];
+      accum_words<Tr, kGrad>(xl[q], dl[kGrad ? q : 0], k, s1, s2);
+    }
+  }
+  // Streamed rows, U vectors per tensor in flight.
+  int64_t q = KR + KL;
+  for (; q + U <= nk; q += U) {
+    uint4 xw[U], dw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
       xw[u] = ld16(xrow(q + u));
       if constexpr (kGrad) dw[u] = ld16(drow(q + u));
     }
 #pragma unroll
-    for (int u = 0; u < kStreamUnroll; ++u) accum_words<Tr, kGrad>(xw[u], dw[u], k, s1, s2);
+    for (int u = 0; u < U; ++u) accum_words<Tr, kGrad>(xw[u], dw[u], k, s1, s2);
   }
   for (; q < nk; ++q) {
     const uint4 xw = ld16(xrow(q));
@@ -657,57 +694,71 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     if constexpr (kGrad) dw = ld16(drow(q));
     accum_words<Tr, kGrad>(xw, dw, k, s1, s2);
   }
-  // Workgroup partial per channel: one channel slot of the vector at a time.
-  for (int j = 0; j < VEC; ++j) {
-    red[tid] = make_float2(s1[j], s2[j]);
-    __syncthreads();
-    if (tid < (1 << a.tx_shift)) {
-      const int64_t cv2 = static_cast<int64_t>(ct) * (1 << a.tx_shift) + tid;
-      if (cv2 < a.cv) {
-        float sa = 0.f, sb = 0.f;
-        for (int t = 0; t < ry; ++t) {
-          const float2 v = red[(t << a.tx_shift) + tid];
-          sa += v.x;
-          sb += v.y;
-        }
-        a.partial[g * a.c + cv2 * VEC + j] = make_float2(sa, sb);
-      }
+  // Workgroup partial per channel: sum the row lanes of each wave with
+  // shuffles, then the waves through LDS, then one coherent store per
+  // channel.
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    if (off < (1 << a.tx_shift)) break;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      s1[j] += __shfl_xor(s1[j], off, 64);
+      s2[j] += __shfl_xor(s2[j], off, 64);
     }
-    __syncthreads();
   }
-  grid.sync();
-
-  // ---- phase 2: per-channel finals ---------------------------------------
+  const int width = (1 << a.tx_shift) * VEC;  // channels of this tile
   {
     const int wave = tid >> 6;
     const int lane = tid & 63;
-    for (int ch = blockIdx.x; ch < a.c; ch += gridDim.x) {
+    if (lane < (1 << a.tx_shift)) {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) red[wave * width + lane * VEC + j] = make_float2(s1[j], s2[j]);
+    }
+  }
+  __syncthreads();
+  if (tid < width && static_cast<int64_t>(ct) * width + tid < static_cast<int64_t>(a.cv) * VEC) {
+    float sa = 0.f, sb = 0.f;
+#pragma unroll
+    for (int w = 0; w < kFusedThreads / 64; ++w) {
+      const float2 v = red[w * width + tid];
+      sa += v.x;
+      sb += v.y;
+    }
+    store_shared(&a.partial[g * a.c + static_cast<int64_t>(ct) * width + tid],
+                 __builtin_bit_cast(uint64_t, make_float2(sa, sb)));
+  }
+  grid_barrier(a, 1);
+
+  // ---- phase 2: per-channel finals ---------------------------------------
+  // Channel ch belongs to workgroup ch % gridDim.x; each wave of the
+  // workgroup finishes one of its channels at a time, so all of a
+  // workgroup's partial loads are in flight together.
+  {
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    constexpr int kWaves = kFusedThreads / 64;
+    for (int ch = blockIdx.x + wave * gridDim.x; ch < a.c; ch += kWaves * gridDim.x) {
       double t1 = 0.0, t2 = 0.0;
-      for (int64_t gg = tid; gg < a.groups; gg += kFusedThreads) {
-        const float2 v = a.partial[gg * a.c + ch];
+      for (int64_t gg = lane; gg < a.groups; gg += 64) {
+        const float2 v = __builtin_bit_cast(float2, load_shared(&a.partial[gg * a.c + ch]));
         t1 += v.x;
         t2 += v.y;
       }
       const double2 w = wave_sum(t1, t2);
-      if (lane == 0) dred[wave] = w;
-      __syncthreads();
-      if (tid == 0) {
-        double u1 = 0.0, u2 = 0.0;
-        for (int i = 0; i < kFusedThreads / 64; ++i) {
-          u1 += dred[i].x;
-          u2 += dred[i].y;
-        }
-        finish_channel<Tr, kGrad>(a.fin, ch, u1, u2, a.coef);
+      if (lane == 0) {
+        const float4 cfc = finish_channel<Tr, kGrad>(a.fin, ch, w.x, w.y);
+        store_shared(&a.coef[ch], __builtin_bit_cast(uint64_t, make_float2(cfc.x, cfc.y)));
+        store_shared(reinterpret_cast<float2*>(&a.coef[ch]) + 1,
+                     __builtin_bit_cast(uint64_t, make_float2(cfc.z, cfc.w)));
       }
-      __syncthreads();
     }
     zero_side_outputs<kGrad>(a.fin);
   }
-  grid.sync();
+  grid_barrier(a, 2);
 
   // ---- phase 3: outputs --------------------------------------------------
   // Make the resident words opaque so only the packed words (not their
-  // phase-1 float conversions) stay live across the syncs.
+  // phase-1 float conversions) stay live across the barriers.
 #pragma unroll
   for (int r = 0; r < KR; ++r) {
     asm volatile("" : "+v"(xr[r].x), "+v"(xr[r].y), "+v"(xr[r].z), "+v"(xr[r].w));
@@ -716,18 +767,26 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   }
   float4 cf[VEC];
 #pragma unroll
-  for (int j = 0; j < VEC; ++j)
-    cf[j] = active ? a.coef[c0 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int j = 0; j < VEC; ++j) {
+    if (active) {
+      const float2 lo = __builtin_bit_cast(float2, load_shared(&a.coef[c0 + j]));
+      const float2 hi =
+          __builtin_bit_cast(float2, load_shared(reinterpret_cast<float2*>(&a.coef[c0 + j]) + 1));
+      cf[j] = make_float4(lo.x, lo.y, hi.x, hi.y);
+    } else {
+      cf[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
   q = nk - 1;
-  for (; q >= KR + KL + kStreamUnroll - 1; q -= kStreamUnroll) {
-    uint4 xw[kStreamUnroll], dw[kStreamUnroll];
+  for (; q >= KR + KL + U - 1; q -= U) {
+    uint4 xw[U], dw[U];
 #pragma unroll
-    for (int u = 0; u < kStreamUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       xw[u] = ld16(xrow(q - u));
       if constexpr (kGrad) dw[u] = ld16(drow(q - u));
     }
 #pragma unroll
-    for (int u = 0; u < kStreamUnroll; ++u)
+    for (int u = 0; u < U; ++u)
       st16(po + base + (q - u) * rstride, apply_words<Tr, kGrad>(xw[u], dw[u], cf));
   }
   for (; q >= KR + KL; --q) {
@@ -895,10 +954,51 @@ bool make_fused_plan(const BnGeometry& g, int vec, int blocks_per_cu, FusedPlan*
   return true;
 }
 
+// Per-device state of the fused kernels' grid barrier: a monotonic arrival
+// counter in device memory (zeroed once), its value before the next launch,
+// and the event and stream of the last fused launch.  Fused launches on one
+// device are chained (a launch on another stream waits for the previous
+// one), so at most one persistent grid is resident at a time and every
+// launch knows the counter's starting value.
+struct BarrierState {
+  std::mutex mu;
+  unsigned long long* counter = nullptr;  // [0] arrivals, [1] timeout flag
+  unsigned long long base = 0;
+  hipEvent_t last = nullptr;
+  hipStream_t last_stream = nullptr;
+  bool used = false;
+};
+
+BarrierState* barrier_state() {
+  static BarrierState states[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  return &states[dev];
+}
+
 template <class Tr, bool kGrad>
 hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
                         const void* dy, void* out, const FinArgs& fin, float2* partial,
                         float4* coef, hipStream_t stream) {
+  BarrierState* bs = barrier_state();
+  if (!bs) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(bs->mu);
+  if (!bs->counter) {
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, 256);
+    if (e != hipSuccess) return e;
+    e = hipMemset(p, 0, 256);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&bs->last, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      (void)hipFree(p);
+      return e;
+    }
+    bs->counter = static_cast<unsigned long long*>(p);
+  }
+  if (bs->used && bs->last_stream != stream) {
+    hipError_t e = hipStreamWaitEvent(stream, bs->last, 0);
+    if (e != hipSuccess) return e;
+  }
   FusedArgs fa;
   fa.x = x;
   fa.dy = dy;
@@ -912,15 +1012,25 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   fa.rows_per_g = fp.rows_per_g;
   fa.partial = partial;
   fa.coef = coef;
+  fa.barrier = bs->counter;
+  fa.base = bs->base;
+  fa.timeout_flag = reinterpret_cast<unsigned*>(bs->counter + 1);
   fa.fin = fin;
   fa.fin.groups = fp.groups;
-  void* args[] = {&fa};
-  LaunchScope scope(stream, kGrad ? "tfma_bn_grad_fused" : "tfma_bn_fwd_fused");
-  hipError_t e = hipLaunchCooperativeKernel(fused_kernel<Tr, kGrad>(), dim3(fp.blocks),
-                                            dim3(kFusedThreads), args,
-                                            fused_smem<Tr, kGrad>(), stream);
+  {
+    LaunchScope scope(stream, kGrad ? "tfma_bn_grad_fused" : "tfma_bn_fwd_fused");
+    constexpr int KR = fused_kr<Tr, kGrad>();
+    constexpr int KL = fused_kl<Tr, kGrad>();
+    const size_t smem = fused_smem<Tr, kGrad>();
+    hipLaunchKernelGGL((bn_fused_nhwc_kernel<Tr, kGrad, KR, KL>), dim3(fp.blocks),
+                       dim3(kFusedThreads), smem, stream, fa);
+  }
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return hipGetLastError();
+  bs->base += 2ull * static_cast<unsigned long long>(fp.blocks);  // two barriers
+  bs->last_stream = stream;
+  bs->used = true;
+  return hipEventRecord(bs->last, stream);
 }
 
 // Partial-sum region: large enough for the split plan (either alignment)

@@ -63,7 +63,9 @@ struct TBF16 {
   using C = float;
   static constexpr int kVec = 8;
   __device__ static inline C ld(S s) { return bf16_to_f32(s); }
-  __device__ static inline S st(C c) { return f32_to_bf16(c); }
+  // gfx950 converts with v_cvt_pk_bf16_f32 (round to nearest even, as
+  // f32_to_bf16; NaN payloads may differ from the host helper's).
+  __device__ static inline S st(C c) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(c)); }
   __device__ static inline C rnd(C c) { return ld(st(c)); }
 };
 
