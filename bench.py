@@ -67,7 +67,27 @@ def parse():
                    help="skip the Adam / elementwise component lines")
     p.add_argument("--trace", default="tfma_bn_grad_fused",
                    help="kernel timed for the roofline object")
+    p.add_argument("--calibrate", action="store_true",
+                   help="also run a plain 256 MiB device copy (torch copy_) so a "
+                        "rocprofv3 --pmc run can scale FETCH_SIZE/WRITE_SIZE")
     return p.parse_args()
+
+
+def read_traffic(kernel):
+    """Counter-derived HBM bytes per launch of `kernel` from the committed
+    rocprofv3 --pmc summary (profiles/pmc_traffic.txt, lines
+    "<kernel> hbm_bytes_per_launch=<N>"), or None."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 2 and parts[0] == kernel and parts[1].startswith(
+                        "hbm_bytes_per_launch="):
+                    return int(parts[1].split("=", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def _events(torch):
@@ -189,10 +209,12 @@ def components(torch, ops, dev):
     return out
 
 
-def cpu_baseline(torch, dev):
-    """TF-CPU restatement (oracle, C + OpenMP) on one float16 fwd+grad pass
-    over the four cfg2 shapes.  Inputs are drawn on the GPU and copied to
-    host memory before timing."""
+def cpu_baseline(torch, dev, min_seconds=10.0):
+    """TF-CPU restatement (oracle, C + OpenMP on up to 16 host cores) on the
+    same workload: FusedBatchNormV3 + FusedBatchNormGradV3 over the four cfg2
+    shapes in float16 and bfloat16, repeated until at least `min_seconds` of
+    CPU time.  Inputs are drawn on the GPU and copied to host memory before
+    timing."""
     import numpy as np
     sys.path.insert(0, ROOT)
     from oracle import oracle
@@ -200,24 +222,32 @@ def cpu_baseline(torch, dev):
     oracle.set_threads(threads)
     gen = torch.Generator(device=dev)
     gen.manual_seed(2)
-    total_bytes, secs = 0, 0.0
-    for shape in SHAPES:
-        c = shape[-1]
-        x = torch.randn(shape, generator=gen, device=dev).half().cpu().numpy()
-        dy = torch.randn(shape, generator=gen, device=dev).half().cpu().numpy()
-        scale = np.random.default_rng(0).uniform(0.5, 1.5, c).astype(np.float32)
-        offset = np.zeros(c, np.float32)
-        t = time.perf_counter()
-        _, _, _, sm, sv = oracle.bn_fwd(x, scale, offset, epsilon=EPS, dtype="float16")
-        oracle.bn_grad(dy, x, scale, sm, sv, epsilon=EPS, dtype="float16")
-        secs += time.perf_counter() - t
-        total_bytes += 10 * x.size
-        del x, dy
+    total_bytes, secs, passes = 0, 0.0, 0
+    while passes == 0 or secs < min_seconds:
+        for tdt, name in ((torch.float16, "float16"), (torch.bfloat16, "bfloat16")):
+            for shape in SHAPES:
+                c = shape[-1]
+                x = torch.randn(shape, generator=gen, device=dev).to(tdt)
+                dy = torch.randn(shape, generator=gen, device=dev).to(tdt)
+                if tdt == torch.bfloat16:
+                    x = x.view(torch.int16).cpu().numpy().view(np.uint16)
+                    dy = dy.view(torch.int16).cpu().numpy().view(np.uint16)
+                else:
+                    x, dy = x.cpu().numpy(), dy.cpu().numpy()
+                scale = np.random.default_rng(0).uniform(0.5, 1.5, c).astype(np.float32)
+                offset = np.zeros(c, np.float32)
+                t = time.perf_counter()
+                _, _, _, sm, sv = oracle.bn_fwd(x, scale, offset, epsilon=EPS, dtype=name)
+                oracle.bn_grad(dy, x, scale, sm, sv, epsilon=EPS, dtype=name)
+                secs += time.perf_counter() - t
+                total_bytes += 10 * x.size
+                del x, dy
+        passes += 1
     gbps = total_bytes / secs / 1e9
     return {"value": round(gbps, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "seconds": round(secs, 2),
-            "sample": "one float16 FusedBatchNormV3+GradV3 pass over the 4 cfg2 shapes "
-                      f"({total_bytes // 10} elements; algorithmic bytes / wall time)"}
+            "sample": f"{passes} pass(es) of FusedBatchNormV3+GradV3 over the 4 cfg2 shapes in "
+                      "f16 and bf16 (the full bench step); algorithmic bytes / wall time"}
 
 
 def main():
@@ -264,10 +294,12 @@ def main():
         "peak": PEAK_GBPS,
         "unit": "GB/s",
         "frac": round(achieved / PEAK_GBPS, 4) if achieved else None,
-        "traffic": None,
+        "traffic": read_traffic(args.trace),
         "launches": launches,
+        "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
         "avg_launch_us": round(1e3 * traced_ms / launches, 2) if launches else None,
         "algorithmic_bytes_per_step": kernel_bytes_per_step,
+        "algorithmic_bytes_per_launch": kernel_bytes_per_step // len(pairs),
     }
     result = {
         "metric": "achieved HBM GB/s (% of peak) for FusedBN fwd+grad, fused Adam, eltwise",
@@ -292,6 +324,13 @@ def main():
         },
         "roofline": roofline,
     }
+    if args.calibrate:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_components:
         result["components"] = components(torch, ops, dev)
     if not args.no_cpu:
