@@ -317,8 +317,9 @@ void oracle_adam(int dt, void* var, void* m, void* v, const void* grad, int64_t 
     }
     return;
   }
-  const float b1p = (float)b1p_, b2p = (float)b2p_, lr = (float)lr_;
-  const float b1 = (float)b1_, b2 = (float)b2_, eps = (float)eps_;
+  /* The scalars are T tensors in TF: round them to T first. */
+  const float b1p = rnd(dt, (float)b1p_), b2p = rnd(dt, (float)b2p_), lr = rnd(dt, (float)lr_);
+  const float b1 = rnd(dt, (float)b1_), b2 = rnd(dt, (float)b2_), eps = rnd(dt, (float)eps_);
   /* alpha = lr * sqrt(1 - beta2_power) / (1 - beta1_power), in T */
   const float alpha = rnd(dt, rnd(dt, lr * rnd(dt, sqrtf(rnd(dt, 1.0f - b2p)))) /
                                   rnd(dt, 1.0f - b1p));

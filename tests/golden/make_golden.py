@@ -71,8 +71,8 @@ def adam_cases(store):
         v = oracle.to_storage(np.zeros(n), dt)
         g = oracle.to_storage(rng.choice([-1.0, 1.0], n) * rng.uniform(0.5, 1.0, n), dt)
         store[f"adam_{dt}/var0"], store[f"adam_{dt}/grad"] = var.copy(), g.copy()
-        # Scalars exactly representable in every T.
-        b1p, b2p, lr, b1, b2, eps = 0.875, 0.9990234375, 0.0009765625, 0.875, 0.9990234375, 0.0078125
+        # Scalars exactly representable in every T (bfloat16 keeps 8 significant bits).
+        b1p, b2p, lr, b1, b2, eps = 0.875, 0.99609375, 0.0009765625, 0.875, 0.99609375, 0.0078125
         oracle.adam(var, m, v, g, b1p, b2p, lr, b1, b2, eps, dtype=dt)
         gd = oracle.to_f32(g, dt).astype(np.float64)
         v0 = oracle.to_f32(store[f"adam_{dt}/var0"], dt).astype(np.float64)
