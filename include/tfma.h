@@ -229,6 +229,54 @@ int TFMA_MusaShiftedAffineMap(void* stream, const TFMA_Tensor* data_left,
                               TFMA_Tensor* output, TFMA_Status* status);
 
 /* ---------------------------------------------------------------------------
+ * Graph rewrite (host only).  Replaces the reference's fusion pass:
+ * FusionPattern match/apply/priority (musa_ext/graph/fusion/
+ * fusion_pattern_manager.h:54-82) driven by OptimizeFusion
+ * (musa_ext/mu/optimizer/musa_graph_optimizer.cc:5843-5994), and the grouped
+ * optimizer rewrite (musa_graph_optimizer.cc:2014-2120), which the reference
+ * has for SGD only and this pass does for ResourceApplyAdam.
+ *
+ * Input and output are serialized tensorflow.GraphDef protos (what a
+ * TF_InitGraph optimizer's optimize_func receives and returns in TF_Buffers).
+ * Patterns, in priority order:
+ *   "MusaBiasAddRelu"       Relu(BiasAdd(x, b))     -> MusaBiasAddRelu(x, b)
+ *   "MusaAddV2Relu"         Relu(AddV2|Add(x, y))   -> MusaAddV2Relu(x, y)
+ *   "MusaShiftedAffineMap"  AddV2|Add(Mul(x, a), b) -> MusaShiftedAffineMap(x, a, b)
+ *   "MusaGroupedResourceApplyAdam"  >= 2 ResourceApplyAdam nodes sharing
+ *       device, T, use_locking, use_nesterov and the six scalar inputs, none
+ *       depending on another, distinct var/m/v ->
+ *       MusaGroupedResourceApplyAdam(vars N, ms N, vs N, beta1_power,
+ *       beta2_power, lr, beta1, beta2, epsilon, grads N; attrs N, T,
+ *       use_locking, use_nesterov).
+ * A fused node keeps the name, device and control inputs of the node it
+ * replaces and gains the absorbed node's control inputs; the absorbed node
+ * must have that node as its only data consumer, the same device and T
+ * (float, half or bfloat16), and must not be fetched.
+ *
+ * fetch_nodes: names ("name" or "name:port") that must survive; may be NULL.
+ * device_filter: rewrite only nodes whose device string contains it (the
+ *   reference matches on "MUSA"); NULL or "" = every node.
+ * disabled_patterns: comma-separated pattern names to skip (the reference's
+ *   disabled_fusion_patterns parameter, musa_graph_optimizer.cc:5448-5475).
+ * On success *optimized is a malloc'd buffer the caller frees with
+ * TFMA_FreeBuffer.  A malformed GraphDef is TFMA_INVALID_ARGUMENT.
+ * ------------------------------------------------------------------------- */
+typedef struct TFMA_GraphRewriteStats {
+  int32_t bias_add_relu;      /* fused nodes created per pattern */
+  int32_t add_v2_relu;
+  int32_t mul_add;
+  int32_t adam_groups;        /* grouped Adam nodes created */
+  int32_t adam_grouped_nodes; /* ResourceApplyAdam nodes they replaced */
+} TFMA_GraphRewriteStats;
+
+int TFMA_OptimizeGraph(const void* graph_def, size_t graph_def_bytes,
+                       const char* const* fetch_nodes, int num_fetch,
+                       const char* device_filter, const char* disabled_patterns,
+                       void** optimized, size_t* optimized_bytes,
+                       TFMA_GraphRewriteStats* stats, TFMA_Status* status);
+void TFMA_FreeBuffer(void* buffer);
+
+/* ---------------------------------------------------------------------------
  * Kernel timing.  No reference counterpart (the reference removed its kernel
  * timing macros and points to external profilers).  When a kernel whose name
  * contains `name_substr` is launched by this library, HIP events are

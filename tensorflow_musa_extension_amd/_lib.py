@@ -44,6 +44,12 @@ class TFMA_Status(ctypes.Structure):
     _fields_ = [("code", ctypes.c_int32), ("message", ctypes.c_char * 500)]
 
 
+class TFMA_GraphRewriteStats(ctypes.Structure):
+    _fields_ = [("bias_add_relu", ctypes.c_int32), ("add_v2_relu", ctypes.c_int32),
+                ("mul_add", ctypes.c_int32), ("adam_groups", ctypes.c_int32),
+                ("adam_grouped_nodes", ctypes.c_int32)]
+
+
 LIB_NAME = "libtfma.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
@@ -76,11 +82,15 @@ SIGNATURES = {
     "TFMA_MusaBiasAddRelu": [_vp, _T, _T, _cs, _T, _S],
     "TFMA_MusaAddV2Relu": [_vp, _T, _T, _T, _S],
     "TFMA_MusaShiftedAffineMap": [_vp, _T, _T, _T, _T, _S],
+    "TFMA_OptimizeGraph": [_vp, _sz, ctypes.POINTER(_cs), _i, _cs, _cs, ctypes.POINTER(_vp),
+                           ctypes.POINTER(_sz), ctypes.POINTER(TFMA_GraphRewriteStats), _S],
+    "TFMA_FreeBuffer": [_vp],
     "TFMA_TraceEnable": [_cs, _S],
     "TFMA_TraceRead": [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), _S],
     "TFMA_LastKernelName": [],
 }
-_RESTYPES = {"TFMA_Version": ctypes.c_char_p, "TFMA_LastKernelName": ctypes.c_char_p}
+_RESTYPES = {"TFMA_Version": ctypes.c_char_p, "TFMA_LastKernelName": ctypes.c_char_p,
+             "TFMA_FreeBuffer": None}
 
 _lib = None
 _load_error = None
