@@ -506,14 +506,20 @@ constexpr unsigned kSpinLimit = 1u << 24;  // ~0.5 s, then give up (flagged)
 // Resident 16-byte vectors per thread and per input tensor: KR in VGPRs (the
 // largest counts that compile without spills - the 8-wide types carry twice
 // the per-channel state), KL in LDS (the LDS budget split over the inputs).
+// PA/PB: streamed vectors per tensor prefetched for phase 3 while the grid
+// barriers are pending - PA after the first barrier's arrival (by waves with
+// no phase-2 channel), PB after the second's (by every wave).
 template <class Tr> struct Resident {
   static constexpr int kRegFwd = 28, kRegGrad = 10, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kPaFwd = 4, kPbFwd = 8, kPaGrad = 4, kPbGrad = 8;
 };
 template <> struct Resident<TF16> {
   static constexpr int kRegFwd = 12, kRegGrad = 8, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kPaFwd = 0, kPbFwd = 4, kPaGrad = 0, kPbGrad = 0;
 };
 template <> struct Resident<TBF16> {
   static constexpr int kRegFwd = 10, kRegGrad = 4, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kPaFwd = 4, kPbFwd = 4, kPaGrad = 4, kPbGrad = 8;
 };
 
 struct FusedArgs {
@@ -553,12 +559,21 @@ __device__ inline uint64_t load_shared(const void* p) {
                            __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Waits until every workgroup of the grid has arrived `k` times (k = 1, 2).
-__device__ inline void grid_barrier(const FusedArgs& a, unsigned k) {
+// Split-phase grid barrier.  grid_arrive: every thread's stores (and loads)
+// are complete, then the workgroup counts itself in.  grid_wait: returns once
+// every workgroup of the grid has arrived `k` times (k = 1, 2).  Between the
+// two halves a workgroup may issue loads that do not depend on other
+// workgroups (the phase-3 prefetch), so the barrier's latency overlaps with
+// memory traffic.
+__device__ inline void grid_arrive(const FusedArgs& a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // my shared stores are done
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == 0)
     __hip_atomic_fetch_add(a.barrier, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline void grid_wait(const FusedArgs& a, unsigned k) {
+  if (threadIdx.x == 0) {
     const unsigned long long target = a.base + static_cast<unsigned long long>(k) * gridDim.x;
     unsigned spins = 0;
     while (__hip_atomic_load(a.barrier, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
@@ -727,34 +742,64 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     store_shared(&a.partial[g * a.c + static_cast<int64_t>(ct) * width + tid],
                  __builtin_bit_cast(uint64_t, make_float2(sa, sb)));
   }
-  grid_barrier(a, 1);
+  grid_arrive(a);
+
+  // Phase-3 prefetch, part A: the last streamed rows (phase 3 runs
+  // last-to-first), loaded by the waves that have no phase-2 channel so the
+  // partial loads of the others do not queue behind them.
+  constexpr int PA = kGrad ? Resident<Tr>::kPaGrad : Resident<Tr>::kPaFwd;
+  constexpr int PB = kGrad ? Resident<Tr>::kPbGrad : Resident<Tr>::kPbFwd;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  constexpr int kWaves = kFusedThreads / 64;
+  const bool pre_a =
+      PA > 0 && static_cast<int>(blockIdx.x) + wave * static_cast<int>(gridDim.x) >= a.c;
+  uint4 pax[PA > 0 ? PA : 1], pad[kGrad && PA > 0 ? PA : 1];
+  if (pre_a) {
+#pragma unroll
+    for (int p = 0; p < PA; ++p) {
+      if (nk - 1 - p >= KR + KL) {
+        pax[p] = ld16(xrow(nk - 1 - p));
+        if constexpr (kGrad) pad[p] = ld16(drow(nk - 1 - p));
+      }
+    }
+  }
+  const int64_t qb = nk - 1 - (pre_a ? PA : 0);  // first row of part B
+  grid_wait(a, 1);
 
   // ---- phase 2: per-channel finals ---------------------------------------
   // Channel ch belongs to workgroup ch % gridDim.x; each wave of the
   // workgroup finishes one of its channels at a time, so all of a
   // workgroup's partial loads are in flight together.
-  {
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-    constexpr int kWaves = kFusedThreads / 64;
-    for (int ch = blockIdx.x + wave * gridDim.x; ch < a.c; ch += kWaves * gridDim.x) {
-      double t1 = 0.0, t2 = 0.0;
-      for (int64_t gg = lane; gg < a.groups; gg += 64) {
-        const float2 v = __builtin_bit_cast(float2, load_shared(&a.partial[gg * a.c + ch]));
-        t1 += v.x;
-        t2 += v.y;
-      }
-      const double2 w = wave_sum(t1, t2);
-      if (lane == 0) {
-        const float4 cfc = finish_channel<Tr, kGrad>(a.fin, ch, w.x, w.y);
-        store_shared(&a.coef[ch], __builtin_bit_cast(uint64_t, make_float2(cfc.x, cfc.y)));
-        store_shared(reinterpret_cast<float2*>(&a.coef[ch]) + 1,
-                     __builtin_bit_cast(uint64_t, make_float2(cfc.z, cfc.w)));
-      }
+  for (int ch = blockIdx.x + wave * gridDim.x; ch < a.c; ch += kWaves * gridDim.x) {
+    double t1 = 0.0, t2 = 0.0;
+    for (int64_t gg = lane; gg < a.groups; gg += 64) {
+      const float2 v = __builtin_bit_cast(float2, load_shared(&a.partial[gg * a.c + ch]));
+      t1 += v.x;
+      t2 += v.y;
     }
-    zero_side_outputs<kGrad>(a.fin);
+    const double2 w = wave_sum(t1, t2);
+    if (lane == 0) {
+      const float4 cfc = finish_channel<Tr, kGrad>(a.fin, ch, w.x, w.y);
+      store_shared(&a.coef[ch], __builtin_bit_cast(uint64_t, make_float2(cfc.x, cfc.y)));
+      store_shared(reinterpret_cast<float2*>(&a.coef[ch]) + 1,
+                   __builtin_bit_cast(uint64_t, make_float2(cfc.z, cfc.w)));
+    }
   }
-  grid_barrier(a, 2);
+  zero_side_outputs<kGrad>(a.fin);
+  grid_arrive(a);
+
+  // Prefetch part B: the next rows, in flight during the second barrier and
+  // the coefficient loads.
+  uint4 pbx[PB > 0 ? PB : 1], pbd[kGrad && PB > 0 ? PB : 1];
+#pragma unroll
+  for (int p = 0; p < PB; ++p) {
+    if (qb - p >= KR + KL) {
+      pbx[p] = ld16(xrow(qb - p));
+      if constexpr (kGrad) pbd[p] = ld16(drow(qb - p));
+    }
+  }
+  grid_wait(a, 2);
 
   // ---- phase 3: outputs --------------------------------------------------
   // Make the resident words opaque so only the packed words (not their
@@ -777,7 +822,19 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       cf[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
-  q = nk - 1;
+  // Prefetched rows first, then the remaining streamed rows last-to-first.
+  if (pre_a) {
+#pragma unroll
+    for (int p = 0; p < PA; ++p)
+      if (nk - 1 - p >= KR + KL)
+        st16(po + base + (nk - 1 - p) * rstride,
+             apply_words<Tr, kGrad>(pax[p], pad[kGrad ? p : 0], cf));
+  }
+#pragma unroll
+  for (int p = 0; p < PB; ++p)
+    if (qb - p >= KR + KL)
+      st16(po + base + (qb - p) * rstride, apply_words<Tr, kGrad>(pbx[p], pbd[kGrad ? p : 0], cf));
+  q = qb - PB;
   for (; q >= KR + KL + U - 1; q -= U) {
     uint4 xw[U], dw[U];
 #pragma unroll

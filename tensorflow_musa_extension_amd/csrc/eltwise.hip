@@ -23,12 +23,25 @@ namespace {
 
 constexpr int kThreads = 256;
 
-enum Kind : int { kFullK = 0, kScalarK = 1, kRowK = 2, kChanK = 3, kGatherK = 4 };
+// kRowOddK: a row operand (inner extent 1) whose period is not a multiple of
+// the vector width - one modulo per vector, then consecutive elements with a
+// wrap at the period.  kGatherK: anything else - one division per vector,
+// then an incremental walk of (index, position within the inner extent).
+// Both read the operand's `period` values from a copy in LDS that each
+// workgroup makes first (per-element gathers from global memory are limited
+// by the L1's request rate, not by bytes); kGatherGlobalK is the same walk
+// from global memory, for periods larger than the LDS copy allows.
+enum Kind : int {
+  kFullK = 0, kScalarK = 1, kRowK = 2, kChanK = 3, kRowOddK = 4, kGatherK = 5, kGatherGlobalK = 6
+};
+constexpr uint32_t kStageBytes = 16384;  // per staged operand
+constexpr bool staged_kind(int k) { return k == kRowOddK || k == kGatherK; }
 
 struct Operand {
   const void* p;
   int kind;
   uint32_t period;
+  uint32_t inner;
   FastDiv div_inner;
   FastDiv div_period;
 };
@@ -41,34 +54,61 @@ __device__ inline S gather_one(const Operand& o, uint32_t i) {
   return p[idx];
 }
 
-template <typename S, int V>
-__device__ inline void fetch(const Operand& o, uint32_t i0, S (&out)[V]) {
-  const S* p = static_cast<const S*>(o.p);
-  switch (o.kind) {
-    case kFullK:
-      vload<S, V>(p + i0, out);
-      break;
-    case kScalarK: {
-      const S s = p[0];
-#pragma unroll
-      for (int j = 0; j < V; ++j) out[j] = s;
-      break;
+// Loads the V operand values for flat indices i0 .. i0+V-1.  K is the
+// operand kind when known at compile time (the vector kernels are
+// instantiated per kind, so no branch separates the loads of one unrolled
+// iteration from the next and every load is in flight before the first use);
+// kAnyK switches on o.kind at run time.
+constexpr int kAnyK = -1;
+
+// p is the operand's data: o.p, or its LDS copy for the staged kinds.
+template <int K, typename S, int V>
+__device__ inline void fetch(const Operand& o, const S* p, uint32_t i0, S (&out)[V]) {
+  if constexpr (K == kAnyK) {
+    switch (o.kind) {
+      case kFullK: fetch<kFullK, S, V>(o, p, i0, out); break;
+      case kScalarK: fetch<kScalarK, S, V>(o, p, i0, out); break;
+      case kRowK: fetch<kRowK, S, V>(o, p, i0, out); break;
+      case kChanK: fetch<kChanK, S, V>(o, p, i0, out); break;
+      case kRowOddK: fetch<kRowOddK, S, V>(o, p, i0, out); break;
+      default: fetch<kGatherK, S, V>(o, p, i0, out); break;
     }
-    case kRowK: {
-      const uint32_t idx = i0 - o.div_period.div(i0) * o.period;
-      vload<S, V>(p + idx, out);
-      break;
-    }
-    case kChanK: {
-      const S s = gather_one<S>(o, i0);
+  } else if constexpr (K == kFullK) {
+    vload<S, V>(p + i0, out);
+  } else if constexpr (K == kScalarK) {
+    const S s = p[0];
 #pragma unroll
-      for (int j = 0; j < V; ++j) out[j] = s;
-      break;
-    }
-    default:
+    for (int j = 0; j < V; ++j) out[j] = s;
+  } else if constexpr (K == kRowK) {
+    const uint32_t idx = i0 - o.div_period.div(i0) * o.period;
+    vload<S, V>(p + idx, out);
+  } else if constexpr (K == kChanK) {
+    const S s = gather_one<S>(o, i0);
 #pragma unroll
-      for (int j = 0; j < V; ++j) out[j] = gather_one<S>(o, i0 + j);
-      break;
+    for (int j = 0; j < V; ++j) out[j] = s;
+  } else if constexpr (K == kRowOddK) {
+    uint32_t idx = i0 - o.div_period.div(i0) * o.period;
+    if (idx + V <= o.period) {  // no wrap: constant offsets from one base
+#pragma unroll
+      for (int j = 0; j < V; ++j) out[j] = p[idx + j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        out[j] = p[idx];
+        idx = idx + 1 == o.period ? 0 : idx + 1;
+      }
+    }
+  } else {
+    const uint32_t q = o.div_inner.div(i0);
+    uint32_t r = i0 - q * o.inner;
+    uint32_t idx = q - o.div_period.div(q) * o.period;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      out[j] = p[idx];
+      const bool next = ++r == o.inner;
+      r = next ? 0 : r;
+      idx = next ? (idx + 1 == o.period ? 0 : idx + 1) : idx;
+    }
   }
 }
 
@@ -97,13 +137,29 @@ constexpr int arity() {
   return OP == EwOp::kRelu ? 1 : (OP == EwOp::kMulAdd ? 3 : 2);
 }
 
-// Flat kernel over n < 2^31 elements; `a` is always full-size.
-template <class Tr, EwOp OP, int V, int UNROLL>
+// Flat kernel over n < 2^31 elements; `a` is always full-size.  KB / KC are
+// the kinds of the b / c operands (kAnyK: decided per access at run time).
+template <class Tr, EwOp OP, int V, int UNROLL, int KB, int KC>
 __global__ __launch_bounds__(kThreads) void ew_flat_kernel(
     const typename Tr::S* __restrict__ a, Operand b, Operand c,
     typename Tr::S* __restrict__ out, uint32_t n) {
   using S = typename Tr::S;
   constexpr int kArity = arity<OP>();
+  extern __shared__ __align__(16) unsigned char ew_lds[];
+  const S* pb = static_cast<const S*>(b.p);
+  const S* pc = static_cast<const S*>(c.p);
+  if constexpr (kArity >= 2 && staged_kind(KB)) {
+    S* l = reinterpret_cast<S*>(ew_lds);
+    for (uint32_t k = threadIdx.x; k < b.period; k += kThreads) l[k] = pb[k];
+    pb = l;
+  }
+  if constexpr (kArity >= 3 && staged_kind(KC)) {
+    S* l = reinterpret_cast<S*>(ew_lds + (staged_kind(KB) ? kStageBytes : 0));
+    for (uint32_t k = threadIdx.x; k < c.period; k += kThreads) l[k] = pc[k];
+    pc = l;
+  }
+  if constexpr ((kArity >= 2 && staged_kind(KB)) || (kArity >= 3 && staged_kind(KC)))
+    __syncthreads();
   const uint32_t nv = n / V;
   const uint32_t stride = gridDim.x * kThreads;
   const uint32_t tid = blockIdx.x * kThreads + threadIdx.x;
@@ -114,8 +170,8 @@ __global__ __launch_bounds__(kThreads) void ew_flat_kernel(
     for (int u = 0; u < UNROLL; ++u) {
       const uint32_t i0 = (i + u * stride) * V;
       vload<S, V>(a + i0, av[u]);
-      if constexpr (kArity >= 2) fetch<S, V>(b, i0, bv[u]);
-      if constexpr (kArity >= 3) fetch<S, V>(c, i0, cv[u]);
+      if constexpr (kArity >= 2) fetch<KB, S, V>(b, pb, i0, bv[u]);
+      if constexpr (kArity >= 3) fetch<KC, S, V>(c, pc, i0, cv[u]);
     }
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
@@ -131,8 +187,8 @@ __global__ __launch_bounds__(kThreads) void ew_flat_kernel(
     const uint32_t i0 = i * V;
     S av[V], bv[V], cv[V], ov[V];
     vload<S, V>(a + i0, av);
-    if constexpr (kArity >= 2) fetch<S, V>(b, i0, bv);
-    if constexpr (kArity >= 3) fetch<S, V>(c, i0, cv);
+    if constexpr (kArity >= 2) fetch<KB, S, V>(b, pb, i0, bv);
+    if constexpr (kArity >= 3) fetch<KC, S, V>(c, pc, i0, cv);
 #pragma unroll
     for (int j = 0; j < V; ++j)
       ov[j] = ew_apply<Tr, OP>(av[j], kArity >= 2 ? bv[j] : S(0),
@@ -183,9 +239,18 @@ const char* op_kernel_name(EwOp op) {
   return "tfma_ew";
 }
 
+int blocks_per_cu() {
+  static int v = [] {
+    const char* e = getenv("TFMA_EW_BLOCKS_PER_CU");
+    const int b = e ? atoi(e) : 0;
+    return b > 0 ? b : 8;
+  }();
+  return v;
+}
+
 int64_t grid_for(int64_t units, int unroll) {
   int64_t blocks = (units + kThreads * unroll - 1) / (kThreads * unroll);
-  const int64_t max_blocks = static_cast<int64_t>(DeviceCUs()) * 16;
+  const int64_t max_blocks = static_cast<int64_t>(DeviceCUs()) * blocks_per_cu();
   if (blocks > max_blocks) blocks = max_blocks;
   if (blocks < 1) blocks = 1;
   return blocks;
@@ -197,6 +262,7 @@ Operand make_operand(const BcastOperand& o, int elem_bytes, int V,
   Operand r;
   r.p = o.data;
   r.period = 1;
+  r.inner = 1;
   const bool aligned = (reinterpret_cast<uintptr_t>(o.data) & 15) == 0;
   switch (o.mode) {
     case BcastMode::kFull:
@@ -216,17 +282,75 @@ Operand make_operand(const BcastOperand& o, int elem_bytes, int V,
       r.div_inner = FastDiv(static_cast<uint32_t>(o.inner));
       r.div_period = FastDiv(static_cast<uint32_t>(o.period));
       r.period = static_cast<uint32_t>(o.period);
+      r.inner = static_cast<uint32_t>(o.inner);
       if (o.inner == 1 && o.period % V == 0 && aligned) {
         r.kind = kRowK;
       } else if (o.inner % V == 0) {
         r.kind = kChanK;
+      } else if (o.period * elem_bytes > kStageBytes) {
+        r.kind = kGatherGlobalK;
+      } else if (o.inner == 1) {
+        r.kind = kRowOddK;
       } else {
         r.kind = kGatherK;
       }
       break;
   }
-  (void)elem_bytes;
   return r;
+}
+
+// Vector-path launch with the operand kinds as compile-time parameters.
+template <class Tr, EwOp OP, int KB, int KC>
+void launch_vec(const Operand& ob, const Operand& oc, const typename Tr::S* a,
+                typename Tr::S* out, uint32_t n, hipStream_t stream) {
+  constexpr int V = Tr::kVec;
+  constexpr int U = 2;
+  constexpr bool sb = arity<OP>() >= 2 && staged_kind(KB);
+  constexpr bool sc = arity<OP>() >= 3 && staged_kind(KC);
+  // A staged workgroup copies the operand once; fewer, longer-lived
+  // workgroups keep that copy cheap.
+  const size_t lds = sc ? (sb ? 2 : 1) * kStageBytes : (sb ? (ob.period * sizeof(typename Tr::S)) : 0);
+  int64_t blocks = grid_for(n / V, U);
+  const int64_t cap = static_cast<int64_t>(DeviceCUs()) * 4;
+  if ((sb || sc) && blocks > cap) blocks = cap;
+  hipLaunchKernelGGL((ew_flat_kernel<Tr, OP, V, U, KB, KC>), dim3(blocks),
+                     dim3(kThreads), lds, stream, a, ob, oc, out, n);
+}
+
+template <class Tr, EwOp OP, int KB>
+void pick_kc(const Operand& ob, const Operand& oc, const typename Tr::S* a,
+             typename Tr::S* out, uint32_t n, hipStream_t stream) {
+  if constexpr (arity<OP>() < 3) {
+    launch_vec<Tr, OP, KB, kFullK>(ob, oc, a, out, n, stream);  // c unused
+  } else {
+    switch (oc.kind) {
+      case kFullK: launch_vec<Tr, OP, KB, kFullK>(ob, oc, a, out, n, stream); break;
+      case kScalarK: launch_vec<Tr, OP, KB, kScalarK>(ob, oc, a, out, n, stream); break;
+      case kRowK: launch_vec<Tr, OP, KB, kRowK>(ob, oc, a, out, n, stream); break;
+      case kChanK: launch_vec<Tr, OP, KB, kChanK>(ob, oc, a, out, n, stream); break;
+      case kRowOddK: launch_vec<Tr, OP, KB, kRowOddK>(ob, oc, a, out, n, stream); break;
+      case kGatherK: launch_vec<Tr, OP, KB, kGatherK>(ob, oc, a, out, n, stream); break;
+      default: launch_vec<Tr, OP, KB, kGatherGlobalK>(ob, oc, a, out, n, stream); break;
+    }
+  }
+}
+
+template <class Tr, EwOp OP>
+void pick_kb(const Operand& ob, const Operand& oc, const typename Tr::S* a,
+             typename Tr::S* out, uint32_t n, hipStream_t stream) {
+  if constexpr (arity<OP>() < 2) {
+    launch_vec<Tr, OP, kFullK, kFullK>(ob, oc, a, out, n, stream);  // b, c unused
+  } else {
+    switch (ob.kind) {
+      case kFullK: pick_kc<Tr, OP, kFullK>(ob, oc, a, out, n, stream); break;
+      case kScalarK: pick_kc<Tr, OP, kScalarK>(ob, oc, a, out, n, stream); break;
+      case kRowK: pick_kc<Tr, OP, kRowK>(ob, oc, a, out, n, stream); break;
+      case kChanK: pick_kc<Tr, OP, kChanK>(ob, oc, a, out, n, stream); break;
+      case kRowOddK: pick_kc<Tr, OP, kRowOddK>(ob, oc, a, out, n, stream); break;
+      case kGatherK: pick_kc<Tr, OP, kGatherK>(ob, oc, a, out, n, stream); break;
+      default: pick_kc<Tr, OP, kGatherGlobalK>(ob, oc, a, out, n, stream); break;
+    }
+  }
 }
 
 template <class Tr, EwOp OP>
@@ -244,10 +368,7 @@ hipError_t launch_ew(int64_t n, const BcastOperand& a, const BcastOperand& b,
   const uint32_t n32 = static_cast<uint32_t>(n);
   LaunchScope scope(stream, op_kernel_name(OP));
   if (vec_ok) {
-    constexpr int U = 2;
-    hipLaunchKernelGGL((ew_flat_kernel<Tr, OP, V, U>), dim3(grid_for(n / V, U)),
-                       dim3(kThreads), 0, stream, static_cast<const S*>(a.data),
-                       ob, oc, static_cast<S*>(out), n32);
+    pick_kb<Tr, OP>(ob, oc, static_cast<const S*>(a.data), static_cast<S*>(out), n32, stream);
   } else {
     // Re-classify for V = 1 (rows and channels become per-element gathers).
     bool dummy = true;
@@ -256,7 +377,7 @@ hipError_t launch_ew(int64_t n, const BcastOperand& a, const BcastOperand& b,
     oc = kArity >= 3 ? make_operand(c, sizeof(S), 1, &dummy)
                      : make_operand(a, sizeof(S), 1, &dummy);
     constexpr int U = 4;
-    hipLaunchKernelGGL((ew_flat_kernel<Tr, OP, 1, U>), dim3(grid_for(n, U)),
+    hipLaunchKernelGGL((ew_flat_kernel<Tr, OP, 1, U, kAnyK, kAnyK>), dim3(grid_for(n, U)),
                        dim3(kThreads), 0, stream, static_cast<const S*>(a.data),
                        ob, oc, static_cast<S*>(out), n32);
   }

@@ -46,6 +46,11 @@ BCAST = [
     ((4096,), (8192, 4096)),        # broadcast operand first
     ((64, 33), ()),                 # scalar
     ((64, 33), (64, 1)),            # column broadcast (inner > 1)
+    ((37, 3), (3,)),                # period shorter than a vector: wraps inside it
+    ((9, 7, 11), (7, 1)),           # inner 11, period 7: incremental walk
+    ((5, 1021), (1021,)),           # odd period, wrap in a few vectors
+    ((3, 9001), (9001,)),           # odd period too long for the LDS copy
+    ((9000, 3), (9000, 1)),         # inner 3, long period: global walk
     ((4, 1, 5), (1, 3, 1)),         # neither operand full: strided path
     ((2, 3, 4, 8), (3, 1, 8)),      # two broadcast runs: strided path
     ((0, 4), (4,)),                 # empty
