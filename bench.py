@@ -57,6 +57,16 @@ def resnet50_shapes():
     return shapes
 
 
+def cfg5_shapes():
+    """cfg5: 145 fp32 tensors, 1,310,982,144 parameters (24 x {4 x [2048,2048],
+    [2048,8192], [8192,2048]} + [50304,2048])."""
+    shapes = []
+    for _ in range(24):
+        shapes += [(2048, 2048)] * 4 + [(2048, 8192), (8192, 2048)]
+    shapes.append((50304, 2048))
+    return shapes
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -172,6 +182,12 @@ def components(torch, ops, dev):
     g = 1e-3 * torch.randn(n, generator=gen, device=dev)
     adam = ops.bind(ops.ResourceApplyAdam, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7, g)
     out["adam_f32_25.6M"] = rate([adam], 28 * n)
+    # Mixed precision (fp32 state, bf16 grad): 24 B of state + 2 B of grad.
+    gb = g.to(torch.bfloat16)
+    mixed = ops.bind(ops.MusaResourceApplyAdamMixed, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999,
+                     1e-7, gb)
+    out["adam_mixed_bf16grad_25.6M"] = rate([mixed], 26 * n)
+    del gb
 
     shapes = resnet50_shapes()
     tv = [0.02 * torch.randn(s, generator=gen, device=dev) for s in shapes]
@@ -182,7 +198,20 @@ def components(torch, ops, dev):
     grouped = ops.bind(ops.MusaGroupedResourceApplyAdam, tv, tm, tvv, tg, 0.9, 0.999, 1e-3, 0.9,
                        0.999, 1e-7)
     out["grouped_adam_f32_resnet50_161"] = rate([grouped], 28 * total)
-    del var, m, v, g, tv, tm, tvv, tg
+    del var, m, v, g, tv, tm, tvv, tg, grouped, adam, mixed
+
+    # cfg5: 1.31B parameters in 145 tensors, 21 GB of state resident.
+    shapes5 = cfg5_shapes()
+    tv = [0.02 * torch.randn(s, generator=gen, device=dev) for s in shapes5]
+    tm = [(1e-4 * torch.randn(s, generator=gen, device=dev)).abs_() for s in shapes5]
+    tvv = [(1e-4 * torch.randn(s, generator=gen, device=dev)).abs_() for s in shapes5]
+    tg = [1e-3 * torch.randn(s, generator=gen, device=dev) for s in shapes5]
+    total5 = sum(t.numel() for t in tv)
+    grouped5 = ops.bind(ops.MusaGroupedResourceApplyAdam, tv, tm, tvv, tg, 0.9, 0.999, 1e-3,
+                        0.9, 0.999, 1e-7)
+    out["grouped_adam_f32_cfg5_145"] = rate([grouped5], 28 * total5, reps_=10)
+    del tv, tm, tvv, tg, grouped5
+    torch.cuda.empty_cache()
 
     for dt, name in ((torch.float32, "f32"), (torch.float16, "f16")):
         s = torch.tensor([], dtype=dt).element_size()

@@ -161,6 +161,22 @@ int TFMA_ResourceApplyAdam(void* stream, TFMA_Tensor* var, TFMA_Tensor* m,
                            int use_locking, int use_nesterov,
                            TFMA_Status* status);
 
+/* Mixed-precision Adam: fp32 var/m/v (T = float state) with a float, half or
+ * bfloat16 gradient and float host scalars.  Same op name, inputs, attrs and
+ * error messages as the reference's MusaResourceApplyAdamMixed
+ * (musa_ext/kernels/training/musa_applyadam_mixed_op.cc:125-302, registered
+ * :265-300; kernel musa_applyadam_mixed_kernel.mu:55-103).  The update is
+ * bit-identical to TF's Cast(grad, float) followed by the fp32
+ * ResourceApplyAdam, the pair the reference's Cast-folding rewrite replaces
+ * (musa_ext/graph/fusion/adam_mixed_fusion.cc:93-216); the reference's own
+ * kernel uses a different operation order and a double-precision alpha. */
+int TFMA_MusaResourceApplyAdamMixed(void* stream, TFMA_Tensor* var, TFMA_Tensor* m,
+                                    TFMA_Tensor* v, const TFMA_Tensor* beta1_power,
+                                    const TFMA_Tensor* beta2_power, const TFMA_Tensor* lr,
+                                    const TFMA_Tensor* beta1, const TFMA_Tensor* beta2,
+                                    const TFMA_Tensor* epsilon, const TFMA_Tensor* grad,
+                                    int use_locking, int use_nesterov, TFMA_Status* status);
+
 /* Multi-tensor Adam: N independent ResourceApplyAdam updates with shared
  * host scalars in one launch; each element's result is bit-identical to
  * TFMA_ResourceApplyAdam on that tensor.  No reference op exists; it follows
@@ -168,7 +184,10 @@ int TFMA_ResourceApplyAdam(void* stream, TFMA_Tensor* var, TFMA_Tensor* m,
  * MusaGroupedResourceApplyGradientDescentMixed
  * (reference: musa_ext/kernels/training/musa_applygradientdescent_op.cc:
  * 305-448, kernel musa_applygradientdescent_kernel.mu:31-105) with inputs
- * vars/ms/vs/grads: N tensors each.  The per-launch tensor table lives in
+ * vars/ms/vs/grads: N tensors each.  With fp32 vars the grads may all be
+ * half or bfloat16 instead (attr Tgrad, as the reference op's T/Tgrad pair):
+ * each tensor then updates as TFMA_MusaResourceApplyAdamMixed.  The
+ * per-launch tensor table lives in
  * `workspace` (TFMA_GroupedApplyAdamWorkspaceBytes); the library uploads it
  * on the stream, so the workspace must stay allocated until the launch has
  * run. */
@@ -242,12 +261,20 @@ int TFMA_MusaShiftedAffineMap(void* stream, const TFMA_Tensor* data_left,
  *   "MusaBiasAddRelu"       Relu(BiasAdd(x, b))     -> MusaBiasAddRelu(x, b)
  *   "MusaAddV2Relu"         Relu(AddV2|Add(x, y))   -> MusaAddV2Relu(x, y)
  *   "MusaShiftedAffineMap"  AddV2|Add(Mul(x, a), b) -> MusaShiftedAffineMap(x, a, b)
- *   "MusaGroupedResourceApplyAdam"  >= 2 ResourceApplyAdam nodes sharing
- *       device, T, use_locking, use_nesterov and the six scalar inputs, none
+ *   "MusaResourceApplyAdamMixed"  ResourceApplyAdam<float> whose grad is
+ *       Cast<half|bfloat16 -> float>(g) -> MusaResourceApplyAdamMixed (T = the
+ *       Cast's SrcT) reading g; the Cast is removed when nothing else reads
+ *       it (reference pattern MusaAdamMixedFusion, adam_mixed_fusion.cc:93-216,
+ *       priority 40).
+ *   "MusaGroupedResourceApplyAdam"  >= 2 ResourceApplyAdam or
+ *       MusaResourceApplyAdamMixed nodes sharing device, state and gradient
+ *       dtypes, use_locking, use_nesterov and the six scalar inputs, none
  *       depending on another, distinct var/m/v ->
  *       MusaGroupedResourceApplyAdam(vars N, ms N, vs N, beta1_power,
- *       beta2_power, lr, beta1, beta2, epsilon, grads N; attrs N, T,
- *       use_locking, use_nesterov).
+ *       beta2_power, lr, beta1, beta2, epsilon, grads N; attrs N, T (state),
+ *       Tgrad, use_locking, use_nesterov).
+ * The reference's names MusaShiftedAffineMapFusion and MusaAdamMixedFusion
+ * are accepted in disabled_patterns as well.
  * A fused node keeps the name, device and control inputs of the node it
  * replaces and gains the absorbed node's control inputs; the absorbed node
  * must have that node as its only data consumer, the same device and T
@@ -266,7 +293,8 @@ typedef struct TFMA_GraphRewriteStats {
   int32_t add_v2_relu;
   int32_t mul_add;
   int32_t adam_groups;        /* grouped Adam nodes created */
-  int32_t adam_grouped_nodes; /* ResourceApplyAdam nodes they replaced */
+  int32_t adam_grouped_nodes; /* Adam nodes they replaced */
+  int32_t adam_mixed;         /* Cast folded into MusaResourceApplyAdamMixed */
 } TFMA_GraphRewriteStats;
 
 int TFMA_OptimizeGraph(const void* graph_def, size_t graph_def_bytes,

@@ -169,6 +169,18 @@ def adam(var, m, v, grad, beta1_power, beta2_power, lr, beta1, beta2, epsilon,
                     int(bool(use_nesterov)))
 
 
+def adam_mixed(var, m, v, grad, beta1_power, beta2_power, lr, beta1, beta2, epsilon,
+               use_nesterov=False, grad_dtype="float16"):
+    """MusaResourceApplyAdamMixed as the TF-CPU pair it replaces
+    (reference: musa_ext/graph/fusion/adam_mixed_fusion.cc:93-216 folds
+    Cast(grad, float) -> ResourceApplyAdam<float>): widen the half/bfloat16
+    grad to float32 (exact) and run the float32 ResourceApplyAdam on the
+    float32 var/m/v."""
+    g32 = np.ascontiguousarray(to_f32(grad, grad_dtype), dtype=np.float32)
+    adam(var, m, v, g32, beta1_power, beta2_power, lr, beta1, beta2, epsilon,
+         use_nesterov=use_nesterov, dtype="float32")
+
+
 def eltwise(op, inputs, dtype="float32"):
     """TF-CPU elementwise op with broadcasting: add, add_relu, mul, mul_add
     (inputs[0]*inputs[1] rounded, + inputs[2]) or relu."""

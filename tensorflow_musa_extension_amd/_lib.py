@@ -47,7 +47,7 @@ class TFMA_Status(ctypes.Structure):
 class TFMA_GraphRewriteStats(ctypes.Structure):
     _fields_ = [("bias_add_relu", ctypes.c_int32), ("add_v2_relu", ctypes.c_int32),
                 ("mul_add", ctypes.c_int32), ("adam_groups", ctypes.c_int32),
-                ("adam_grouped_nodes", ctypes.c_int32)]
+                ("adam_grouped_nodes", ctypes.c_int32), ("adam_mixed", ctypes.c_int32)]
 
 
 LIB_NAME = "libtfma.so"
@@ -72,6 +72,8 @@ SIGNATURES = {
     "TFMA_FusedBatchNormGradV3": [_vp, _T, _T, _T, _T, _T, _T, _f, _cs, _i, _T, _T, _T, _T,
                                   _T, _vp, _sz, _S],
     "TFMA_ResourceApplyAdam": [_vp, _T, _T, _T, _T, _T, _T, _T, _T, _T, _T, _i, _i, _S],
+    "TFMA_MusaResourceApplyAdamMixed": [_vp, _T, _T, _T, _T, _T, _T, _T, _T, _T, _T, _i, _i,
+                                        _S],
     "TFMA_GroupedApplyAdamWorkspaceBytes": [_i, _T, ctypes.POINTER(_sz), _S],
     "TFMA_GroupedResourceApplyAdam": [_vp, _i, _T, _T, _T, _T, _T, _T, _T, _T, _T, _T, _i, _i,
                                       _vp, _sz, _S],

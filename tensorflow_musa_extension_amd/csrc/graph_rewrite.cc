@@ -5,7 +5,11 @@
 //   Relu(BiasAdd(x, b))        -> MusaBiasAddRelu(x, b)          priority 100
 //   Relu(AddV2|Add(x, y))      -> MusaAddV2Relu(x, y)            priority  90
 //   AddV2|Add(Mul(x, a), b)    -> MusaShiftedAffineMap(x, a, b)  priority  80
-//   k >= 2 ResourceApplyAdam with the same scalars, dtype, attrs and device
+//   ResourceApplyAdam<float>(..., Cast<half|bfloat16 -> float>(g))
+//                              -> MusaResourceApplyAdamMixed(..., g)  priority 40
+//                                 (musa_ext/graph/fusion/adam_mixed_fusion.cc:93-216)
+//   k >= 2 ResourceApplyAdam / MusaResourceApplyAdamMixed with the same
+//   scalars, state and gradient dtypes, attrs and device
 //                              -> MusaGroupedResourceApplyAdam
 //
 // Semantics follow the reference's pattern framework: a pattern matches from
@@ -337,6 +341,7 @@ void add_control_inputs(const Node& from, std::vector<std::string>* to) {
 // ---------------------------------------------------------------------------
 struct Pattern {
   const char* name;
+  const char* alias;  // the reference's name for the same rewrite, if any
   int priority;
   bool (*apply)(Graph* g, int i);
 };
@@ -452,14 +457,45 @@ bool apply_mul_add(Graph* g, int i) {
   return false;
 }
 
+// ResourceApplyAdam<float> whose grad is Cast(SrcT = half|bfloat16, DstT =
+// float): the Adam node becomes MusaResourceApplyAdamMixed (T = SrcT) reading
+// the Cast's input; the Cast goes away when nothing else reads it.
+bool apply_adam_mixed(Graph* g, int i) {
+  Node& adam = g->nodes[i];
+  if (adam.removed || adam.op != "ResourceApplyAdam" || !g->on_device(adam)) return false;
+  int64_t t = 0;
+  if (!attr_varint(adam, "T", 6, &t) || t != TFMA_FLOAT) return false;
+  if (adam.inputs.size() < 10 || is_control(adam.inputs[9])) return false;
+  int port;
+  const Node* cast = g->producer(adam.inputs[9], &port);
+  if (!cast || port != 0 || cast->op != "Cast" || cast->inputs.empty() ||
+      is_control(cast->inputs[0]))
+    return false;
+  int64_t src = 0, dst = 0;
+  if (!attr_varint(*cast, "DstT", 6, &dst) || dst != TFMA_FLOAT) return false;
+  if (!attr_varint(*cast, "SrcT", 6, &src) || (src != TFMA_HALF && src != TFMA_BFLOAT16))
+    return false;
+  const int ci = g->index.at(cast->name);
+  int other = 0;
+  for (const auto& c : g->consumers(cast->name))
+    if (c.first != i || c.second != 9) ++other;
+  adam.op = "MusaResourceApplyAdamMixed";
+  for (auto& kv : adam.attrs)
+    if (kv.first == "T") kv.second = attr_of_type(src);
+  adam.inputs[9] = g->nodes[ci].inputs[0];
+  if (other == 0 && !g->fetch.count(g->nodes[ci].name)) absorb(g, ci, i);
+  return true;
+}
+
 const Pattern kPatterns[] = {
-    {"MusaBiasAddRelu", 100, apply_bias_add_relu},
-    {"MusaAddV2Relu", 90, apply_add_v2_relu},
-    {"MusaShiftedAffineMap", 80, apply_mul_add},
+    {"MusaBiasAddRelu", nullptr, 100, apply_bias_add_relu},
+    {"MusaAddV2Relu", nullptr, 90, apply_add_v2_relu},
+    {"MusaShiftedAffineMap", "MusaShiftedAffineMapFusion", 80, apply_mul_add},
+    {"MusaResourceApplyAdamMixed", "MusaAdamMixedFusion", 40, apply_adam_mixed},
 };
 
-bool pattern_disabled(const std::set<std::string>& disabled, const char* name) {
-  return disabled.count(name) > 0;
+bool pattern_disabled(const std::set<std::string>& disabled, const Pattern& p) {
+  return disabled.count(p.name) > 0 || (p.alias && disabled.count(p.alias) > 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -521,14 +557,28 @@ std::string tensor_key(const std::string& in) {
 // ancestor sets always describe the current graph and a group never closes a
 // cycle with an earlier one.
 int group_adam_once(Graph* g) {
+  // State and gradient dtypes: ResourceApplyAdam has both = T;
+  // MusaResourceApplyAdamMixed has float state and T gradients.
+  auto dtypes = [](const Node& n, int64_t* state, int64_t* grad) {
+    int64_t t = 0;
+    if (!attr_varint(n, "T", 6, &t)) return false;
+    if (n.op == "ResourceApplyAdam") {
+      *state = *grad = t;
+      return fusable_type(t) || t == TFMA_DOUBLE;
+    }
+    if (n.op == "MusaResourceApplyAdamMixed") {
+      *state = TFMA_FLOAT;
+      *grad = t;
+      return fusable_type(t);
+    }
+    return false;
+  };
   std::vector<int> cand;
   for (int i = 0; i < static_cast<int>(g->nodes.size()); ++i) {
     const Node& n = g->nodes[i];
-    int64_t t = 0;
-    if (n.removed || n.op != "ResourceApplyAdam" || g->fetch.count(n.name) || !g->on_device(n))
-      continue;
-    if (!attr_varint(n, "T", 6, &t)) continue;
-    if (!(fusable_type(t) || t == TFMA_DOUBLE)) continue;
+    int64_t st = 0, gt = 0;
+    if (n.removed || g->fetch.count(n.name) || !g->on_device(n)) continue;
+    if (!dtypes(n, &st, &gt)) continue;
     bool ok = n.inputs.size() >= 10;
     for (size_t k = 0; k < n.inputs.size() && ok; ++k) ok = is_control(n.inputs[k]) == (k >= 10);
     if (ok) cand.push_back(i);
@@ -546,12 +596,12 @@ int group_adam_once(Graph* g) {
   std::map<std::string, std::vector<int>> by_key;
   for (int i : cand) {
     const Node& n = g->nodes[i];
-    int64_t t = 0, lock = 0, nest = 0;
-    attr_varint(n, "T", 6, &t);
+    int64_t st = 0, gt = 0, lock = 0, nest = 0;
+    dtypes(n, &st, &gt);
     attr_varint(n, "use_locking", 5, &lock);
     attr_varint(n, "use_nesterov", 5, &nest);
-    std::string key = n.device + '\x1f' + std::to_string(t) + '\x1f' + std::to_string(lock) +
-                      '\x1f' + std::to_string(nest);
+    std::string key = n.device + '\x1f' + std::to_string(st) + '\x1f' + std::to_string(gt) +
+                      '\x1f' + std::to_string(lock) + '\x1f' + std::to_string(nest);
     for (int k = 3; k < 9; ++k) key += '\x1f' + tensor_key(n.inputs[k]);
     by_key[key].push_back(i);
   }
@@ -588,12 +638,13 @@ int group_adam_once(Graph* g) {
         if (is_control(in) && !members.count(in.substr(1)) &&
             std::find(gn.inputs.begin(), gn.inputs.end(), in) == gn.inputs.end())
           gn.inputs.push_back(in);
-    int64_t t = 0, lock = 0, nest = 0;
-    attr_varint(first, "T", 6, &t);
+    int64_t st = 0, gt = 0, lock = 0, nest = 0;
+    dtypes(first, &st, &gt);
     attr_varint(first, "use_locking", 5, &lock);
     attr_varint(first, "use_nesterov", 5, &nest);
     gn.attrs = {{"N", attr_of_int(static_cast<int64_t>(grp.size()))},
-                {"T", attr_of_type(t)},
+                {"T", attr_of_type(st)},
+                {"Tgrad", attr_of_type(gt)},
                 {"use_locking", attr_of_bool(lock != 0)},
                 {"use_nesterov", attr_of_bool(nest != 0)}};
     // Control consumers of the members now depend on the group (the
@@ -681,7 +732,7 @@ int TFMA_OptimizeGraph(const void* graph_def, size_t graph_def_bytes,
   // reverse until a whole round changes nothing (at most 50 rounds).
   std::vector<const Pattern*> pats;
   for (const auto& p : kPatterns)
-    if (!pattern_disabled(disabled, p.name)) pats.push_back(&p);
+    if (!pattern_disabled(disabled, p)) pats.push_back(&p);
   std::stable_sort(pats.begin(), pats.end(),
                    [](const Pattern* a, const Pattern* b) { return a->priority > b->priority; });
   for (const Pattern* p : pats) {
@@ -692,7 +743,8 @@ int TFMA_OptimizeGraph(const void* graph_def, size_t graph_def_bytes,
       for (int i = n - 1; i >= 0; --i) changed += p->apply(&g, i) ? 1 : 0;
       if (p->apply == apply_bias_add_relu) local.bias_add_relu += changed;
       else if (p->apply == apply_add_v2_relu) local.add_v2_relu += changed;
-      else local.mul_add += changed;
+      else if (p->apply == apply_mul_add) local.mul_add += changed;
+      else local.adam_mixed += changed;
       if (!changed) break;
     }
   }

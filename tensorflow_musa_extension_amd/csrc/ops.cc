@@ -808,13 +808,29 @@ int check_adam_scalars(const TFMA_Tensor* const* sc, int dt, AdamScalars* out, D
   return TFMA_OK;
 }
 
+// mixed = false: var, m, v and grad share one dtype (ResourceApplyAdam).
+// mixed = true: fp32 var/m/v with a float, half or bfloat16 grad
+// (MusaResourceApplyAdamMixed, musa_applyadam_mixed_op.cc:160-183).
+// *dt / *gdt receive the state and gradient dtypes.
 int check_adam_triple(const TFMA_Tensor* var, const TFMA_Tensor* m, const TFMA_Tensor* v,
-                      const TFMA_Tensor* grad, int* dt, TFMA_Status* st) {
+                      const TFMA_Tensor* grad, bool mixed, int* dt, int* gdt,
+                      TFMA_Status* st) {
   if (!valid_tensor(var) || !valid_tensor(m) || !valid_tensor(v) || !valid_tensor(grad))
     return set_status(st, TFMA_INVALID_ARGUMENT, "ResourceApplyAdam: invalid tensor");
   if ((!var->data && num_elements(var) > 0) || (!m->data && num_elements(m) > 0) ||
       (!v->data && num_elements(v) > 0))
-    return set_status(st, TFMA_FAILED_PRECONDITION, "Adam variables (var/m/v) not initialized.");
+    return set_status(st, TFMA_FAILED_PRECONDITION,
+                      mixed ? "Mixed-precision Adam variables (var/m/v) not initialized."
+                            : "Adam variables (var/m/v) not initialized.");
+  if (mixed) {
+    const TFMA_Tensor* state[3] = {var, m, v};
+    static const char* names[3] = {"var", "m", "v"};
+    for (int i = 0; i < 3; ++i)
+      if (state[i]->dtype != TFMA_FLOAT)
+        return set_status(st, TFMA_INVALID_ARGUMENT,
+                          "MusaResourceApplyAdamMixed requires fp32 %s, got %s", names[i],
+                          dtype_name(state[i]->dtype));
+  }
   if (!same_shape(var, m))
     return set_status(st, TFMA_INVALID_ARGUMENT, "var and m must have the same shape. var: %s m: %s",
                       shape_str(var).c_str(), shape_str(m).c_str());
@@ -825,30 +841,32 @@ int check_adam_triple(const TFMA_Tensor* var, const TFMA_Tensor* m, const TFMA_T
     return set_status(st, TFMA_INVALID_ARGUMENT,
                       "var and grad must have the same shape. var: %s grad: %s",
                       shape_str(var).c_str(), shape_str(grad).c_str());
-  if (m->dtype != var->dtype || v->dtype != var->dtype || grad->dtype != var->dtype)
+  if (mixed) {
+    if (grad->dtype != TFMA_FLOAT && grad->dtype != TFMA_HALF && grad->dtype != TFMA_BFLOAT16)
+      return set_status(st, TFMA_INVALID_ARGUMENT,
+                        "MusaResourceApplyAdamMixed: grad dtype %s is not float, half or bfloat16",
+                        dtype_name(grad->dtype));
+  } else if (m->dtype != var->dtype || v->dtype != var->dtype || grad->dtype != var->dtype) {
     return set_status(st, TFMA_INVALID_ARGUMENT,
                       "ResourceApplyAdam: var, m, v and grad must have the same dtype");
+  }
   if (!grad->data && num_elements(grad) > 0)
     return set_status(st, TFMA_INVALID_ARGUMENT, "ResourceApplyAdam: grad data is null");
   *dt = var->dtype;
+  *gdt = grad->dtype;
   return TFMA_OK;
 }
 
-}  // namespace
-
-int TFMA_ResourceApplyAdam(void* stream, TFMA_Tensor* var, TFMA_Tensor* m, TFMA_Tensor* v,
-                           const TFMA_Tensor* beta1_power, const TFMA_Tensor* beta2_power,
-                           const TFMA_Tensor* lr, const TFMA_Tensor* beta1,
-                           const TFMA_Tensor* beta2, const TFMA_Tensor* epsilon,
-                           const TFMA_Tensor* grad, int use_locking, int use_nesterov,
-                           TFMA_Status* status) {
-  int dt = 0;
-  if (check_adam_triple(var, m, v, grad, &dt, status) != TFMA_OK) return status->code;
-  DType t;
-  if (!to_dtype(dt, &t))
-    return set_status(status, TFMA_UNIMPLEMENTED, "ResourceApplyAdam: dtype %s is not supported",
+int apply_adam(void* stream, TFMA_Tensor* var, TFMA_Tensor* m, TFMA_Tensor* v,
+               const TFMA_Tensor* const* sc, const TFMA_Tensor* grad, int use_locking,
+               int use_nesterov, bool mixed, const char* op, TFMA_Status* status) {
+  int dt = 0, gdt = 0;
+  if (check_adam_triple(var, m, v, grad, mixed, &dt, &gdt, status) != TFMA_OK)
+    return status->code;
+  DType t, tg;
+  if (!to_dtype(dt, &t) || !to_dtype(gdt, &tg))
+    return set_status(status, TFMA_UNIMPLEMENTED, "%s: dtype %s is not supported", op,
                       dtype_name(dt));
-  const TFMA_Tensor* sc[6] = {beta1_power, beta2_power, lr, beta1, beta2, epsilon};
   AdamScalars s;
   if (check_adam_scalars(sc, dt, &s, t, status) != TFMA_OK) return status->code;
   VarLocks locks;
@@ -861,9 +879,33 @@ int TFMA_ResourceApplyAdam(void* stream, TFMA_Tensor* var, TFMA_Tensor* m, TFMA_
   const int64_t n = num_elements(var);
   if (n == 0) return ok(status);
   return hip_status(status,
-                    LaunchApplyAdam(t, var->data, m->data, v->data, grad->data, n, s,
+                    LaunchApplyAdam(t, tg, var->data, m->data, v->data, grad->data, n, s,
                                     use_nesterov != 0, as_stream(stream)),
-                    "ResourceApplyAdam");
+                    op);
+}
+
+}  // namespace
+
+int TFMA_ResourceApplyAdam(void* stream, TFMA_Tensor* var, TFMA_Tensor* m, TFMA_Tensor* v,
+                           const TFMA_Tensor* beta1_power, const TFMA_Tensor* beta2_power,
+                           const TFMA_Tensor* lr, const TFMA_Tensor* beta1,
+                           const TFMA_Tensor* beta2, const TFMA_Tensor* epsilon,
+                           const TFMA_Tensor* grad, int use_locking, int use_nesterov,
+                           TFMA_Status* status) {
+  const TFMA_Tensor* sc[6] = {beta1_power, beta2_power, lr, beta1, beta2, epsilon};
+  return apply_adam(stream, var, m, v, sc, grad, use_locking, use_nesterov, false,
+                    "ResourceApplyAdam", status);
+}
+
+int TFMA_MusaResourceApplyAdamMixed(void* stream, TFMA_Tensor* var, TFMA_Tensor* m,
+                                    TFMA_Tensor* v, const TFMA_Tensor* beta1_power,
+                                    const TFMA_Tensor* beta2_power, const TFMA_Tensor* lr,
+                                    const TFMA_Tensor* beta1, const TFMA_Tensor* beta2,
+                                    const TFMA_Tensor* epsilon, const TFMA_Tensor* grad,
+                                    int use_locking, int use_nesterov, TFMA_Status* status) {
+  const TFMA_Tensor* sc[6] = {beta1_power, beta2_power, lr, beta1, beta2, epsilon};
+  return apply_adam(stream, var, m, v, sc, grad, use_locking, use_nesterov, true,
+                    "MusaResourceApplyAdamMixed", status);
 }
 
 int TFMA_GroupedApplyAdamWorkspaceBytes(int n, const TFMA_Tensor* vars, size_t* bytes,
@@ -884,20 +926,33 @@ int TFMA_GroupedResourceApplyAdam(void* stream, int n, TFMA_Tensor* vars, TFMA_T
                                   size_t workspace_bytes, TFMA_Status* status) {
   if (n < 1 || !vars || !ms || !vs || !grads)
     return set_status(status, TFMA_INVALID_ARGUMENT, "N must be >= 1");
-  int dt0 = 0;
+  // The gradients may be half or bfloat16 under fp32 state (the attr Tgrad
+  // of the grouped op, after MusaGroupedResourceApplyGradientDescentMixed's
+  // T/Tgrad pair, musa_applygradientdescent_op.cc:305-314).
+  const bool mixed = valid_tensor(&vars[0]) && valid_tensor(&grads[0]) &&
+                     vars[0].dtype == TFMA_FLOAT && grads[0].dtype != TFMA_FLOAT;
+  int dt0 = 0, gdt0 = 0;
   std::vector<AdamTensorEntry> table;
   table.reserve(n);
   int64_t chunks = 0;
   for (int i = 0; i < n; ++i) {
-    int dt = 0;
-    if (check_adam_triple(&vars[i], &ms[i], &vs[i], &grads[i], &dt, status) != TFMA_OK) {
+    int dt = 0, gdt = 0;
+    if (check_adam_triple(&vars[i], &ms[i], &vs[i], &grads[i], mixed, &dt, &gdt, status) !=
+        TFMA_OK) {
       std::string msg = status->message;
       return set_status(status, status->code, "tensor %d: %s", i, msg.c_str());
     }
-    if (i == 0) dt0 = dt;
+    if (i == 0) {
+      dt0 = dt;
+      gdt0 = gdt;
+    }
     if (dt != dt0)
       return set_status(status, TFMA_INVALID_ARGUMENT,
                         "tensor %d has dtype %s, expected %s", i, dtype_name(dt), dtype_name(dt0));
+    if (gdt != gdt0)
+      return set_status(status, TFMA_INVALID_ARGUMENT,
+                        "tensor %d has grad dtype %s, expected %s", i, dtype_name(gdt),
+                        dtype_name(gdt0));
     const int64_t ne = num_elements(&vars[i]);
     if (ne == 0) continue;
     AdamTensorEntry e;
@@ -910,8 +965,8 @@ int TFMA_GroupedResourceApplyAdam(void* stream, int n, TFMA_Tensor* vars, TFMA_T
     chunks += (ne + kGroupedAdamChunk - 1) / kGroupedAdamChunk;
     table.push_back(e);
   }
-  DType t;
-  if (!to_dtype(dt0, &t))
+  DType t, tg;
+  if (!to_dtype(dt0, &t) || !to_dtype(gdt0, &tg))
     return set_status(status, TFMA_UNIMPLEMENTED,
                       "MusaGroupedResourceApplyAdam: dtype %s is not supported", dtype_name(dt0));
   const TFMA_Tensor* sc[6] = {beta1_power, beta2_power, lr, beta1, beta2, epsilon};
@@ -937,7 +992,7 @@ int TFMA_GroupedResourceApplyAdam(void* stream, int n, TFMA_Tensor* vars, TFMA_T
   hipError_t e = pinned_ring().upload(workspace, table.data(),
                                       table.size() * sizeof(AdamTensorEntry), strm);
   if (e != hipSuccess) return hip_status(status, e, "MusaGroupedResourceApplyAdam table upload");
-  e = LaunchGroupedApplyAdam(t, static_cast<const AdamTensorEntry*>(workspace),
+  e = LaunchGroupedApplyAdam(t, tg, static_cast<const AdamTensorEntry*>(workspace),
                              static_cast<int>(table.size()), chunks, s, use_nesterov != 0,
                              strm);
   return hip_status(status, e, "MusaGroupedResourceApplyAdam");

@@ -45,7 +45,9 @@ struct AdamScalars {
   double alpha, beta1, beta2, epsilon, one_minus_beta1, one_minus_beta2;
 };
 
-hipError_t LaunchApplyAdam(DType t, void* var, void* m, void* v,
+// t: dtype of var/m/v; tg: dtype of grad (tg == t, or t = f32 with a f16 or
+// bf16 gradient).
+hipError_t LaunchApplyAdam(DType t, DType tg, void* var, void* m, void* v,
                            const void* grad, int64_t n, const AdamScalars& s,
                            bool nesterov, hipStream_t stream);
 
@@ -60,7 +62,7 @@ struct AdamTensorEntry {
 };
 constexpr int64_t kGroupedAdamChunk = 8192;  // elements per workgroup chunk
 
-hipError_t LaunchGroupedApplyAdam(DType t, const AdamTensorEntry* dev_table,
+hipError_t LaunchGroupedApplyAdam(DType t, DType tg, const AdamTensorEntry* dev_table,
                                   int n_tensors, int64_t total_chunks,
                                   const AdamScalars& s, bool nesterov,
                                   hipStream_t stream);

@@ -13,7 +13,9 @@ from . import _lib
 from .errors import raise_for_status
 
 PATTERNS = ("MusaBiasAddRelu", "MusaAddV2Relu", "MusaShiftedAffineMap",
-            "MusaGroupedResourceApplyAdam")
+            "MusaResourceApplyAdamMixed", "MusaGroupedResourceApplyAdam",
+            # the reference's names for two of them
+            "MusaShiftedAffineMapFusion", "MusaAdamMixedFusion")
 
 
 def optimize_graph_def(graph_def: bytes, fetch=(), device_filter=None, disabled_patterns=()):
@@ -24,7 +26,8 @@ def optimize_graph_def(graph_def: bytes, fetch=(), device_filter=None, disabled_
       rewritten (the reference uses "MUSA"); None rewrites every node.
     disabled_patterns: pattern names from PATTERNS to skip.
     Returns (serialized GraphDef, stats dict with the number of fused nodes per
-    pattern, grouped Adam nodes created and ResourceApplyAdam nodes grouped).
+    pattern, grouped Adam nodes created, Adam nodes grouped and Casts folded
+    into MusaResourceApplyAdamMixed).
     """
     lib = _lib.load()
     data = bytes(graph_def)

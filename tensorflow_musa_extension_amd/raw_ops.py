@@ -226,6 +226,18 @@ def ResourceApplyAdam(var, m, v, beta1_power, beta2_power, lr, beta1, beta2, eps
           int(bool(use_nesterov)), keep=(scal,))
 
 
+def MusaResourceApplyAdamMixed(var, m, v, beta1_power, beta2_power, lr, beta1, beta2, epsilon,
+                               grad, use_locking=False, use_nesterov=False):
+    """The reference's MusaResourceApplyAdamMixed: fp32 var/m/v updated in
+    place from a float, half or bfloat16 grad; float host scalars."""
+    scal = [host_scalar(s, torch.float32) for s in
+            (beta1_power, beta2_power, lr, beta1, beta2, epsilon)]
+    dvar, dm, dv, dg = _desc(var, "var"), _desc(m, "m"), _desc(v, "v"), _desc(grad, "grad")
+    _call("TFMA_MusaResourceApplyAdamMixed", _stream(var), _ref(dvar), _ref(dm), _ref(dv),
+          *[_ref(s[1]) for s in scal], _ref(dg), int(bool(use_locking)),
+          int(bool(use_nesterov)), keep=(scal,))
+
+
 def _tensor_array(ts, name):
     arr = (_lib.TFMA_Tensor * len(ts))()
     for i, t in enumerate(ts):
@@ -237,7 +249,8 @@ def MusaGroupedResourceApplyAdam(vars, ms, vs, grads, beta1_power, beta2_power, 
                                  beta2, epsilon, use_locking=False, use_nesterov=False,
                                  workspace=None):
     """N ResourceApplyAdam updates with shared scalars in one launch
-    (inputs vars/ms/vs/grads: N tensors each)."""
+    (inputs vars/ms/vs/grads: N tensors each).  With float32 vars the grads
+    may all be float16 or bfloat16 (mixed precision)."""
     n = len(vars)
     if not (len(ms) == len(vs) == len(grads) == n) or n < 1:
         raise ValueError("vars, ms, vs, grads must be non-empty lists of equal length")

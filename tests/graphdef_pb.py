@@ -80,7 +80,7 @@ class G:
                 a.b = v
             elif isinstance(v, str):
                 a.s = v.encode()
-            elif k in ("T", "dtype", "Tgrad", "U"):
+            elif k in ("T", "dtype", "Tgrad", "U", "SrcT", "DstT"):
                 a.type = v
             else:
                 a.i = v

@@ -144,6 +144,32 @@ def test_adam_validation():
     assert code == _lib.UNIMPLEMENTED
 
 
+def test_adam_mixed_validation():
+    """MusaResourceApplyAdamMixed's checks and messages
+    (musa_applyadam_mixed_op.cc:160-207); nothing reaches the device."""
+    _, descs = scalars()
+    mixed = lambda var, m, v, g: call("TFMA_MusaResourceApplyAdamMixed", None, ref(var), ref(m),
+                                      ref(v), *[ref(d) for d in descs], ref(g), 0, 0)
+    f, h = T((4, 3)), T((4, 3), _lib.DT_HALF)
+    code, msg = mixed(T((4, 3), ptr=None), f, f, h)
+    assert code == _lib.FAILED_PRECONDITION
+    assert msg == "Mixed-precision Adam variables (var/m/v) not initialized."
+    code, msg = mixed(h, f, f, h)
+    assert code == _lib.INVALID_ARGUMENT and msg == "MusaResourceApplyAdamMixed requires fp32 var, got half"
+    code, msg = mixed(f, T((4, 3), _lib.DT_BFLOAT16), f, h)
+    assert msg == "MusaResourceApplyAdamMixed requires fp32 m, got bfloat16"
+    code, msg = mixed(f, f, T((4, 3), _lib.DT_DOUBLE), h)
+    assert msg == "MusaResourceApplyAdamMixed requires fp32 v, got double"
+    code, msg = mixed(f, f, f, T((4, 2), _lib.DT_HALF))
+    assert msg == "var and grad must have the same shape. var: [4,3] grad: [4,2]"
+    code, msg = mixed(f, f, f, T((4, 3), _lib.DT_INT32))
+    assert code == _lib.INVALID_ARGUMENT and "grad dtype int32" in msg
+    hd = scalars(dtype=_lib.DT_HALF)[1]
+    code, msg = call("TFMA_MusaResourceApplyAdamMixed", None, ref(f), ref(f), ref(f),
+                     *[ref(d) for d in hd], ref(h), 0, 0)
+    assert code == _lib.INVALID_ARGUMENT and msg == "beta1_power has dtype half, expected float"
+
+
 def test_adam_locking_is_deadlock_free():
     """Concurrent use_locking calls over overlapping var/m/v sets in every
     order complete (locks are taken in address order).  Empty tensors make

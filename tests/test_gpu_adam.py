@@ -155,3 +155,123 @@ def test_adam_errors(dev):
         ops.ResourceApplyAdam(a, b, a.clone(), 0.9, 0.999, LR, B1, B2, EPS, a.clone())
     with pytest.raises(tfma.InvalidArgumentError, match="var and grad must have the same shape"):
         ops.ResourceApplyAdam(a, a.clone(), a.clone(), 0.9, 0.999, LR, B1, B2, EPS, b)
+
+
+# ---------------------------------------------------------------------------
+# Mixed precision: fp32 var/m/v, half / bfloat16 / float grad
+# ---------------------------------------------------------------------------
+def _mixed_case(dev, rng, n, gdt, offset=0):
+    var = gen(rng, n + offset, "float32", scale=0.02)
+    m = oracle.to_storage(np.abs(1e-4 * rng.standard_normal(n + offset)), "float32")
+    v = oracle.to_storage(np.abs(1e-4 * rng.standard_normal(n + offset)), "float32")
+    dev_t = [to_dev(a, "float32", dev)[offset:] for a in (var, m, v)]
+    return dev_t, [var[offset:].copy(), m[offset:].copy(), v[offset:].copy()]
+
+
+@pytest.mark.parametrize("gdt", ["float16", "bfloat16", "float32"])
+@pytest.mark.parametrize("nesterov", [False, True])
+@pytest.mark.parametrize("n,offset", [(1, 0), (5, 0), (65537, 0), (10007, 1), (1 << 20, 0)])
+def test_adam_mixed_bitwise(dev, gdt, nesterov, n, offset):
+    rng = np.random.default_rng(n + offset)
+    (tv, tm, tw), (rv, rm, rw) = _mixed_case(dev, rng, n, gdt, offset)
+    b1p, b2p = 1.0, 1.0
+    for _ in range(3):
+        b1p, b2p = _t_scalar(b1p * B1, "float32"), _t_scalar(b2p * B2, "float32")
+        g = gen(rng, n + offset, gdt, scale=1e-3)[offset:]
+        gd = to_dev(g, gdt, dev)
+        ops.MusaResourceApplyAdamMixed(tv, tm, tw, b1p, b2p, LR, B1, B2, EPS, gd,
+                                       use_nesterov=nesterov)
+        oracle.adam_mixed(rv, rm, rw, np.ascontiguousarray(g), b1p, b2p, _t_scalar(LR, "float32"),
+                          _t_scalar(B1, "float32"), _t_scalar(B2, "float32"),
+                          _t_scalar(EPS, "float32"), use_nesterov=nesterov, grad_dtype=gdt)
+    torch.cuda.synchronize()
+    for name, t, r in (("var", tv, rv), ("m", tm, rm), ("v", tw, rw)):
+        assert_bitwise(to_np(t, "float32"), r, f"mixed {gdt} {name}")
+
+
+def test_adam_mixed_equals_cast_then_fp32_adam(dev):
+    """The mixed op is exactly Cast(grad, float) followed by fp32 Adam."""
+    rng = np.random.default_rng(9)
+    n = 300001
+    (tv, tm, tw), _ = _mixed_case(dev, rng, n, "bfloat16")
+    cv, cm, cw = tv.clone(), tm.clone(), tw.clone()
+    g = to_dev(gen(rng, n, "bfloat16", scale=1e-3), "bfloat16", dev)
+    ops.MusaResourceApplyAdamMixed(tv, tm, tw, 0.81, 0.998, LR, B1, B2, EPS, g)
+    ops.ResourceApplyAdam(cv, cm, cw, 0.81, 0.998, LR, B1, B2, EPS, g.float())
+    torch.cuda.synchronize()
+    for a, b in ((tv, cv), (tm, cm), (tw, cw)):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+@pytest.mark.parametrize("gdt", ["float16", "bfloat16"])
+def test_grouped_mixed_equals_single_mixed_and_oracle(dev, gdt):
+    rng = np.random.default_rng(4)
+    shapes = [(64,), (3, 3, 64, 64), (1000, 2048), (7,), (0,), (8193,)]
+    vars_, ms, vs, grads, refs = [], [], [], [], []
+    for s in shapes:
+        n = int(np.prod(s))
+        (tv, tm, tw), ref = _mixed_case(dev, rng, n, gdt)
+        vars_.append(tv)
+        ms.append(tm)
+        vs.append(tw)
+        refs.append(ref)
+        grads.append(to_dev(gen(rng, n, gdt, scale=1e-3), gdt, dev))
+    single = [(v.clone(), m.clone(), w.clone()) for v, m, w in zip(vars_, ms, vs)]
+    ops.MusaGroupedResourceApplyAdam(vars_, ms, vs, grads, 0.729, 0.997, LR, B1, B2, EPS)
+    for (v, m, w), g in zip(single, grads):
+        ops.MusaResourceApplyAdamMixed(v, m, w, 0.729, 0.997, LR, B1, B2, EPS, g)
+    torch.cuda.synchronize()
+    for i, (v, m, w) in enumerate(zip(vars_, ms, vs)):
+        rv, rm, rw = refs[i]
+        oracle.adam_mixed(rv, rm, rw, to_np(grads[i], gdt), _t_scalar(0.729, "float32"),
+                          _t_scalar(0.997, "float32"), _t_scalar(LR, "float32"),
+                          _t_scalar(B1, "float32"), _t_scalar(B2, "float32"),
+                          _t_scalar(EPS, "float32"), grad_dtype=gdt)
+        for name, a, b, r in (("var", v, single[i][0], rv), ("m", m, single[i][1], rm),
+                              ("v", w, single[i][2], rw)):
+            assert_bitwise(to_np(a, "float32"), to_np(b, "float32"), f"tensor {i} {name} vs single")
+            assert_bitwise(to_np(a, "float32"), r, f"tensor {i} {name} vs oracle")
+
+
+def test_grouped_mixed_rejects_mixed_grad_dtypes(dev):
+    f32 = dict(dtype=torch.float32, device=dev)
+    vs = [torch.zeros(8, **f32) for _ in range(2)]
+    grads = [torch.zeros(8, dtype=torch.float16, device=dev),
+             torch.zeros(8, dtype=torch.bfloat16, device=dev)]
+    with pytest.raises(tfma.InvalidArgumentError, match="grad dtype bfloat16, expected half"):
+        ops.MusaGroupedResourceApplyAdam(vs, [v.clone() for v in vs], [v.clone() for v in vs],
+                                         grads, 0.9, 0.999, LR, B1, B2, EPS)
+
+
+def test_grouped_adam_cfg5_sampled(dev):
+    """cfg5: 145 fp32 tensors, 1.31B parameters (21 GB of state), one grouped
+    step.  Every 1009th element of every tensor, and the whole of one
+    [2048,2048] tensor, is checked bitwise against the oracle on the same
+    inputs (copied to the host before the step)."""
+    from bench import cfg5_shapes
+    shapes = cfg5_shapes()
+    assert len(shapes) == 145 and sum(int(np.prod(s)) for s in shapes) == 1_310_982_144
+    gen_ = torch.Generator(device=dev)
+    gen_.manual_seed(5)
+    tv = [0.02 * torch.randn(s, generator=gen_, device=dev) for s in shapes]
+    tm = [(1e-4 * torch.randn(s, generator=gen_, device=dev)).abs_() for s in shapes]
+    tw = [(1e-4 * torch.randn(s, generator=gen_, device=dev)).abs_() for s in shapes]
+    tg = [1e-3 * torch.randn(s, generator=gen_, device=dev) for s in shapes]
+    k, whole = 1009, 7
+
+    def sample(ts, i):
+        return ts[i].reshape(-1).cpu().numpy().copy() if i == whole else \
+            ts[i].reshape(-1)[::k].cpu().numpy().copy()
+
+    before = [[sample(ts, i) for ts in (tv, tm, tw, tg)] for i in range(len(shapes))]
+    b1p, b2p = _t_scalar(B1 ** 4, "float32"), _t_scalar(B2 ** 4, "float32")
+    ops.MusaGroupedResourceApplyAdam(tv, tm, tw, tg, b1p, b2p, LR, B1, B2, EPS)
+    torch.cuda.synchronize()
+    for i in range(len(shapes)):
+        rv, rm, rw, rg = before[i]
+        oracle.adam(rv, rm, rw, rg, b1p, b2p, _t_scalar(LR, "float32"), _t_scalar(B1, "float32"),
+                    _t_scalar(B2, "float32"), _t_scalar(EPS, "float32"))
+        for name, ts, r in (("var", tv, rv), ("m", tm, rm), ("v", tw, rw)):
+            assert_bitwise(sample(ts, i), r, f"cfg5 tensor {i} {name}")
+    del tv, tm, tw, tg
+    torch.cuda.empty_cache()

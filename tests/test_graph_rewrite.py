@@ -395,3 +395,89 @@ def test_random_graphs_keep_values(seed):
     removed = len(g.gd.node) - len(gd.node)
     assert removed == stats["bias_add_relu"] + stats["add_v2_relu"] + stats["mul_add"]
     assert optimize_graph_def(gd.SerializeToString(), fetch=fetch)[1]["bias_add_relu"] == 0
+
+
+# ---------------------------------------------------------------------------
+# Cast folding into MusaResourceApplyAdamMixed (reference MusaAdamMixedFusion)
+# ---------------------------------------------------------------------------
+DT_BF16 = 14
+
+
+def mixed_graph(n, src=DT_HALF, dst=DT_FLOAT, t=DT_FLOAT, extra_cast_consumer=False):
+    g = G()
+    for s in SCALARS:
+        g.node(s, "Const", dtype=DT_FLOAT)
+    for i in range(n):
+        for r in ("var", "m", "v"):
+            g.node(f"{r}{i}", "VarHandleOp", dtype=DT_FLOAT)
+        g.node(f"g{i}", "Placeholder", dtype=src)
+        g.node(f"cast{i}", "Cast", [f"g{i}", "^init"] if i == 0 else [f"g{i}"], SrcT=src, DstT=dst)
+    g.node("init", "NoOp")
+    for i in range(n):
+        g.node(f"adam{i}", "ResourceApplyAdam",
+               [f"var{i}", f"m{i}", f"v{i}"] + SCALARS + [f"cast{i}"],
+               T=t, use_locking=False, use_nesterov=False)
+    if extra_cast_consumer:
+        g.node("probe", "Identity", ["cast0"], T=dst)
+    return g
+
+
+def test_cast_folded_into_mixed_adam():
+    gd, stats = run(mixed_graph(1), disabled_patterns=["MusaGroupedResourceApplyAdam"])
+    check_well_formed(gd)
+    a = nodes(gd)["adam0"]
+    assert a.op == "MusaResourceApplyAdamMixed" and a.attr["T"].type == DT_HALF
+    assert list(a.input) == ["var0", "m0", "v0"] + SCALARS + ["g0", "^init"]
+    assert "cast0" not in nodes(gd) and stats["adam_mixed"] == 1
+
+
+def test_cast_with_other_consumer_is_kept():
+    gd, stats = run(mixed_graph(1, src=DT_BF16, extra_cast_consumer=True))
+    a = nodes(gd)["adam0"]
+    assert a.op == "MusaResourceApplyAdamMixed" and a.attr["T"].type == DT_BF16
+    assert a.input[9] == "g0" and "cast0" in nodes(gd)
+    assert list(nodes(gd)["probe"].input) == ["cast0"]
+
+
+@pytest.mark.parametrize("kw", [dict(src=DT_FLOAT), dict(dst=DT_HALF), dict(t=DT_HALF),
+                                dict(src=DT_DOUBLE)])
+def test_cast_folding_negative(kw):
+    gd, stats = run(mixed_graph(1, **kw))
+    assert nodes(gd)["adam0"].op == "ResourceApplyAdam" and stats["adam_mixed"] == 0
+
+
+def test_cast_folding_disabled_by_reference_name_and_filter():
+    for kw in (dict(disabled_patterns=["MusaAdamMixedFusion"]),
+               dict(disabled_patterns=["MusaResourceApplyAdamMixed"]),
+               dict(device_filter="GPU")):
+        gd, stats = run(mixed_graph(1), **kw)
+        assert stats["adam_mixed"] == 0, kw
+    gd, stats = run(mixed_graph(1), fetch=["cast0"],
+                    disabled_patterns=["MusaGroupedResourceApplyAdam"])
+    assert nodes(gd)["adam0"].op == "MusaResourceApplyAdamMixed" and "cast0" in nodes(gd)
+
+
+def test_mixed_adam_nodes_grouped_with_tgrad():
+    gd, stats = run(mixed_graph(4))
+    check_well_formed(gd)
+    grp = [n for n in gd.node if n.op == "MusaGroupedResourceApplyAdam"]
+    assert len(grp) == 1 and stats["adam_mixed"] == 4 and stats["adam_grouped_nodes"] == 4
+    gn = grp[0]
+    assert gn.attr["T"].type == DT_FLOAT and gn.attr["Tgrad"].type == DT_HALF
+    assert list(gn.input)[-5:] == ["g0", "g1", "g2", "g3", "^init"]
+    assert not [n for n in gd.node if n.op == "Cast"]
+
+
+def test_plain_and_mixed_adam_are_separate_groups():
+    g = mixed_graph(2)
+    for i in range(2, 4):
+        for r in ("var", "m", "v"):
+            g.node(f"{r}{i}", "VarHandleOp", dtype=DT_FLOAT)
+        g.node(f"g{i}", "Placeholder", dtype=DT_FLOAT)
+        g.node(f"adam{i}", "ResourceApplyAdam", [f"var{i}", f"m{i}", f"v{i}"] + SCALARS + [f"g{i}"],
+               T=DT_FLOAT, use_locking=False, use_nesterov=False)
+    gd, stats = run(g)
+    check_well_formed(gd)
+    grp = sorted((n.attr["Tgrad"].type, n.attr["N"].i) for n in gd.node
+                 if n.op == "MusaGroupedResourceApplyAdam")
+    assert grp == [(DT_FLOAT, 2), (DT_HALF, 2)]

@@ -305,6 +305,32 @@ def test_adam_first_step_closed_form():
         np.testing.assert_array_equal(var[:4], var0[:4])
 
 
+@pytest.mark.parametrize("gdt", ["float16", "bfloat16"])
+def test_adam_mixed_first_step_closed_form(gdt):
+    """fp32 state with a 16-bit grad: the first step from m = v = 0 in float64
+    from the 16-bit grad's exact value (m = g(1-b1), v = g^2(1-b2), var -=
+    alpha*m/(sqrt(v)+eps)).  A grad rounded to anything coarser than its own
+    value, or a state rounded to 16 bits, misses the float32-level bound."""
+    rng = np.random.default_rng(43)
+    n = 4096
+    g = oracle.to_storage(1e-3 * rng.standard_normal(n), gdt)
+    var0 = (0.02 * rng.standard_normal(n)).astype(np.float32)
+    var, m, v = var0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    f = lambda a: np.float64(np.float32(a))
+    b1, b2, lr, eps = 0.9, 0.999, 1e-3, 1e-7
+    oracle.adam_mixed(var, m, v, g, f(b1), f(b2), f(lr), f(b1), f(b2), f(eps), grad_dtype=gdt)
+    gd = oracle.to_f32(g, gdt).astype(np.float64)
+    m1 = gd * (1 - f(b1))
+    v1 = gd * gd * (1 - f(b2))
+    alpha = f(lr) * np.sqrt(1 - f(b2)) / (1 - f(b1))
+    var1 = var0 - alpha * m1 / (np.sqrt(v1) + f(eps))
+    np.testing.assert_allclose(m, m1, rtol=2e-7, atol=0)
+    np.testing.assert_allclose(v, v1, rtol=5e-7, atol=0)
+    upd = np.max(np.abs(var1 - var0))
+    bound = 2e-6 * upd + np.spacing(np.abs(var1).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(var - var1) <= bound)
+
+
 @pytest.mark.parametrize("dtype,tol", [("float16", 2e-3), ("bfloat16", 1.6e-2),
                                        ("float64", 1e-12)])
 def test_adam_other_dtypes_vs_f64(dtype, tol):
