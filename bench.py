@@ -14,11 +14,13 @@ value = algorithmic bytes per step (fwd 2*s*E + grad 3*s*E per pair) x steps
 roofline: the dominant kernel (tfma_bn_grad_fused: reads x, dy, writes dx,
         3*s*E bytes per launch) timed with HIP events recorded on its
         stream around each of its launches inside the timed region.
-cpu_baseline: the TF-CPU restatement (oracle/, C + OpenMP) on one float16
-        fwd+grad pass over the four shapes, on the host's cores.
-components: the other north-star kernels (Adam, grouped Adam, elementwise
-        chains) at their config shapes, each rep timed with HIP events after
-        a 1 GiB read that evicts the Infinity Cache.
+cpu_baseline: the TF-CPU restatement (oracle/, C + OpenMP) on the same
+        BN workload (both dtypes, four shapes), repeated for >= 10 s on up to
+        16 host cores.
+components: the other kernels (Adam, mixed-precision Adam, grouped Adam at
+        the ResNet-50 and 1.31e9-parameter configs, the elementwise chains,
+        ReluGrad, BiasAddGrad) at their config shapes, each rep timed with HIP
+        events after a 1 GiB read that evicts the Infinity Cache.
 """
 import argparse
 import json
@@ -232,6 +234,11 @@ def components(torch, ops, dev):
         bo = torch.randn(4095, generator=gen, device=dev).to(dt)
         out[f"bias_add_relu_{name}_8191x4095"] = rate([ops.bind(ops.MusaBiasAddRelu, xo, bo)],
                                                       2 * s * xo.numel() + s * 4095)
+        # The backward side of the chains: ReluGrad (2 reads, 1 write) and
+        # BiasAddGrad (one read of the gradient).
+        out[f"relu_grad_{name}_8192x4096"] = rate([ops.bind(ops.ReluGrad, a_full, x)], 3 * s * E)
+        out[f"bias_add_grad_{name}_8192x4096"] = rate([ops.bind(ops.BiasAddGrad, a_full)],
+                                                      s * E + s * 4096)
         del x, b, a_full, b_full, xo, bo
     torch.cuda.synchronize()
     del flush

@@ -221,6 +221,31 @@ int TFMA_AddV2(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* y,
 int TFMA_Mul(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* y,
              TFMA_Tensor* z, TFMA_Status* status);
 
+/* ReluGrad: backprops = gradients * (features > 0), a multiply as in TF's
+ * CPU kernel (a NaN or infinite gradient at features <= 0 gives NaN; a
+ * negative one gives -0).  Replaces MusaReluGradOp<T>::Compute
+ * (reference: musa_ext/kernels/nn/musa_relu_grad_op.cc:10-61, registered
+ * :51-57 for float, half, bfloat16), including its same-shape check and
+ * message.  Also takes double. */
+int TFMA_ReluGrad(void* stream, const TFMA_Tensor* gradients, const TFMA_Tensor* features,
+                  TFMA_Tensor* backprops, TFMA_Status* status);
+
+/* BiasAddGrad: output[c] = sum of out_backprop over every dimension except
+ * the channel one (the last for "NHWC", dimension 1 for "NCHW" when rank >=
+ * 2).  Replaces MusaBiasAddGradOp<T>::Compute
+ * (reference: musa_ext/kernels/nn/musa_biasadd_grad_op.cc:24-110,
+ * registered :112-123) for T in {FLOAT, HALF, BFLOAT16, DOUBLE, INT32,
+ * INT64}: rank 1 is returned as is (:50-58), an empty reduction gives zeros
+ * (:64-69).  Half and bfloat16 accumulate in float (as TF's CPU kernel);
+ * integers wrap.  The sum runs in a fixed order (deterministic) in two
+ * kernels; `workspace` holds the per-group partials
+ * (TFMA_BiasAddGradWorkspaceBytes). */
+int TFMA_BiasAddGradWorkspaceBytes(const TFMA_Tensor* out_backprop, const char* data_format,
+                                   size_t* bytes, TFMA_Status* status);
+int TFMA_BiasAddGrad(void* stream, const TFMA_Tensor* out_backprop, const char* data_format,
+                     TFMA_Tensor* output, void* workspace, size_t workspace_bytes,
+                     TFMA_Status* status);
+
 /* Fused Relu(BiasAdd(value, bias)).  No live reference op: the reference
  * runs BiasAdd then Relu (musa_biasadd_op.cc:10-70, musa_relu_op.cc:10-62);
  * its only fused kernel, BiasAddReluKernel

@@ -16,7 +16,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liboracle.so")
 DT = {"float32": 1, "float64": 2, "bfloat16": 14, "float16": 19}
-EW_OPS = {"add": 0, "add_relu": 1, "mul": 2, "mul_add": 3, "relu": 4}
+EW_OPS = {"add": 0, "add_relu": 1, "mul": 2, "mul_add": 3, "relu": 4, "relu_grad": 5}
 
 _lib = None
 
@@ -38,6 +38,7 @@ def load():
     lib.oracle_bn_grad.argtypes = [i, i, vp, vp, i64, i64, i64, vp, vp, vp, f, i, vp, vp, vp]
     lib.oracle_adam.argtypes = [i, vp, vp, vp, vp, i64, d, d, d, d, d, d, i]
     lib.oracle_eltwise.argtypes = [i, i, i, vp, vp, vp, i, vp, vp]
+    lib.oracle_bias_add_grad.argtypes = [i, vp, i64, i64, i64, vp]
     lib.oracle_set_threads.argtypes = [i]
     lib.oracle_get_threads.restype = i
     lib.oracle_f32_to_f16.argtypes = [f]
@@ -49,6 +50,7 @@ def load():
     lib.oracle_bf16_to_f32.argtypes = [ctypes.c_uint16]
     lib.oracle_bf16_to_f32.restype = f
     for fn in ("oracle_bn_fwd", "oracle_bn_grad", "oracle_adam", "oracle_eltwise",
+               "oracle_bias_add_grad",
                "oracle_set_threads"):
         getattr(lib, fn).restype = None
     _lib = lib
@@ -181,9 +183,28 @@ def adam_mixed(var, m, v, grad, beta1_power, beta2_power, lr, beta1, beta2, epsi
          use_nesterov=use_nesterov, dtype="float32")
 
 
+def bias_add_grad(x, data_format="NHWC", dtype="float32"):
+    """TF-CPU BiasAddGrad: sum over every dimension but the channel one (last
+    for NHWC, 1 for NCHW); floating types in double, rounded once to T;
+    int32/int64 wrap.  A rank-1 input is returned as is (the reference's
+    identity case, musa_biasadd_grad_op.cc:52-58)."""
+    x = np.ascontiguousarray(x)
+    if x.ndim == 1:
+        return x.copy()
+    cd = 1 if data_format.startswith("NC") else x.ndim - 1
+    c = x.shape[cd]
+    outer = int(np.prod(x.shape[:cd]))
+    inner = int(np.prod(x.shape[cd + 1:]))
+    out = np.zeros(c, dtype=x.dtype)
+    codes = dict(DT, int32=3, int64=9)
+    load().oracle_bias_add_grad(codes[dtype], _p(x), outer, c, inner, _p(out))
+    return out
+
+
 def eltwise(op, inputs, dtype="float32"):
     """TF-CPU elementwise op with broadcasting: add, add_relu, mul, mul_add
-    (inputs[0]*inputs[1] rounded, + inputs[2]) or relu."""
+    (inputs[0]*inputs[1] rounded, + inputs[2]), relu, or relu_grad
+    (inputs[0] = gradients, inputs[1] = features)."""
     lib = load()
     ins = [_c(a) for a in inputs]
     out_shape = np.broadcast_shapes(*[a.shape for a in ins])

@@ -346,7 +346,10 @@ void oracle_adam(int dt, void* var, void* m, void* v, const void* grad, int64_t 
 }
 
 /* Elementwise ops with TF broadcasting.  op: 0 add, 1 add+relu, 2 mul,
- * 3 mul+add (in0*in1 rounded, + in2), 4 relu.  Each input i has rank
+ * 3 mul+add (in0*in1 rounded, + in2), 4 relu, 5 relu grad (in0 = gradients,
+ * in1 = features: gradients * (features > 0), TF's ReluGrad as a multiply,
+ * so a NaN or infinite gradient at features <= 0 gives NaN and a negative
+ * gradient gives -0).  Each input i has rank
  * in_ndims[i] <= 8 and dims in_dims[8*i ...]; out has rank out_ndims. */
 void oracle_eltwise(int dt, int op, int nin, const void* const* ins, const int64_t* in_dims,
                     const int* in_ndims, int out_ndims, const int64_t* out_dims, void* out) {
@@ -380,6 +383,7 @@ void oracle_eltwise(int dt, int op, int nin, const void* const* ins, const int64
       case 1: r = rnd(dt, a + ld(dt, ins[1], off[1])); r = r < 0.f ? 0.f : r; break;
       case 2: r = a * ld(dt, ins[1], off[1]); break;
       case 3: r = rnd(dt, a * ld(dt, ins[1], off[1])) + ld(dt, ins[2], off[2]); break;
+      case 5: r = a * (ld(dt, ins[1], off[1]) > 0.f ? 1.f : 0.f); break;
       default: r = a < 0.f ? 0.f : a; break;
     }
     if (op == 4 && !(a < 0.f)) {
@@ -389,5 +393,40 @@ void oracle_eltwise(int dt, int op, int nin, const void* const* ins, const int64
     } else {
       st(dt, out, i, r);
     }
+  }
+}
+
+/* BiasAddGrad: out[c] = sum of x over every dimension except the channel
+ * dimension (the last for NHWC, 1 for NCHW; reference
+ * musa_ext/kernels/nn/musa_biasadd_grad_op.cc:31-52).  x is viewed as
+ * [outer, C, inner].  Floating types are summed in double and rounded once to
+ * T (TF sums half/bfloat16 in float, float in float, in Eigen's order);
+ * int32 / int64 wrap modulo 2^32 / 2^64 as TF's integer sum does. */
+void oracle_bias_add_grad(int dt, const void* x, int64_t outer, int64_t c, int64_t inner,
+                          void* out) {
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+#endif
+  for (int64_t ch = 0; ch < c; ++ch) {
+    if (dt == 3 || dt == 9) {
+      uint64_t acc = 0;
+      for (int64_t o = 0; o < outer; ++o)
+        for (int64_t k = 0; k < inner; ++k) {
+          const int64_t idx = (o * c + ch) * inner + k;
+          acc += dt == 3 ? (uint64_t)(int64_t)((const int32_t*)x)[idx]
+                         : (uint64_t)((const int64_t*)x)[idx];
+        }
+      if (dt == 3) ((int32_t*)out)[ch] = (int32_t)(uint32_t)acc;
+      else ((int64_t*)out)[ch] = (int64_t)acc;
+      continue;
+    }
+    double acc = 0.0;
+    for (int64_t o = 0; o < outer; ++o)
+      for (int64_t k = 0; k < inner; ++k) {
+        const int64_t idx = (o * c + ch) * inner + k;
+        acc += dt == DT_DOUBLE ? ((const double*)x)[idx] : (double)ld(dt, x, idx);
+      }
+    if (dt == DT_DOUBLE) ((double*)out)[ch] = acc;
+    else st(dt, out, ch, (float)acc);
   }
 }

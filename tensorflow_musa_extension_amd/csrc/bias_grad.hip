@@ -1,0 +1,285 @@
+// BiasAddGrad for gfx950: the per-channel sum of out_backprop over every
+// dimension but the channel one (reference op:
+// musa_ext/kernels/nn/musa_biasadd_grad_op.cc:24-110, channel dimension
+// :31-40; TF-CPU semantics: half and bfloat16 accumulate in float, float in
+// float, double in double, int32/int64 wrap).
+//
+// x is viewed as [outer, C, inner]: inner = 1 for NHWC (and any rank with the
+// channel last), inner = H*W... for NCHW.
+//   stage 1, inner == 1 ("rows"): workgroup (g, tile) sums a range of rows for
+//            a tile of channel vectors - lanes along 16-byte channel vectors,
+//            so a wave reads whole row segments - then the rows of the
+//            workgroup through LDS; one partial per (g, channel).
+//   stage 1, inner > 1 ("planes"): workgroup (g, channel) sums the channel's
+//            planes of a range of images; one partial per (g, channel).
+//   stage 2: per channel, the partials in group order, cast to T.
+// Every sum runs in a fixed order, so results are deterministic.  Memory:
+// one read of x (s*E bytes), partials of G*C accumulators.
+#include "device_util.h"
+#include "tfma_internal.h"
+
+namespace tfma {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 8;
+
+// Per dtype: storage type S, accumulator A, the widening load and the
+// final conversion back to S.
+template <typename TS, typename TA>
+struct Plain {
+  using S = TS;
+  using A = TA;
+  __device__ static A ld(S s) { return static_cast<A>(s); }
+  __device__ static S out(A a) { return static_cast<S>(a); }
+};
+using BagF32 = Plain<float, float>;
+using BagF64 = Plain<double, double>;
+using BagI32 = Plain<int32_t, uint32_t>;  // wraps modulo 2^32 like TF's int32 sum
+using BagI64 = Plain<int64_t, uint64_t>;
+template <class Tr>
+struct Narrow {  // half / bfloat16, accumulated in float
+  using S = uint16_t;
+  using A = float;
+  __device__ static A ld(S s) { return Tr::ld(s); }
+  __device__ static S out(A a) { return Tr::st(a); }
+};
+using BagF16 = Narrow<TF16>;
+using BagBF16 = Narrow<TBF16>;
+
+template <class B, int VEC>
+__global__ __launch_bounds__(kThreads) void bag_rows_kernel(
+    const typename B::S* __restrict__ x, int64_t rows, int c, int64_t cv, int tx_shift,
+    int64_t rows_per_g, typename B::A* __restrict__ partial) {
+  using S = typename B::S;
+  using A = typename B::A;
+  extern __shared__ unsigned char bag_lds[];
+  A* red = reinterpret_cast<A*>(bag_lds);  // [ry][tx * VEC]
+  const int tx = threadIdx.x & ((1 << tx_shift) - 1);
+  const int ty = threadIdx.x >> tx_shift;
+  const int ry = kThreads >> tx_shift;
+  const int width = (1 << tx_shift) * VEC;
+  const int64_t cvi = static_cast<int64_t>(blockIdx.y) * (1 << tx_shift) + tx;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_g;
+  int64_t r1 = r0 + rows_per_g;
+  if (r1 > rows) r1 = rows;
+  A acc[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) acc[j] = A(0);
+  if (cvi < cv) {
+    const S* __restrict__ p = x + cvi * VEC;
+    int64_t r = r0 + ty;
+    for (; r + (kUnroll - 1) * ry < r1; r += kUnroll * ry) {
+      S v[kUnroll][VEC];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) vload<S, VEC>(p + (r + u * ry) * c, v[u]);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[j] += B::ld(v[u][j]);
+    }
+    for (; r < r1; r += ry) {
+      S v[VEC];
+      vload<S, VEC>(p + r * c, v);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc[j] += B::ld(v[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) red[ty * width + tx * VEC + j] = acc[j];
+  __syncthreads();
+  const int64_t ch = static_cast<int64_t>(blockIdx.y) * width + threadIdx.x;
+  if (static_cast<int>(threadIdx.x) < width && ch < c) {
+    A s = A(0);
+    for (int k = 0; k < ry; ++k) s += red[k * width + threadIdx.x];
+    partial[static_cast<int64_t>(blockIdx.x) * c + ch] = s;
+  }
+}
+
+template <class B>
+__global__ __launch_bounds__(kThreads) void bag_planes_kernel(
+    const typename B::S* __restrict__ x, int64_t outer, int c, int64_t inner,
+    int64_t outer_per_g, FastDiv div_inner, typename B::A* __restrict__ partial) {
+  using S = typename B::S;
+  using A = typename B::A;
+  __shared__ A red[kThreads / 64];
+  const int ch = blockIdx.x;
+  const int64_t o0 = static_cast<int64_t>(blockIdx.y) * outer_per_g;
+  int64_t o1 = o0 + outer_per_g;
+  if (o1 > outer) o1 = outer;
+  const int64_t count = (o1 - o0) * inner;  // < 2^32 (checked by the host)
+  A acc = A(0);
+  constexpr int U = 4;
+  auto at = [&](int64_t k) {
+    const uint32_t q = div_inner.div(static_cast<uint32_t>(k));
+    const int64_t i = k - static_cast<int64_t>(q) * inner;
+    return x[((o0 + q) * c + ch) * inner + i];
+  };
+  int64_t k = threadIdx.x;
+  for (; k + (U - 1) * kThreads < count; k += U * kThreads) {
+    S v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = at(k + u * kThreads);
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += B::ld(v[u]);
+  }
+  for (; k < count; k += kThreads) acc += B::ld(at(k));
+  // Fixed-order reduction: lanes by shuffle, then the waves in order.
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    A s = A(0);
+    for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+    partial[static_cast<int64_t>(blockIdx.y) * c + ch] = s;
+  }
+}
+
+// One wave per channel: lane l sums groups l, l+64, ... and the lanes are
+// combined by a fixed shuffle tree.
+template <class B>
+__global__ __launch_bounds__(kThreads) void bag_finalize_kernel(
+    const typename B::A* __restrict__ partial, int64_t groups, int c,
+    typename B::S* __restrict__ out) {
+  using A = typename B::A;
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (ch >= c) return;  // whole wave: ch is uniform across it
+  A s = A(0);
+  for (int64_t g = lane; g < groups; g += 64) s += partial[g * c + ch];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (lane == 0) out[ch] = B::out(s);
+}
+
+__global__ __launch_bounds__(kThreads) void zero_bytes_kernel(uint8_t* __restrict__ p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads)
+    p[i] = 0;
+}
+
+struct BagPlan {
+  bool rows;         // inner == 1
+  int vec;
+  int64_t cv;
+  int tx_shift;
+  int ct;
+  int64_t per_g;     // rows (or images) per group
+  int64_t groups;
+};
+
+constexpr int64_t kTargetBlocks = 2048;
+
+BagPlan make_bag_plan(int64_t outer, int64_t c, int64_t inner, int esize, bool aligned) {
+  BagPlan p{};
+  p.rows = inner == 1;
+  if (p.rows) {
+    const int kv = 16 / esize;
+    p.vec = (aligned && c % kv == 0) ? kv : 1;
+    p.cv = c / p.vec;
+    int s = 0;
+    while ((int64_t(1) << s) < p.cv && s < 5) ++s;  // at most 32 lanes along channels
+    p.tx_shift = s;
+    const int ry = kThreads >> s;
+    p.ct = static_cast<int>((p.cv + (1 << s) - 1) >> s);
+    int64_t gt = kTargetBlocks / p.ct;
+    if (gt < 1) gt = 1;
+    int64_t rpg = (outer + gt - 1) / gt;
+    const int64_t min_rows = static_cast<int64_t>(ry) * kUnroll;
+    if (rpg < min_rows) rpg = min_rows;
+    p.per_g = rpg;
+    p.groups = (outer + rpg - 1) / rpg;
+  } else {
+    p.vec = 1;
+    int64_t gt = kTargetBlocks / c;
+    if (gt < 1) gt = 1;
+    int64_t opg = (outer + gt - 1) / gt;
+    const int64_t min_imgs = (kThreads * 4 + inner - 1) / inner;
+    if (opg < min_imgs) opg = min_imgs;
+    // The flat index within a group stays below 2^31.
+    const int64_t max_imgs = ((int64_t(1) << 31) - 1) / inner;
+    if (opg > max_imgs) opg = max_imgs;
+    if (opg < 1) opg = 1;
+    p.per_g = opg;
+    p.groups = (outer + opg - 1) / opg;
+  }
+  if (p.groups < 1) p.groups = 1;
+  return p;
+}
+
+template <class B>
+hipError_t launch_bag(const void* x, int64_t outer, int64_t c, int64_t inner, void* out,
+                      void* workspace, hipStream_t stream) {
+  using S = typename B::S;
+  using A = typename B::A;
+  const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  const BagPlan p = make_bag_plan(outer, c, inner, sizeof(S), aligned);
+  A* partial = static_cast<A*>(workspace);
+  const S* xs = static_cast<const S*>(x);
+  {
+    LaunchScope scope(stream, "tfma_bias_add_grad_reduce");
+    if (p.rows) {
+      const size_t smem = static_cast<size_t>(kThreads) * p.vec * sizeof(A);
+      constexpr int V = 16 / sizeof(S);
+      if (p.vec == V) {
+        hipLaunchKernelGGL((bag_rows_kernel<B, V>), dim3(p.groups, p.ct), dim3(kThreads), smem,
+                           stream, xs, outer, static_cast<int>(c), p.cv, p.tx_shift, p.per_g,
+                           partial);
+      } else {
+        hipLaunchKernelGGL((bag_rows_kernel<B, 1>), dim3(p.groups, p.ct), dim3(kThreads), smem,
+                           stream, xs, outer, static_cast<int>(c), p.cv, p.tx_shift, p.per_g,
+                           partial);
+      }
+    } else {
+      hipLaunchKernelGGL((bag_planes_kernel<B>), dim3(c, p.groups), dim3(kThreads), 0, stream,
+                         xs, outer, static_cast<int>(c), inner, p.per_g,
+                         FastDiv(static_cast<uint32_t>(inner)), partial);
+    }
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  LaunchScope scope(stream, "tfma_bias_add_grad_finalize");
+  hipLaunchKernelGGL((bag_finalize_kernel<B>), dim3((c + kThreads / 64 - 1) / (kThreads / 64)),
+                     dim3(kThreads), 0, stream, partial, p.groups, static_cast<int>(c),
+                     static_cast<S*>(out));
+  return hipGetLastError();
+}
+
+size_t acc_bytes(int dt) {
+  return (dt == TFMA_DOUBLE || dt == TFMA_INT64) ? 8 : 4;
+}
+
+}  // namespace
+
+size_t BiasAddGradWorkspaceBytes(int dt, int64_t outer, int64_t c, int64_t inner, int esize) {
+  const BagPlan p = make_bag_plan(outer, c, inner, esize, true);
+  const BagPlan q = make_bag_plan(outer, c, inner, esize, false);
+  const int64_t g = p.groups > q.groups ? p.groups : q.groups;
+  return (static_cast<size_t>(g) * c * acc_bytes(dt) + 255) & ~size_t(255);
+}
+
+hipError_t LaunchBiasAddGrad(int dt, const void* x, int64_t outer, int64_t c, int64_t inner,
+                             void* out, void* workspace, hipStream_t stream) {
+  switch (dt) {
+    case TFMA_FLOAT: return launch_bag<BagF32>(x, outer, c, inner, out, workspace, stream);
+    case TFMA_HALF: return launch_bag<BagF16>(x, outer, c, inner, out, workspace, stream);
+    case TFMA_BFLOAT16: return launch_bag<BagBF16>(x, outer, c, inner, out, workspace, stream);
+    case TFMA_DOUBLE: return launch_bag<BagF64>(x, outer, c, inner, out, workspace, stream);
+    case TFMA_INT32: return launch_bag<BagI32>(x, outer, c, inner, out, workspace, stream);
+    case TFMA_INT64: return launch_bag<BagI64>(x, outer, c, inner, out, workspace, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t LaunchZeroBytes(void* p, int64_t n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  int64_t blocks = (n + kThreads - 1) / kThreads;
+  if (blocks > 1024) blocks = 1024;
+  LaunchScope scope(stream, "tfma_zero_bytes");
+  hipLaunchKernelGGL(zero_bytes_kernel, dim3(blocks), dim3(kThreads), 0, stream,
+                     static_cast<uint8_t*>(p), n);
+  return hipGetLastError();
+}
+
+}  // namespace tfma

@@ -127,6 +127,10 @@ __device__ inline typename Tr::S ew_apply(typename Tr::S a, typename Tr::S b,
   } else if constexpr (OP == EwOp::kMulAdd) {
     const C t = Tr::rnd(x * Tr::ld(b));
     return Tr::st(t + Tr::ld(c));
+  } else if constexpr (OP == EwOp::kReluGrad) {
+    // TF: gradients * (features > 0), a multiply - NaN or inf gradients at
+    // features <= 0 give NaN, negative ones give -0.
+    return Tr::st(x * (Tr::ld(b) > C(0) ? C(1) : C(0)));
   } else {  // kRelu
     return x < C(0) ? Tr::st(C(0)) : a;
   }
@@ -235,6 +239,7 @@ const char* op_kernel_name(EwOp op) {
     case EwOp::kMul: return "tfma_ew_mul";
     case EwOp::kMulAdd: return "tfma_ew_mul_add";
     case EwOp::kRelu: return "tfma_ew_relu";
+    case EwOp::kReluGrad: return "tfma_ew_relu_grad";
   }
   return "tfma_ew";
 }
@@ -407,6 +412,7 @@ hipError_t dispatch_op(EwOp op, int64_t n, const BcastOperand& a,
     case EwOp::kMul: return launch_ew<Tr, EwOp::kMul>(n, a, b, c, out, stream);
     case EwOp::kMulAdd: return launch_ew<Tr, EwOp::kMulAdd>(n, a, b, c, out, stream);
     case EwOp::kRelu: return launch_ew<Tr, EwOp::kRelu>(n, a, b, c, out, stream);
+    case EwOp::kReluGrad: return launch_ew<Tr, EwOp::kReluGrad>(n, a, b, c, out, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -421,6 +427,8 @@ hipError_t dispatch_strided(EwOp op, int64_t n, const void* a, const void* b,
     case EwOp::kMul: return launch_ew_strided<Tr, EwOp::kMul>(n, a, b, c, sh, out, stream);
     case EwOp::kMulAdd: return launch_ew_strided<Tr, EwOp::kMulAdd>(n, a, b, c, sh, out, stream);
     case EwOp::kRelu: return launch_ew_strided<Tr, EwOp::kRelu>(n, a, b, c, sh, out, stream);
+    case EwOp::kReluGrad:
+      return launch_ew_strided<Tr, EwOp::kReluGrad>(n, a, b, c, sh, out, stream);
   }
   return hipErrorInvalidValue;
 }

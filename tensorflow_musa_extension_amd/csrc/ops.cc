@@ -1017,6 +1017,118 @@ int TFMA_Relu(void* stream, const TFMA_Tensor* features, TFMA_Tensor* activation
   return run_elementwise(stream, EwOp::kRelu, "Relu", ins, 1, activations, false, status);
 }
 
+int TFMA_ReluGrad(void* stream, const TFMA_Tensor* gradients, const TFMA_Tensor* features,
+                  TFMA_Tensor* backprops, TFMA_Status* status) {
+  if (!valid_tensor(gradients) || !valid_tensor(features))
+    return set_status(status, TFMA_INVALID_ARGUMENT, "ReluGrad: invalid tensor");
+  if (!same_shape(gradients, features))
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "Inputs to ReluGrad must have the same shape. gradients: %s, features: %s",
+                      shape_str(gradients).c_str(), shape_str(features).c_str());
+  const TFMA_Tensor* ins[2] = {gradients, features};
+  return run_elementwise(stream, EwOp::kReluGrad, "ReluGrad", ins, 2, backprops, false, status);
+}
+
+namespace {
+
+// BiasAddGrad geometry: [outer, C, inner] around the channel dimension.
+int bias_grad_geometry(const TFMA_Tensor* x, const char* data_format, const TFMA_Tensor* out,
+                       int64_t* outer, int64_t* c, int64_t* inner, TFMA_Status* st) {
+  if (!valid_tensor(x) || (out && !valid_tensor(out)))
+    return set_status(st, TFMA_INVALID_ARGUMENT, "BiasAddGrad: invalid tensor");
+  const std::string fmt = data_format ? data_format : "NHWC";
+  if (fmt != "NHWC" && fmt != "NCHW")
+    return set_status(st, TFMA_INVALID_ARGUMENT, "Invalid data format");
+  if (x->ndims < 1)
+    return set_status(st, TFMA_INVALID_ARGUMENT, "Input tensor must be at least 1D: %s",
+                      shape_str(x).c_str());
+  switch (x->dtype) {
+    case TFMA_FLOAT: case TFMA_HALF: case TFMA_BFLOAT16: case TFMA_DOUBLE:
+    case TFMA_INT32: case TFMA_INT64:
+      break;
+    default:
+      return set_status(st, TFMA_UNIMPLEMENTED, "BiasAddGrad: dtype %s is not supported",
+                        dtype_name(x->dtype));
+  }
+  const int cd = (fmt == "NCHW" && x->ndims > 1) ? 1 : x->ndims - 1;
+  *c = x->dims[cd];
+  *outer = 1;
+  *inner = 1;
+  for (int d = 0; d < cd; ++d) *outer *= x->dims[d];
+  for (int d = cd + 1; d < x->ndims; ++d) *inner *= x->dims[d];
+  if (out) {
+    if (out->dtype != x->dtype)
+      return set_status(st, TFMA_INVALID_ARGUMENT, "BiasAddGrad: output dtype %s, expected %s",
+                        dtype_name(out->dtype), dtype_name(x->dtype));
+    if (out->ndims != 1 || out->dims[0] != *c)
+      return set_status(st, TFMA_INVALID_ARGUMENT, "BiasAddGrad: output shape %s, expected [%lld]",
+                        shape_str(out).c_str(), static_cast<long long>(*c));
+  }
+  if (*inner >= (int64_t(1) << 31) || *c >= (int64_t(1) << 31))
+    return set_status(st, TFMA_UNIMPLEMENTED, "BiasAddGrad: dimension too large");
+  return TFMA_OK;
+}
+
+int elem_size(int dt) {
+  switch (dt) {
+    case TFMA_HALF: case TFMA_BFLOAT16: return 2;
+    case TFMA_DOUBLE: case TFMA_INT64: return 8;
+    default: return 4;
+  }
+}
+
+}  // namespace
+
+int TFMA_BiasAddGradWorkspaceBytes(const TFMA_Tensor* out_backprop, const char* data_format,
+                                   size_t* bytes, TFMA_Status* status) {
+  int64_t outer = 0, c = 0, inner = 0;
+  if (bias_grad_geometry(out_backprop, data_format, nullptr, &outer, &c, &inner, status) !=
+      TFMA_OK)
+    return status->code;
+  if (!bytes) return set_status(status, TFMA_INVALID_ARGUMENT, "bytes is null");
+  *bytes = (out_backprop->ndims < 2 || c == 0)
+               ? 0
+               : BiasAddGradWorkspaceBytes(out_backprop->dtype, outer, c, inner,
+                                           elem_size(out_backprop->dtype));
+  return ok(status);
+}
+
+int TFMA_BiasAddGrad(void* stream, const TFMA_Tensor* out_backprop, const char* data_format,
+                     TFMA_Tensor* output, void* workspace, size_t workspace_bytes,
+                     TFMA_Status* status) {
+  int64_t outer = 0, c = 0, inner = 0;
+  if (bias_grad_geometry(out_backprop, data_format, output, &outer, &c, &inner, status) !=
+      TFMA_OK)
+    return status->code;
+  if (c == 0) return ok(status);
+  if (!output->data) return set_status(status, TFMA_INVALID_ARGUMENT, "BiasAddGrad: null output");
+  const int es = elem_size(out_backprop->dtype);
+  hipStream_t strm = as_stream(stream);
+  // Rank 1: nothing to reduce; the output is the input (reference :50-58).
+  if (out_backprop->ndims == 1) {
+    if (!out_backprop->data)
+      return set_status(status, TFMA_INVALID_ARGUMENT, "BiasAddGrad: null input");
+    return hip_status(status,
+                      hipMemcpyAsync(output->data, out_backprop->data, static_cast<size_t>(c) * es,
+                                     hipMemcpyDeviceToDevice, strm),
+                      "BiasAddGrad");
+  }
+  // Nothing summed: zeros (reference :64-69).
+  if (outer == 0 || inner == 0)
+    return hip_status(status, LaunchZeroBytes(output->data, c * es, strm), "BiasAddGrad");
+  if (!out_backprop->data)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "BiasAddGrad: null input");
+  const size_t need = BiasAddGradWorkspaceBytes(out_backprop->dtype, outer, c, inner, es);
+  if (!workspace || workspace_bytes < need)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "BiasAddGrad: workspace of %zu bytes required, got %zu", need,
+                      workspace ? workspace_bytes : size_t(0));
+  return hip_status(status,
+                    LaunchBiasAddGrad(out_backprop->dtype, out_backprop->data, outer, c, inner,
+                                      output->data, workspace, strm),
+                    "BiasAddGrad");
+}
+
 int TFMA_AddV2(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* y, TFMA_Tensor* z,
                TFMA_Status* status) {
   const TFMA_Tensor* ins[2] = {x, y};

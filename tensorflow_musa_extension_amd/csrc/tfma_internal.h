@@ -68,9 +68,19 @@ hipError_t LaunchGroupedApplyAdam(DType t, DType tg, const AdamTensorEntry* dev_
                                   hipStream_t stream);
 
 // ---------------------------------------------------------------------------
+// BiasAddGrad (dt: TFMA_DataType code; x viewed as [outer, c, inner])
+// ---------------------------------------------------------------------------
+size_t BiasAddGradWorkspaceBytes(int dt, int64_t outer, int64_t c, int64_t inner, int esize);
+hipError_t LaunchBiasAddGrad(int dt, const void* x, int64_t outer, int64_t c, int64_t inner,
+                             void* out, void* workspace, hipStream_t stream);
+// Zero-fills n bytes with a kernel (capturable, unlike a memset node).
+hipError_t LaunchZeroBytes(void* p, int64_t n, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
 // Elementwise
 // ---------------------------------------------------------------------------
-enum class EwOp { kAdd, kAddRelu, kMul, kMulAdd, kRelu };
+// kReluGrad: a = gradients, b = features (TF's gradients * (features > 0)).
+enum class EwOp { kAdd, kAddRelu, kMul, kMulAdd, kRelu, kReluGrad };
 
 // How an input of an elementwise kernel maps a flat output index i to its
 // own flat index: kFull: i; kScalar: 0; kPeriodic: (i / inner) % period.

@@ -33,6 +33,8 @@ _TORCH_TO_TF = {
     torch.float16: _lib.DT_HALF,
     torch.bfloat16: _lib.DT_BFLOAT16,
     torch.float64: _lib.DT_DOUBLE,
+    torch.int32: _lib.DT_INT32,
+    torch.int64: _lib.DT_INT64,
 }
 
 FusedBatchNormV3Result = collections.namedtuple(
@@ -313,6 +315,41 @@ def Relu(features, out=None):
     out = torch.empty_like(features) if out is None else out
     df, do = _desc(features, "features"), _desc(out, "activations")
     _call("TFMA_Relu", _stream(features), _ref(df), _ref(do))
+    return out
+
+
+def ReluGrad(gradients, features, out=None):
+    """tf.raw_ops.ReluGrad: gradients * (features > 0)."""
+    out = torch.empty_like(gradients) if out is None else out
+    dg, df, do = _desc(gradients, "gradients"), _desc(features, "features"), _desc(out, "backprops")
+    _call("TFMA_ReluGrad", _stream(gradients), _ref(dg), _ref(df), _ref(do))
+    return out
+
+
+def bias_add_grad_workspace_bytes(out_backprop, data_format="NHWC"):
+    lib = _lib.load()
+    status = _lib.TFMA_Status()
+    nbytes = ctypes.c_size_t(0)
+    d = _lib.make_tensor(None, _TORCH_TO_TF[out_backprop.dtype], out_backprop.shape)
+    lib.TFMA_BiasAddGradWorkspaceBytes(_ref(d), _fmt(data_format), ctypes.byref(nbytes),
+                                       ctypes.byref(status))
+    raise_for_status(status)
+    return nbytes.value
+
+
+def BiasAddGrad(out_backprop, data_format="NHWC", out=None, workspace=None):
+    """tf.raw_ops.BiasAddGrad: per-channel sum over every other dimension
+    (channel = last dim for NHWC, dim 1 for NCHW)."""
+    nd = out_backprop.dim()
+    cd = 1 if (str(data_format).upper().startswith("NC") and nd > 1) else nd - 1
+    c = out_backprop.shape[cd] if nd >= 1 else 0
+    out = torch.empty(c, dtype=out_backprop.dtype, device=out_backprop.device) if out is None else out
+    if workspace is None:
+        need = bias_add_grad_workspace_bytes(out_backprop, data_format) if nd >= 1 else 0
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=out_backprop.device)
+    dx, do = _desc(out_backprop, "out_backprop"), _desc(out, "output")
+    _call("TFMA_BiasAddGrad", _stream(out_backprop), _ref(dx), _fmt(data_format), _ref(do),
+          ctypes.c_void_p(workspace.data_ptr()), workspace.numel(), keep=(workspace,))
     return out
 
 

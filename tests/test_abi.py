@@ -170,6 +170,25 @@ def test_adam_mixed_validation():
     assert code == _lib.INVALID_ARGUMENT and msg == "beta1_power has dtype half, expected float"
 
 
+def test_relu_grad_and_bias_add_grad_validation():
+    code, msg = call("TFMA_ReluGrad", None, ref(T((4, 3))), ref(T((3, 4))), ref(T((4, 3))))
+    assert code == _lib.INVALID_ARGUMENT
+    assert msg == "Inputs to ReluGrad must have the same shape. gradients: [4,3], features: [3,4]"
+    n = ctypes.c_size_t(0)
+    code, msg = call("TFMA_BiasAddGradWorkspaceBytes", ref(T((2, 3))), b"NCDHW", ctypes.byref(n))
+    assert code == _lib.INVALID_ARGUMENT and msg == "Invalid data format"
+    code, msg = call("TFMA_BiasAddGradWorkspaceBytes", ref(T(())), b"NHWC", ctypes.byref(n))
+    assert msg == "Input tensor must be at least 1D: []"
+    code, msg = call("TFMA_BiasAddGradWorkspaceBytes", ref(T((64, 7, 9))), b"NCHW", ctypes.byref(n))
+    assert code == _lib.OK and n.value > 0
+    code, msg = call("TFMA_BiasAddGrad", None, ref(T((64, 7, 9))), b"NCHW", ref(T((9,))),
+                     ctypes.c_void_p(FAKE), 1 << 20)
+    assert code == _lib.INVALID_ARGUMENT and "output shape [9], expected [7]" in msg
+    code, msg = call("TFMA_BiasAddGrad", None, ref(T((64, 7, 9))), b"NCHW", ref(T((7,))),
+                     ctypes.c_void_p(FAKE), 1)
+    assert code == _lib.INVALID_ARGUMENT and "workspace of" in msg
+
+
 def test_adam_locking_is_deadlock_free():
     """Concurrent use_locking calls over overlapping var/m/v sets in every
     order complete (locks are taken in address order).  Empty tensors make

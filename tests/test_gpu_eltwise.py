@@ -123,3 +123,63 @@ def test_errors(dev):
         ops.BiasAdd(x, torch.zeros(4, device=dev))
     with pytest.raises(tfma.InvalidArgumentError, match="Incompatible shapes for Add"):
         ops.AddV2(x, torch.zeros(3, device=dev))
+
+
+def _assert_bitwise_nan_aware(got, want, dtype, name):
+    """Bitwise, except that NaN payloads may differ (the device's bf16
+    conversion keeps payload bits Eigen canonicalises)."""
+    nan_w = np.isnan(oracle.to_f32(want, dtype))
+    assert np.array_equal(np.isnan(oracle.to_f32(got, dtype)), nan_w), name
+    assert_bitwise(got[~nan_w], want[~nan_w], name)
+
+
+@pytest.mark.parametrize("dtype", DTYPES + ["float64"])
+@pytest.mark.parametrize("shape", [(8192, 4096), (8191, 4095), (3, 5), (1,), (0, 7)])
+def test_relu_grad(dev, dtype, shape):
+    rng = np.random.default_rng(21)
+    g = rng.standard_normal(shape)
+    f = rng.standard_normal(shape)
+    if g.size >= 6:  # NaN / inf gradients, signed zeros, features at 0
+        g.ravel()[:6] = [np.nan, np.inf, -np.inf, -2.0, 0.0, -0.0]
+        f.ravel()[:6] = [-1.0, 0.0, 1.0, -3.0, 0.0, 5.0]
+    if dtype == "float64":
+        out = ops.ReluGrad(torch.from_numpy(g).to(dev), torch.from_numpy(f).to(dev))
+        torch.cuda.synchronize()
+        assert_bitwise(out.cpu().numpy(), g * (f > 0).astype(np.float64), "float64")
+        return
+    gs, fs = oracle.to_storage(g, dtype), oracle.to_storage(f, dtype)
+    out = ops.ReluGrad(to_dev(gs, dtype, dev), to_dev(fs, dtype, dev))
+    torch.cuda.synchronize()
+    _assert_bitwise_nan_aware(to_np(out, dtype), oracle.eltwise("relu_grad", [gs, fs], dtype),
+                              dtype, f"relu_grad {dtype} {shape}")
+
+
+def test_relu_grad_shape_mismatch(dev):
+    a = torch.zeros(4, 3, device=dev)
+    with pytest.raises(tfma.InvalidArgumentError,
+                       match=r"Inputs to ReluGrad must have the same shape. gradients: \[4,3\], "
+                             r"features: \[3,4\]"):
+        ops.ReluGrad(a, torch.zeros(3, 4, device=dev))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_signed_zero_products(dev, dtype):
+    """Products that are -0 stay -0 (TF rounds the float product to T), in the
+    vector body and in the tail: Mul, Mul+Add with a -0 addend, ReluGrad."""
+    n = 8 * 5 + 5  # vectors and a tail for every dtype's vector width
+    x = np.tile([-2.0, 2.0, -0.0, 0.0, -1.5], n // 5)
+    y = np.tile([0.0, -0.0, 3.0, -3.0, -0.0], n // 5)
+    z = np.full(n, -0.0)
+    xs, ys, zs = (oracle.to_storage(a, dtype) for a in (x, y, z))
+    dx, dy_, dz = (to_dev(a, dtype, dev) for a in (xs, ys, zs))
+    outs = {"mul": ops.Mul(dx, dy_), "mul_add": ops.MusaShiftedAffineMap(dx, dy_, dz),
+            "relu_grad": ops.ReluGrad(dx, dy_)}
+    torch.cuda.synchronize()
+    want = {"mul": oracle.eltwise("mul", [xs, ys], dtype),
+            "mul_add": oracle.eltwise("mul_add", [xs, ys, zs], dtype),
+            "relu_grad": oracle.eltwise("relu_grad", [xs, ys], dtype)}
+    for k, t in outs.items():
+        w = want[k]
+        assert np.all(np.signbit(oracle.to_f32(w, dtype)[:4]) == [True, True, True, True]) or \
+            k == "relu_grad"
+        assert_bitwise(to_np(t, dtype), w, f"{dtype} {k}")

@@ -15,6 +15,7 @@ import pytest
 import torch
 
 from oracle import oracle
+from tests.helpers import assert_bitwise
 
 rng_global = np.random.default_rng(1234)
 
@@ -416,3 +417,61 @@ def test_bias_add_nchw_channel_dim():
         assert np.all(out[:, c] == b[c])
     out = oracle.bias_add(np.zeros((2, 2, 3), np.float32), b)
     assert np.all(out[..., 2] == 3)
+
+
+# ---------------------------------------------------------------------------
+# ReluGrad / BiasAddGrad
+# ---------------------------------------------------------------------------
+def test_relu_grad_matches_numpy_multiply():
+    """ReluGrad = gradients * (features > 0) as a multiply: checked against
+    numpy's float32 / float16 multiply and torch's bfloat16 one, including the
+    special values (NaN and inf gradients, -0, features = 0)."""
+    rng = np.random.default_rng(50)
+    g = rng.standard_normal(4000)
+    f = rng.standard_normal(4000)
+    g[:6] = [np.nan, np.inf, -np.inf, -2.0, 0.0, -0.0]
+    f[:6] = [-1.0, 0.0, 1.0, -3.0, 0.0, 5.0]
+    for dt, npdt in (("float32", np.float32), ("float16", np.float16)):
+        gs, fs = g.astype(npdt), f.astype(npdt)
+        want = gs * (fs > 0).astype(npdt)
+        got = oracle.eltwise("relu_grad", [gs, fs], dt)
+        assert_bitwise(got, want, dt)
+    gb, fb = oracle.to_storage(g, "bfloat16"), oracle.to_storage(f, "bfloat16")
+    tg = torch.from_numpy(gb.view(np.int16)).view(torch.bfloat16)
+    tf_ = torch.from_numpy(fb.view(np.int16)).view(torch.bfloat16)
+    want = (tg * (tf_ > 0).to(torch.bfloat16)).view(torch.int16).numpy().view(np.uint16)
+    got = oracle.eltwise("relu_grad", [gb, fb], "bfloat16")
+    # NaN payloads differ (Eigen's canonical 0x7fc0/0xffc0 vs torch's): compare
+    # NaN positions, and every other element bitwise.
+    nan_w = np.isnan(oracle.to_f32(want, "bfloat16"))
+    assert np.array_equal(np.isnan(oracle.to_f32(got, "bfloat16")), nan_w)
+    assert_bitwise(got[~nan_w], want[~nan_w], "bfloat16")
+
+
+@pytest.mark.parametrize("shape,fmt", [((2, 8, 8, 32), "NHWC"), ((2, 32, 8, 8), "NCHW"),
+                                       ((37, 5), "NHWC"), ((3, 4, 5, 6, 7), "NCHW")])
+def test_bias_add_grad_matches_numpy(shape, fmt):
+    """Against numpy's float64 sum over the non-channel axes (the reference's
+    own test shapes, test/ops/biasadd_grad_op_test.py:16-86, and two more)."""
+    rng = np.random.default_rng(51)
+    x = rng.standard_normal(shape)
+    axes = tuple(i for i in range(len(shape)) if i != (1 if fmt == "NCHW" else len(shape) - 1))
+    want = x.sum(axis=axes)
+    np.testing.assert_allclose(oracle.bias_add_grad(x.astype(np.float32), fmt, "float32"), want,
+                               rtol=1e-6, atol=1e-5)
+    assert np.max(np.abs(oracle.bias_add_grad(x, fmt, "float64") - want)) < 1e-12
+    h = x.astype(np.float16)
+    got = oracle.to_f32(oracle.bias_add_grad(h, fmt, "float16"), "float16")
+    np.testing.assert_allclose(got, h.astype(np.float64).sum(axis=axes), rtol=1e-3, atol=1e-2)
+
+
+def test_bias_add_grad_integers_wrap_and_special_ranks():
+    x32 = np.full((3, 5), 2**30, dtype=np.int32)  # sum 3 * 2^30 wraps in int32
+    assert_bitwise(oracle.bias_add_grad(x32, "NHWC", "int32"),
+                   np.sum(x32, axis=0, dtype=np.int32), "int32")
+    x64 = np.arange(24, dtype=np.int64).reshape(2, 3, 4)
+    np.testing.assert_array_equal(oracle.bias_add_grad(x64, "NCHW", "int64"), x64.sum(axis=(0, 2)))
+    v = np.arange(7, dtype=np.float32)
+    np.testing.assert_array_equal(oracle.bias_add_grad(v, "NHWC", "float32"), v)  # rank 1
+    np.testing.assert_array_equal(oracle.bias_add_grad(np.zeros((0, 16), np.float32), "NHWC",
+                                                       "float32"), np.zeros(16, np.float32))
