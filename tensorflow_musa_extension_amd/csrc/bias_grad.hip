@@ -59,8 +59,11 @@ __global__ __launch_bounds__(kThreads) void bag_rows_kernel(
   const int ty = threadIdx.x >> tx_shift;
   const int ry = kThreads >> tx_shift;
   const int width = (1 << tx_shift) * VEC;
-  const int64_t cvi = static_cast<int64_t>(blockIdx.y) * (1 << tx_shift) + tx;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_g;
+  // Channel tiles vary fastest across workgroups, so the workgroups running
+  // together read adjacent segments of the same rows instead of one column
+  // of many rows (which concentrates on few memory channels).
+  const int64_t cvi = static_cast<int64_t>(blockIdx.x) * (1 << tx_shift) + tx;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * rows_per_g;
   int64_t r1 = r0 + rows_per_g;
   if (r1 > rows) r1 = rows;
   A acc[VEC];
@@ -88,15 +91,18 @@ __global__ __launch_bounds__(kThreads) void bag_rows_kernel(
 #pragma unroll
   for (int j = 0; j < VEC; ++j) red[ty * width + tx * VEC + j] = acc[j];
   __syncthreads();
-  const int64_t ch = static_cast<int64_t>(blockIdx.y) * width + threadIdx.x;
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * width + threadIdx.x;
   if (static_cast<int>(threadIdx.x) < width && ch < c) {
     A s = A(0);
     for (int k = 0; k < ry; ++k) s += red[k * width + threadIdx.x];
-    partial[static_cast<int64_t>(blockIdx.x) * c + ch] = s;
+    partial[static_cast<int64_t>(blockIdx.y) * c + ch] = s;
   }
 }
 
-template <class B>
+// VEC > 1 when every plane is a whole number of aligned 16-byte vectors
+// (inner % VEC == 0 and x aligned): `inner` and the flat index then count
+// vectors.
+template <class B, int VEC>
 __global__ __launch_bounds__(kThreads) void bag_planes_kernel(
     const typename B::S* __restrict__ x, int64_t outer, int c, int64_t inner,
     int64_t outer_per_g, FastDiv div_inner, typename B::A* __restrict__ partial) {
@@ -107,23 +113,30 @@ __global__ __launch_bounds__(kThreads) void bag_planes_kernel(
   const int64_t o0 = static_cast<int64_t>(blockIdx.y) * outer_per_g;
   int64_t o1 = o0 + outer_per_g;
   if (o1 > outer) o1 = outer;
-  const int64_t count = (o1 - o0) * inner;  // < 2^32 (checked by the host)
+  const int64_t count = (o1 - o0) * inner;  // < 2^31 (checked by the host)
   A acc = A(0);
-  constexpr int U = 4;
-  auto at = [&](int64_t k) {
+  constexpr int U = VEC > 1 ? 4 : 8;
+  auto at = [&](int64_t k, S (&v)[VEC]) {
     const uint32_t q = div_inner.div(static_cast<uint32_t>(k));
     const int64_t i = k - static_cast<int64_t>(q) * inner;
-    return x[((o0 + q) * c + ch) * inner + i];
+    vload<S, VEC>(x + (((o0 + q) * c + ch) * inner + i) * VEC, v);
   };
   int64_t k = threadIdx.x;
   for (; k + (U - 1) * kThreads < count; k += U * kThreads) {
-    S v[U];
+    S v[U][VEC];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = at(k + u * kThreads);
+    for (int u = 0; u < U; ++u) at(k + u * kThreads, v[u]);
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc += B::ld(v[u]);
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc += B::ld(v[u][j]);
   }
-  for (; k < count; k += kThreads) acc += B::ld(at(k));
+  for (; k < count; k += kThreads) {
+    S v[VEC];
+    at(k, v);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) acc += B::ld(v[j]);
+  }
   // Fixed-order reduction: lanes by shuffle, then the waves in order.
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
@@ -147,7 +160,16 @@ __global__ __launch_bounds__(kThreads) void bag_finalize_kernel(
   const int lane = threadIdx.x & 63;
   if (ch >= c) return;  // whole wave: ch is uniform across it
   A s = A(0);
-  for (int64_t g = lane; g < groups; g += 64) s += partial[g * c + ch];
+  constexpr int L = 8;  // loads in flight per lane; added in group order
+  int64_t g = lane;
+  for (; g + (L - 1) * 64 < groups; g += L * 64) {
+    A v[L];
+#pragma unroll
+    for (int u = 0; u < L; ++u) v[u] = partial[(g + u * 64) * c + ch];
+#pragma unroll
+    for (int u = 0; u < L; ++u) s += v[u];
+  }
+  for (; g < groups; g += 64) s += partial[g * c + ch];
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
   if (lane == 0) out[ch] = B::out(s);
@@ -169,7 +191,7 @@ struct BagPlan {
   int64_t groups;
 };
 
-constexpr int64_t kTargetBlocks = 2048;
+constexpr int64_t kTargetBlocks = 1024;
 
 BagPlan make_bag_plan(int64_t outer, int64_t c, int64_t inner, int esize, bool aligned) {
   BagPlan p{};
@@ -191,11 +213,12 @@ BagPlan make_bag_plan(int64_t outer, int64_t c, int64_t inner, int esize, bool a
     p.per_g = rpg;
     p.groups = (outer + rpg - 1) / rpg;
   } else {
-    p.vec = 1;
+    const int kv = 16 / esize;
+    p.vec = (aligned && inner % kv == 0) ? kv : 1;
     int64_t gt = kTargetBlocks / c;
     if (gt < 1) gt = 1;
     int64_t opg = (outer + gt - 1) / gt;
-    const int64_t min_imgs = (kThreads * 4 + inner - 1) / inner;
+    const int64_t min_imgs = (static_cast<int64_t>(kThreads) * 8 * p.vec + inner - 1) / inner;
     if (opg < min_imgs) opg = min_imgs;
     // The flat index within a group stays below 2^31.
     const int64_t max_imgs = ((int64_t(1) << 31) - 1) / inner;
@@ -223,16 +246,22 @@ hipError_t launch_bag(const void* x, int64_t outer, int64_t c, int64_t inner, vo
       const size_t smem = static_cast<size_t>(kThreads) * p.vec * sizeof(A);
       constexpr int V = 16 / sizeof(S);
       if (p.vec == V) {
-        hipLaunchKernelGGL((bag_rows_kernel<B, V>), dim3(p.groups, p.ct), dim3(kThreads), smem,
+        hipLaunchKernelGGL((bag_rows_kernel<B, V>), dim3(p.ct, p.groups), dim3(kThreads), smem,
                            stream, xs, outer, static_cast<int>(c), p.cv, p.tx_shift, p.per_g,
                            partial);
       } else {
-        hipLaunchKernelGGL((bag_rows_kernel<B, 1>), dim3(p.groups, p.ct), dim3(kThreads), smem,
+        hipLaunchKernelGGL((bag_rows_kernel<B, 1>), dim3(p.ct, p.groups), dim3(kThreads), smem,
                            stream, xs, outer, static_cast<int>(c), p.cv, p.tx_shift, p.per_g,
                            partial);
       }
+    } else if (p.vec > 1) {
+      constexpr int V = 16 / sizeof(S);
+      const int64_t iv = inner / V;
+      hipLaunchKernelGGL((bag_planes_kernel<B, V>), dim3(c, p.groups), dim3(kThreads), 0, stream,
+                         xs, outer, static_cast<int>(c), iv, p.per_g,
+                         FastDiv(static_cast<uint32_t>(iv)), partial);
     } else {
-      hipLaunchKernelGGL((bag_planes_kernel<B>), dim3(c, p.groups), dim3(kThreads), 0, stream,
+      hipLaunchKernelGGL((bag_planes_kernel<B, 1>), dim3(c, p.groups), dim3(kThreads), 0, stream,
                          xs, outer, static_cast<int>(c), inner, p.per_g,
                          FastDiv(static_cast<uint32_t>(inner)), partial);
     }

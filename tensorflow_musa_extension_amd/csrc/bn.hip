@@ -159,8 +159,10 @@ __global__ __launch_bounds__(kThreads) void bn_nhwc_reduce_kernel(
   const int ty = threadIdx.x >> tx_shift;
   const int ry = kThreads >> tx_shift;
   const int width = (1 << tx_shift) * VEC;
-  const int64_t cvi = static_cast<int64_t>(blockIdx.y) * (1 << tx_shift) + tx;
-  const int64_t g = blockIdx.x;
+  // Channel tiles vary fastest across workgroups (adjacent row segments
+  // are read together rather than one column of many rows).
+  const int64_t cvi = static_cast<int64_t>(blockIdx.x) * (1 << tx_shift) + tx;
+  const int64_t g = blockIdx.y;
   const int64_t r0 = g * rows_per_g;
   int64_t r1 = r0 + rows_per_g;
   if (r1 > rows) r1 = rows;
@@ -199,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void bn_nhwc_reduce_kernel(
 #pragma unroll
   for (int j = 0; j < VEC; ++j) red[ty * width + tx * VEC + j] = make_float2(s1[j], s2[j]);
   __syncthreads();
-  const int64_t cbase = static_cast<int64_t>(blockIdx.y) * width;
+  const int64_t cbase = static_cast<int64_t>(blockIdx.x) * width;
   for (int cl = threadIdx.x; cl < width; cl += kThreads) {
     if (cbase + cl >= c) break;
     float a = 0.f, b = 0.f;
@@ -413,9 +415,9 @@ __global__ __launch_bounds__(kThreads) void bn_nhwc_apply_kernel(
   const int tx = threadIdx.x & ((1 << tx_shift) - 1);
   const int ty = threadIdx.x >> tx_shift;
   const int ry = kThreads >> tx_shift;
-  const int64_t cvi = static_cast<int64_t>(blockIdx.y) * (1 << tx_shift) + tx;
+  const int64_t cvi = static_cast<int64_t>(blockIdx.x) * (1 << tx_shift) + tx;
   if (cvi >= cv) return;
-  const int64_t g = groups - 1 - blockIdx.x;  // reverse of the reduce order
+  const int64_t g = groups - 1 - blockIdx.y;  // reverse of the reduce order
   const int64_t r0 = g * rows_per_g;
   int64_t r1 = r0 + rows_per_g;
   if (r1 > rows) r1 = rows;
@@ -877,7 +879,7 @@ hipError_t launch_reduce(const Plan& p, const BnGeometry& g, const void* x,
     const size_t smem = static_cast<size_t>(kThreads) * VEC * sizeof(float2);
     LaunchScope scope(stream, kGrad ? "tfma_bn_grad_reduce" : "tfma_bn_fwd_reduce");
     hipLaunchKernelGGL((bn_nhwc_reduce_kernel<Tr, VEC, kGrad>),
-                       dim3(p.groups, p.ct), dim3(kThreads), smem, stream,
+                       dim3(p.ct, p.groups), dim3(kThreads), smem, stream,
                        static_cast<const S*>(x), static_cast<const S*>(dy),
                        mean_in, g.rows, static_cast<int>(g.c), p.cv, p.tx_shift,
                        p.rows_per_g, partial);
@@ -901,7 +903,7 @@ hipError_t launch_apply(const Plan& p, const BnGeometry& g, const void* x,
   if (p.nhwc) {
     LaunchScope scope(stream, kGrad ? "tfma_bn_grad_apply" : "tfma_bn_fwd_apply");
     hipLaunchKernelGGL((bn_nhwc_apply_kernel<Tr, VEC, kGrad>),
-                       dim3(p.groups, p.ct), dim3(kThreads), 0, stream,
+                       dim3(p.ct, p.groups), dim3(kThreads), 0, stream,
                        static_cast<const S*>(x), static_cast<const S*>(dy),
                        static_cast<S*>(out), coef, g.rows, static_cast<int>(g.c),
                        p.cv, p.tx_shift, p.rows_per_g, p.groups);
