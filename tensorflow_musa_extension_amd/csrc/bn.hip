@@ -540,6 +540,10 @@ struct FusedArgs {
   unsigned long long* barrier;  // device-wide arrival counter
   unsigned long long base;      // its value when this launch starts
   unsigned* timeout_flag;
+  unsigned* queues;             // [ct][wave] chunk counters, zero between launches
+  int dyn_rows;                 // streamed rows per thread handed out dynamically
+  int dyn_chunk;                // rows per thread in one dynamic chunk
+  int shards;                   // chunk counters per (ct, wave)
   FinArgs fin;
 };
 
@@ -836,8 +840,11 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   for (int p = 0; p < PB; ++p)
     if (qb - p >= KR + KL)
       st16(po + base + (qb - p) * rstride, apply_words<Tr, kGrad>(pbx[p], pbd[kGrad ? p : 0], cf));
+  // The lowest dyn_rows streamed rows of every thread are not processed by
+  // their owner but handed out in chunks after the owner's other rows.
+  const int64_t qlo = KR + KL + a.dyn_rows;
   q = qb - PB;
-  for (; q >= KR + KL + U - 1; q -= U) {
+  for (; q >= qlo + U - 1; q -= U) {
     uint4 xw[U], dw[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -848,7 +855,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     for (int u = 0; u < U; ++u)
       st16(po + base + (q - u) * rstride, apply_words<Tr, kGrad>(xw[u], dw[u], cf));
   }
-  for (; q >= KR + KL; --q) {
+  for (; q >= qlo; --q) {
     const uint4 xw = ld16(xrow(q));
     uint4 dw = xw;
     if constexpr (kGrad) dw = ld16(drow(q));
@@ -865,6 +872,91 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
 #pragma unroll
   for (int r = 0; r < KR; ++r)
     if (r < nk) st16(po + base + r * rstride, apply_words<Tr, kGrad>(xr[r], dr[kGrad ? r : 0], cf));
+
+  // Dynamic tail: chunk j of group g' covers the owner rows q in
+  // [KR+KL + j*B, KR+KL + (j+1)*B) below the owner's static rows.  Wave w of
+  // any workgroup of channel tile ct takes chunks of wave w of the others
+  // (same lanes, same channels, same coefficients).  Groups are split into
+  // `shards` of whole runs of 8 consecutive groups (8 consecutive workgroups
+  // sit on the 8 different XCDs), each with its own counter per (ct, w), so
+  // no single counter serializes the whole grid.  The next claim is issued
+  // before the current chunk is processed.  Results do not depend on which
+  // wave writes them.
+  if (a.dyn_rows > 0) {
+    const int B = a.dyn_chunk;
+    const int S = a.shards;
+    const int64_t nb8 = (a.groups + 7) / 8;
+    const int shard = static_cast<int>((g / 8) % S);
+    const int64_t kb = shard < nb8 ? (nb8 - shard + S - 1) / S : 0;
+    const int64_t members = kb * 8;
+    const unsigned jn = static_cast<unsigned>((a.dyn_rows + B - 1) / B);
+    const unsigned total = jn * static_cast<unsigned>(members);
+    unsigned* ctr = a.queues + (static_cast<int64_t>(ct) * S + shard) * kWaves + wave;
+    auto claim = [&]() {
+      unsigned v = 0;
+      if (lane == 0) v = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return v;
+    };
+    unsigned next = claim();
+    while (true) {
+      const unsigned cidx = __builtin_amdgcn_readfirstlane(next);
+      if (cidx >= total) break;
+      next = claim();
+      const int64_t i = cidx % static_cast<unsigned>(members);
+      const int64_t j = cidx / static_cast<unsigned>(members);
+      const int64_t go = 8 * (shard + static_cast<int64_t>(S) * (i / 8)) + (i % 8);
+      if (go >= a.groups) continue;
+      const int64_t o0 = go * a.rows_per_g;
+      int64_t o1 = o0 + a.rows_per_g;
+      if (o1 > a.rows) o1 = a.rows;
+      const int64_t onk = (active && o0 + ty < o1) ? (o1 - o0 - ty + ry - 1) / ry : 0;
+      const bool opre = PA > 0 && static_cast<int>(go * a.ct + ct) +
+                                          wave * static_cast<int>(gridDim.x) >= a.c;
+      int64_t qhi = onk - 1 - (opre ? PA : 0) - PB;  // owner's last streamed row
+      if (qhi > qlo - 1) qhi = qlo - 1;              // owner's static rows end at qlo
+      const int64_t qa = KR + KL + j * B;
+      int64_t qb2 = qa + B - 1;
+      if (qb2 > qhi) qb2 = qhi;
+      const int64_t obase = (o0 + ty) * a.c;
+      int64_t qq = qa;
+      for (; qq + U - 1 <= qb2; qq += U) {
+        uint4 xw[U], dw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          xw[u] = ld16(px + obase + (qq + u) * rstride);
+          if constexpr (kGrad) dw[u] = ld16(pd + obase + (qq + u) * rstride);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          st16(po + obase + (qq + u) * rstride, apply_words<Tr, kGrad>(xw[u], dw[u], cf));
+      }
+      for (; qq <= qb2; ++qq) {
+        const uint4 xw = ld16(px + obase + qq * rstride);
+        uint4 dw = xw;
+        if constexpr (kGrad) dw = ld16(pd + obase + qq * rstride);
+        st16(po + obase + qq * rstride, apply_words<Tr, kGrad>(xw, dw, cf));
+      }
+    }
+  }
+
+  // Exit: the last workgroup to leave (third arrival on the barrier counter)
+  // zeroes the chunk counters for the next launch.
+  __syncthreads();
+  if (wave == 0) {
+    unsigned long long old = 0;
+    // Relaxed: every counter this workgroup touched was updated by atomics
+    // whose results it has already used.
+    if (lane == 0)
+      old = __hip_atomic_fetch_add(a.barrier, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long last_lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(old));
+    const unsigned long long last_hi =
+        __builtin_amdgcn_readfirstlane(static_cast<unsigned>(old >> 32));
+    const unsigned long long was = (last_hi << 32) | last_lo;
+    if (was == a.base + 3ull * gridDim.x - 1 && a.dyn_rows > 0) {
+      for (int i = lane; i < a.ct * a.shards * kWaves; i += 64)
+        __hip_atomic_store(a.queues + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -989,7 +1081,20 @@ struct FusedPlan {
   int64_t groups;
   int64_t rows_per_g;
   int blocks;
+  int dyn_rows;   // per-thread streamed rows handed out dynamically
+  int dyn_chunk;  // rows per thread in one chunk
 };
+
+// Share of each thread's streamed rows (after the prefetched ones) that is
+// handed out dynamically in phase 3 (percent; TFMA_BN_DYN_PCT, default 20).
+int dyn_pct() {
+  static int v = [] {
+    const char* e = getenv("TFMA_BN_DYN_PCT");
+    const int p = e ? atoi(e) : 20;
+    return p < 0 ? 0 : (p > 100 ? 100 : p);
+  }();
+  return v;
+}
 
 bool make_fused_plan(const BnGeometry& g, int vec, int blocks_per_cu, FusedPlan* fp) {
   if (!g.nhwc || blocks_per_cu < 1 || g.c % vec != 0) return false;
@@ -1010,7 +1115,27 @@ bool make_fused_plan(const BnGeometry& g, int vec, int blocks_per_cu, FusedPlan*
   fp->rows_per_g = (g.rows + groups - 1) / groups;
   fp->groups = (g.rows + fp->rows_per_g - 1) / fp->rows_per_g;
   fp->blocks = static_cast<int>(fp->groups * fp->ct);
+  fp->dyn_rows = 0;
+  fp->dyn_chunk = 1;
   return true;
+}
+
+// Fills in the dynamic share for kernel <Tr, kGrad>: resident rows KR + KL,
+// prefetched rows PA + PB and U rows per loop step (chunks of 2U rows).
+void set_dynamic_share(FusedPlan* fp, int resident, int prefetched, int u) {
+  const int ry = kFusedThreads >> fp->tx_shift;
+  const int64_t nk = (fp->rows_per_g + ry - 1) / ry;
+  const int64_t streamed = nk - resident - prefetched;
+  static const int mult = [] {
+    const char* e = getenv("TFMA_BN_DYN_CHUNK");  // chunk = mult * U rows per thread
+    const int m = e ? atoi(e) : 2;
+    return m < 1 ? 1 : (m > 8 ? 8 : m);
+  }();
+  const int chunk = mult * u;
+  int64_t d = streamed * dyn_pct() / 100 / chunk * chunk;
+  if (d < chunk) d = 0;
+  fp->dyn_rows = static_cast<int>(d);
+  fp->dyn_chunk = chunk;
 }
 
 // Per-device state of the fused kernels' grid barrier: a monotonic arrival
@@ -1019,6 +1144,10 @@ bool make_fused_plan(const BnGeometry& g, int vec, int blocks_per_cu, FusedPlan*
 // device are chained (a launch on another stream waits for the previous
 // one), so at most one persistent grid is resident at a time and every
 // launch knows the counter's starting value.
+// The allocation also holds the dynamic-chunk counters (from byte 256),
+// which the last workgroup of each launch zeroes again.
+constexpr size_t kQueueOffset = 256;
+constexpr size_t kStateBytes = 256 + 4096 * sizeof(unsigned);  // <= 512 tiles x 8 waves
 struct BarrierState {
   std::mutex mu;
   unsigned long long* counter = nullptr;  // [0] arrivals, [1] timeout flag
@@ -1044,9 +1173,9 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   std::lock_guard<std::mutex> lk(bs->mu);
   if (!bs->counter) {
     void* p = nullptr;
-    hipError_t e = hipMalloc(&p, 256);
+    hipError_t e = hipMalloc(&p, kStateBytes);
     if (e != hipSuccess) return e;
-    e = hipMemset(p, 0, 256);
+    e = hipMemset(p, 0, kStateBytes);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&bs->last, hipEventDisableTiming);
     if (e != hipSuccess) {
       (void)hipFree(p);
@@ -1074,6 +1203,20 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   fa.barrier = bs->counter;
   fa.base = bs->base;
   fa.timeout_flag = reinterpret_cast<unsigned*>(bs->counter + 1);
+  fa.queues = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(bs->counter) + kQueueOffset);
+  {
+    FusedPlan fd = fp;
+    constexpr int kPre = kGrad ? Resident<Tr>::kPaGrad + Resident<Tr>::kPbGrad
+                               : Resident<Tr>::kPaFwd + Resident<Tr>::kPbFwd;
+    set_dynamic_share(&fd, fused_kr<Tr, kGrad>() + fused_kl<Tr, kGrad>(), kPre, kGrad ? 4 : 8);
+    fa.dyn_chunk = fd.dyn_chunk;
+    const size_t slots = (kStateBytes - kQueueOffset) / sizeof(unsigned);
+    const size_t per_shard = static_cast<size_t>(fp.ct) * (kFusedThreads / 64);
+    size_t shards = slots / per_shard;
+    if (shards > 16) shards = 16;
+    fa.shards = shards > 0 ? static_cast<int>(shards) : 1;
+    fa.dyn_rows = shards > 0 ? fd.dyn_rows : 0;
+  }
   fa.fin = fin;
   fa.fin.groups = fp.groups;
   {
@@ -1086,7 +1229,8 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  bs->base += 2ull * static_cast<unsigned long long>(fp.blocks);  // two barriers
+  // Two barriers and the exit count.
+  bs->base += 3ull * static_cast<unsigned long long>(fp.blocks);
   bs->last_stream = stream;
   bs->used = true;
   return hipEventRecord(bs->last, stream);
