@@ -1,7 +1,8 @@
 /*
  * tfcpu_oracle.c - CPU restatement of TensorFlow's CPU kernels for the hot
- * path (FusedBatchNormV3 / FusedBatchNormGradV3, ResourceApplyAdam, and the
- * elementwise ops behind BiasAdd+Relu, AddV2+Relu, Mul+Add).
+ * path (FusedBatchNormV3 / FusedBatchNormGradV3, ResourceApplyAdam, the
+ * elementwise ops behind BiasAdd+Relu, AddV2+Relu, Mul+Add, and their
+ * backward counterparts ReluGrad and BiasAddGrad).
  *
  * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP
  * library and the CPU baseline ("port") that bench.py times; nothing in the
@@ -17,7 +18,9 @@
  *   - Adam inputs / alpha / dtypes: musa_ext/kernels/training/
  *     musa_applyadam_op.cc:158-186, 224-246, 645-682 (alpha is computed the
  *     TF-CPU way, in T, not in double as the reference does).
- *   - BiasAdd channel dimension: musa_ext/kernels/nn/musa_biasadd_op.cc:31-52.
+ *   - BiasAdd channel dimension: musa_ext/kernels/nn/musa_biasadd_op.cc:31-52;
+ *     BiasAddGrad: musa_ext/kernels/nn/musa_biasadd_grad_op.cc:31-69;
+ *     ReluGrad: musa_ext/kernels/nn/musa_relu_grad_op.cc:19-46.
  *   - Broadcasting: musa_ext/kernels/math/musa_add_op.cc:194-220, 397-403;
  *     musa_ext/kernels/fusion/musa_shifted_affine_map_op.cc:108-165.
  * Summation order is the one deliberate difference from TF: BN sums are
