@@ -187,10 +187,13 @@ int TFMA_MusaResourceApplyAdamMixed(void* stream, TFMA_Tensor* var, TFMA_Tensor*
  * vars/ms/vs/grads: N tensors each.  With fp32 vars the grads may all be
  * half or bfloat16 instead (attr Tgrad, as the reference op's T/Tgrad pair):
  * each tensor then updates as TFMA_MusaResourceApplyAdamMixed.  The
- * per-launch tensor table lives in
- * `workspace` (TFMA_GroupedApplyAdamWorkspaceBytes); the library uploads it
- * on the stream, so the workspace must stay allocated until the launch has
- * run. */
+ * per-launch table (the tensor entries and a tensor index per 8192-element
+ * chunk; its size depends on the tensors' element counts, hence `vars`)
+ * lives in `workspace` (TFMA_GroupedApplyAdamWorkspaceBytes); the library
+ * uploads it on the stream, so the workspace must stay allocated until the
+ * launch has run.  The library also keeps device copies of the last few
+ * tables per device: a call with the same tensors as an earlier one uploads
+ * nothing and leaves the workspace untouched. */
 int TFMA_GroupedApplyAdamWorkspaceBytes(int n, const TFMA_Tensor* vars,
                                         size_t* bytes, TFMA_Status* status);
 

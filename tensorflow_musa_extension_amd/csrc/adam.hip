@@ -157,8 +157,8 @@ __global__ __launch_bounds__(kThreads) void adam_chunk_kernel(
 }
 
 // Grouped variant: workgroup b updates chunk b of the concatenation of all
-// tensors; the tensor is found by binary search over first_chunk (uniform
-// across the workgroup, so it runs on scalar loads).
+// tensors; its tensor is chunk_map[b] (the uint32 array after the n_tensors
+// entries), two dependent scalar loads instead of a binary search.
 template <class Tr, class Tg, bool kNesterov>
 __global__ __launch_bounds__(kThreads) void adam_grouped_kernel(
     const AdamTensorEntry* __restrict__ table, int n_tensors,
@@ -166,12 +166,8 @@ __global__ __launch_bounds__(kThreads) void adam_grouped_kernel(
   using S = typename Tr::S;
   using SG = typename Tg::S;
   const int64_t b = blockIdx.x;
-  int lo = 0, hi = n_tensors;
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (table[mid].first_chunk <= b) lo = mid; else hi = mid;
-  }
-  const AdamTensorEntry e = table[lo];
+  const uint32_t* __restrict__ chunk_map = reinterpret_cast<const uint32_t*>(table + n_tensors);
+  const AdamTensorEntry e = table[chunk_map[b]];
   const int64_t start = (b - e.first_chunk) * kGroupedAdamChunk;
   int64_t len = e.n - start;
   if (len > kGroupedAdamChunk) len = kGroupedAdamChunk;

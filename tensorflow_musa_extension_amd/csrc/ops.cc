@@ -226,7 +226,7 @@ class VarLocks {
 // ---------------------------------------------------------------------------
 class PinnedRing {
  public:
-  static constexpr size_t kSlotBytes = 64 * 1024;
+  static constexpr size_t kSlotBytes = 1024 * 1024;
   static constexpr int kSlots = 16;
 
   // Copies `bytes` from `src` to device `dst` on `stream`.
@@ -234,7 +234,7 @@ class PinnedRing {
                     hipStream_t stream) {
     std::lock_guard<std::mutex> lk(mu_);
     if (bytes > kSlotBytes) {
-      // Large table: synchronous copy (rare; > 1300 tensors).
+      // Larger than a slot (> ~256M parameters of chunk map): synchronous copy.
       hipError_t e = hipStreamSynchronize(stream);
       if (e != hipSuccess) return e;
       return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
@@ -281,6 +281,103 @@ class PinnedRing {
 PinnedRing& pinned_ring() {
   static PinnedRing* r = new PinnedRing();
   return *r;
+}
+
+// ---------------------------------------------------------------------------
+// Device copies of recently used grouped-Adam tables, per device.  Training
+// calls the grouped update with the same tensors every step, so the table
+// (tensor pointers, sizes, chunk offsets) repeats; a call whose table equals
+// a cached one launches on the cached copy and uploads nothing.  A slot is
+// refilled only after the event recorded behind its last use has completed;
+// a call on another stream first waits for the slot's fill.
+// ---------------------------------------------------------------------------
+class AdamTableCache {
+ public:
+  static constexpr int kSlots = 8;
+  static constexpr int kDevices = 64;
+
+  // The cached device table equal to `t`, made ready on `stream`, or null.
+  // On success the caller launches and then calls mark_used().
+  const void* find(int dev, const std::vector<uint8_t>& t, hipStream_t stream, int* slot) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (dev < 0 || dev >= kDevices) return nullptr;
+    for (int i = 0; i < kSlots; ++i) {
+      Slot& s = slots_[dev][i];
+      if (!s.valid || s.host.size() != t.size() || memcmp(s.host.data(), t.data(), t.size()) != 0)
+        continue;
+      if (s.fill_stream != stream && hipStreamWaitEvent(stream, s.ready, 0) != hipSuccess)
+        return nullptr;
+      s.tick = ++tick_;
+      *slot = i;
+      return s.dev;
+    }
+    return nullptr;
+  }
+
+  void mark_used(int dev, int slot, hipStream_t stream) {
+    std::lock_guard<std::mutex> lk(mu_);
+    (void)hipEventRecord(slots_[dev][slot].used, stream);
+  }
+
+  // Keeps a copy of the table the caller has just uploaded to `ws` on
+  // `stream` (the copy is enqueued behind the launch that reads `ws`).
+  // Best effort: any failure just leaves the table uncached.
+  void fill(int dev, const std::vector<uint8_t>& t, const void* ws, hipStream_t stream) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (dev < 0 || dev >= kDevices) return;
+    int pick = -1;
+    for (int i = 0; i < kSlots; ++i) {
+      Slot& s = slots_[dev][i];
+      if (s.valid && hipEventQuery(s.used) != hipSuccess) continue;  // still in use
+      if (pick < 0 || !s.valid || (slots_[dev][pick].valid && s.tick < slots_[dev][pick].tick))
+        pick = i;
+      if (!s.valid) break;
+    }
+    if (pick < 0) return;
+    Slot& s = slots_[dev][pick];
+    const size_t bytes = t.size();
+    s.valid = false;
+    if (!s.ready) {
+      if (hipEventCreateWithFlags(&s.ready, hipEventDisableTiming) != hipSuccess) return;
+      if (hipEventCreateWithFlags(&s.used, hipEventDisableTiming) != hipSuccess) return;
+    }
+    if (s.cap < bytes) {
+      if (s.dev) (void)hipFree(s.dev);  // its last use has completed
+      s.dev = nullptr;
+      s.cap = 0;
+      void* p = nullptr;
+      if (hipMalloc(&p, bytes) != hipSuccess) return;
+      s.dev = p;
+      s.cap = bytes;
+    }
+    if (hipMemcpyAsync(s.dev, ws, bytes, hipMemcpyDeviceToDevice, stream) != hipSuccess) return;
+    if (hipEventRecord(s.ready, stream) != hipSuccess) return;
+    if (hipEventRecord(s.used, stream) != hipSuccess) return;
+    s.host = t;
+    s.fill_stream = stream;
+    s.tick = ++tick_;
+    s.valid = true;
+  }
+
+ private:
+  struct Slot {
+    bool valid = false;
+    std::vector<uint8_t> host;
+    void* dev = nullptr;
+    size_t cap = 0;
+    hipEvent_t ready = nullptr;
+    hipEvent_t used = nullptr;
+    hipStream_t fill_stream = nullptr;
+    uint64_t tick = 0;
+  };
+  std::mutex mu_;
+  Slot slots_[kDevices][kSlots];
+  uint64_t tick_ = 0;
+};
+
+AdamTableCache& adam_table_cache() {
+  static AdamTableCache* c = new AdamTableCache();
+  return *c;
 }
 
 // ---------------------------------------------------------------------------
@@ -908,12 +1005,26 @@ int TFMA_MusaResourceApplyAdamMixed(void* stream, TFMA_Tensor* var, TFMA_Tensor*
                     "MusaResourceApplyAdamMixed", status);
 }
 
+namespace {
+// Table blob of the grouped update: the tensor entries, then one uint32
+// tensor index per chunk (so a workgroup finds its tensor with one load).
+size_t grouped_table_bytes(int entries, int64_t chunks) {
+  return static_cast<size_t>(entries) * sizeof(AdamTensorEntry) +
+         static_cast<size_t>(chunks) * sizeof(uint32_t);
+}
+}  // namespace
+
 int TFMA_GroupedApplyAdamWorkspaceBytes(int n, const TFMA_Tensor* vars, size_t* bytes,
                                         TFMA_Status* status) {
-  (void)vars;
-  if (n < 1 || !bytes)
+  if (n < 1 || !bytes || !vars)
     return set_status(status, TFMA_INVALID_ARGUMENT, "N must be >= 1");
-  *bytes = (static_cast<size_t>(n) * sizeof(AdamTensorEntry) + 255) & ~size_t(255);
+  int64_t chunks = 0;
+  for (int i = 0; i < n; ++i) {
+    if (!valid_tensor(&vars[i]))
+      return set_status(status, TFMA_INVALID_ARGUMENT, "tensor %d: invalid tensor", i);
+    chunks += (num_elements(&vars[i]) + kGroupedAdamChunk - 1) / kGroupedAdamChunk;
+  }
+  *bytes = (grouped_table_bytes(n, chunks) + 255) & ~size_t(255);
   return ok(status);
 }
 
@@ -988,13 +1099,32 @@ int TFMA_GroupedResourceApplyAdam(void* stream, int n, TFMA_Tensor* vars, TFMA_T
     locks.lock();
   }
   if (table.empty()) return ok(status);
+  // Blob: entries, then the tensor index of every chunk.
+  std::vector<uint8_t> blob(grouped_table_bytes(static_cast<int>(table.size()), chunks));
+  memcpy(blob.data(), table.data(), table.size() * sizeof(AdamTensorEntry));
+  uint32_t* cmap = reinterpret_cast<uint32_t*>(blob.data() + table.size() * sizeof(AdamTensorEntry));
+  for (size_t i = 0; i < table.size(); ++i) {
+    const int64_t end = i + 1 < table.size() ? table[i + 1].first_chunk : chunks;
+    for (int64_t c = table[i].first_chunk; c < end; ++c) cmap[c] = static_cast<uint32_t>(i);
+  }
   hipStream_t strm = as_stream(stream);
-  hipError_t e = pinned_ring().upload(workspace, table.data(),
-                                      table.size() * sizeof(AdamTensorEntry), strm);
+  int dev = -1;
+  (void)hipGetDevice(&dev);
+  int slot = -1;
+  AdamTableCache& cache = adam_table_cache();
+  if (const void* cached = cache.find(dev, blob, strm, &slot)) {
+    hipError_t e = LaunchGroupedApplyAdam(t, tg, static_cast<const AdamTensorEntry*>(cached),
+                                          static_cast<int>(table.size()), chunks, s,
+                                          use_nesterov != 0, strm);
+    cache.mark_used(dev, slot, strm);
+    return hip_status(status, e, "MusaGroupedResourceApplyAdam");
+  }
+  hipError_t e = pinned_ring().upload(workspace, blob.data(), blob.size(), strm);
   if (e != hipSuccess) return hip_status(status, e, "MusaGroupedResourceApplyAdam table upload");
   e = LaunchGroupedApplyAdam(t, tg, static_cast<const AdamTensorEntry*>(workspace),
                              static_cast<int>(table.size()), chunks, s, use_nesterov != 0,
                              strm);
+  if (e == hipSuccess) cache.fill(dev, blob, workspace, strm);
   return hip_status(status, e, "MusaGroupedResourceApplyAdam");
 }
 

@@ -103,11 +103,55 @@ def eltwise_cases(store):
         store[f"ew_{dt}/relu"] = oracle.eltwise("relu", [x], dt)
 
 
+def backward_cases(store):
+    """ReluGrad, BiasAddGrad and mixed-precision Adam (fp32 state, 16-bit grad)."""
+    rng = np.random.default_rng(13)
+    for dt in ("float32", "float16", "bfloat16"):
+        g = rng.standard_normal((33, 17))
+        f = rng.standard_normal((33, 17))
+        g.ravel()[:6] = [np.nan, np.inf, -np.inf, -2.0, 0.0, -0.0]
+        f.ravel()[:6] = [-1.0, 0.0, 1.0, -3.0, 0.0, 5.0]
+        gs, fs = oracle.to_storage(g, dt), oracle.to_storage(f, dt)
+        rg = oracle.eltwise("relu_grad", [gs, fs], dt)
+        with np.errstate(invalid="ignore"):  # inf * 0 is NaN, as in TF
+            want = oracle.to_f32(gs, dt).astype(np.float64) * (oracle.to_f32(fs, dt) > 0)
+            got = oracle.to_f32(rg, dt).astype(np.float64)
+            assert np.array_equal(np.isnan(got), np.isnan(want))
+            ok = ~np.isnan(want)
+            assert np.array_equal(got[ok], want[ok]) and np.array_equal(
+                np.signbit(got[ok]), np.signbit(want[ok])), dt
+        store[f"relu_grad_{dt}/g"], store[f"relu_grad_{dt}/f"], store[f"relu_grad_{dt}/out"] = gs, fs, rg
+        for shape, fmt in (((2, 8, 8, 32), "NHWC"), ((2, 32, 8, 8), "NCHW")):
+            x = oracle.to_storage(rng.standard_normal(shape), dt)
+            out = oracle.bias_add_grad(x, fmt, dt)
+            axes = tuple(i for i in range(4) if i != (1 if fmt == "NCHW" else 3))
+            ref = oracle.to_f32(x, dt).astype(np.float64).sum(axis=axes)
+            tol = 1e-6 if dt == "float32" else 1e-2
+            assert np.max(np.abs(oracle.to_f32(out, dt) - ref)) <= tol * np.max(np.abs(ref))
+            store[f"bias_add_grad_{dt}_{fmt}/x"], store[f"bias_add_grad_{dt}_{fmt}/out"] = x, out
+    for gdt in ("float16", "bfloat16"):
+        n = 1031
+        var = (0.02 * rng.standard_normal(n)).astype(np.float32)
+        m = np.zeros(n, np.float32)
+        v = np.zeros(n, np.float32)
+        g = oracle.to_storage(1e-3 * rng.standard_normal(n), gdt)
+        store[f"adam_mixed_{gdt}/var0"], store[f"adam_mixed_{gdt}/grad"] = var.copy(), g.copy()
+        sc = [np.float32(a) for a in (0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7)]
+        oracle.adam_mixed(var, m, v, g, *[float(a) for a in sc], grad_dtype=gdt)
+        gd = oracle.to_f32(g, gdt).astype(np.float64)
+        f = lambda a: np.float64(np.float32(a))
+        m1 = gd * (1 - f(0.9))
+        assert np.allclose(m, m1, rtol=2e-7, atol=0), gdt
+        store[f"adam_mixed_{gdt}/var"], store[f"adam_mixed_{gdt}/m"], store[f"adam_mixed_{gdt}/v"] = var, m, v
+        store[f"adam_mixed_{gdt}/scalars"] = np.array([float(a) for a in sc])
+
+
 def main():
     store = {}
     bn_cases(store)
     adam_cases(store)
     eltwise_cases(store)
+    backward_cases(store)
     np.savez_compressed(OUT, **store)
     print(f"wrote {OUT}: {len(store)} arrays, {os.path.getsize(OUT)} bytes")
 

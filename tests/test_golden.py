@@ -103,3 +103,61 @@ def test_gpu_adam_and_eltwise_match_golden(g, dev, dt):
         assert_bitwise(to_np(arr, dt), g[f"adam_{dt}/{k}"], f"adam {dt} {k}")
     for k, t in outs.items():
         assert_bitwise(to_np(t, dt), g[f"ew_{dt}/{k}"], f"{dt} {k}")
+
+
+def _nan_aware_bitwise(got, want, dtype, name):
+    nan_w = np.isnan(oracle.to_f32(want, dtype))
+    assert np.array_equal(np.isnan(oracle.to_f32(got, dtype)), nan_w), name
+    assert_bitwise(got[~nan_w], want[~nan_w], name)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+def test_oracle_reproduces_backward_ops(g, dt):
+    _nan_aware_bitwise(oracle.eltwise("relu_grad", [g[f"relu_grad_{dt}/g"], g[f"relu_grad_{dt}/f"]],
+                                      dt), g[f"relu_grad_{dt}/out"], dt, "relu_grad")
+    for fmt in ("NHWC", "NCHW"):
+        assert_bitwise(oracle.bias_add_grad(g[f"bias_add_grad_{dt}_{fmt}/x"], fmt, dt),
+                       g[f"bias_add_grad_{dt}_{fmt}/out"], f"bias_add_grad {fmt}")
+
+
+@pytest.mark.parametrize("gdt", ["float16", "bfloat16"])
+def test_oracle_reproduces_adam_mixed(g, gdt):
+    var = g[f"adam_mixed_{gdt}/var0"].copy()
+    m, v = np.zeros_like(var), np.zeros_like(var)
+    oracle.adam_mixed(var, m, v, g[f"adam_mixed_{gdt}/grad"], *g[f"adam_mixed_{gdt}/scalars"],
+                      grad_dtype=gdt)
+    for k, arr in (("var", var), ("m", m), ("v", v)):
+        assert_bitwise(arr, g[f"adam_mixed_{gdt}/{k}"], f"adam_mixed {gdt} {k}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", DTYPES)
+def test_gpu_backward_ops_match_golden(g, dev, dt):
+    import torch
+    import tensorflow_musa_extension_amd as tfma
+    from tests.helpers import to_dev, to_np
+    ops = tfma.raw_ops
+    rg = ops.ReluGrad(to_dev(g[f"relu_grad_{dt}/g"], dt, dev), to_dev(g[f"relu_grad_{dt}/f"], dt, dev))
+    outs = {fmt: ops.BiasAddGrad(to_dev(g[f"bias_add_grad_{dt}_{fmt}/x"], dt, dev), data_format=fmt)
+            for fmt in ("NHWC", "NCHW")}
+    torch.cuda.synchronize()
+    _nan_aware_bitwise(to_np(rg, dt), g[f"relu_grad_{dt}/out"], dt, "relu_grad")
+    tol = 1e-5 if dt == "float32" else 1e-2
+    for fmt, t in outs.items():
+        assert_close(to_np(t, dt), g[f"bias_add_grad_{dt}_{fmt}/out"], dt, tol, f"bias_add_grad {fmt}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("gdt", ["float16", "bfloat16"])
+def test_gpu_adam_mixed_matches_golden(g, dev, gdt):
+    import torch
+    import tensorflow_musa_extension_amd as tfma
+    from tests.helpers import to_dev, to_np
+    ops = tfma.raw_ops
+    var = torch.from_numpy(g[f"adam_mixed_{gdt}/var0"].copy()).to(dev)
+    m, v = torch.zeros_like(var), torch.zeros_like(var)
+    ops.MusaResourceApplyAdamMixed(var, m, v, *g[f"adam_mixed_{gdt}/scalars"],
+                                   to_dev(g[f"adam_mixed_{gdt}/grad"], gdt, dev))
+    torch.cuda.synchronize()
+    for k, t in (("var", var), ("m", m), ("v", v)):
+        assert_bitwise(t.cpu().numpy(), g[f"adam_mixed_{gdt}/{k}"], f"adam_mixed {gdt} {k}")

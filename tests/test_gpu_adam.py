@@ -275,3 +275,36 @@ def test_grouped_adam_cfg5_sampled(dev):
             assert_bitwise(sample(ts, i), r, f"cfg5 tensor {i} {name}")
     del tv, tm, tw, tg
     torch.cuda.empty_cache()
+
+
+def test_grouped_repeated_steps_use_cached_table(dev):
+    """The same tensors every step (as in training): the second and later
+    calls run on the library's cached device table - on the caller's stream
+    and on a second stream - and still match the oracle bit for bit."""
+    rng = np.random.default_rng(12)
+    shapes = [(64,), (3, 3, 64, 64), (1000, 2048), (7,)]
+    vars_ = [to_dev(gen(rng, s, "float32", scale=0.02), "float32", dev) for s in shapes]
+    ms = [torch.zeros(s, device=dev) for s in shapes]
+    vs = [torch.zeros(s, device=dev) for s in shapes]
+    grads = [to_dev(gen(rng, s, "float32", scale=1e-3), "float32", dev) for s in shapes]
+    refs = [[to_np(v, "float32").copy(), np.zeros(int(np.prod(s)), np.float32).reshape(s),
+             np.zeros(int(np.prod(s)), np.float32).reshape(s)] for v, s in zip(vars_, shapes)]
+    side = torch.cuda.Stream(device=dev)
+    b1p = b2p = 1.0
+    for step in range(4):
+        b1p, b2p = _t_scalar(b1p * B1, "float32"), _t_scalar(b2p * B2, "float32")
+        if step == 2:
+            side.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(side):
+                ops.MusaGroupedResourceApplyAdam(vars_, ms, vs, grads, b1p, b2p, LR, B1, B2, EPS)
+            torch.cuda.current_stream(dev).wait_stream(side)
+        else:
+            ops.MusaGroupedResourceApplyAdam(vars_, ms, vs, grads, b1p, b2p, LR, B1, B2, EPS)
+        for (rv, rm, rw), gt in zip(refs, grads):
+            oracle.adam(rv, rm, rw, to_np(gt, "float32"), b1p, b2p, _t_scalar(LR, "float32"),
+                        _t_scalar(B1, "float32"), _t_scalar(B2, "float32"),
+                        _t_scalar(EPS, "float32"))
+    torch.cuda.synchronize()
+    for i, (v, m, w) in enumerate(zip(vars_, ms, vs)):
+        for name, t, r in (("var", v, refs[i][0]), ("m", m, refs[i][1]), ("v", w, refs[i][2])):
+            assert_bitwise(to_np(t, "float32"), r, f"tensor {i} {name}")
