@@ -520,7 +520,7 @@ template <> struct Resident<TF16> {
   static constexpr int kPaFwd = 0, kPbFwd = 4, kPaGrad = 0, kPbGrad = 0;
 };
 template <> struct Resident<TBF16> {
-  static constexpr int kRegFwd = 10, kRegGrad = 4, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kRegFwd = 8, kRegGrad = 4, kLdsFwd = 18, kLdsGrad = 9;
   static constexpr int kPaFwd = 4, kPbFwd = 4, kPaGrad = 4, kPbGrad = 8;
 };
 
@@ -539,6 +539,8 @@ struct FusedArgs {
   float4* coef;
   unsigned long long* barrier;  // device-wide arrival counter
   unsigned long long base;      // its value when this launch starts
+  unsigned* sub;                // 8 arrival counters (workgroup id mod 8), 256 B apart
+  unsigned sub_last[2][8];      // value class r's last arrival at barrier k sees
   unsigned* timeout_flag;
   unsigned* queues;             // [ct][wave] chunk counters, zero between launches
   int dyn_rows;                 // streamed rows per thread handed out dynamically
@@ -571,16 +573,34 @@ __device__ inline uint64_t load_shared(const void* p) {
 // two halves a workgroup may issue loads that do not depend on other
 // workgroups (the phase-3 prefetch), so the barrier's latency overlaps with
 // memory traffic.
-__device__ inline void grid_arrive(const FusedArgs& a) {
+// Arrivals are counted in two levels: workgroup b counts itself on counter
+// b mod 8 (consecutive workgroups sit on different XCDs), and the last of
+// each of those classes counts the class on the global counter.  When all
+// workgroups arrive at once (after the finals), 256 atomics on one address
+// queue for ~4 us; 8 classes of 32 do not.
+__device__ inline unsigned barrier_classes() { return gridDim.x < 8 ? gridDim.x : 8; }
+
+__device__ inline void grid_arrive(const FusedArgs& a, unsigned k) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // my shared stores are done
   __syncthreads();
-  if (threadIdx.x == 0)
-    __hip_atomic_fetch_add(a.barrier, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) {
+    const unsigned r = blockIdx.x & 7;
+    // Uniform selects, not a dynamic index into the by-value arguments
+    // (which would put them in scratch memory).
+    unsigned last = a.sub_last[k - 1][0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) last = r == static_cast<unsigned>(i) ? a.sub_last[k - 1][i] : last;
+    const unsigned old =
+        __hip_atomic_fetch_add(a.sub + 64 * r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == last)
+      __hip_atomic_fetch_add(a.barrier, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 __device__ inline void grid_wait(const FusedArgs& a, unsigned k) {
   if (threadIdx.x == 0) {
-    const unsigned long long target = a.base + static_cast<unsigned long long>(k) * gridDim.x;
+    const unsigned long long target =
+        a.base + static_cast<unsigned long long>(k) * barrier_classes();
     unsigned spins = 0;
     while (__hip_atomic_load(a.barrier, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
       __builtin_amdgcn_s_sleep(2);
@@ -748,7 +768,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     store_shared(&a.partial[g * a.c + static_cast<int64_t>(ct) * width + tid],
                  __builtin_bit_cast(uint64_t, make_float2(sa, sb)));
   }
-  grid_arrive(a);
+  grid_arrive(a, 1);
 
   // Phase-3 prefetch, part A: the last streamed rows (phase 3 runs
   // last-to-first), loaded by the waves that have no phase-2 channel so the
@@ -793,7 +813,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     }
   }
   zero_side_outputs<kGrad>(a.fin);
-  grid_arrive(a);
+  grid_arrive(a, 2);
 
   // Prefetch part B: the next rows, in flight during the second barrier and
   // the coefficient loads.
@@ -939,8 +959,8 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     }
   }
 
-  // Exit: the last workgroup to leave (third arrival on the barrier counter)
-  // zeroes the chunk counters for the next launch.
+  // Exit: the last workgroup to leave (counted on the global barrier counter
+  // after both barriers) zeroes the chunk counters for the next launch.
   __syncthreads();
   if (wave == 0) {
     unsigned long long old = 0;
@@ -952,7 +972,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     const unsigned long long last_hi =
         __builtin_amdgcn_readfirstlane(static_cast<unsigned>(old >> 32));
     const unsigned long long was = (last_hi << 32) | last_lo;
-    if (was == a.base + 3ull * gridDim.x - 1 && a.dyn_rows > 0) {
+    if (was == a.base + 2ull * barrier_classes() + gridDim.x - 1 && a.dyn_rows > 0) {
       for (int i = lane; i < a.ct * a.shards * kWaves; i += 64)
         __hip_atomic_store(a.queues + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1147,11 +1167,14 @@ void set_dynamic_share(FusedPlan* fp, int resident, int prefetched, int u) {
 // The allocation also holds the dynamic-chunk counters (from byte 256),
 // which the last workgroup of each launch zeroes again.
 constexpr size_t kQueueOffset = 256;
-constexpr size_t kStateBytes = 256 + 4096 * sizeof(unsigned);  // <= 512 tiles x 8 waves
+constexpr size_t kQueueBytes = 4096 * sizeof(unsigned);  // <= 512 tiles x 8 waves
+constexpr size_t kSubOffset = kQueueOffset + kQueueBytes;  // 8 class counters, 256 B apart
+constexpr size_t kStateBytes = kSubOffset + 8 * 256;
 struct BarrierState {
   std::mutex mu;
   unsigned long long* counter = nullptr;  // [0] arrivals, [1] timeout flag
   unsigned long long base = 0;
+  unsigned sub_base[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // class counters (mod 2^32)
   hipEvent_t last = nullptr;
   hipStream_t last_stream = nullptr;
   bool used = false;
@@ -1202,6 +1225,12 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   fa.coef = coef;
   fa.barrier = bs->counter;
   fa.base = bs->base;
+  fa.sub = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(bs->counter) + kSubOffset);
+  for (int r = 0; r < 8; ++r) {
+    const unsigned members = static_cast<unsigned>((fp.blocks + 7 - r) / 8);
+    fa.sub_last[0][r] = bs->sub_base[r] + members - 1;
+    fa.sub_last[1][r] = bs->sub_base[r] + 2 * members - 1;
+  }
   fa.timeout_flag = reinterpret_cast<unsigned*>(bs->counter + 1);
   fa.queues = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(bs->counter) + kQueueOffset);
   {
@@ -1210,7 +1239,7 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
                                : Resident<Tr>::kPaFwd + Resident<Tr>::kPbFwd;
     set_dynamic_share(&fd, fused_kr<Tr, kGrad>() + fused_kl<Tr, kGrad>(), kPre, kGrad ? 4 : 8);
     fa.dyn_chunk = fd.dyn_chunk;
-    const size_t slots = (kStateBytes - kQueueOffset) / sizeof(unsigned);
+    const size_t slots = kQueueBytes / sizeof(unsigned);
     const size_t per_shard = static_cast<size_t>(fp.ct) * (kFusedThreads / 64);
     size_t shards = slots / per_shard;
     if (shards > 16) shards = 16;
@@ -1229,8 +1258,12 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // Two barriers and the exit count.
-  bs->base += 3ull * static_cast<unsigned long long>(fp.blocks);
+  // Per barrier: each class counter gets one arrival per member, the global
+  // counter one per non-empty class; the exit counts every workgroup.
+  const unsigned long long classes = fp.blocks < 8 ? fp.blocks : 8;
+  for (int r = 0; r < 8; ++r)
+    bs->sub_base[r] += 2u * static_cast<unsigned>((fp.blocks + 7 - r) / 8);
+  bs->base += 2ull * classes + static_cast<unsigned long long>(fp.blocks);
   bs->last_stream = stream;
   bs->used = true;
   return hipEventRecord(bs->last, stream);
