@@ -540,7 +540,7 @@ struct FusedArgs {
   unsigned long long* barrier;  // device-wide arrival counter
   unsigned long long base;      // its value when this launch starts
   unsigned* sub;                // 8 arrival counters (workgroup id mod 8), 256 B apart
-  unsigned sub_last[2][8];      // value class r's last arrival at barrier k sees
+  unsigned sub_last[3][8];      // value class r's last arrival sees at barrier 1, 2, exit
   unsigned* timeout_flag;
   unsigned* queues;             // [ct][wave] chunk counters, zero between launches
   int dyn_rows;                 // streamed rows per thread handed out dynamically
@@ -959,22 +959,32 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     }
   }
 
-  // Exit: the last workgroup to leave (counted on the global barrier counter
-  // after both barriers) zeroes the chunk counters for the next launch.
-  __syncthreads();
-  if (wave == 0) {
-    unsigned long long old = 0;
-    // Relaxed: every counter this workgroup touched was updated by atomics
-    // whose results it has already used.
-    if (lane == 0)
-      old = __hip_atomic_fetch_add(a.barrier, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned long long last_lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(old));
-    const unsigned long long last_hi =
-        __builtin_amdgcn_readfirstlane(static_cast<unsigned>(old >> 32));
-    const unsigned long long was = (last_hi << 32) | last_lo;
-    if (was == a.base + 2ull * barrier_classes() + gridDim.x - 1 && a.dyn_rows > 0) {
-      for (int i = lane; i < a.ct * a.shards * kWaves; i += 64)
-        __hip_atomic_store(a.queues + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Exit (only when chunks were handed out): counted like a third barrier
+  // arrival - class counter, then the global counter - and the workgroup
+  // that completes the count zeroes the chunk counters for the next launch.
+  // Relaxed: every counter this workgroup touched was updated by atomics
+  // whose results it has already used.
+  if (a.dyn_rows > 0) {
+    __syncthreads();
+    if (wave == 0) {
+      unsigned done = 0;
+      if (lane == 0) {
+        const unsigned r = blockIdx.x & 7;
+        unsigned last = a.sub_last[2][0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) last = r == static_cast<unsigned>(i) ? a.sub_last[2][i] : last;
+        const unsigned old =
+            __hip_atomic_fetch_add(a.sub + 64 * r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == last) {
+          const unsigned long long g =
+              __hip_atomic_fetch_add(a.barrier, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          done = g == a.base + 3ull * barrier_classes() - 1;
+        }
+      }
+      if (__builtin_amdgcn_readfirstlane(done)) {
+        for (int i = lane; i < a.ct * a.shards * kWaves; i += 64)
+          __hip_atomic_store(a.queues + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
 }
@@ -1230,6 +1240,7 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
     const unsigned members = static_cast<unsigned>((fp.blocks + 7 - r) / 8);
     fa.sub_last[0][r] = bs->sub_base[r] + members - 1;
     fa.sub_last[1][r] = bs->sub_base[r] + 2 * members - 1;
+    fa.sub_last[2][r] = bs->sub_base[r] + 3 * members - 1;
   }
   fa.timeout_flag = reinterpret_cast<unsigned*>(bs->counter + 1);
   fa.queues = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(bs->counter) + kQueueOffset);
@@ -1258,12 +1269,14 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // Per barrier: each class counter gets one arrival per member, the global
-  // counter one per non-empty class; the exit counts every workgroup.
+  // Per barrier (and per exit count, when chunks were handed out): each
+  // class counter gets one arrival per member, the global counter one per
+  // non-empty class.
+  const unsigned rounds = fa.dyn_rows > 0 ? 3u : 2u;
   const unsigned long long classes = fp.blocks < 8 ? fp.blocks : 8;
   for (int r = 0; r < 8; ++r)
-    bs->sub_base[r] += 2u * static_cast<unsigned>((fp.blocks + 7 - r) / 8);
-  bs->base += 2ull * classes + static_cast<unsigned long long>(fp.blocks);
+    bs->sub_base[r] += rounds * static_cast<unsigned>((fp.blocks + 7 - r) / 8);
+  bs->base += rounds * classes;
   bs->last_stream = stream;
   bs->used = true;
   return hipEventRecord(bs->last, stream);
