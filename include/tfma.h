@@ -335,13 +335,24 @@ void TFMA_FreeBuffer(void* buffer);
 /* ---------------------------------------------------------------------------
  * Kernel timing.  No reference counterpart (the reference removed its kernel
  * timing macros and points to external profilers).  When a kernel whose name
- * contains `name_substr` is launched by this library, HIP events are
- * recorded on the launch stream right before and after it; TFMA_TraceRead
- * returns the summed event time and the launch count.  TFMA_TraceEnable(NULL)
+ * contains `name_substr` is launched by this library, HIP events on the
+ * launch stream bracket it (the fused BatchNorm kernels carry them as the
+ * dispatch's own start and end events, hipExtLaunchKernelGGL; the others get
+ * event records right before and after the launch); TFMA_TraceRead returns
+ * the summed event time and the launch count.  TFMA_TraceEnable(NULL)
  * switches tracing off.  Not thread-safe against concurrent launches.
  * ------------------------------------------------------------------------- */
 int TFMA_TraceEnable(const char* name_substr, TFMA_Status* status);
 int TFMA_TraceRead(double* total_ms, int64_t* launches, TFMA_Status* status);
+
+/* Whether a fused BatchNorm launch on the current device gave up one of its
+ * grid-barrier waits (the bounded spin, ~0.5 s, ran out because the grid was
+ * not co-resident; that launch's outputs are wrong).  *timed_out = 1 if so;
+ * reset != 0 clears the flag.  Waits for the device to go idle
+ * (hipDeviceSynchronize) before reading: a diagnostic, not for hot loops.
+ * No reference counterpart: the reference's BatchNorm kernels have no
+ * grid-wide wait. */
+int TFMA_FusedBatchNormBarrierTimedOut(int32_t* timed_out, int32_t reset, TFMA_Status* status);
 
 /* Name of the last kernel this library launched on the calling thread (for
  * tests that check which path an op took). */

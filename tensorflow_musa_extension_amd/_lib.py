@@ -93,6 +93,7 @@ SIGNATURES = {
     "TFMA_TraceEnable": [_cs, _S],
     "TFMA_TraceRead": [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), _S],
     "TFMA_LastKernelName": [],
+    "TFMA_FusedBatchNormBarrierTimedOut": [ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, _S],
 }
 _RESTYPES = {"TFMA_Version": ctypes.c_char_p, "TFMA_LastKernelName": ctypes.c_char_p,
              "TFMA_FreeBuffer": None}

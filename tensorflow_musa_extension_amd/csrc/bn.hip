@@ -31,6 +31,8 @@
 // element, which keeps sum((x-K)^2) - sum(x-K)^2/n free of cancellation
 // when |mean| >> std; partials add exactly like plain sums because every
 // workgroup uses the same K.
+#include <hip/hip_ext.h>
+
 #include <mutex>
 
 #include "device_util.h"
@@ -1170,7 +1172,9 @@ void set_dynamic_share(FusedPlan* fp, int resident, int prefetched, int u) {
 
 // Per-device state of the fused kernels' grid barrier: a monotonic arrival
 // counter in device memory (zeroed once), its value before the next launch,
-// and the event and stream of the last fused launch.  Fused launches on one
+// and the event and stream of the last fused launch.  The event is the
+// dispatch's own end event (hipExtLaunchKernelGGL), not a marker after it:
+// a marker between kernels costs microseconds.  Fused launches on one
 // device are chained (a launch on another stream waits for the previous
 // one), so at most one persistent grid is resident at a time and every
 // launch knows the counter's starting value.
@@ -1185,7 +1189,8 @@ struct BarrierState {
   unsigned long long* counter = nullptr;  // [0] arrivals, [1] timeout flag
   unsigned long long base = 0;
   unsigned sub_base[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // class counters (mod 2^32)
-  hipEvent_t last = nullptr;
+  hipEvent_t last = nullptr;   // end of the last launch when it was not traced
+  hipEvent_t chain = nullptr;  // end of the last launch (`last` or a trace event)
   hipStream_t last_stream = nullptr;
   bool used = false;
 };
@@ -1209,7 +1214,8 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
     hipError_t e = hipMalloc(&p, kStateBytes);
     if (e != hipSuccess) return e;
     e = hipMemset(p, 0, kStateBytes);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&bs->last, hipEventDisableTiming);
+    if (e == hipSuccess)
+      e = hipEventCreateWithFlags(&bs->last, hipEventDisableTiming | hipEventReleaseToDevice);
     if (e != hipSuccess) {
       (void)hipFree(p);
       return e;
@@ -1217,7 +1223,7 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
     bs->counter = static_cast<unsigned long long*>(p);
   }
   if (bs->used && bs->last_stream != stream) {
-    hipError_t e = hipStreamWaitEvent(stream, bs->last, 0);
+    hipError_t e = hipStreamWaitEvent(stream, bs->chain, 0);
     if (e != hipSuccess) return e;
   }
   FusedArgs fa;
@@ -1259,14 +1265,18 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   }
   fa.fin = fin;
   fa.fin.groups = fp.groups;
+  const char* name = kGrad ? "tfma_bn_grad_fused" : "tfma_bn_fwd_fused";
+  SetLastKernel(name);
+  const TraceEvents tev = TraceTake(name);
+  hipEvent_t end = tev.end ? tev.end : bs->last;
   {
-    LaunchScope scope(stream, kGrad ? "tfma_bn_grad_fused" : "tfma_bn_fwd_fused");
     constexpr int KR = fused_kr<Tr, kGrad>();
     constexpr int KL = fused_kl<Tr, kGrad>();
     const size_t smem = fused_smem<Tr, kGrad>();
-    hipLaunchKernelGGL((bn_fused_nhwc_kernel<Tr, kGrad, KR, KL>), dim3(fp.blocks),
-                       dim3(kFusedThreads), smem, stream, fa);
+    hipExtLaunchKernelGGL((bn_fused_nhwc_kernel<Tr, kGrad, KR, KL>), dim3(fp.blocks),
+                          dim3(kFusedThreads), smem, stream, tev.start, end, 0u, fa);
   }
+  TraceCommit(tev);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // Per barrier (and per exit count, when chunks were handed out): each
@@ -1277,10 +1287,34 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   for (int r = 0; r < 8; ++r)
     bs->sub_base[r] += rounds * static_cast<unsigned>((fp.blocks + 7 - r) / 8);
   bs->base += rounds * classes;
+  bs->chain = end;
   bs->last_stream = stream;
   bs->used = true;
-  return hipEventRecord(bs->last, stream);
+  return hipSuccess;
 }
+
+}  // namespace
+
+hipError_t BnBarrierTimedOut(bool reset, bool* timed_out) {
+  *timed_out = false;
+  BarrierState* bs = barrier_state();
+  if (!bs) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(bs->mu);
+  if (!bs->counter) return hipSuccess;  // no fused launch on this device yet
+  hipError_t e = hipDeviceSynchronize();
+  unsigned flag = 0;
+  if (e == hipSuccess)
+    e = hipMemcpy(&flag, bs->counter + 1, sizeof(flag), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return e;
+  *timed_out = flag != 0;
+  if (reset && flag) {
+    const unsigned zero = 0;
+    e = hipMemcpy(bs->counter + 1, &zero, sizeof(zero), hipMemcpyHostToDevice);
+  }
+  return e;
+}
+
+namespace {
 
 // Partial-sum region: large enough for the split plan (either alignment)
 // and for the fused plan's at most fused_group_bound() row groups.

@@ -654,6 +654,18 @@ int TFMA_GetDeviceCount(int* count, TFMA_Status* status) {
   return ok(status);
 }
 
+int TFMA_FusedBatchNormBarrierTimedOut(int32_t* timed_out, int32_t reset,
+                                       TFMA_Status* status) {
+  if (!timed_out) return set_status(status, TFMA_INVALID_ARGUMENT, "timed_out is null");
+  bool t = false;
+  const hipError_t e = BnBarrierTimedOut(reset != 0, &t);
+  if (e != hipSuccess)
+    return set_status(status, TFMA_INTERNAL, "FusedBatchNorm barrier flag: %s",
+                      hipGetErrorString(e));
+  *timed_out = t ? 1 : 0;
+  return ok(status);
+}
+
 int TFMA_FusedBatchNormWorkspaceBytes(const TFMA_Tensor* x, const char* data_format,
                                       size_t* bytes, TFMA_Status* status) {
   if (!bytes || !valid_tensor(x))

@@ -22,6 +22,18 @@ void TraceBefore(hipStream_t stream, const char* kernel_name);
 void TraceAfter(hipStream_t stream);
 void SetLastKernel(const char* kernel_name);
 
+// Event pair for one launch of `kernel_name` when tracing is on for it (both
+// null otherwise).  The launcher hands them to hipExtLaunchKernelGGL, which
+// records them as the dispatch's own begin and end, so no marker packets sit
+// between kernels; TraceCommit then queues the pair.  The events are never
+// destroyed, and are handed out again only after they have completed.
+struct TraceEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t end = nullptr;
+};
+TraceEvents TraceTake(const char* kernel_name);
+void TraceCommit(const TraceEvents& ev);
+
 // Brackets one kernel launch: records the kernel name and, when tracing is
 // on for this name, HIP events around the launch.
 struct LaunchScope {
@@ -164,5 +176,8 @@ struct BnGradArgs {
 hipError_t LaunchBnGrad(DType t, const BnGeometry& g, const BnGradArgs& a,
                         void* workspace, size_t workspace_bytes,
                         hipStream_t stream);
+// Reads (and with `reset` clears) the current device's barrier-timeout flag
+// after a device synchronize.
+hipError_t BnBarrierTimedOut(bool reset, bool* timed_out);
 
 }  // namespace tfma

@@ -44,8 +44,10 @@ hipEvent_t take_event(TraceState& s) {
     s.pool.pop_back();
     return e;
   }
+  // Device-scope release: a default event would also write the caches back
+  // for the host (system scope), which costs microseconds between kernels.
   hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventReleaseToDevice) != hipSuccess) return nullptr;
   return e;
 }
 
@@ -78,6 +80,30 @@ void TraceBefore(hipStream_t stream, const char* kernel_name) {
   if (hipEventRecord(p.start, stream) != hipSuccess) return;
   t_cur = p;
   t_open = true;
+}
+
+TraceEvents TraceTake(const char* kernel_name) {
+  TraceEvents ev;
+  TraceState& s = state();
+  if (!s.enabled) return ev;
+  std::lock_guard<std::mutex> lk(s.mu);
+  if (!s.enabled || strstr(kernel_name, s.substr.c_str()) == nullptr) return ev;
+  ev.start = take_event(s);
+  ev.end = take_event(s);
+  if (!ev.start || !ev.end) {
+    if (ev.start) s.pool.push_back(ev.start);
+    if (ev.end) s.pool.push_back(ev.end);
+    ev = TraceEvents();
+  }
+  return ev;
+}
+
+void TraceCommit(const TraceEvents& ev) {
+  if (!ev.start) return;
+  TraceState& s = state();
+  std::lock_guard<std::mutex> lk(s.mu);
+  s.pending.push_back(Pending{ev.start, ev.end});
+  if (s.pending.size() > 4096) drain(s);
 }
 
 void TraceAfter(hipStream_t stream) {

@@ -397,5 +397,17 @@ def trace_read():
     return ms.value, n.value
 
 
+def fused_batch_norm_barrier_timed_out(reset=False):
+    """True if a fused BatchNorm launch on the current device gave up a grid
+    barrier wait (its outputs are then wrong); synchronizes the device."""
+    lib = _lib.load()
+    status = _lib.TFMA_Status()
+    flag = ctypes.c_int32(0)
+    lib.TFMA_FusedBatchNormBarrierTimedOut(ctypes.byref(flag), 1 if reset else 0,
+                                           ctypes.byref(status))
+    raise_for_status(status)
+    return bool(flag.value)
+
+
 def last_kernel_name():
     return _lib.load().TFMA_LastKernelName().decode()

@@ -228,6 +228,51 @@ def test_largest_shape_invariants(dev):
     torch.cuda.synchronize()
 
 
+def test_fused_launches_alternate_streams(dev):
+    """Fused (persistent) launches issued on two streams in turn.  The library
+    chains each launch to the previous one's end event, so only one grid is
+    resident at a time: every output must equal the single-stream result bit
+    for bit and no grid-barrier wait may have given up, with tracing off and
+    on (a traced launch's end event is a trace event)."""
+    torch.manual_seed(3)
+    eps = 1.001e-5
+    cases = []
+    for shape, dt in (((16, 14, 14, 256), torch.float16), ((8, 7, 7, 512), torch.bfloat16)):
+        c = shape[-1]
+        cases.append((torch.randn(shape, device=dev).to(dt), torch.randn(shape, device=dev).to(dt),
+                      torch.rand(c, device=dev) + 0.5, 0.1 * torch.randn(c, device=dev)))
+    e = torch.empty(0, device=dev)
+
+    def step(x, dy, scale, offset):
+        f = ops.FusedBatchNormV3(x, scale, offset, e, e, epsilon=eps)
+        g = ops.FusedBatchNormGradV3(dy, x, scale, f.reserve_space_1, f.reserve_space_2,
+                                     f.reserve_space_3, epsilon=eps)
+        assert ops.last_kernel_name() == "tfma_bn_grad_fused"
+        return [f.y, f.batch_mean, f.batch_variance, g.x_backprop, g.scale_backprop,
+                g.offset_backprop]
+
+    ops.fused_batch_norm_barrier_timed_out(reset=True)
+    want = [[t.clone() for t in step(*c)] for c in cases]
+    torch.cuda.synchronize()
+    streams = (torch.cuda.Stream(), torch.cuda.Stream())
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for trace in (None, "tfma_bn_grad_fused"):
+        ops.trace_enable(trace)
+        got = []
+        for i in range(12):
+            with torch.cuda.stream(streams[i % 2]):
+                got.append((i % len(cases), step(*cases[i % len(cases)])))
+        torch.cuda.synchronize()
+        ms, n = ops.trace_read()
+        ops.trace_enable(None)
+        assert n == (12 if trace else 0)
+        assert not ops.fused_batch_norm_barrier_timed_out()
+        for k, outs in got:
+            for w, g in zip(want[k], outs):
+                assert torch.equal(w, g)
+
+
 def test_shape_errors(dev):
     f32 = dict(dtype=torch.float32, device=dev)
     x = torch.zeros((2, 3, 3, 4), **f32)
