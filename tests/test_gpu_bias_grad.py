@@ -18,7 +18,9 @@ TOL = {"float32": 1e-5, "float16": 1e-2, "bfloat16": 1e-2}
 
 CASES = [((2, 8, 8, 32), "NHWC"), ((2, 32, 8, 8), "NCHW"), ((8192, 4096), "NHWC"),
          ((8191, 4095), "NHWC"), ((256, 7, 7, 2048), "NHWC"), ((4, 16, 7, 7), "NCHW"),
-         ((3, 5, 2, 3, 4), "NCHW"), ((1, 3), "NHWC"), ((100000, 3), "NHWC"), ((64, 2, 1000), "NCHW")]
+         ((3, 5, 2, 3, 4), "NCHW"), ((1, 3), "NHWC"), ((100000, 3), "NHWC"), ((64, 2, 1000), "NCHW"),
+         # very wide channel dimensions (4.2M channels of rows; 20000 NCHW planes)
+         ((2, 4200000), "NHWC"), ((2, 20000, 3), "NCHW")]
 
 
 @pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
