@@ -435,12 +435,43 @@ hipError_t dispatch_strided(EwOp op, int64_t n, const void* a, const void* b,
 
 }  // namespace
 
-hipError_t LaunchElementwise(DType t, EwOp op, int64_t n,
-                             const BcastOperand& a, const BcastOperand& b,
-                             const BcastOperand& c, void* out,
-                             hipStream_t stream) {
-  if (n <= 0) return hipSuccess;
-  if (n >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+namespace {
+
+constexpr int64_t kMaxFlat = (int64_t(1) << 31) - 1;  // flat indices stay 32-bit
+
+int64_t gcd64(int64_t x, int64_t y) {
+  while (y) {
+    const int64_t r = x % y;
+    x = y;
+    y = r;
+  }
+  return x;
+}
+
+// Chunk length for n > kMaxFlat: a multiple of 16 elements (16-byte aligned
+// chunk starts for every dtype) and of each periodic operand's cycle, so
+// every chunk starts at broadcast phase 0; 0 when no such chunk fits.
+int64_t flat_chunk(const BcastOperand* ops) {
+  int64_t cycle = 16;
+  for (int i = 0; i < 3; ++i) {
+    if (ops[i].mode != BcastMode::kPeriodic) continue;
+    const int64_t len = ops[i].inner * ops[i].period;
+    if (len <= 0 || len > kMaxFlat) return 0;
+    cycle = cycle / gcd64(cycle, len) * len;
+    if (cycle > kMaxFlat) return 0;
+  }
+  return kMaxFlat / cycle * cycle;
+}
+
+BcastOperand shifted(const BcastOperand& o, int64_t off, int esize) {
+  BcastOperand r = o;
+  if (o.mode == BcastMode::kFull) r.data = static_cast<const char*>(o.data) + off * esize;
+  return r;
+}
+
+hipError_t dispatch_flat(DType t, EwOp op, int64_t n, const BcastOperand& a,
+                         const BcastOperand& b, const BcastOperand& c, void* out,
+                         hipStream_t stream) {
   switch (t) {
     case DType::kF32: return dispatch_op<TF32>(op, n, a, b, c, out, stream);
     case DType::kF16: return dispatch_op<TF16>(op, n, a, b, c, out, stream);
@@ -448,6 +479,35 @@ hipError_t LaunchElementwise(DType t, EwOp op, int64_t n,
     case DType::kF64: return dispatch_op<TF64>(op, n, a, b, c, out, stream);
   }
   return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool ElementwiseFlatOk(int64_t n, const BcastOperand& a, const BcastOperand& b,
+                       const BcastOperand& c) {
+  if (n <= kMaxFlat) return true;
+  const BcastOperand ops[3] = {a, b, c};
+  return flat_chunk(ops) > 0;
+}
+
+hipError_t LaunchElementwise(DType t, EwOp op, int64_t n,
+                             const BcastOperand& a, const BcastOperand& b,
+                             const BcastOperand& c, void* out,
+                             hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  if (n <= kMaxFlat) return dispatch_flat(t, op, n, a, b, c, out, stream);
+  const BcastOperand ops[3] = {a, b, c};
+  const int64_t chunk = flat_chunk(ops);
+  if (chunk <= 0) return hipErrorInvalidValue;
+  const int esize = t == DType::kF64 ? 8 : (t == DType::kF32 ? 4 : 2);
+  for (int64_t off = 0; off < n; off += chunk) {
+    const int64_t len = n - off < chunk ? n - off : chunk;
+    const hipError_t e =
+        dispatch_flat(t, op, len, shifted(a, off, esize), shifted(b, off, esize),
+                      shifted(c, off, esize), static_cast<char*>(out) + off * esize, stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t LaunchElementwiseStrided(DType t, EwOp op, int64_t n,

@@ -499,7 +499,7 @@ int run_elementwise(void* stream, EwOp op, const char* op_name,
   const int nd = out->ndims;
   const TFMA_Tensor* ord[3] = {ins[0], n_in > 1 ? ins[1] : ins[0], n_in > 2 ? ins[2] : ins[0]};
   BcastOperand o[3];
-  bool fast = n < (int64_t(1) << 31);
+  bool fast = true;
   for (int i = 0; i < n_in && fast; ++i) fast = classify(ord[i], nd, out->dims, &o[i]);
   if (fast && o[0].mode != BcastMode::kFull && commutative01 && n_in > 1 &&
       o[1].mode == BcastMode::kFull) {
@@ -507,10 +507,13 @@ int run_elementwise(void* stream, EwOp op, const char* op_name,
     std::swap(o[0], o[1]);
   }
   if (fast && o[0].mode != BcastMode::kFull) fast = false;
-  hipError_t e;
   if (fast) {
     if (n_in < 2) o[1] = o[0];
     if (n_in < 3) o[2] = o[0];
+    fast = ElementwiseFlatOk(n, o[0], o[1], o[2]);
+  }
+  hipError_t e;
+  if (fast) {
     e = LaunchElementwise(t, op, n, o[0], o[1], o[2], out->data, as_stream(stream));
   } else {
     StridedShape sh{};
@@ -559,9 +562,9 @@ int bias_add_impl(void* stream, const TFMA_Tensor* value, const TFMA_Tensor* bia
   if (!value->data || !bias->data || !output->data)
     return set_status(st, TFMA_INVALID_ARGUMENT, "%s: null data pointer", name);
   hipError_t e;
-  if (n < (int64_t(1) << 31)) {
-    BcastOperand a{value->data, BcastMode::kFull, 1, 1};
-    BcastOperand b{bias->data, BcastMode::kPeriodic, inner, bias->dims[0]};
+  const BcastOperand a{value->data, BcastMode::kFull, 1, 1};
+  const BcastOperand b{bias->data, BcastMode::kPeriodic, inner, bias->dims[0]};
+  if (ElementwiseFlatOk(n, a, b, a)) {
     e = LaunchElementwise(t, relu ? EwOp::kAddRelu : EwOp::kAdd, n, a, b, a,
                           output->data, as_stream(stream));
   } else {

@@ -105,7 +105,12 @@ struct BcastOperand {
 };
 
 // out[i] = op(a[i], b[i], c[i]) for i < n.  Operands past the op's arity are
-// ignored.  a is the "value" input; all operands have dtype t.
+// ignored.  a is the "value" input; all operands have dtype t.  Above 2^31
+// elements the range runs in chunks whose length is a multiple of every
+// periodic operand's cycle (inner * period); ElementwiseFlatOk says whether
+// that is possible (a cycle below 2^31 elements), else use the strided path.
+bool ElementwiseFlatOk(int64_t n, const BcastOperand& a, const BcastOperand& b,
+                       const BcastOperand& c);
 hipError_t LaunchElementwise(DType t, EwOp op, int64_t n,
                              const BcastOperand& a, const BcastOperand& b,
                              const BcastOperand& c, void* out,

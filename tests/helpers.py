@@ -66,3 +66,44 @@ def ulp_diff_f32(a, b):
     ai = np.where(ai < 0, np.int64(-(2**31)) - ai, ai)
     bi = np.where(bi < 0, np.int64(-(2**31)) - bi, bi)
     return np.abs(ai - bi)
+
+
+def _ord16(t):
+    """float16/bfloat16 device tensor -> int32 tensor ordered like the values
+    (adjacent representable values differ by 1; -0 and +0 both map to 0)."""
+    b = t.contiguous().view(torch.int16).int()
+    return torch.where(b < 0, -(b & 0x7FFF), b)
+
+
+def bn_max_ulp(got, ref_fn, rows, c, rows_per=1 << 20):
+    """Largest distance in units of the last place between a 16-bit BN output
+    got ([rows, c] viewable) and ref_fn(r0, r1) - the float32 closed form for
+    rows [r0, r1), rounded to got's dtype here - over every element, in
+    chunks of rows_per rows (all on the device)."""
+    worst = 0
+    g2 = got.view(rows, c)
+    for r in range(0, rows, rows_per):
+        r1 = min(rows, r + rows_per)
+        ref = ref_fn(r, r1).to(got.dtype)
+        worst = max(worst, int((_ord16(g2[r:r1]) - _ord16(ref)).abs().max()))
+    return worst
+
+
+def bn_fwd_ref32(x, mean, var, scale, offset, eps, rows, c):
+    """float32 y = (x - mean) * (1/sqrt(var + eps) * scale) + offset,
+    in the fused kernel's operation order, per row range (for bn_max_ulp)."""
+    a = (1.0 / torch.sqrt(var + eps)) * scale
+    xv = x.view(rows, c)
+    return lambda r0, r1: (xv[r0:r1].float() - mean) * a + offset
+
+
+def bn_grad_ref32(dy, x, scale, mean, var, offset_bp, scale_bp, eps, rows, c):
+    """float32 dx = scale*k * ((dy - mean_dy) - (x - mean) * k^2 * mean(dy*(x-mean)))
+    from the kernel's own outputs (offset_bp = sum dy, scale_bp = k * sum
+    dy*(x-mean)), in the fused kernel's operation order (for bn_max_ulp)."""
+    k = 1.0 / torch.sqrt(var + eps)
+    gk = scale * k
+    mean_dy = (offset_bp.double() / rows).float()
+    k2 = (k * k) * (scale_bp.double() / k.double() / rows).float()
+    xv, dv = x.view(rows, c), dy.view(rows, c)
+    return lambda r0, r1: gk * ((dv[r0:r1].float() - mean_dy) - (xv[r0:r1].float() - mean) * k2)

@@ -13,7 +13,8 @@ import torch
 
 import tensorflow_musa_extension_amd as tfma
 from oracle import oracle
-from tests.helpers import assert_close, gen, to_dev, to_np
+from tests.helpers import (assert_close, bn_fwd_ref32, bn_grad_ref32, bn_max_ulp, gen,
+                           to_dev, to_np)
 
 pytestmark = pytest.mark.gpu
 ops = tfma.raw_ops
@@ -195,7 +196,8 @@ def test_cfg2_full_size(dev, shape, dtype):
 def test_largest_shape_invariants(dev):
     """[256,56,56,256] f16 (cfg2's largest): size-independent properties.
     Per channel: mean(y) = offset and var(y) = scale^2 var/(var+eps) (both
-    measured in float64 on the device); the grad's dx sums to 0."""
+    measured in float64 on the device); y and dx elementwise within 1 ulp of
+    the float32 closed form."""
     torch.manual_seed(0)
     shape = (256, 56, 56, 256)
     x = torch.randn(shape, device=dev).half()
@@ -218,13 +220,19 @@ def test_largest_shape_invariants(dev):
                                     fwd.reserve_space_3, epsilon=eps)
     dyd = dy.double().reshape(-1, 256)
     assert torch.allclose(grad.offset_backprop.double(), dyd.sum(0), rtol=1e-5, atol=1e-2)
-    dxd = grad.x_backprop.double().reshape(-1, 256)
-    # sum(dx) = 0 up to the f16 rounding of each dx (|dx| up to ~4, rounding
-    # error std up to ~6e-4): over n = 802816 rows the sum has std ~0.5 and
-    # a max over 256 channels below ~2; a wrong mean term would give
-    # |sum| ~ n * 1e-3 = 800.
-    worst = float(dxd.sum(0).abs().max())
-    assert worst < 5.0, worst
+    # Every element of y and dx within 1 ulp of the float32 closed form from
+    # the kernel's own statistics, in its operation order.  (sum(dx) = 0 is
+    # not a usable check for 16-bit dx: where scale*k is near a short binary
+    # fraction, scale*k*dy falls on or halfway between f16 values and the
+    # small mean terms bias every rounding the same way - TF-CPU's f16 output
+    # does this too, with |sum(dx)| in the hundreds at this size.)
+    rows = xd.shape[0]
+    mu, sig = fwd.reserve_space_1, fwd.reserve_space_2
+    assert bn_max_ulp(fwd.y, bn_fwd_ref32(x, mu, sig, scale, offset, eps, rows, 256), rows,
+                      256) <= 1
+    ref = bn_grad_ref32(dy, x, scale, mu, sig, grad.offset_backprop, grad.scale_backprop, eps,
+                        rows, 256)
+    assert bn_max_ulp(grad.x_backprop, ref, rows, 256) <= 1
     torch.cuda.synchronize()
 
 
