@@ -12,8 +12,9 @@ before the timed region.
 value = algorithmic bytes per step (fwd 2*s*E + grad 3*s*E per pair) x steps
         / wall time of the timed region (HIP events around K steps).
 roofline: the dominant kernel (tfma_bn_grad_fused: reads x, dy, writes dx,
-        3*s*E bytes per launch) timed with HIP events recorded on its
-        stream around each of its launches inside the timed region.
+        3*s*E bytes per launch) timed with HIP events on its stream for each
+        of its launches inside the timed region (the events are the
+        dispatch's own start/stop events, hipExtLaunchKernelGGL).
 cpu_baseline: the TF-CPU restatement (oracle/, C + OpenMP) on the same
         BN workload (both dtypes, four shapes), repeated for >= 10 s on up to
         16 host cores.
@@ -21,6 +22,9 @@ components: the other kernels (Adam, mixed-precision Adam, grouped Adam at
         the ResNet-50 and 1.31e9-parameter configs, the elementwise chains,
         ReluGrad, BiasAddGrad) at their config shapes, each rep timed with HIP
         events after a 1 GiB read that evicts the Infinity Cache.
+host_path: pageable host<->device copies (256 MiB) through the library's
+        staged path, beside the HIP runtime's own pageable copy and a pinned
+        copy (the PCIe ceiling), in GB/s.
 """
 import argparse
 import json
@@ -245,6 +249,42 @@ def components(torch, ops, dev):
     return out
 
 
+def host_path(torch, tfma, dev, mib=256, reps=5):
+    """Host<->device copies of a pageable buffer through the library's staged
+    path (TFMA_MemcpyHtoD / TFMA_MemcpyDtoH, synchronous), beside the HIP
+    runtime's own pageable copy (torch copy_) and a pinned-source copy (the
+    PCIe ceiling).  GB/s, best of `reps`."""
+    import numpy as np
+    se = tfma.stream_executor
+    n = mib << 20
+    a = np.random.default_rng(0).integers(0, 256, n, dtype=np.uint8)
+    out = np.empty(n, np.uint8)
+    d = torch.empty(n, dtype=torch.uint8, device=dev)
+    pin = torch.from_numpy(a).pin_memory()
+
+    def best(fn):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return round(n / min(ts) / 1e9, 1)
+
+    r = {f"h2d_pageable_{mib}MiB": {
+            "GB/s": best(lambda: se.memcpy_htod(d, a, sync=True)),
+            "runtime_GB/s": best(lambda: d.copy_(torch.from_numpy(a))),
+            "pinned_GB/s": best(lambda: d.copy_(pin, non_blocking=True))},
+         f"d2h_pageable_{mib}MiB": {
+            "GB/s": best(lambda: se.memcpy_dtoh(out, d, sync=True)),
+            "runtime_GB/s": best(lambda: torch.from_numpy(out).copy_(d))}}
+    if not np.array_equal(out, a):
+        raise RuntimeError("host path round trip mismatch")
+    return r
+
+
 def cpu_baseline(torch, dev, min_seconds=10.0):
     """TF-CPU restatement (oracle, C + OpenMP on up to 16 host cores) on the
     same workload: FusedBatchNormV3 + FusedBatchNormGradV3 over the four cfg2
@@ -369,6 +409,7 @@ def main():
         del src, dst
     if not args.no_components:
         result["components"] = components(torch, ops, dev)
+        result["host_path"] = host_path(torch, tfma, dev)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, dev)
     print(json.dumps(result), flush=True)

@@ -358,6 +358,54 @@ int TFMA_FusedBatchNormBarrierTimedOut(int32_t* timed_out, int32_t reset, TFMA_S
  * tests that check which path an op took). */
 const char* TFMA_LastKernelName(void);
 
+/* ---------------------------------------------------------------------------
+ * Host data path of the stream executor: what the SP_StreamExecutor copy,
+ * dependency and callback slots forward to (TF: memcpy_htod /
+ * sync_memcpy_htod, memcpy_dtoh / sync_memcpy_dtoh, create_stream_dependency,
+ * host_callback).  All act on the current device.
+ * ------------------------------------------------------------------------- */
+
+/* Host -> device copy of `size` bytes.  A pageable source is staged through
+ * pinned blocks in 4 MiB chunks (the host copy of one chunk overlaps the DMA
+ * of the previous one); the call returns once the source has been read, so
+ * the caller may reuse it at once, also when sync == 0.  A pinned source is
+ * copied directly; a device source becomes a device-to-device copy.
+ * sync != 0: on the null stream, returns when the copy is done (`stream` is
+ * ignored).  Replaces plugin_se_memcpy_htod / plugin_se_sync_memcpy_htod and
+ * MemcpyHtoDWithPinnedBounce (reference: musa_ext/mu/musa_se_plugin.cc:
+ * 127-211, 621-641, 730-747); errors: null pointers with size > 0 ->
+ * INVALID_ARGUMENT ("null host pointer for src in memcpy_htod"), HIP
+ * failures -> INTERNAL. */
+int TFMA_MemcpyHtoD(void* stream, void* device_dst, const void* host_src, uint64_t size,
+                    int32_t sync, TFMA_Status* status);
+
+/* Device -> host copy.  sync != 0 into pageable memory: staged in 4 MiB
+ * chunks (DMA of one chunk overlaps the host copy of the previous one);
+ * otherwise one hipMemcpyAsync on `stream` (the null stream when sync).
+ * Replaces plugin_se_memcpy_dtoh / plugin_se_sync_memcpy_dtoh
+ * (musa_se_plugin.cc:599-619, 712-728). */
+int TFMA_MemcpyDtoH(void* stream, void* host_dst, const void* device_src, uint64_t size,
+                    int32_t sync, TFMA_Status* status);
+
+/* Work enqueued on `dependent` after this call waits for the work enqueued
+ * on `other` before it.  Events come from a per-device pool and are reused
+ * once the recorded work has run (the reference creates and later destroys
+ * one per call).  Replaces plugin_se_create_stream_dependency
+ * (musa_se_plugin.cc:365-432); null stream -> INVALID_ARGUMENT. */
+int TFMA_CreateStreamDependency(void* dependent, void* other, TFMA_Status* status);
+
+/* Runs fn(arg) on a host thread once the work enqueued on `stream` before it
+ * has completed (hipLaunchHostFunc).  Replaces plugin_se_host_callback
+ * (musa_se_plugin.cc:808-835; the TF adapter wraps SE_StatusCallbackFn). */
+int TFMA_HostCallback(void* stream, void (*fn)(void*), void* arg, TFMA_Status* status);
+
+/* Staging pool of the current device: pinned blocks allocated so far, host
+ * allocations, reuses of a free block, and entries (blocks or dependency
+ * events) still waiting for their work.  No reference counterpart (the
+ * reference logs these counters, pinned_memory_pool.cc:120-160). */
+int TFMA_StagingPoolStats(uint64_t* blocks, uint64_t* host_allocs, uint64_t* reuses,
+                          uint64_t* pending, TFMA_Status* status);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

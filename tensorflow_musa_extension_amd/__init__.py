@@ -9,11 +9,12 @@ libtfma.so binds to (both carry the soname libamdhip64.so.7).
 """
 import torch  # noqa: F401  (loads the process's HIP runtime)
 
-from . import _lib, errors, graph_rewrite, raw_ops  # noqa: F401
+from . import _lib, errors, graph_rewrite, raw_ops, stream_executor  # noqa: F401
 from .errors import (FailedPreconditionError, InternalError,  # noqa: F401
                      InvalidArgumentError, OpError, UnimplementedError)
 
-__all__ = ["raw_ops", "errors", "graph_rewrite", "load_library", "device_count", "LIB_PATH"]
+__all__ = ["raw_ops", "errors", "graph_rewrite", "stream_executor", "load_library", "device_count",
+           "LIB_PATH"]
 
 LIB_PATH = _lib.LIB_PATH
 

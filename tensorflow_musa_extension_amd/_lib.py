@@ -94,6 +94,11 @@ SIGNATURES = {
     "TFMA_TraceRead": [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), _S],
     "TFMA_LastKernelName": [],
     "TFMA_FusedBatchNormBarrierTimedOut": [ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, _S],
+    "TFMA_MemcpyHtoD": [_vp, _vp, _vp, ctypes.c_uint64, ctypes.c_int32, _S],
+    "TFMA_MemcpyDtoH": [_vp, _vp, _vp, ctypes.c_uint64, ctypes.c_int32, _S],
+    "TFMA_CreateStreamDependency": [_vp, _vp, _S],
+    "TFMA_HostCallback": [_vp, _vp, _vp, _S],
+    "TFMA_StagingPoolStats": [ctypes.POINTER(ctypes.c_uint64)] * 4 + [_S],
 }
 _RESTYPES = {"TFMA_Version": ctypes.c_char_p, "TFMA_LastKernelName": ctypes.c_char_p,
              "TFMA_FreeBuffer": None}

@@ -264,3 +264,27 @@ def test_trace_api_without_device():
     assert lib.TFMA_TraceRead(ctypes.byref(ms), ctypes.byref(n), ctypes.byref(st)) == _lib.OK
     assert ms.value == 0 and n.value == 0
     assert lib.TFMA_TraceEnable(None, ctypes.byref(st)) == _lib.OK
+
+
+def test_host_path_validation_without_device():
+    """The host data path's argument checks (musa_se_plugin.cc:103-111,
+    365-371, 808-812): zero-size copies succeed, null pointers and streams
+    are InvalidArgument - all before any device call."""
+    lib = _lib.load()
+    st = _lib.TFMA_Status()
+    buf = ctypes.create_string_buffer(16)
+    assert lib.TFMA_MemcpyHtoD(None, None, None, 0, 0, ctypes.byref(st)) == _lib.OK
+    assert lib.TFMA_MemcpyDtoH(None, None, None, 0, 1, ctypes.byref(st)) == _lib.OK
+    assert lib.TFMA_MemcpyHtoD(None, ctypes.cast(buf, ctypes.c_void_p), None, 16, 0,
+                               ctypes.byref(st)) == _lib.INVALID_ARGUMENT
+    assert b"null host pointer for src in memcpy_htod" in st.message
+    assert lib.TFMA_MemcpyHtoD(None, None, ctypes.cast(buf, ctypes.c_void_p), 16, 0,
+                               ctypes.byref(st)) == _lib.INVALID_ARGUMENT
+    assert lib.TFMA_MemcpyDtoH(None, None, ctypes.cast(buf, ctypes.c_void_p), 16, 1,
+                               ctypes.byref(st)) == _lib.INVALID_ARGUMENT
+    assert b"null host pointer for dst in memcpy_dtoh" in st.message
+    assert lib.TFMA_CreateStreamDependency(None, ctypes.c_void_p(1),
+                                           ctypes.byref(st)) == _lib.INVALID_ARGUMENT
+    assert b"null stream in create_stream_dependency" in st.message
+    assert lib.TFMA_HostCallback(ctypes.c_void_p(1), None, None,
+                                 ctypes.byref(st)) == _lib.INVALID_ARGUMENT
