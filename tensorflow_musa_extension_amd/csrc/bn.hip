@@ -545,6 +545,7 @@ struct FusedArgs {
   unsigned sub_last[3][8];      // value class r's last arrival sees at barrier 1, 2, exit
   unsigned* timeout_flag;
   unsigned* queues;             // [ct][wave] chunk counters, zero between launches
+  int reset_at_exit;            // recorded into a graph: zero every counter at exit
   int dyn_rows;                 // streamed rows per thread handed out dynamically
   int dyn_chunk;                // rows per thread in one dynamic chunk
   int shards;                   // chunk counters per (ct, wave)
@@ -961,12 +962,15 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     }
   }
 
-  // Exit (only when chunks were handed out): counted like a third barrier
-  // arrival - class counter, then the global counter - and the workgroup
-  // that completes the count zeroes the chunk counters for the next launch.
-  // Relaxed: every counter this workgroup touched was updated by atomics
-  // whose results it has already used.
-  if (a.dyn_rows > 0) {
+  // Exit (when chunks were handed out, and in a launch recorded into a
+  // graph): counted like a third barrier arrival - class counter, then the
+  // global counter - and the workgroup that completes the count zeroes the
+  // chunk counters for the next launch; in a recorded launch also the
+  // barrier and class counters, so every replay starts from zero.  Relaxed:
+  // every counter this workgroup touched was updated by atomics whose
+  // results it has already used, and no workgroup reads a counter after its
+  // exit arrival.
+  if (a.dyn_rows > 0 || a.reset_at_exit) {
     __syncthreads();
     if (wave == 0) {
       unsigned done = 0;
@@ -984,8 +988,16 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
         }
       }
       if (__builtin_amdgcn_readfirstlane(done)) {
-        for (int i = lane; i < a.ct * a.shards * kWaves; i += 64)
-          __hip_atomic_store(a.queues + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.dyn_rows > 0) {
+          for (int i = lane; i < a.ct * a.shards * kWaves; i += 64)
+            __hip_atomic_store(a.queues + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (a.reset_at_exit) {
+          if (lane < 8)
+            __hip_atomic_store(a.sub + 64 * lane, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (lane == 0)
+            __hip_atomic_store(a.barrier, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
   }
@@ -1179,7 +1191,12 @@ void set_dynamic_share(FusedPlan* fp, int resident, int prefetched, int u) {
 // one), so at most one persistent grid is resident at a time and every
 // launch knows the counter's starting value.
 // The allocation also holds the dynamic-chunk counters (from byte 256),
-// which the last workgroup of each launch zeroes again.
+// which the last workgroup of each launch zeroes again.  A second, identical
+// region serves launches recorded into a graph (stream capture): they start
+// from zero counters and zero them again at exit, so replays need no host
+// bookkeeping; they are not chained to other fused launches (the graph
+// orders them), so a replay must not overlap other fused BatchNorm work on
+// the device.
 constexpr size_t kQueueOffset = 256;
 constexpr size_t kQueueBytes = 4096 * sizeof(unsigned);  // <= 512 tiles x 8 waves
 constexpr size_t kSubOffset = kQueueOffset + kQueueBytes;  // 8 class counters, 256 B apart
@@ -1211,9 +1228,9 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   std::lock_guard<std::mutex> lk(bs->mu);
   if (!bs->counter) {
     void* p = nullptr;
-    hipError_t e = hipMalloc(&p, kStateBytes);
+    hipError_t e = hipMalloc(&p, 2 * kStateBytes);
     if (e != hipSuccess) return e;
-    e = hipMemset(p, 0, kStateBytes);
+    e = hipMemset(p, 0, 2 * kStateBytes);
     if (e == hipSuccess)
       e = hipEventCreateWithFlags(&bs->last, hipEventDisableTiming | hipEventReleaseToDevice);
     if (e != hipSuccess) {
@@ -1222,7 +1239,17 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
     }
     bs->counter = static_cast<unsigned long long*>(p);
   }
-  if (bs->used && bs->last_stream != stream) {
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  {
+    const hipError_t e = hipStreamIsCapturing(stream, &cap);
+    if (e != hipSuccess) return e;
+  }
+  const bool recorded = cap != hipStreamCaptureStatusNone;
+  unsigned long long* region =
+      recorded ? reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(bs->counter) +
+                                                       kStateBytes)
+               : bs->counter;
+  if (!recorded && bs->used && bs->last_stream != stream) {
     hipError_t e = hipStreamWaitEvent(stream, bs->chain, 0);
     if (e != hipSuccess) return e;
   }
@@ -1239,17 +1266,19 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   fa.rows_per_g = fp.rows_per_g;
   fa.partial = partial;
   fa.coef = coef;
-  fa.barrier = bs->counter;
-  fa.base = bs->base;
-  fa.sub = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(bs->counter) + kSubOffset);
+  fa.barrier = region;
+  fa.base = recorded ? 0 : bs->base;
+  fa.sub = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(region) + kSubOffset);
   for (int r = 0; r < 8; ++r) {
     const unsigned members = static_cast<unsigned>((fp.blocks + 7 - r) / 8);
-    fa.sub_last[0][r] = bs->sub_base[r] + members - 1;
-    fa.sub_last[1][r] = bs->sub_base[r] + 2 * members - 1;
-    fa.sub_last[2][r] = bs->sub_base[r] + 3 * members - 1;
+    const unsigned sb = recorded ? 0u : bs->sub_base[r];
+    fa.sub_last[0][r] = sb + members - 1;
+    fa.sub_last[1][r] = sb + 2 * members - 1;
+    fa.sub_last[2][r] = sb + 3 * members - 1;
   }
-  fa.timeout_flag = reinterpret_cast<unsigned*>(bs->counter + 1);
-  fa.queues = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(bs->counter) + kQueueOffset);
+  fa.timeout_flag = reinterpret_cast<unsigned*>(region + 1);
+  fa.queues = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(region) + kQueueOffset);
+  fa.reset_at_exit = recorded ? 1 : 0;
   {
     FusedPlan fd = fp;
     constexpr int kPre = kGrad ? Resident<Tr>::kPaGrad + Resident<Tr>::kPbGrad
@@ -1267,6 +1296,14 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   fa.fin.groups = fp.groups;
   const char* name = kGrad ? "tfma_bn_grad_fused" : "tfma_bn_fwd_fused";
   SetLastKernel(name);
+  if (recorded) {  // no events, no tracing, no chain bookkeeping inside a graph
+    constexpr int KR = fused_kr<Tr, kGrad>();
+    constexpr int KL = fused_kl<Tr, kGrad>();
+    const size_t smem = fused_smem<Tr, kGrad>();
+    hipLaunchKernelGGL((bn_fused_nhwc_kernel<Tr, kGrad, KR, KL>), dim3(fp.blocks),
+                       dim3(kFusedThreads), smem, stream, fa);
+    return hipGetLastError();
+  }
   const TraceEvents tev = TraceTake(name);
   hipEvent_t end = tev.end ? tev.end : bs->last;
   {
@@ -1302,14 +1339,17 @@ hipError_t BnBarrierTimedOut(bool reset, bool* timed_out) {
   std::lock_guard<std::mutex> lk(bs->mu);
   if (!bs->counter) return hipSuccess;  // no fused launch on this device yet
   hipError_t e = hipDeviceSynchronize();
-  unsigned flag = 0;
-  if (e == hipSuccess)
-    e = hipMemcpy(&flag, bs->counter + 1, sizeof(flag), hipMemcpyDeviceToHost);
-  if (e != hipSuccess) return e;
-  *timed_out = flag != 0;
-  if (reset && flag) {
-    const unsigned zero = 0;
-    e = hipMemcpy(bs->counter + 1, &zero, sizeof(zero), hipMemcpyHostToDevice);
+  for (int region = 0; region < 2 && e == hipSuccess; ++region) {
+    unsigned* fl = reinterpret_cast<unsigned*>(
+        reinterpret_cast<char*>(bs->counter) + region * kStateBytes + sizeof(unsigned long long));
+    unsigned flag = 0;
+    e = hipMemcpy(&flag, fl, sizeof(flag), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) break;
+    *timed_out = *timed_out || flag != 0;
+    if (reset && flag) {
+      const unsigned zero = 0;
+      e = hipMemcpy(fl, &zero, sizeof(zero), hipMemcpyHostToDevice);
+    }
   }
   return e;
 }

@@ -1104,6 +1104,17 @@ int TFMA_GroupedResourceApplyAdam(void* stream, int n, TFMA_Tensor* vars, TFMA_T
     return set_status(status, TFMA_INVALID_ARGUMENT,
                       "MusaGroupedResourceApplyAdam: workspace of %zu bytes required, got %zu",
                       need, workspace ? workspace_bytes : size_t(0));
+  if (!table.empty()) {
+    // The tensor table is staged per call (a pinned ring slot or a cached
+    // device copy, both reused by later calls), so a graph replay would read
+    // a table that has since changed.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(as_stream(stream), &cap) == hipSuccess &&
+        cap != hipStreamCaptureStatusNone)
+      return set_status(status, TFMA_UNIMPLEMENTED,
+                        "MusaGroupedResourceApplyAdam cannot be recorded into a graph: its tensor "
+                        "table is staged per call; use ResourceApplyAdam per tensor there");
+  }
   VarLocks locks;
   if (use_locking) {
     for (int i = 0; i < n; ++i) {
