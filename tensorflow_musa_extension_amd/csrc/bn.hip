@@ -641,6 +641,14 @@ __device__ inline uint4 apply_words(const uint4& xw, const uint4& dw,
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __device__ inline uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+// Phase-3 re-reads are the last use of their lines: non-temporal loads keep
+// them from displacing the lines the remaining re-reads will still hit in the
+// Infinity Cache (measured: the grad kernel 1.9 % faster on cfg2; making the
+// phase-1 loads non-temporal as well is 17 % slower).
+__device__ inline uint4 ld16_last(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 // Outputs are written once and not read again by the op: non-temporal.
 __device__ inline void st16(void* p, const uint4& v) {
   __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(p));
@@ -871,17 +879,17 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     uint4 xw[U], dw[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      xw[u] = ld16(xrow(q - u));
-      if constexpr (kGrad) dw[u] = ld16(drow(q - u));
+      xw[u] = ld16_last(xrow(q - u));
+      if constexpr (kGrad) dw[u] = ld16_last(drow(q - u));
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
       st16(po + base + (q - u) * rstride, apply_words<Tr, kGrad>(xw[u], dw[u], cf));
   }
   for (; q >= qlo; --q) {
-    const uint4 xw = ld16(xrow(q));
+    const uint4 xw = ld16_last(xrow(q));
     uint4 dw = xw;
-    if constexpr (kGrad) dw = ld16(drow(q));
+    if constexpr (kGrad) dw = ld16_last(drow(q));
     st16(po + base + q * rstride, apply_words<Tr, kGrad>(xw, dw, cf));
   }
 #pragma unroll
@@ -946,17 +954,17 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
         uint4 xw[U], dw[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          xw[u] = ld16(px + obase + (qq + u) * rstride);
-          if constexpr (kGrad) dw[u] = ld16(pd + obase + (qq + u) * rstride);
+          xw[u] = ld16_last(px + obase + (qq + u) * rstride);
+          if constexpr (kGrad) dw[u] = ld16_last(pd + obase + (qq + u) * rstride);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u)
           st16(po + obase + (qq + u) * rstride, apply_words<Tr, kGrad>(xw[u], dw[u], cf));
       }
       for (; qq <= qb2; ++qq) {
-        const uint4 xw = ld16(px + obase + qq * rstride);
+        const uint4 xw = ld16_last(px + obase + qq * rstride);
         uint4 dw = xw;
-        if constexpr (kGrad) dw = ld16(pd + obase + qq * rstride);
+        if constexpr (kGrad) dw = ld16_last(pd + obase + qq * rstride);
         st16(po + obase + qq * rstride, apply_words<Tr, kGrad>(xw, dw, cf));
       }
     }
