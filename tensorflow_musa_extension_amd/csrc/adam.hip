@@ -110,9 +110,9 @@ __device__ inline void adam_range(typename Tr::S* __restrict__ var, typename Tr:
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t off = (i + u * kThreads) * VEC;
-        vstore<S, VEC>(m + off, mv[u]);
-        vstore<S, VEC>(v + off, vv[u]);
-        vstore<S, VEC>(var + off, xv[u]);
+        vstore_nt<S, VEC>(m + off, mv[u]);
+        vstore_nt<S, VEC>(v + off, vv[u]);
+        vstore_nt<S, VEC>(var + off, xv[u]);
       }
     }
     for (; i < nv; i += kThreads) {
@@ -126,9 +126,9 @@ __device__ inline void adam_range(typename Tr::S* __restrict__ var, typename Tr:
 #pragma unroll
       for (int j = 0; j < VEC; ++j)
         adam_elem<Tr, Tg, kNesterov>(xv[j], mv[j], vv[j], gv[j], p);
-      vstore<S, VEC>(m + off, mv);
-      vstore<S, VEC>(v + off, vv);
-      vstore<S, VEC>(var + off, xv);
+      vstore_nt<S, VEC>(m + off, mv);
+      vstore_nt<S, VEC>(v + off, vv);
+      vstore_nt<S, VEC>(var + off, xv);
     }
     done = nv * VEC;
   }

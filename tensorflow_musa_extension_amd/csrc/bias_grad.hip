@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kThreads) void bag_rows_kernel(
     for (; r + (kUnroll - 1) * ry < r1; r += kUnroll * ry) {
       S v[kUnroll][VEC];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) vload<S, VEC>(p + (r + u * ry) * c, v[u]);
+      for (int u = 0; u < kUnroll; ++u) vload_nt<S, VEC>(p + (r + u * ry) * c, v[u]);
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
@@ -83,7 +83,7 @@ __global__ __launch_bounds__(kThreads) void bag_rows_kernel(
     }
     for (; r < r1; r += ry) {
       S v[VEC];
-      vload<S, VEC>(p + r * c, v);
+      vload_nt<S, VEC>(p + r * c, v);
 #pragma unroll
       for (int j = 0; j < VEC; ++j) acc[j] += B::ld(v[j]);
     }
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(kThreads) void bag_planes_kernel(
   auto at = [&](int64_t k, S (&v)[VEC]) {
     const uint32_t q = div_inner.div(static_cast<uint32_t>(k));
     const int64_t i = k - static_cast<int64_t>(q) * inner;
-    vload<S, VEC>(x + (((o0 + q) * c + ch) * inner + i) * VEC, v);
+    vload_nt<S, VEC>(x + (((o0 + q) * c + ch) * inner + i) * VEC, v);
   };
   int64_t k = threadIdx.x;
   for (; k + (U - 1) * kThreads < count; k += U * kThreads) {

@@ -118,6 +118,44 @@ __device__ inline void vstore(S* __restrict__ p, const S (&in)[N]) {
   }
 }
 
+// Non-temporal variants (the line is not kept in the caches for reuse).
+// Measured on MI355X with the Infinity Cache flushed between reps: loads of
+// BiasAddGrad's single-use input 5 % faster, Adam's stores 0.5-2 % faster;
+// the elementwise kernels and Adam's loads are slower with them, so those
+// keep vload/vstore.
+typedef unsigned int nt_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int nt_u32x2 __attribute__((ext_vector_type(2)));
+template <typename W> struct NtWord { using T = W; };
+template <> struct NtWord<uint4> { using T = nt_u32x4; };
+template <> struct NtWord<uint2> { using T = nt_u32x2; };
+
+template <typename S, int N>
+__device__ inline void vload_nt(const S* __restrict__ p, S (&out)[N]) {
+  using W = typename Raw<S, N>::Word;
+  if constexpr (sizeof(W) == sizeof(S) * N) {
+    using T = typename NtWord<W>::T;
+    const T w = __builtin_nontemporal_load(reinterpret_cast<const T*>(p));
+    __builtin_memcpy(out, &w, sizeof(W));
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) out[j] = __builtin_nontemporal_load(p + j);
+  }
+}
+
+template <typename S, int N>
+__device__ inline void vstore_nt(S* __restrict__ p, const S (&in)[N]) {
+  using W = typename Raw<S, N>::Word;
+  if constexpr (sizeof(W) == sizeof(S) * N) {
+    using T = typename NtWord<W>::T;
+    T w;
+    __builtin_memcpy(&w, in, sizeof(W));
+    __builtin_nontemporal_store(w, reinterpret_cast<T*>(p));
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) __builtin_nontemporal_store(in[j], p + j);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Unsigned 32-bit division by a runtime-invariant divisor d >= 1 with a
 // multiply-high (round-up method, Granlund & Montgomery, PLDI 1994):
