@@ -76,14 +76,6 @@ __device__ inline void adam_elem(typename Tr::S& var, typename Tr::S& m,
 // loads 2.6-4.5 % faster from 2^27 up.
 constexpr int64_t kStreamElems = int64_t(1) << 26;
 
-template <bool kNt, typename S, int N>
-__device__ inline void vload_sel(const S* __restrict__ p, S (&out)[N]) {
-  if constexpr (kNt)
-    vload_nt<S, N>(p, out);
-  else
-    vload<S, N>(p, out);
-}
-
 // Updates elements [0, len) of one contiguous range with the whole
 // workgroup: 16-byte vectors, U per tensor in flight per thread, when every
 // pointer is aligned for them; element by element otherwise.

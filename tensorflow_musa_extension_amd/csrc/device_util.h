@@ -121,8 +121,8 @@ __device__ inline void vstore(S* __restrict__ p, const S (&in)[N]) {
 // Non-temporal variants (the line is not kept in the caches for reuse).
 // Measured on MI355X with the Infinity Cache flushed between reps: loads of
 // BiasAddGrad's single-use input 5 % faster, Adam's stores 0.5-2 % faster;
-// the elementwise kernels and Adam's loads are slower with them, so those
-// keep vload/vstore.
+// Adam's loads and the elementwise kernels' loads and stores only pay off
+// above a size (their launchers choose with vload_sel / vstore_sel).
 typedef unsigned int nt_u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int nt_u32x2 __attribute__((ext_vector_type(2)));
 template <typename W> struct NtWord { using T = W; };
@@ -154,6 +154,22 @@ __device__ inline void vstore_nt(S* __restrict__ p, const S (&in)[N]) {
 #pragma unroll
     for (int j = 0; j < N; ++j) __builtin_nontemporal_store(in[j], p + j);
   }
+}
+
+template <bool kNt, typename S, int N>
+__device__ inline void vload_sel(const S* __restrict__ p, S (&out)[N]) {
+  if constexpr (kNt)
+    vload_nt<S, N>(p, out);
+  else
+    vload<S, N>(p, out);
+}
+
+template <bool kNt, typename S, int N>
+__device__ inline void vstore_sel(S* __restrict__ p, const S (&in)[N]) {
+  if constexpr (kNt)
+    vstore_nt<S, N>(p, in);
+  else
+    vstore<S, N>(p, in);
 }
 
 // ---------------------------------------------------------------------------
