@@ -10,7 +10,9 @@ One step = fwd + grad for all 8 (dtype, shape) pairs.  Inputs are synthetic
 before the timed region.
 
 value = algorithmic bytes per step (fwd 2*s*E + grad 3*s*E per pair) x steps
-        / wall time of the timed region (HIP events around K steps).
+        / wall time of the timed region (HIP events around K steps);
+        elements_per_s counts each pair's E elements once for the forward and
+        once for the grad.
 roofline: the dominant kernel (tfma_bn_grad_fused: reads x, dy, writes dx,
         3*s*E bytes per launch) timed with HIP events on its stream for each
         of its launches inside the timed region (the events are the
@@ -21,7 +23,8 @@ cpu_baseline: the TF-CPU restatement (oracle/, C + OpenMP) on the same
 components: the other kernels (Adam, mixed-precision Adam, grouped Adam at
         the ResNet-50 and 1.31e9-parameter configs, the elementwise chains,
         ReluGrad, BiasAddGrad) at their config shapes, each rep timed with HIP
-        events after a 1 GiB read that evicts the Infinity Cache.
+        events after a 1 GiB read that evicts the Infinity Cache (GB/s, % of
+        peak, Gelem/s).
 host_path: pageable host<->device copies (256 MiB) through the library's
         staged path, beside the HIP runtime's own pageable copy and a pinned
         copy (the PCIe ceiling), in GB/s.
@@ -176,10 +179,12 @@ def components(torch, ops, dev):
     reps, warm = 20, 3
     flush = torch.ones(1 << 28, device=dev)  # 1 GiB, read between reps
 
-    def rate(calls, nbytes, reps_=reps):
+    def rate(calls, nbytes, elems, reps_=reps):
         ms = time_calls(torch, calls, reps_, warm, flush=flush)
         gbps = nbytes / (ms / 1e3) / 1e9
-        return {"ms": round(ms, 4), "GB/s": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1)}
+        return {"ms": round(ms, 4), "GB/s": round(gbps, 1),
+                "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
+                "Gelem/s": round(elems / (ms / 1e3) / 1e9, 2)}
 
     n = 25_600_000
     var = 0.02 * torch.randn(n, generator=gen, device=dev)
@@ -187,12 +192,12 @@ def components(torch, ops, dev):
     v = torch.zeros(n, device=dev)
     g = 1e-3 * torch.randn(n, generator=gen, device=dev)
     adam = ops.bind(ops.ResourceApplyAdam, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7, g)
-    out["adam_f32_25.6M"] = rate([adam], 28 * n)
+    out["adam_f32_25.6M"] = rate([adam], 28 * n, n)
     # Mixed precision (fp32 state, bf16 grad): 24 B of state + 2 B of grad.
     gb = g.to(torch.bfloat16)
     mixed = ops.bind(ops.MusaResourceApplyAdamMixed, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999,
                      1e-7, gb)
-    out["adam_mixed_bf16grad_25.6M"] = rate([mixed], 26 * n)
+    out["adam_mixed_bf16grad_25.6M"] = rate([mixed], 26 * n, n)
     del gb
 
     shapes = resnet50_shapes()
@@ -203,7 +208,7 @@ def components(torch, ops, dev):
     total = sum(t.numel() for t in tv)
     grouped = ops.bind(ops.MusaGroupedResourceApplyAdam, tv, tm, tvv, tg, 0.9, 0.999, 1e-3, 0.9,
                        0.999, 1e-7)
-    out["grouped_adam_f32_resnet50_161"] = rate([grouped], 28 * total)
+    out["grouped_adam_f32_resnet50_161"] = rate([grouped], 28 * total, total)
     del var, m, v, g, tv, tm, tvv, tg, grouped, adam, mixed
 
     # cfg5: 1.31B parameters in 145 tensors, 21 GB of state resident.
@@ -215,7 +220,7 @@ def components(torch, ops, dev):
     total5 = sum(t.numel() for t in tv)
     grouped5 = ops.bind(ops.MusaGroupedResourceApplyAdam, tv, tm, tvv, tg, 0.9, 0.999, 1e-3,
                         0.9, 0.999, 1e-7)
-    out["grouped_adam_f32_cfg5_145"] = rate([grouped5], 28 * total5, reps_=10)
+    out["grouped_adam_f32_cfg5_145"] = rate([grouped5], 28 * total5, total5, reps_=10)
     del tv, tm, tvv, tg, grouped5
     torch.cuda.empty_cache()
 
@@ -225,24 +230,26 @@ def components(torch, ops, dev):
         b = torch.randn(4096, generator=gen, device=dev).to(dt)
         E = x.numel()
         out[f"bias_add_relu_{name}_8192x4096"] = rate([ops.bind(ops.MusaBiasAddRelu, x, b)],
-                                                      2 * s * E + s * 4096)
+                                                      2 * s * E + s * 4096, E)
         out[f"add_v2_relu_{name}_8192x4096"] = rate([ops.bind(ops.MusaAddV2Relu, x, b)],
-                                                    2 * s * E + s * 4096)
+                                                    2 * s * E + s * 4096, E)
         a_full = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
         b_full = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
         out[f"mul_add_full_{name}_8192x4096"] = rate(
-            [ops.bind(ops.MusaShiftedAffineMap, x, a_full, b_full)], 4 * s * E)
+            [ops.bind(ops.MusaShiftedAffineMap, x, a_full, b_full)], 4 * s * E, E)
         out[f"mul_add_row_{name}_8192x4096"] = rate(
-            [ops.bind(ops.MusaShiftedAffineMap, x, b, b)], 2 * s * E + 2 * s * 4096)
+            [ops.bind(ops.MusaShiftedAffineMap, x, b, b)], 2 * s * E + 2 * s * 4096, E)
         xo = torch.randn(8191, 4095, generator=gen, device=dev).to(dt)
         bo = torch.randn(4095, generator=gen, device=dev).to(dt)
         out[f"bias_add_relu_{name}_8191x4095"] = rate([ops.bind(ops.MusaBiasAddRelu, xo, bo)],
-                                                      2 * s * xo.numel() + s * 4095)
+                                                      2 * s * xo.numel() + s * 4095,
+                                                      xo.numel())
         # The backward side of the chains: ReluGrad (2 reads, 1 write) and
         # BiasAddGrad (one read of the gradient).
-        out[f"relu_grad_{name}_8192x4096"] = rate([ops.bind(ops.ReluGrad, a_full, x)], 3 * s * E)
+        out[f"relu_grad_{name}_8192x4096"] = rate([ops.bind(ops.ReluGrad, a_full, x)], 3 * s * E,
+                                                  E)
         out[f"bias_add_grad_{name}_8192x4096"] = rate([ops.bind(ops.BiasAddGrad, a_full)],
-                                                      s * E + s * 4096)
+                                                      s * E + s * 4096, E)
         del x, b, a_full, b_full, xo, bo
     torch.cuda.synchronize()
     del flush
@@ -382,6 +389,7 @@ def main():
         "value": round(value, 1),
         "unit": "GB/s",
         "pct_of_peak": round(100 * value / PEAK_GBPS, 2),
+        "elements_per_s": round(2 * sum(e for _, _, e, _ in pairs) / (ms_per_step / 1e3)),
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -389,13 +397,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 compute on f16/bf16 data",
+        "dtype": "f32",
         "data": "synthetic",
         "config": {
             "workload": "cfg2: FusedBatchNormV3 fwd + FusedBatchNormGradV3, NHWC, "
                         "is_training, eps=1.001e-5, f16 and bf16 x/dy, f32 stats, shapes "
                         + ", ".join("x".join(map(str, s)) for s in SHAPES),
             "bytes_per_step": bytes_per_step,
+            "storage_dtypes": ["f16", "bf16"],
             "parallelism": "single GPU",
         },
         "roofline": roofline,
