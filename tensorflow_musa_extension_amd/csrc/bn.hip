@@ -874,16 +874,19 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   // The lowest dyn_rows streamed rows of every thread are not processed by
   // their owner but handed out in chunks after the owner's other rows.
   const int64_t qlo = KR + KL + a.dyn_rows;
+  // Phase-3 rows in flight per tensor: the grad's loop has the registers for
+  // 6 (0.8 % faster than 4); the forward gains nothing beyond its 8.
+  constexpr int U3 = kGrad ? 6 : U;
   q = qb - PB;
-  for (; q >= qlo + U - 1; q -= U) {
-    uint4 xw[U], dw[U];
+  for (; q >= qlo + U3 - 1; q -= U3) {
+    uint4 xw[U3], dw[U3];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < U3; ++u) {
       xw[u] = ld16_last(xrow(q - u));
       if constexpr (kGrad) dw[u] = ld16_last(drow(q - u));
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U3; ++u)
       st16(po + base + (q - u) * rstride, apply_words<Tr, kGrad>(xw[u], dw[u], cf));
   }
   for (; q >= qlo; --q) {
