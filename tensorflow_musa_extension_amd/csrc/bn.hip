@@ -27,9 +27,10 @@
 //                are walked in the reverse of the reduce order, so the
 //                lines the reduce touched last - still in the 256 MB
 //                Infinity Cache - are re-read first.
-// The forward statistics use sums of (x - K) with K = the channel's first
-// element, which keeps sum((x-K)^2) - sum(x-K)^2/n free of cancellation
-// when |mean| >> std; partials add exactly like plain sums because every
+// The forward statistics use sums of (x - K) with K = chan_shift(), the
+// median of five of the channel's elements, which keeps sum((x-K)^2) -
+// sum(x-K)^2/n free of cancellation when |mean| >> std and when single
+// elements are outliers; partials add exactly like plain sums because every
 // workgroup uses the same K.
 #include <hip/hip_ext.h>
 
@@ -127,9 +128,67 @@ size_t coef_bytes(const BnGeometry& g) {
 }
 
 // ---------------------------------------------------------------------------
+// Shift K of the forward's sums of (x - K) and (x - K)^2: the median of five
+// elements spread over the channel (its elements 0, n/4, n/2, 3n/4, n-1).
+// The variance sum((x-K)^2) - sum(x-K)^2 / n cancels in proportion to
+// ((mean - K) / std)^2, so K must sit near the mean: the channel's first
+// element would do unless it is an outlier (one at 1e3 among N(0,1) values
+// put the float32 statistics off by 1e-4); the median of five stays within a
+// few standard deviations unless three of the five are outliers.  A
+// non-finite median gives K = 0, so infinities and NaNs reach the sums as in
+// an unshifted sum.  Every kernel and the finals compute K with this
+// function from the same five elements, so they agree bit for bit.
+// ---------------------------------------------------------------------------
+__device__ inline void cmp_swap(float& lo, float& hi) {
+  const float a = fminf(lo, hi), b = fmaxf(lo, hi);
+  lo = a;
+  hi = b;
+}
+
+__device__ inline float shift_of(float (&v)[5]) {
+  // Optimal 9-comparator sorting network for five elements.
+  cmp_swap(v[0], v[1]);
+  cmp_swap(v[3], v[4]);
+  cmp_swap(v[2], v[4]);
+  cmp_swap(v[2], v[3]);
+  cmp_swap(v[0], v[3]);
+  cmp_swap(v[0], v[2]);
+  cmp_swap(v[1], v[4]);
+  cmp_swap(v[1], v[3]);
+  cmp_swap(v[1], v[2]);
+  return __builtin_isfinite(v[2]) ? v[2] : 0.f;
+}
+
+// Element j of channel ch: NHWC (hw = 1) at j*c + ch, NCHW at
+// (j / hw)*c*hw + ch*hw + j % hw.
+__device__ inline int64_t chan_elem(int64_t j, int64_t ch, int64_t c, int64_t hw) {
+  return (j / hw) * c * hw + ch * hw + j % hw;
+}
+
+__device__ inline void shift_rows(int64_t n, int64_t (&js)[5]) {
+  js[0] = 0;
+  js[1] = n / 4;
+  js[2] = n / 2;
+  js[3] = (3 * n) / 4;
+  js[4] = n - 1;
+}
+
+template <class Tr>
+__device__ inline float chan_shift(const typename Tr::S* x, int64_t ch, int64_t n, int64_t c,
+                                   int64_t hw) {
+  if (n <= 0) return 0.f;
+  int64_t js[5];
+  shift_rows(n, js);
+  float v[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) v[i] = Tr::ld(x[chan_elem(js[i], ch, c, hw)]);
+  return shift_of(v);
+}
+
+// ---------------------------------------------------------------------------
 // 1. Reduce.
 // ---------------------------------------------------------------------------
-// kGrad = false: s1 += x - K, s2 += (x - K)^2, K = first element of channel.
+// kGrad = false: s1 += x - K, s2 += (x - K)^2, K = chan_shift() of the channel.
 // kGrad = true:  s1 += dy,    s2 += dy * (x - mean).
 template <class Tr, int VEC, bool kGrad>
 __device__ inline void accum(const typename Tr::S (&xv)[VEC],
@@ -178,7 +237,7 @@ __global__ __launch_bounds__(kThreads) void bn_nhwc_reduce_kernel(
       for (int j = 0; j < VEC; ++j) k[j] = mean_in[c0 + j];
     } else {
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) k[j] = Tr::ld(x[c0 + j]);
+      for (int j = 0; j < VEC; ++j) k[j] = chan_shift<Tr>(x, c0 + j, rows, c, 1);
     }
     const S* __restrict__ px = x + c0;
     const S* __restrict__ pd = kGrad ? dy + c0 : nullptr;
@@ -229,7 +288,7 @@ __global__ __launch_bounds__(kThreads) void bn_nchw_reduce_kernel(
   const int64_t n0 = g * ipg;
   int64_t n1 = n0 + ipg;
   if (n1 > nimg) n1 = nimg;
-  float kk = kGrad ? mean_in[ch] : Tr::ld(x[static_cast<int64_t>(ch) * plane]);
+  float kk = kGrad ? mean_in[ch] : chan_shift<Tr>(x, ch, nimg * plane, c, plane);
   float k[VEC], s1[VEC], s2[VEC];
 #pragma unroll
   for (int j = 0; j < VEC; ++j) { k[j] = kk; s1[j] = 0.f; s2[j] = 0.f; }
@@ -265,8 +324,8 @@ struct FinArgs {
   int64_t groups;
   int c;
   int64_t n;          // elements per channel
-  const void* x;      // forward shift source (first element of each channel)
-  int64_t k_stride;   // element stride between channels' first elements
+  const void* x;      // forward shift source (chan_shift() samples)
+  int64_t k_stride;   // element stride between channels (1 NHWC, H*W NCHW)
   const float* scale;
   const float* offset;
   const float* mean_in;
@@ -296,7 +355,7 @@ __device__ inline float4 finish_channel(const FinArgs& a, int ch, double s1, dou
   const double n = static_cast<double>(a.n);
   if constexpr (!kGrad) {
     const float kshift =
-        Tr::ld(static_cast<const typename Tr::S*>(a.x)[ch * a.k_stride]);
+        chan_shift<Tr>(static_cast<const typename Tr::S*>(a.x), ch, a.n, a.c, a.k_stride);
     const double mean = static_cast<double>(kshift) + s1 / n;
     double m2 = s2 - s1 * s1 / n;
     if (m2 < 0.0) m2 = 0.0;
@@ -522,7 +581,7 @@ template <> struct Resident<TF16> {
   static constexpr int kPaFwd = 0, kPbFwd = 4, kPaGrad = 0, kPbGrad = 0;
 };
 template <> struct Resident<TBF16> {
-  static constexpr int kRegFwd = 8, kRegGrad = 4, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kRegFwd = 7, kRegGrad = 4, kLdsFwd = 18, kLdsGrad = 9;
   static constexpr int kPaFwd = 4, kPbFwd = 4, kPaGrad = 4, kPbGrad = 8;
 };
 
@@ -696,7 +755,17 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   }
   if (active) {
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) k[j] = kGrad ? a.fin.mean_in[c0 + j] : Tr::ld(px[j]);
+    for (int j = 0; j < VEC; ++j) k[j] = kGrad ? a.fin.mean_in[c0 + j] : 0.f;
+  }
+  const int width = (1 << a.tx_shift) * VEC;  // channels of this tile
+  uint4 kw[kGrad ? 1 : 5];
+  if constexpr (!kGrad) {
+    if (active) {
+      int64_t js[5];
+      shift_rows(a.rows, js);
+#pragma unroll
+      for (int i = 0; i < 5; ++i) kw[i] = ld16(px + js[i] * a.c);
+    }
   }
   // Register- and LDS-resident rows: all loads issued before any is used.
   uint4 xr[KR];
@@ -715,6 +784,21 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     if (KR + q < nk) {
       xl[q] = ld16(xrow(KR + q));
       if constexpr (kGrad) dl[q] = ld16(drow(KR + q));
+    }
+  }
+  if constexpr (!kGrad) {
+    if (active) {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        float v[5];
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+          S sv[VEC];
+          __builtin_memcpy(sv, &kw[i], 16);
+          v[i] = Tr::ld(sv[j]);
+        }
+        k[j] = shift_of(v);
+      }
     }
   }
 #pragma unroll
@@ -758,7 +842,6 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       s2[j] += __shfl_xor(s2[j], off, 64);
     }
   }
-  const int width = (1 << a.tx_shift) * VEC;  // channels of this tile
   {
     const int wave = tid >> 6;
     const int lane = tid & 63;

@@ -117,6 +117,29 @@ def test_large_mean_statistics(dev):
     assert_close(fwd.reserve_space_2.cpu().numpy(), rsv, "float32", 1e-5, "variance")
 
 
+@pytest.mark.parametrize("shape,data_format", [((64, 28, 28, 64), "NHWC"),
+                                               ((16, 64, 28, 28), "NCHW"),
+                                               ((256, 14, 14, 1024), "NHWC")])
+def test_outlier_first_element_statistics(dev, shape, data_format):
+    """A channel whose first element is a large outlier (1e3 against N(0,1)
+    data, and -5e2 in a second channel): the statistics must still match
+    TF-CPU's two-pass computation to 1e-5, i.e. the kernels' sums must not
+    be taken around that element."""
+    rng = np.random.default_rng(17)
+    x, scale, offset, dy = _inputs(rng, shape, "float32", data_format)
+    first = (0, 0, 0, slice(None)) if data_format == "NHWC" else (0, slice(None), 0, 0)
+    row0 = x[first].copy()
+    row0[3] = 1e3
+    row0[5] = -5e2
+    x[first] = row0
+    fwd, _ = _run_fwd_grad(dev, x, scale, offset, dy, "float32", data_format, 1e-3)
+    _, rbm, rbv, rsm, rsv = oracle.bn_fwd(x, scale, offset, epsilon=1e-3,
+                                          data_format=data_format)
+    assert_close(fwd.reserve_space_1.cpu().numpy(), rsm, "float32", STAT_TOL, "mean")
+    assert_close(fwd.reserve_space_2.cpu().numpy(), rsv, "float32", 1e-5, "variance")
+    assert_close(fwd.batch_variance.cpu().numpy(), rbv, "float32", 1e-5, "Bessel variance")
+
+
 def test_exponential_avg_factor_and_inference(dev):
     rng = np.random.default_rng(11)
     shape = (4, 6, 6, 32)
