@@ -159,6 +159,58 @@ __device__ inline float shift_of(float (&v)[5]) {
   return __builtin_isfinite(v[2]) ? v[2] : 0.f;
 }
 
+// The shifts of the VEC channels of five sample vectors (the fused kernel's
+// K).  Same selection as shift_of() per channel.  For half the network runs
+// on packed channel pairs (v_pk_min/max_f16, IEEE minNum/maxNum like fminf/
+// fmaxf): widening half to float is exact and order-preserving, so the
+// median is the same element, and the five samples stay packed in 20
+// registers instead of 40 floats - registers the resident rows can use.
+template <class Tr>
+__device__ inline void shift_words(const uint4 (&kw)[5], float (&k)[Tr::kVec]) {
+  using S = typename Tr::S;
+#pragma unroll
+  for (int j = 0; j < Tr::kVec; ++j) {
+    float v[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      S sv[Tr::kVec];
+      __builtin_memcpy(sv, &kw[i], 16);
+      v[i] = Tr::ld(sv[j]);
+    }
+    k[j] = shift_of(v);
+  }
+}
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__device__ inline void cmp_swap2(half2v& lo, half2v& hi) {
+  const half2v a = __builtin_elementwise_min(lo, hi), b = __builtin_elementwise_max(lo, hi);
+  lo = a;
+  hi = b;
+}
+
+template <>
+__device__ inline void shift_words<TF16>(const uint4 (&kw)[5], float (&k)[8]) {
+  half2v v[5][4];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) __builtin_memcpy(v[i], &kw[i], 16);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    cmp_swap2(v[0][w], v[1][w]);
+    cmp_swap2(v[3][w], v[4][w]);
+    cmp_swap2(v[2][w], v[4][w]);
+    cmp_swap2(v[2][w], v[3][w]);
+    cmp_swap2(v[0][w], v[3][w]);
+    cmp_swap2(v[0][w], v[2][w]);
+    cmp_swap2(v[1][w], v[4][w]);
+    cmp_swap2(v[1][w], v[3][w]);
+    cmp_swap2(v[1][w], v[2][w]);
+    const float lo = static_cast<float>(v[2][w].x), hi = static_cast<float>(v[2][w].y);
+    k[2 * w] = __builtin_isfinite(lo) ? lo : 0.f;
+    k[2 * w + 1] = __builtin_isfinite(hi) ? hi : 0.f;
+  }
+}
+
 // Element j of channel ch: NHWC (hw = 1) at j*c + ch, NCHW at
 // (j / hw)*c*hw + ch*hw + j % hw.
 __device__ inline int64_t chan_elem(int64_t j, int64_t ch, int64_t c, int64_t hw) {
@@ -567,21 +619,36 @@ __global__ __launch_bounds__(kThreads) void bn_nchw_apply_kernel(
 constexpr int kFusedThreads = 512;
 constexpr unsigned kSpinLimit = 1u << 24;  // ~0.5 s, then give up (flagged)
 // Resident 16-byte vectors per thread and per input tensor: KR in VGPRs (the
-// largest counts that compile without spills - the 8-wide types carry twice
-// the per-channel state), KL in LDS (the LDS budget split over the inputs).
+// largest counts that compile without spills at 256 VGPRs), KL in LDS (the
+// LDS budget split over the inputs).  kOpaque*: the register rows are made
+// opaque right after their phase-1 use; without it the compiler keeps half
+// rows split into 16-bit pieces (8 registers per row instead of 4) until
+// phase 3, and with it the bf16 and f32 forwards schedule worse - so it is
+// chosen per type and direction, by the spill-free KR it allows.
+// kRegFwdSmall: the forward's register rows when a thread has at most
+// kSmallFwdRows rows (the 14x14 and 7x7 stage shapes): there fewer register
+// rows measured faster even where that leaves rows to stream (each register
+// row adds unrolled code to a kernel run about once, and the resident loads
+// arrive as one burst that streams worse than the pipelined loop).
 // PA/PB: streamed vectors per tensor prefetched for phase 3 while the grid
 // barriers are pending - PA after the first barrier's arrival (by waves with
 // no phase-2 channel), PB after the second's (by every wave).
 template <class Tr> struct Resident {
-  static constexpr int kRegFwd = 28, kRegGrad = 10, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr bool kOpaqueFwd = false, kOpaqueGrad = true;
+  static constexpr int kRegFwd = 26, kRegGrad = 11, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 4, kPbFwd = 8, kPaGrad = 4, kPbGrad = 8;
 };
 template <> struct Resident<TF16> {
-  static constexpr int kRegFwd = 12, kRegGrad = 8, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr bool kOpaqueFwd = true, kOpaqueGrad = true;
+  static constexpr int kRegFwd = 30, kRegGrad = 13, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 0, kPbFwd = 4, kPaGrad = 0, kPbGrad = 0;
 };
 template <> struct Resident<TBF16> {
-  static constexpr int kRegFwd = 7, kRegGrad = 4, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr bool kOpaqueFwd = false, kOpaqueGrad = true;
+  static constexpr int kRegFwd = 30, kRegGrad = 9, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 4, kPbFwd = 4, kPaGrad = 4, kPbGrad = 8;
 };
 
@@ -708,6 +775,29 @@ __device__ inline uint4 ld16_last(const void* p) {
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
+// Loads of a workgroup's own rows through a buffer resource (gfx9 word 3
+// 0x00020000: raw, stride 0) that covers rows [r0, r1) of one tensor.  An
+// offset at or past its end - a row past the group, or any row of an
+// inactive lane (offset + 2^31) - is out of range: the load returns zeros
+// and makes no memory request.  Loads that may not be needed are issued that
+// way instead of inside a branch: a load inside `if (q < nk)` ended up
+// waiting for its data before the next load issued (the compiler copies the
+// loaded registers at the branch join), which serialized the resident-row
+// loads of the forward kernels.  Offsets are 32-bit (one VGPR per address
+// instead of two); the host keeps a group's span below 2^31 bytes.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+__device__ inline __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                           static_cast<int>(bytes > 0 ? bytes : 0), 0x00020000);
+}
+__device__ inline uint4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ inline uint4 bld16_last(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2 /* nt */);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 // Outputs are written once and not read again by the op: non-temporal.
 __device__ inline void st16(void* p, const uint4& v) {
   __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(p));
@@ -741,6 +831,18 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   const int64_t base = (r0 + ty) * a.c;                     // my first row
   auto xrow = [&](int64_t q) { return px + base + q * rstride; };
   auto drow = [&](int64_t q) { return pd + base + q * rstride; };
+  // This group's rows as buffer resources: roff(q) is the byte offset of my
+  // row q, out of range past the group (and for an inactive lane);
+  // roff_if(q, false) is out of range.
+  const int64_t gbytes = (r1 - r0) * a.c * static_cast<int64_t>(sizeof(S));
+  const auto rx = rows_rsrc(static_cast<const S*>(a.x) + r0 * a.c, gbytes);
+  const auto rd = rows_rsrc(kGrad ? static_cast<const S*>(a.dy) + r0 * a.c : a.x, gbytes);
+  const uint32_t lane_off =
+      active ? static_cast<uint32_t>((ty * a.c + c0) * static_cast<int64_t>(sizeof(S)))
+             : kOutOfRange;
+  const uint32_t rstride_b = static_cast<uint32_t>(rstride * static_cast<int64_t>(sizeof(S)));
+  auto roff = [&](int64_t q) { return lane_off + static_cast<uint32_t>(q) * rstride_b; };
+  auto roff_if = [&](int64_t q, bool use) { return use ? roff(q) : kOutOfRange; };
   auto lds = [&](int q2, int which) -> uint4& {
     return lds_rows[(q2 * kIn + which) * kFusedThreads + tid];
   };
@@ -758,58 +860,59 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     for (int j = 0; j < VEC; ++j) k[j] = kGrad ? a.fin.mean_in[c0 + j] : 0.f;
   }
   const int width = (1 << a.tx_shift) * VEC;  // channels of this tile
+  // The shift samples: an inactive lane (px = x) reads channels 0..VEC-1 of
+  // the same rows, in bounds, and its k is never used.
   uint4 kw[kGrad ? 1 : 5];
   if constexpr (!kGrad) {
-    if (active) {
-      int64_t js[5];
-      shift_rows(a.rows, js);
+    int64_t js[5];
+    shift_rows(a.rows, js);
 #pragma unroll
-      for (int i = 0; i < 5; ++i) kw[i] = ld16(px + js[i] * a.c);
-    }
+    for (int i = 0; i < 5; ++i) kw[i] = ld16(px + js[i] * a.c);
   }
-  // Register- and LDS-resident rows: all loads issued before any is used.
+  // Register- and LDS-resident rows: all loads issued before any is used,
+  // none of them in a branch (rows past nk are out of range).
   uint4 xr[KR];
   uint4 dr[kGrad ? KR : 1];
   uint4 xl[KL];
   uint4 dl[kGrad ? KL : 1];
 #pragma unroll
   for (int q = 0; q < KR; ++q) {
-    if (q < nk) {
-      xr[q] = ld16(xrow(q));
-      if constexpr (kGrad) dr[q] = ld16(drow(q));
-    }
+    xr[q] = bld16(rx, roff(q));
+    if constexpr (kGrad) dr[q] = bld16(rd, roff(q));
   }
 #pragma unroll
   for (int q = 0; q < KL; ++q) {
-    if (KR + q < nk) {
-      xl[q] = ld16(xrow(KR + q));
-      if constexpr (kGrad) dl[q] = ld16(drow(KR + q));
-    }
+    xl[q] = bld16(rx, roff(KR + q));
+    if constexpr (kGrad) dl[q] = bld16(rd, roff(KR + q));
   }
-  if constexpr (!kGrad) {
-    if (active) {
+  if constexpr (!kGrad) shift_words<Tr>(kw, k);
+  // After its phase-1 use a register row is made opaque, so the compiler
+  // keeps its packed words to phase 3 rather than the half-width pieces it
+  // split them into (for half: twice the registers).
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        float v[5];
-#pragma unroll
-        for (int i = 0; i < 5; ++i) {
-          S sv[VEC];
-          __builtin_memcpy(sv, &kw[i], 16);
-          v[i] = Tr::ld(sv[j]);
-        }
-        k[j] = shift_of(v);
-      }
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < KR; ++q)
+  for (int q = 0; q < KR; ++q) {
     if (q < nk) accum_words<Tr, kGrad>(xr[q], dr[kGrad ? q : 0], k, s1, s2);
+    if constexpr (kGrad ? Resident<Tr>::kOpaqueGrad : Resident<Tr>::kOpaqueFwd) {
+      asm volatile("" : "+v"(xr[q].x), "+v"(xr[q].y), "+v"(xr[q].z), "+v"(xr[q].w));
+      if constexpr (kGrad)
+        asm volatile("" : "+v"(dr[q].x), "+v"(dr[q].y), "+v"(dr[q].z), "+v"(dr[q].w));
+    }
+  }
+  // LDS rows: stored as they arrive (rows past nk hold zeros and are never
+  // used), then accumulated from LDS in a loop, not unrolled - the unrolled
+  // per-row code made the kernel about as large as the 64 KB instruction
+  // cache a CU pair shares, which the small shapes (code run once) paid for.
 #pragma unroll
   for (int q = 0; q < KL; ++q) {
+    lds(q, 0) = xl[q];
+    if constexpr (kGrad) lds(q, kGrad ? 1 : 0) = dl[kGrad ? q : 0];
+  }
+#pragma unroll 2
+  for (int q = 0; q < KL; ++q) {
     if (KR + q < nk) {
-      lds(q, 0) = xl[q];
-      if constexpr (kGrad) lds(q, kGrad ? 1 : 0) = dl[kGrad ? q : 0];
-      accum_words<Tr, kGrad>(xl[q], dl[kGrad ? q : 0], k, s1, s2);
+      const uint4 xw = lds(q, 0);
+      const uint4 dw = kGrad ? lds(q, kGrad ? 1 : 0) : xw;
+      accum_words<Tr, kGrad>(xw, dw, k, s1, s2);
     }
   }
   // Streamed rows, U vectors per tensor in flight.
@@ -824,11 +927,18 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
 #pragma unroll
     for (int u = 0; u < U; ++u) accum_words<Tr, kGrad>(xw[u], dw[u], k, s1, s2);
   }
-  for (; q < nk; ++q) {
-    const uint4 xw = ld16(xrow(q));
-    uint4 dw = xw;
-    if constexpr (kGrad) dw = ld16(drow(q));
-    accum_words<Tr, kGrad>(xw, dw, k, s1, s2);
+  // Fewer than U rows left: all of their loads in flight at once (rows past
+  // nk out of range), not one load-and-wait per row.
+  if (q < nk) {
+    uint4 xw[U], dw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      xw[u] = bld16(rx, roff(q + u));
+      if constexpr (kGrad) dw[u] = bld16(rd, roff(q + u));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (q + u < nk) accum_words<Tr, kGrad>(xw[u], dw[u], k, s1, s2);
   }
   // Workgroup partial per channel: sum the row lanes of each wave with
   // shuffles, then the waves through LDS, then one coherent store per
@@ -878,10 +988,9 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   if (pre_a) {
 #pragma unroll
     for (int p = 0; p < PA; ++p) {
-      if (nk - 1 - p >= KR + KL) {
-        pax[p] = ld16(xrow(nk - 1 - p));
-        if constexpr (kGrad) pad[p] = ld16(drow(nk - 1 - p));
-      }
+      const uint32_t o = roff_if(nk - 1 - p, nk - 1 - p >= KR + KL);
+      pax[p] = bld16(rx, o);
+      if constexpr (kGrad) pad[p] = bld16(rd, o);
     }
   }
   const int64_t qb = nk - 1 - (pre_a ? PA : 0);  // first row of part B
@@ -914,10 +1023,9 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   uint4 pbx[PB > 0 ? PB : 1], pbd[kGrad && PB > 0 ? PB : 1];
 #pragma unroll
   for (int p = 0; p < PB; ++p) {
-    if (qb - p >= KR + KL) {
-      pbx[p] = ld16(xrow(qb - p));
-      if constexpr (kGrad) pbd[p] = ld16(drow(qb - p));
-    }
+    const uint32_t o = roff_if(qb - p, qb - p >= KR + KL);
+    pbx[p] = bld16(rx, o);
+    if constexpr (kGrad) pbd[p] = bld16(rd, o);
   }
   grid_wait(a, 2);
 
@@ -972,13 +1080,19 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     for (int u = 0; u < U3; ++u)
       st16(po + base + (q - u) * rstride, apply_words<Tr, kGrad>(xw[u], dw[u], cf));
   }
-  for (; q >= qlo; --q) {
-    const uint4 xw = ld16_last(xrow(q));
-    uint4 dw = xw;
-    if constexpr (kGrad) dw = ld16_last(drow(q));
-    st16(po + base + q * rstride, apply_words<Tr, kGrad>(xw, dw, cf));
-  }
+  if (q >= qlo) {  // fewer than U3 rows left: loads issued together
+    uint4 xw[U3], dw[U3];
 #pragma unroll
+    for (int u = 0; u < U3; ++u) {
+      const uint32_t o = roff_if(q - u, q - u >= qlo);
+      xw[u] = bld16_last(rx, o);
+      if constexpr (kGrad) dw[u] = bld16_last(rd, o);
+    }
+#pragma unroll
+    for (int u = 0; u < U3; ++u)
+      if (q - u >= qlo) st16(po + base + (q - u) * rstride, apply_words<Tr, kGrad>(xw[u], dw[u], cf));
+  }
+#pragma unroll 2
   for (int q2 = 0; q2 < KL; ++q2) {
     if (KR + q2 < nk) {
       const uint4 xw = lds(q2, 0);
@@ -1181,10 +1295,11 @@ constexpr int fused_kr() { return kGrad ? Resident<Tr>::kRegGrad : Resident<Tr>:
 template <class Tr, bool kGrad>
 constexpr int fused_kl() { return kGrad ? Resident<Tr>::kLdsGrad : Resident<Tr>::kLdsFwd; }
 
-template <class Tr, bool kGrad>
+constexpr int64_t kSmallFwdRows = 64;
+
+template <class Tr, bool kGrad, int KR = fused_kr<Tr, kGrad>()>
 const void* fused_kernel() {
-  return reinterpret_cast<const void*>(
-      &bn_fused_nhwc_kernel<Tr, kGrad, fused_kr<Tr, kGrad>(), fused_kl<Tr, kGrad>()>);
+  return reinterpret_cast<const void*>(&bn_fused_nhwc_kernel<Tr, kGrad, KR, fused_kl<Tr, kGrad>()>);
 }
 
 template <class Tr, bool kGrad>
@@ -1203,6 +1318,10 @@ int fused_blocks_per_cu() {
     hipError_t e = hipFuncSetAttribute(fused_kernel<Tr, kGrad>(),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        static_cast<int>(fused_smem<Tr, kGrad>()));
+    if (e == hipSuccess && !kGrad)  // the small-shape forward: same LDS, fewer VGPRs
+      e = hipFuncSetAttribute(fused_kernel<Tr, kGrad, Resident<Tr>::kRegFwdSmall>(),
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(fused_smem<Tr, kGrad>()));
     if (e == hipSuccess)
       e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fused_kernel<Tr, kGrad>(),
                                                        kFusedThreads, fused_smem<Tr, kGrad>());
@@ -1251,6 +1370,13 @@ bool make_fused_plan(const BnGeometry& g, int vec, int blocks_per_cu, FusedPlan*
   if (groups > max_groups) groups = max_groups;
   if (groups > fused_group_bound()) groups = fused_group_bound();
   fp->rows_per_g = (g.rows + groups - 1) / groups;
+  // The kernel reads a workgroup's own rows through a buffer resource with
+  // 32-bit offsets (rows past the group are out of range and read nothing):
+  // the group's span plus the rows a thread may address past its last one
+  // (fewer than 64 row passes) must stay below 2^31 bytes.
+  const int64_t esz = 16 / vec;
+  if ((fp->rows_per_g + 64 * static_cast<int64_t>(ry)) * g.c * esz >= (int64_t{1} << 31))
+    return false;
   fp->groups = (g.rows + fp->rows_per_g - 1) / fp->rows_per_g;
   fp->blocks = static_cast<int>(fp->groups * fp->ct);
   fp->dyn_rows = 0;
@@ -1373,11 +1499,15 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   fa.timeout_flag = reinterpret_cast<unsigned*>(region + 1);
   fa.queues = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(region) + kQueueOffset);
   fa.reset_at_exit = recorded ? 1 : 0;
+  const int ry = kFusedThreads >> fp.tx_shift;
+  const int64_t nk_max = (fp.rows_per_g + ry - 1) / ry;  // rows of a thread
+  const bool small = !kGrad && nk_max <= kSmallFwdRows;
+  const int kr = small ? Resident<Tr>::kRegFwdSmall : fused_kr<Tr, kGrad>();
   {
     FusedPlan fd = fp;
     constexpr int kPre = kGrad ? Resident<Tr>::kPaGrad + Resident<Tr>::kPbGrad
                                : Resident<Tr>::kPaFwd + Resident<Tr>::kPbFwd;
-    set_dynamic_share(&fd, fused_kr<Tr, kGrad>() + fused_kl<Tr, kGrad>(), kPre, kGrad ? 4 : 8);
+    set_dynamic_share(&fd, kr + fused_kl<Tr, kGrad>(), kPre, kGrad ? 4 : 8);
     fa.dyn_chunk = fd.dyn_chunk;
     const size_t slots = kQueueBytes / sizeof(unsigned);
     const size_t per_shard = static_cast<size_t>(fp.ct) * (kFusedThreads / 64);
@@ -1390,22 +1520,21 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   fa.fin.groups = fp.groups;
   const char* name = kGrad ? "tfma_bn_grad_fused" : "tfma_bn_fwd_fused";
   SetLastKernel(name);
+  const void* kern = small ? fused_kernel<Tr, kGrad, Resident<Tr>::kRegFwdSmall>()
+                           : fused_kernel<Tr, kGrad>();
+  const size_t smem = fused_smem<Tr, kGrad>();
+  void* kargs[] = {&fa};
   if (recorded) {  // no events, no tracing, no chain bookkeeping inside a graph
-    constexpr int KR = fused_kr<Tr, kGrad>();
-    constexpr int KL = fused_kl<Tr, kGrad>();
-    const size_t smem = fused_smem<Tr, kGrad>();
-    hipLaunchKernelGGL((bn_fused_nhwc_kernel<Tr, kGrad, KR, KL>), dim3(fp.blocks),
-                       dim3(kFusedThreads), smem, stream, fa);
-    return hipGetLastError();
+    hipError_t le = hipLaunchKernel(kern, dim3(fp.blocks), dim3(kFusedThreads), kargs, smem,
+                                    stream);
+    return le != hipSuccess ? le : hipGetLastError();
   }
   const TraceEvents tev = TraceTake(name);
   hipEvent_t end = tev.end ? tev.end : bs->last;
   {
-    constexpr int KR = fused_kr<Tr, kGrad>();
-    constexpr int KL = fused_kl<Tr, kGrad>();
-    const size_t smem = fused_smem<Tr, kGrad>();
-    hipExtLaunchKernelGGL((bn_fused_nhwc_kernel<Tr, kGrad, KR, KL>), dim3(fp.blocks),
-                          dim3(kFusedThreads), smem, stream, tev.start, end, 0u, fa);
+    hipError_t le = hipExtLaunchKernel(kern, dim3(fp.blocks), dim3(kFusedThreads), kargs, smem,
+                                       stream, tev.start, end, 0);
+    if (le != hipSuccess) return le;
   }
   TraceCommit(tev);
   hipError_t e = hipGetLastError();
