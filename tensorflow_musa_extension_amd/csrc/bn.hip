@@ -1318,10 +1318,12 @@ int fused_blocks_per_cu() {
     hipError_t e = hipFuncSetAttribute(fused_kernel<Tr, kGrad>(),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        static_cast<int>(fused_smem<Tr, kGrad>()));
-    if (e == hipSuccess && !kGrad)  // the small-shape forward: same LDS, fewer VGPRs
-      e = hipFuncSetAttribute(fused_kernel<Tr, kGrad, Resident<Tr>::kRegFwdSmall>(),
-                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                              static_cast<int>(fused_smem<Tr, kGrad>()));
+    if constexpr (!kGrad) {  // the small-shape forward: same LDS, fewer VGPRs
+      if (e == hipSuccess)
+        e = hipFuncSetAttribute(fused_kernel<Tr, kGrad, Resident<Tr>::kRegFwdSmall>(),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(fused_smem<Tr, kGrad>()));
+    }
     if (e == hipSuccess)
       e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fused_kernel<Tr, kGrad>(),
                                                        kFusedThreads, fused_smem<Tr, kGrad>());
@@ -1520,8 +1522,10 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   fa.fin.groups = fp.groups;
   const char* name = kGrad ? "tfma_bn_grad_fused" : "tfma_bn_fwd_fused";
   SetLastKernel(name);
-  const void* kern = small ? fused_kernel<Tr, kGrad, Resident<Tr>::kRegFwdSmall>()
-                           : fused_kernel<Tr, kGrad>();
+  const void* kern = fused_kernel<Tr, kGrad>();
+  if constexpr (!kGrad) {
+    if (small) kern = fused_kernel<Tr, kGrad, Resident<Tr>::kRegFwdSmall>();
+  }
   const size_t smem = fused_smem<Tr, kGrad>();
   void* kargs[] = {&fa};
   if (recorded) {  // no events, no tracing, no chain bookkeeping inside a graph
