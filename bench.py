@@ -25,7 +25,9 @@ components: the other kernels (Adam, mixed-precision Adam, grouped Adam at
         the ResNet-50 and 1.31e9-parameter configs, the elementwise chains,
         ReluGrad, BiasAddGrad) at their config shapes, each rep timed with HIP
         events after a 1 GiB read that evicts the Infinity Cache (GB/s, % of
-        peak, Gelem/s).
+        peak, Gelem/s), then the same reps again with events attached to the
+        kernels' own dispatches (kernel_ms, kernel_GB/s, kernel_pct_peak: the
+        kernel's duration without the dispatch and event overhead).
 host_path: pageable host<->device copies (256 MiB) through the library's
         staged path, beside the HIP runtime's own pageable copy and a pinned
         copy (the PCIe ceiling), in GB/s.
@@ -183,12 +185,25 @@ def components(torch, ops, dev):
     reps, warm = 20, 3
     flush = torch.ones(1 << 28, device=dev)  # 1 GiB, read between reps
 
-    def rate(calls, nbytes, elems, reps_=reps):
+    def rate(calls, nbytes, elems, kernel, reps_=reps):
+        """Wall time per call (HIP events around it, which includes the
+        dispatch and event overhead), then, in a second pass, the kernel time
+        per call from events attached to the library's own dispatches of
+        `kernel` (summed over its launches in the call)."""
         ms = time_calls(torch, calls, reps_, warm, flush=flush)
         gbps = nbytes / (ms / 1e3) / 1e9
+        ops.trace_enable(kernel)
+        time_calls(torch, calls, reps_, 0, flush=flush)
+        kms, launches = ops.trace_read()
+        ops.trace_enable(None)
+        kms = kms / reps_
+        kgbps = nbytes / (kms / 1e3) / 1e9 if kms else None
         return {"ms": round(ms, 4), "GB/s": round(gbps, 1),
                 "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
-                "Gelem/s": round(elems / (ms / 1e3) / 1e9, 2)}
+                "Gelem/s": round(elems / (ms / 1e3) / 1e9, 2),
+                "kernel_ms": round(kms, 4) if kms else None,
+                "kernel_GB/s": round(kgbps, 1) if kgbps else None,
+                "kernel_pct_peak": round(100 * kgbps / PEAK_GBPS, 1) if kgbps else None}
 
     n = 25_600_000
     var = 0.02 * torch.randn(n, generator=gen, device=dev)
@@ -196,12 +211,12 @@ def components(torch, ops, dev):
     v = torch.zeros(n, device=dev)
     g = 1e-3 * torch.randn(n, generator=gen, device=dev)
     adam = ops.bind(ops.ResourceApplyAdam, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7, g)
-    out["adam_f32_25.6M"] = rate([adam], 28 * n, n)
+    out["adam_f32_25.6M"] = rate([adam], 28 * n, n, "tfma_adam_flat")
     # Mixed precision (fp32 state, bf16 grad): 24 B of state + 2 B of grad.
     gb = g.to(torch.bfloat16)
     mixed = ops.bind(ops.MusaResourceApplyAdamMixed, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999,
                      1e-7, gb)
-    out["adam_mixed_bf16grad_25.6M"] = rate([mixed], 26 * n, n)
+    out["adam_mixed_bf16grad_25.6M"] = rate([mixed], 26 * n, n, "tfma_adam_flat")
     del gb
 
     shapes = resnet50_shapes()
@@ -212,7 +227,8 @@ def components(torch, ops, dev):
     total = sum(t.numel() for t in tv)
     grouped = ops.bind(ops.MusaGroupedResourceApplyAdam, tv, tm, tvv, tg, 0.9, 0.999, 1e-3, 0.9,
                        0.999, 1e-7)
-    out["grouped_adam_f32_resnet50_161"] = rate([grouped], 28 * total, total)
+    out["grouped_adam_f32_resnet50_161"] = rate([grouped], 28 * total, total,
+                                                "tfma_adam_grouped")
     del var, m, v, g, tv, tm, tvv, tg, grouped, adam, mixed
 
     # cfg5: 1.31B parameters in 145 tensors, 21 GB of state resident.
@@ -224,7 +240,8 @@ def components(torch, ops, dev):
     total5 = sum(t.numel() for t in tv)
     grouped5 = ops.bind(ops.MusaGroupedResourceApplyAdam, tv, tm, tvv, tg, 0.9, 0.999, 1e-3,
                         0.9, 0.999, 1e-7)
-    out["grouped_adam_f32_cfg5_145"] = rate([grouped5], 28 * total5, total5, reps_=10)
+    out["grouped_adam_f32_cfg5_145"] = rate([grouped5], 28 * total5, total5,
+                                            "tfma_adam_grouped", reps_=10)
     del tv, tm, tvv, tg, grouped5
     torch.cuda.empty_cache()
 
@@ -234,26 +251,28 @@ def components(torch, ops, dev):
         b = torch.randn(4096, generator=gen, device=dev).to(dt)
         E = x.numel()
         out[f"bias_add_relu_{name}_8192x4096"] = rate([ops.bind(ops.MusaBiasAddRelu, x, b)],
-                                                      2 * s * E + s * 4096, E)
+                                                      2 * s * E + s * 4096, E, "tfma_ew_add_relu")
         out[f"add_v2_relu_{name}_8192x4096"] = rate([ops.bind(ops.MusaAddV2Relu, x, b)],
-                                                    2 * s * E + s * 4096, E)
+                                                    2 * s * E + s * 4096, E, "tfma_ew_add_relu")
         a_full = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
         b_full = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
         out[f"mul_add_full_{name}_8192x4096"] = rate(
-            [ops.bind(ops.MusaShiftedAffineMap, x, a_full, b_full)], 4 * s * E, E)
+            [ops.bind(ops.MusaShiftedAffineMap, x, a_full, b_full)], 4 * s * E, E,
+            "tfma_ew_mul_add")
         out[f"mul_add_row_{name}_8192x4096"] = rate(
-            [ops.bind(ops.MusaShiftedAffineMap, x, b, b)], 2 * s * E + 2 * s * 4096, E)
+            [ops.bind(ops.MusaShiftedAffineMap, x, b, b)], 2 * s * E + 2 * s * 4096, E,
+            "tfma_ew_mul_add")
         xo = torch.randn(8191, 4095, generator=gen, device=dev).to(dt)
         bo = torch.randn(4095, generator=gen, device=dev).to(dt)
         out[f"bias_add_relu_{name}_8191x4095"] = rate([ops.bind(ops.MusaBiasAddRelu, xo, bo)],
                                                       2 * s * xo.numel() + s * 4095,
-                                                      xo.numel())
+                                                      xo.numel(), "tfma_ew_add_relu")
         # The backward side of the chains: ReluGrad (2 reads, 1 write) and
         # BiasAddGrad (one read of the gradient).
         out[f"relu_grad_{name}_8192x4096"] = rate([ops.bind(ops.ReluGrad, a_full, x)], 3 * s * E,
-                                                  E)
+                                                  E, "tfma_ew_relu_grad")
         out[f"bias_add_grad_{name}_8192x4096"] = rate([ops.bind(ops.BiasAddGrad, a_full)],
-                                                      s * E + s * 4096, E)
+                                                      s * E + s * 4096, E, "tfma_bias_add_grad")
         del x, b, a_full, b_full, xo, bo
     torch.cuda.synchronize()
     del flush

@@ -208,13 +208,13 @@ hipError_t launch_flat(void* var, void* m, void* v, const void* grad,
   const bool vec_ok =
       (align & 15) == 0 && (reinterpret_cast<uintptr_t>(grad) & (VEC * sizeof(SG) - 1)) == 0;
   const int64_t blocks = (n + kGroupedAdamChunk - 1) / kGroupedAdamChunk;
-  LaunchScope scope(stream, vec_ok ? "tfma_adam_flat_vec" : "tfma_adam_flat_scalar");
+  const char* const kname = vec_ok ? "tfma_adam_flat_vec" : "tfma_adam_flat_scalar";
   if (n >= kStreamElems)
-    hipLaunchKernelGGL((adam_chunk_kernel<Tr, Tg, kNesterov, true>), dim3(blocks),
+    TFMA_LAUNCH(kname, (adam_chunk_kernel<Tr, Tg, kNesterov, true>), dim3(blocks),
                        dim3(kThreads), 0, stream, static_cast<S*>(var), static_cast<S*>(m),
                        static_cast<S*>(v), static_cast<const SG*>(grad), n, p);
   else
-    hipLaunchKernelGGL((adam_chunk_kernel<Tr, Tg, kNesterov, false>), dim3(blocks),
+    TFMA_LAUNCH(kname, (adam_chunk_kernel<Tr, Tg, kNesterov, false>), dim3(blocks),
                        dim3(kThreads), 0, stream, static_cast<S*>(var), static_cast<S*>(m),
                        static_cast<S*>(v), static_cast<const SG*>(grad), n, p);
   return hipGetLastError();
@@ -225,12 +225,11 @@ hipError_t launch_grouped(const AdamTensorEntry* table, int n_tensors,
                           int64_t total_chunks, const AdamScalars& s,
                           hipStream_t stream) {
   const auto p = make_params<Tr>(s);
-  LaunchScope scope(stream, "tfma_adam_grouped");
   if (total_chunks * kGroupedAdamChunk >= kStreamElems)
-    hipLaunchKernelGGL((adam_grouped_kernel<Tr, Tg, kNesterov, true>), dim3(total_chunks),
+    TFMA_LAUNCH("tfma_adam_grouped", (adam_grouped_kernel<Tr, Tg, kNesterov, true>), dim3(total_chunks),
                        dim3(kThreads), 0, stream, table, n_tensors, p);
   else
-    hipLaunchKernelGGL((adam_grouped_kernel<Tr, Tg, kNesterov, false>), dim3(total_chunks),
+    TFMA_LAUNCH("tfma_adam_grouped", (adam_grouped_kernel<Tr, Tg, kNesterov, false>), dim3(total_chunks),
                        dim3(kThreads), 0, stream, table, n_tensors, p);
   return hipGetLastError();
 }

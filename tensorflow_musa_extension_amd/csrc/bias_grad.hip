@@ -241,35 +241,33 @@ hipError_t launch_bag(const void* x, int64_t outer, int64_t c, int64_t inner, vo
   A* partial = static_cast<A*>(workspace);
   const S* xs = static_cast<const S*>(x);
   {
-    LaunchScope scope(stream, "tfma_bias_add_grad_reduce");
     if (p.rows) {
       const size_t smem = static_cast<size_t>(kThreads) * p.vec * sizeof(A);
       constexpr int V = 16 / sizeof(S);
       if (p.vec == V) {
-        hipLaunchKernelGGL((bag_rows_kernel<B, V>), dim3(p.ct, p.groups), dim3(kThreads), smem,
+        TFMA_LAUNCH("tfma_bias_add_grad_reduce", (bag_rows_kernel<B, V>), dim3(p.ct, p.groups), dim3(kThreads), smem,
                            stream, xs, outer, static_cast<int>(c), p.cv, p.tx_shift, p.per_g,
                            partial);
       } else {
-        hipLaunchKernelGGL((bag_rows_kernel<B, 1>), dim3(p.ct, p.groups), dim3(kThreads), smem,
+        TFMA_LAUNCH("tfma_bias_add_grad_reduce", (bag_rows_kernel<B, 1>), dim3(p.ct, p.groups), dim3(kThreads), smem,
                            stream, xs, outer, static_cast<int>(c), p.cv, p.tx_shift, p.per_g,
                            partial);
       }
     } else if (p.vec > 1) {
       constexpr int V = 16 / sizeof(S);
       const int64_t iv = inner / V;
-      hipLaunchKernelGGL((bag_planes_kernel<B, V>), dim3(c, p.groups), dim3(kThreads), 0, stream,
+      TFMA_LAUNCH("tfma_bias_add_grad_reduce", (bag_planes_kernel<B, V>), dim3(c, p.groups), dim3(kThreads), 0, stream,
                          xs, outer, static_cast<int>(c), iv, p.per_g,
                          FastDiv(static_cast<uint32_t>(iv)), partial);
     } else {
-      hipLaunchKernelGGL((bag_planes_kernel<B, 1>), dim3(c, p.groups), dim3(kThreads), 0, stream,
+      TFMA_LAUNCH("tfma_bias_add_grad_reduce", (bag_planes_kernel<B, 1>), dim3(c, p.groups), dim3(kThreads), 0, stream,
                          xs, outer, static_cast<int>(c), inner, p.per_g,
                          FastDiv(static_cast<uint32_t>(inner)), partial);
     }
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  LaunchScope scope(stream, "tfma_bias_add_grad_finalize");
-  hipLaunchKernelGGL((bag_finalize_kernel<B>), dim3((c + kThreads / 64 - 1) / (kThreads / 64)),
+  TFMA_LAUNCH("tfma_bias_add_grad_finalize", (bag_finalize_kernel<B>), dim3((c + kThreads / 64 - 1) / (kThreads / 64)),
                      dim3(kThreads), 0, stream, partial, p.groups, static_cast<int>(c),
                      static_cast<S*>(out));
   return hipGetLastError();
@@ -305,8 +303,7 @@ hipError_t LaunchZeroBytes(void* p, int64_t n, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   int64_t blocks = (n + kThreads - 1) / kThreads;
   if (blocks > 1024) blocks = 1024;
-  LaunchScope scope(stream, "tfma_zero_bytes");
-  hipLaunchKernelGGL(zero_bytes_kernel, dim3(blocks), dim3(kThreads), 0, stream,
+  TFMA_LAUNCH("tfma_zero_bytes", zero_bytes_kernel, dim3(blocks), dim3(kThreads), 0, stream,
                      static_cast<uint8_t*>(p), n);
   return hipGetLastError();
 }

@@ -1221,15 +1221,13 @@ hipError_t launch_reduce(const Plan& p, const BnGeometry& g, const void* x,
   using S = typename Tr::S;
   if (p.nhwc) {
     const size_t smem = static_cast<size_t>(kThreads) * VEC * sizeof(float2);
-    LaunchScope scope(stream, kGrad ? "tfma_bn_grad_reduce" : "tfma_bn_fwd_reduce");
-    hipLaunchKernelGGL((bn_nhwc_reduce_kernel<Tr, VEC, kGrad>),
+    TFMA_LAUNCH(kGrad ? "tfma_bn_grad_reduce" : "tfma_bn_fwd_reduce", (bn_nhwc_reduce_kernel<Tr, VEC, kGrad>),
                        dim3(p.ct, p.groups), dim3(kThreads), smem, stream,
                        static_cast<const S*>(x), static_cast<const S*>(dy),
                        mean_in, g.rows, static_cast<int>(g.c), p.cv, p.tx_shift,
                        p.rows_per_g, partial);
   } else {
-    LaunchScope scope(stream, kGrad ? "tfma_bn_grad_reduce_nchw" : "tfma_bn_fwd_reduce_nchw");
-    hipLaunchKernelGGL((bn_nchw_reduce_kernel<Tr, VEC, kGrad>),
+    TFMA_LAUNCH(kGrad ? "tfma_bn_grad_reduce_nchw" : "tfma_bn_fwd_reduce_nchw", (bn_nchw_reduce_kernel<Tr, VEC, kGrad>),
                        dim3(p.groups, g.c), dim3(kThreads), 0, stream,
                        static_cast<const S*>(x), static_cast<const S*>(dy),
                        mean_in, g.n, static_cast<int>(g.c), g.h * g.w, p.cv,
@@ -1245,8 +1243,7 @@ hipError_t launch_apply(const Plan& p, const BnGeometry& g, const void* x,
                         hipStream_t stream) {
   using S = typename Tr::S;
   if (p.nhwc) {
-    LaunchScope scope(stream, kGrad ? "tfma_bn_grad_apply" : "tfma_bn_fwd_apply");
-    hipLaunchKernelGGL((bn_nhwc_apply_kernel<Tr, VEC, kGrad>),
+    TFMA_LAUNCH(kGrad ? "tfma_bn_grad_apply" : "tfma_bn_fwd_apply", (bn_nhwc_apply_kernel<Tr, VEC, kGrad>),
                        dim3(p.ct, p.groups), dim3(kThreads), 0, stream,
                        static_cast<const S*>(x), static_cast<const S*>(dy),
                        static_cast<S*>(out), coef, g.rows, static_cast<int>(g.c),
@@ -1257,8 +1254,7 @@ hipError_t launch_apply(const Plan& p, const BnGeometry& g, const void* x,
     const int64_t maxb = static_cast<int64_t>(DeviceCUs()) * 16;
     if (blocks > maxb) blocks = maxb;
     if (blocks < 1) blocks = 1;
-    LaunchScope scope(stream, kGrad ? "tfma_bn_grad_apply_nchw" : "tfma_bn_fwd_apply_nchw");
-    hipLaunchKernelGGL((bn_nchw_apply_kernel<Tr, VEC, kGrad>), dim3(blocks),
+    TFMA_LAUNCH(kGrad ? "tfma_bn_grad_apply_nchw" : "tfma_bn_fwd_apply_nchw", (bn_nchw_apply_kernel<Tr, VEC, kGrad>), dim3(blocks),
                        dim3(kThreads), 0, stream, static_cast<const S*>(x),
                        static_cast<const S*>(dy), static_cast<S*>(out), coef,
                        nvec, p.cv, static_cast<int>(g.c));
@@ -1271,8 +1267,7 @@ hipError_t launch_finalize(const Plan& p, const FinArgs& fa,
                            const float2* partial, float4* coef,
                            hipStream_t stream) {
   const int blocks = (fa.c + kFinCh - 1) / kFinCh;
-  LaunchScope scope(stream, kGrad ? "tfma_bn_grad_finalize" : "tfma_bn_fwd_finalize");
-  hipLaunchKernelGGL((bn_finalize_kernel<Tr, kGrad>), dim3(blocks), dim3(kFinThreads), 0,
+  TFMA_LAUNCH(kGrad ? "tfma_bn_grad_finalize" : "tfma_bn_fwd_finalize", (bn_finalize_kernel<Tr, kGrad>), dim3(blocks), dim3(kFinThreads), 0,
                      stream, partial, fa, coef);
   (void)p;
   return hipGetLastError();
@@ -1639,8 +1634,7 @@ hipError_t forward_t(const BnGeometry& g, const BnFwdArgs& a, void* ws,
     if (e != hipSuccess) return e;
     e = launch_finalize<Tr, false>(p, fa, partial, coef, stream);
   } else {
-    LaunchScope scope(stream, "tfma_bn_infer_coef");
-    hipLaunchKernelGGL(bn_infer_coef_kernel, dim3((g.c + 255) / 256), dim3(256),
+    TFMA_LAUNCH("tfma_bn_infer_coef", bn_infer_coef_kernel, dim3((g.c + 255) / 256), dim3(256),
                        0, stream, fa, coef);
     e = hipGetLastError();
   }
@@ -1702,8 +1696,7 @@ hipError_t LaunchFillF32(float* p, int64_t n, float value, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   int64_t blocks = (n + 255) / 256;
   if (blocks > 1024) blocks = 1024;
-  LaunchScope scope(stream, "tfma_fill_f32");
-  hipLaunchKernelGGL(fill_f32_kernel, dim3(blocks), dim3(256), 0, stream, p, n, value);
+  TFMA_LAUNCH("tfma_fill_f32", fill_f32_kernel, dim3(blocks), dim3(256), 0, stream, p, n, value);
   return hipGetLastError();
 }
 

@@ -339,17 +339,17 @@ void launch_vec(const Operand& ob, const Operand& oc, const typename Tr::S* a,
   if ((sb || sc) && blocks > cap) blocks = cap;
   if constexpr (streams(KB) && streams(KC)) {
     if (nt == 2) {
-      hipLaunchKernelGGL((ew_flat_kernel<Tr, OP, V, U, KB, KC, 2>), dim3(blocks),
+      TFMA_LAUNCH(op_kernel_name(OP), (ew_flat_kernel<Tr, OP, V, U, KB, KC, 2>), dim3(blocks),
                          dim3(kThreads), lds, stream, a, ob, oc, out, n);
       return;
     }
     if (nt == 1) {
-      hipLaunchKernelGGL((ew_flat_kernel<Tr, OP, V, U, KB, KC, 1>), dim3(blocks),
+      TFMA_LAUNCH(op_kernel_name(OP), (ew_flat_kernel<Tr, OP, V, U, KB, KC, 1>), dim3(blocks),
                          dim3(kThreads), lds, stream, a, ob, oc, out, n);
       return;
     }
   }
-  hipLaunchKernelGGL((ew_flat_kernel<Tr, OP, V, U, KB, KC, 0>), dim3(blocks),
+  TFMA_LAUNCH(op_kernel_name(OP), (ew_flat_kernel<Tr, OP, V, U, KB, KC, 0>), dim3(blocks),
                      dim3(kThreads), lds, stream, a, ob, oc, out, n);
 }
 
@@ -402,7 +402,6 @@ hipError_t launch_ew(int64_t n, const BcastOperand& a, const BcastOperand& b,
   Operand oc = kArity >= 3 ? make_operand(c, sizeof(S), V, &vec_ok)
                            : make_operand(a, sizeof(S), V, &vec_ok);
   const uint32_t n32 = static_cast<uint32_t>(n);
-  LaunchScope scope(stream, op_kernel_name(OP));
   if (vec_ok) {
     pick_kb<Tr, OP>(ob, oc, static_cast<const S*>(a.data), static_cast<S*>(out), n32,
                     stream_mode(n * static_cast<int64_t>(sizeof(S))), stream);
@@ -414,7 +413,7 @@ hipError_t launch_ew(int64_t n, const BcastOperand& a, const BcastOperand& b,
     oc = kArity >= 3 ? make_operand(c, sizeof(S), 1, &dummy)
                      : make_operand(a, sizeof(S), 1, &dummy);
     constexpr int U = 4;
-    hipLaunchKernelGGL((ew_flat_kernel<Tr, OP, 1, U, kAnyK, kAnyK, 0>), dim3(grid_for(n, U)),
+    TFMA_LAUNCH(op_kernel_name(OP), (ew_flat_kernel<Tr, OP, 1, U, kAnyK, kAnyK, 0>), dim3(grid_for(n, U)),
                        dim3(kThreads), 0, stream, static_cast<const S*>(a.data),
                        ob, oc, static_cast<S*>(out), n32);
   }
@@ -426,8 +425,7 @@ hipError_t launch_ew_strided(int64_t n, const void* a, const void* b,
                              const void* c, const StridedShape& sh, void* out,
                              hipStream_t stream) {
   using S = typename Tr::S;
-  LaunchScope scope(stream, "tfma_ew_strided");
-  hipLaunchKernelGGL((ew_strided_kernel<Tr, OP>), dim3(grid_for(n, 4)),
+  TFMA_LAUNCH("tfma_ew_strided", (ew_strided_kernel<Tr, OP>), dim3(grid_for(n, 4)),
                      dim3(kThreads), 0, stream, static_cast<const S*>(a),
                      static_cast<const S*>(b), static_cast<const S*>(c), sh,
                      static_cast<S*>(out), n);

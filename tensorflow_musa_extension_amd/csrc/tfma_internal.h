@@ -4,6 +4,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -18,8 +19,6 @@ enum class DType { kF32, kF16, kBF16, kF64 };
 // ---------------------------------------------------------------------------
 // Kernel launch tracing (TFMA_TraceEnable / TFMA_TraceRead).
 // ---------------------------------------------------------------------------
-void TraceBefore(hipStream_t stream, const char* kernel_name);
-void TraceAfter(hipStream_t stream);
 void SetLastKernel(const char* kernel_name);
 
 // Event pair for one launch of `kernel_name` when tracing is on for it (both
@@ -34,16 +33,19 @@ struct TraceEvents {
 TraceEvents TraceTake(const char* kernel_name);
 void TraceCommit(const TraceEvents& ev);
 
-// Brackets one kernel launch: records the kernel name and, when tracing is
-// on for this name, HIP events around the launch.
-struct LaunchScope {
-  hipStream_t stream;
-  LaunchScope(hipStream_t s, const char* name) : stream(s) {
-    SetLastKernel(name);
-    TraceBefore(s, name);
-  }
-  ~LaunchScope() { TraceAfter(stream); }
-};
+// Launches one kernel on `stream` (the arguments of hipLaunchKernelGGL after
+// `name`) and records `name` as the last kernel launched.  When tracing is on
+// for `name`, HIP events ride on the dispatch itself as its start and end, so
+// no marker packets sit between kernels.
+#define TFMA_LAUNCH(name, kernel, grid, block, smem, stream, ...)                      \
+  do {                                                                                 \
+    const char* const tfma_name_ = (name);                                             \
+    ::tfma::SetLastKernel(tfma_name_);                                                 \
+    const ::tfma::TraceEvents tfma_ev_ = ::tfma::TraceTake(tfma_name_);                \
+    hipExtLaunchKernelGGL(kernel, grid, block, smem, stream, tfma_ev_.start, tfma_ev_.end, \
+                          0, __VA_ARGS__);                                             \
+    ::tfma::TraceCommit(tfma_ev_);                                                     \
+  } while (0)
 
 // Number of compute units of the current device (cached per device).
 int DeviceCUs();

@@ -1,7 +1,8 @@
-// Kernel launch tracing: HIP events recorded on the launch stream around
-// every launch whose kernel name contains a chosen substring.  Used by the
-// benchmark to time one kernel inside a timed region on the stream the
-// kernel runs on.
+// Kernel launch tracing: HIP events attached, as its start and end, to the
+// dispatch of every launch whose kernel name contains a chosen substring
+// (TFMA_LAUNCH and the fused BN launcher take them from TraceTake).  Used by
+// the benchmark to time kernels inside a timed region on the stream they
+// run on.
 #include <hip/hip_runtime.h>
 #include <string.h>
 
@@ -34,8 +35,6 @@ TraceState& state() {
   return *s;
 }
 
-thread_local bool t_open = false;
-thread_local Pending t_cur;
 thread_local const char* t_last_kernel = "";
 
 hipEvent_t take_event(TraceState& s) {
@@ -70,18 +69,6 @@ void drain(TraceState& s) {
 
 void SetLastKernel(const char* kernel_name) { t_last_kernel = kernel_name; }
 
-void TraceBefore(hipStream_t stream, const char* kernel_name) {
-  TraceState& s = state();
-  if (!s.enabled) return;  // racy read is fine: tracing is set up before use
-  std::lock_guard<std::mutex> lk(s.mu);
-  if (!s.enabled || strstr(kernel_name, s.substr.c_str()) == nullptr) return;
-  Pending p{take_event(s), take_event(s)};
-  if (!p.start || !p.end) return;
-  if (hipEventRecord(p.start, stream) != hipSuccess) return;
-  t_cur = p;
-  t_open = true;
-}
-
 TraceEvents TraceTake(const char* kernel_name) {
   TraceEvents ev;
   TraceState& s = state();
@@ -106,15 +93,6 @@ void TraceCommit(const TraceEvents& ev) {
   if (s.pending.size() > 4096) drain(s);
 }
 
-void TraceAfter(hipStream_t stream) {
-  if (!t_open) return;
-  t_open = false;
-  TraceState& s = state();
-  std::lock_guard<std::mutex> lk(s.mu);
-  if (hipEventRecord(t_cur.end, stream) != hipSuccess) return;
-  s.pending.push_back(t_cur);
-  if (s.pending.size() > 4096) drain(s);
-}
 
 }  // namespace tfma
 
