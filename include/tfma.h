@@ -346,8 +346,9 @@ int TFMA_TraceEnable(const char* name_substr, TFMA_Status* status);
 int TFMA_TraceRead(double* total_ms, int64_t* launches, TFMA_Status* status);
 
 /* Whether a fused BatchNorm launch on the current device gave up one of its
- * grid-barrier waits (the bounded spin, ~0.5 s, ran out because the grid was
- * not co-resident; that launch's outputs are wrong).  *timed_out = 1 if so;
+ * grid-wide waits - for another workgroup's partials or coefficients (the
+ * bounded spin, ~0.5 s, ran out because the grid was not co-resident; that
+ * launch's outputs are wrong).  *timed_out = 1 if so;
  * reset != 0 clears the flag.  Waits for the device to go idle
  * (hipDeviceSynchronize) before reading: a diagnostic, not for hot loops.
  * No reference counterpart: the reference's BatchNorm kernels have no

@@ -604,20 +604,30 @@ __global__ __launch_bounds__(kThreads) void bn_nchw_apply_kernel(
 //    phase 1: statistics partials.  Each thread's rows are split three ways:
 //             its first KR row-vectors stay in VGPRs, the next KL in LDS
 //             (about 150 KB per workgroup), the rest are streamed;
-//    barrier; phase 2: per-channel finals, channels spread over workgroups;
-//    barrier; phase 3: outputs - streamed rows re-read last-to-first, then the
+//    phase 2: per-channel finals, channels spread over workgroups, each
+//             waiting only for its channel's partials;
+//    phase 3: outputs, each workgroup waiting only for its channel tile's
+//             coefficients - streamed rows re-read last-to-first, then the
 //             LDS- and register-resident rows, which are not read again.
 //    On-chip residency is what removes the second read: on MI355X re-reads
 //    served by the Infinity Cache run at about the same rate as HBM reads.
-//    The grid barrier is a device-wide counter advanced with relaxed
-//    agent-scope atomics (a cooperative launch costs ~18 us and each of its
-//    grid syncs ~33 us on MI355X; this barrier ~3 us).  Values that cross
-//    workgroups (partials, coefficients) are written and read with
-//    agent-scope atomic stores/loads, which are coherent across the XCDs'
-//    L2s, and every thread waits for its stores before arriving.
+//    No grid barrier: every value that crosses workgroups (partials,
+//    coefficients) is a 64-bit word {value, epoch} written and read with
+//    agent-scope atomics (coherent across the XCDs' L2s), and its consumer
+//    polls until the word carries this launch's epoch.  A two-level grid
+//    barrier (relaxed atomics, ~3 us; a cooperative launch's grid sync costs
+//    ~33 us) cost 8-11 us per op between the slowest wave's phase-1 end and
+//    phase 3: the stores' acknowledgement, two atomic levels and the poll,
+//    twice; the epoch words made the 16-op benchmark step 2.9 % faster
+//    (4-6 us on each 7x7 op).  A launch that hands out phase-3 chunks, or
+//    is recorded into a graph, still counts its exit to reset what the next
+//    launch needs reset.
 // ---------------------------------------------------------------------------
 constexpr int kFusedThreads = 512;
 constexpr unsigned kSpinLimit = 1u << 24;  // ~0.5 s, then give up (flagged)
+// Epoch-tagged partials: at most 8 row groups per lane of a finishing wave.
+constexpr int kEpochPerLane = 8;
+constexpr int64_t kMaxEpochGroups = 64 * kEpochPerLane;
 // Resident 16-byte vectors per thread and per input tensor: KR in VGPRs (the
 // largest counts that compile without spills at 256 VGPRs), KL in LDS (the
 // LDS budget split over the inputs).  kOpaque*: the register rows are made
@@ -630,12 +640,12 @@ constexpr unsigned kSpinLimit = 1u << 24;  // ~0.5 s, then give up (flagged)
 // rows measured faster even where that leaves rows to stream (each register
 // row adds unrolled code to a kernel run about once, and the resident loads
 // arrive as one burst that streams worse than the pipelined loop).
-// PA/PB: streamed vectors per tensor prefetched for phase 3 while the grid
-// barriers are pending - PA after the first barrier's arrival (by waves with
-// no phase-2 channel), PB after the second's (by every wave).
+// PA/PB: streamed vectors per tensor prefetched for phase 3 while the
+// cross-workgroup values are pending - PA after the partials are published
+// (by waves with no phase-2 channel), PB after the finals (by every wave).
 template <class Tr> struct Resident {
   static constexpr bool kOpaqueFwd = false, kOpaqueGrad = true;
-  static constexpr int kRegFwd = 26, kRegGrad = 11, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kRegFwd = 24, kRegGrad = 10, kLdsFwd = 18, kLdsGrad = 9;
   static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 4, kPbFwd = 8, kPaGrad = 4, kPbGrad = 8;
 };
@@ -647,7 +657,7 @@ template <> struct Resident<TF16> {
 };
 template <> struct Resident<TBF16> {
   static constexpr bool kOpaqueFwd = false, kOpaqueGrad = true;
-  static constexpr int kRegFwd = 30, kRegGrad = 9, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kRegFwd = 30, kRegGrad = 8, kLdsFwd = 18, kLdsGrad = 9;
   static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 4, kPbFwd = 4, kPaGrad = 4, kPbGrad = 8;
 };
@@ -663,18 +673,28 @@ struct FusedArgs {
   int ct;
   int64_t groups;
   int64_t rows_per_g;
-  float2* partial;
-  float4* coef;
-  unsigned long long* barrier;  // device-wide arrival counter
+  unsigned long long* barrier;  // device-wide exit-arrival counter
   unsigned long long base;      // its value when this launch starts
   unsigned* sub;                // 8 arrival counters (workgroup id mod 8), 256 B apart
-  unsigned sub_last[3][8];      // value class r's last arrival sees at barrier 1, 2, exit
+  unsigned sub_last[8];         // value class r's last exit arrival sees
   unsigned* timeout_flag;
   unsigned* queues;             // [ct][wave] chunk counters, zero between launches
   int reset_at_exit;            // recorded into a graph: zero every counter at exit
   int dyn_rows;                 // streamed rows per thread handed out dynamically
   int dyn_chunk;                // rows per thread in one dynamic chunk
   int shards;                   // chunk counters per (ct, wave)
+  // Values that cross workgroups carry the launch's epoch: each partial is
+  // published as two 64-bit words {value, epoch} in `eslots` ([groups * c]
+  // [2]) and each channel's coefficients as four in `ecoef` ([c][4]), both
+  // library-owned and zeroed once; the waves finishing a channel poll for
+  // its partials, and each workgroup for its tile's coefficients.  Eager
+  // launches get the epoch from the host (`epoch`, below 2^31); a launch
+  // recorded into a graph reads it from `epoch_dev` (2^31 and up) and its
+  // last workgroup to exit advances it for the next replay.
+  unsigned long long* eslots;
+  unsigned long long* ecoef;
+  unsigned epoch;
+  unsigned* epoch_dev;
   FinArgs fin;
 };
 
@@ -696,51 +716,14 @@ __device__ inline uint64_t load_shared(const void* p) {
                            __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Split-phase grid barrier.  grid_arrive: every thread's stores (and loads)
-// are complete, then the workgroup counts itself in.  grid_wait: returns once
-// every workgroup of the grid has arrived `k` times (k = 1, 2).  Between the
-// two halves a workgroup may issue loads that do not depend on other
-// workgroups (the phase-3 prefetch), so the barrier's latency overlaps with
-// memory traffic.
-// Arrivals are counted in two levels: workgroup b counts itself on counter
-// b mod 8 (consecutive workgroups sit on different XCDs), and the last of
-// each of those classes counts the class on the global counter.  When all
-// workgroups arrive at once (after the finals), 256 atomics on one address
-// queue for ~4 us; 8 classes of 32 do not.
+// Exit arrivals (launches that hand out phase-3 chunks, and launches
+// recorded into a graph) are counted in two levels: workgroup b counts
+// itself on counter b mod 8 (consecutive workgroups sit on different XCDs),
+// and the last of each of those classes counts the class on the global
+// counter; 256 atomics on one address queue for ~4 us, 8 classes of 32 do
+// not.  The workgroup that completes the count resets what the next launch
+// needs reset.
 __device__ inline unsigned barrier_classes() { return gridDim.x < 8 ? gridDim.x : 8; }
-
-__device__ inline void grid_arrive(const FusedArgs& a, unsigned k) {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // my shared stores are done
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned r = blockIdx.x & 7;
-    // Uniform selects, not a dynamic index into the by-value arguments
-    // (which would put them in scratch memory).
-    unsigned last = a.sub_last[k - 1][0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) last = r == static_cast<unsigned>(i) ? a.sub_last[k - 1][i] : last;
-    const unsigned old =
-        __hip_atomic_fetch_add(a.sub + 64 * r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == last)
-      __hip_atomic_fetch_add(a.barrier, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
-__device__ inline void grid_wait(const FusedArgs& a, unsigned k) {
-  if (threadIdx.x == 0) {
-    const unsigned long long target =
-        a.base + static_cast<unsigned long long>(k) * barrier_classes();
-    unsigned spins = 0;
-    while (__hip_atomic_load(a.barrier, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(2);
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(a.timeout_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-    }
-  }
-  __syncthreads();
-}
 
 template <class Tr, bool kGrad>
 __device__ inline void accum_words(const uint4& xw, const uint4& dw, const float (&k)[Tr::kVec],
@@ -846,6 +829,14 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   auto lds = [&](int q2, int which) -> uint4& {
     return lds_rows[(q2 * kIn + which) * kFusedThreads + tid];
   };
+
+  // This launch's epoch, in the upper half of the tag word (recorded
+  // launches: 2^31 + 1 + (device word mod 2^31 - 1)).
+  const unsigned epoch =
+      a.epoch_dev ? 0x80000001u + __hip_atomic_load(a.epoch_dev, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT) % 0x7fffffffu
+                  : a.epoch;
+  const uint64_t etag = static_cast<uint64_t>(epoch) << 32;
 
   // ---- phase 1: partial statistics --------------------------------------
   float k[VEC], s1[VEC], s2[VEC];
@@ -969,10 +960,10 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       sa += v.x;
       sb += v.y;
     }
-    store_shared(&a.partial[g * a.c + static_cast<int64_t>(ct) * width + tid],
-                 __builtin_bit_cast(uint64_t, make_float2(sa, sb)));
+    const int64_t slot = g * a.c + static_cast<int64_t>(ct) * width + tid;
+    store_shared(a.eslots + 2 * slot, etag | __builtin_bit_cast(uint32_t, sa));
+    store_shared(a.eslots + 2 * slot + 1, etag | __builtin_bit_cast(uint32_t, sb));
   }
-  grid_arrive(a, 1);
 
   // Phase-3 prefetch, part A: the last streamed rows (phase 3 runs
   // last-to-first), loaded by the waves that have no phase-2 channel so the
@@ -994,7 +985,6 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     }
   }
   const int64_t qb = nk - 1 - (pre_a ? PA : 0);  // first row of part B
-  grid_wait(a, 1);
 
   // ---- phase 2: per-channel finals ---------------------------------------
   // Channel ch belongs to workgroup ch % gridDim.x; each wave of the
@@ -1002,24 +992,63 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   // workgroup's partial loads are in flight together.
   for (int ch = blockIdx.x + wave * gridDim.x; ch < a.c; ch += kWaves * gridDim.x) {
     double t1 = 0.0, t2 = 0.0;
-    for (int64_t gg = lane; gg < a.groups; gg += 64) {
-      const float2 v = __builtin_bit_cast(float2, load_shared(&a.partial[gg * a.c + ch]));
-      t1 += v.x;
-      t2 += v.y;
+    {
+      // Lane l sums groups l, l + 64, ... (at most kMaxGroups / 64 of them):
+      // all their slots are loaded at once, then the ones not yet tagged
+      // with this launch's epoch are polled again.
+      const uint64_t tag = etag;
+      uint64_t v1[kEpochPerLane], v2[kEpochPerLane];
+#pragma unroll
+      for (int i = 0; i < kEpochPerLane; ++i) {
+        const int64_t gg = lane + 64 * i;
+        v1[i] = v2[i] = tag;
+        if (gg < a.groups) {
+          v1[i] = load_shared(a.eslots + 2 * (gg * a.c + ch));
+          v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
+        }
+      }
+      unsigned spins = 0;
+      while (true) {
+        bool ready = true;
+#pragma unroll
+        for (int i = 0; i < kEpochPerLane; ++i)
+          ready = ready && (v1[i] >> 32) == (tag >> 32) && (v2[i] >> 32) == (tag >> 32);
+        if (ready) break;
+        if (++spins > kSpinLimit) {
+          __hip_atomic_store(a.timeout_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < kEpochPerLane; ++i) {
+          const int64_t gg = lane + 64 * i;
+          if ((v1[i] >> 32) != (tag >> 32)) v1[i] = load_shared(a.eslots + 2 * (gg * a.c + ch));
+          if ((v2[i] >> 32) != (tag >> 32))
+            v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kEpochPerLane; ++i) {
+        if (lane + 64 * i < a.groups) {
+          t1 += __builtin_bit_cast(float, static_cast<uint32_t>(v1[i]));
+          t2 += __builtin_bit_cast(float, static_cast<uint32_t>(v2[i]));
+        }
+      }
     }
     const double2 w = wave_sum(t1, t2);
     if (lane == 0) {
       const float4 cfc = finish_channel<Tr, kGrad>(a.fin, ch, w.x, w.y);
-      store_shared(&a.coef[ch], __builtin_bit_cast(uint64_t, make_float2(cfc.x, cfc.y)));
-      store_shared(reinterpret_cast<float2*>(&a.coef[ch]) + 1,
-                   __builtin_bit_cast(uint64_t, make_float2(cfc.z, cfc.w)));
+      const float v4[4] = {cfc.x, cfc.y, cfc.z, cfc.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        store_shared(a.ecoef + 4 * static_cast<int64_t>(ch) + i,
+                     etag | __builtin_bit_cast(uint32_t, v4[i]));
     }
   }
   zero_side_outputs<kGrad>(a.fin);
-  grid_arrive(a, 2);
 
-  // Prefetch part B: the next rows, in flight during the second barrier and
-  // the coefficient loads.
+  // Prefetch part B: the next rows, in flight while the tile's coefficients
+  // are polled.
   uint4 pbx[PB > 0 ? PB : 1], pbd[kGrad && PB > 0 ? PB : 1];
 #pragma unroll
   for (int p = 0; p < PB; ++p) {
@@ -1027,7 +1056,6 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     pbx[p] = bld16(rx, o);
     if constexpr (kGrad) pbd[p] = bld16(rd, o);
   }
-  grid_wait(a, 2);
 
   // ---- phase 3: outputs --------------------------------------------------
   // Make the resident words opaque so only the packed words (not their
@@ -1039,16 +1067,46 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       asm volatile("" : "+v"(dr[r].x), "+v"(dr[r].y), "+v"(dr[r].z), "+v"(dr[r].w));
   }
   float4 cf[VEC];
+  {
+    // The tile's coefficients (4 words per channel, at most 1024 words: two
+    // per thread) are polled until tagged with this launch's epoch, then
+    // shared through `red`, free since phase 1's reduction (the first
+    // __syncthreads orders those reads before these writes).
+    const uint64_t tag = etag;
+    uint64_t v[2];
+    int64_t wi[2];
 #pragma unroll
-  for (int j = 0; j < VEC; ++j) {
-    if (active) {
-      const float2 lo = __builtin_bit_cast(float2, load_shared(&a.coef[c0 + j]));
-      const float2 hi =
-          __builtin_bit_cast(float2, load_shared(reinterpret_cast<float2*>(&a.coef[c0 + j]) + 1));
-      cf[j] = make_float4(lo.x, lo.y, hi.x, hi.y);
-    } else {
-      cf[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < 2; ++i) {
+      wi[i] = tid + kFusedThreads * i;
+      const int64_t chn = static_cast<int64_t>(ct) * width + (wi[i] >> 2);
+      const bool need = (wi[i] >> 2) < width && chn < a.c;
+      v[i] = need ? load_shared(a.ecoef + 4 * chn + (wi[i] & 3)) : tag;
+      if (!need) wi[i] = -1;
     }
+    unsigned spins = 0;
+    while ((v[0] >> 32) != (tag >> 32) || (v[1] >> 32) != (tag >> 32)) {
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(a.timeout_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        if ((v[i] >> 32) != (tag >> 32)) {
+          const int64_t chn = static_cast<int64_t>(ct) * width + (wi[i] >> 2);
+          v[i] = load_shared(a.ecoef + 4 * chn + (wi[i] & 3));
+        }
+      }
+    }
+    float* const cs = reinterpret_cast<float*>(red);  // [width][4] of this tile
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (wi[i] >= 0) cs[wi[i]] = __builtin_bit_cast(float, static_cast<uint32_t>(v[i]));
+    __syncthreads();
+    const float4* const cs4 = reinterpret_cast<const float4*>(cs);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) cf[j] = active ? cs4[tx * VEC + j] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   // Prefetched rows first, then the remaining streamed rows last-to-first.
   if (pre_a) {
@@ -1171,10 +1229,11 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   }
 
   // Exit (when chunks were handed out, and in a launch recorded into a
-  // graph): counted like a third barrier arrival - class counter, then the
-  // global counter - and the workgroup that completes the count zeroes the
-  // chunk counters for the next launch; in a recorded launch also the
-  // barrier and class counters, so every replay starts from zero.  Relaxed:
+  // graph): counted in two levels - class counter, then the global counter -
+  // and the workgroup that completes the count zeroes the chunk counters for
+  // the next launch; in a recorded launch also the exit and class counters,
+  // so every replay starts from zero, and it advances the replays' epoch
+  // word.  Relaxed:
   // every counter this workgroup touched was updated by atomics whose
   // results it has already used, and no workgroup reads a counter after its
   // exit arrival.
@@ -1184,15 +1243,17 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       unsigned done = 0;
       if (lane == 0) {
         const unsigned r = blockIdx.x & 7;
-        unsigned last = a.sub_last[2][0];
+        // Uniform selects over the by-value arguments (a dynamic index
+        // would put them in scratch memory).
+        unsigned last = a.sub_last[0];
 #pragma unroll
-        for (int i = 1; i < 8; ++i) last = r == static_cast<unsigned>(i) ? a.sub_last[2][i] : last;
+        for (int i = 1; i < 8; ++i) last = r == static_cast<unsigned>(i) ? a.sub_last[i] : last;
         const unsigned old =
             __hip_atomic_fetch_add(a.sub + 64 * r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old == last) {
           const unsigned long long g =
               __hip_atomic_fetch_add(a.barrier, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          done = g == a.base + 3ull * barrier_classes() - 1;
+          done = g == a.base + barrier_classes() - 1;
         }
       }
       if (__builtin_amdgcn_readfirstlane(done)) {
@@ -1203,8 +1264,14 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
         if (a.reset_at_exit) {
           if (lane < 8)
             __hip_atomic_store(a.sub + 64 * lane, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (lane == 0)
+          if (lane == 0) {
             __hip_atomic_store(a.barrier, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // Every workgroup read the epoch word at its start: the next
+            // replay gets the next epoch.
+            if (a.epoch_dev)
+              __hip_atomic_store(a.epoch_dev, (epoch - 0x80000001u + 1u) % 0x7fffffffu,
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
         }
       }
     }
@@ -1366,6 +1433,7 @@ bool make_fused_plan(const BnGeometry& g, int vec, int blocks_per_cu, FusedPlan*
   const int64_t max_groups = (g.rows + ry - 1) / ry;
   if (groups > max_groups) groups = max_groups;
   if (groups > fused_group_bound()) groups = fused_group_bound();
+  if (groups > kMaxEpochGroups) groups = kMaxEpochGroups;  // partials a finishing wave reads
   fp->rows_per_g = (g.rows + groups - 1) / groups;
   // The kernel reads a workgroup's own rows through a buffer resource with
   // 32-bit offsets (rows past the group are out of range and read nothing):
@@ -1399,9 +1467,10 @@ void set_dynamic_share(FusedPlan* fp, int resident, int prefetched, int u) {
   fp->dyn_chunk = chunk;
 }
 
-// Per-device state of the fused kernels' grid barrier: a monotonic arrival
-// counter in device memory (zeroed once), its value before the next launch,
-// and the event and stream of the last fused launch.  The event is the
+// Per-device state of the fused kernels: a monotonic exit-arrival counter in
+// device memory (zeroed once), its value before the next launch, the
+// epoch-tagged value regions and the last epoch, and the event and stream of
+// the last fused launch.  The event is the
 // dispatch's own end event (hipExtLaunchKernelGGL), not a marker after it:
 // a marker between kernels costs microseconds.  Fused launches on one
 // device are chained (a launch on another stream waits for the previous
@@ -1414,6 +1483,7 @@ void set_dynamic_share(FusedPlan* fp, int resident, int prefetched, int u) {
 // bookkeeping; they are not chained to other fused launches (the graph
 // orders them), so a replay must not overlap other fused BatchNorm work on
 // the device.
+constexpr size_t kEpochOffset = 16;  // recorded region: the replays' epoch word
 constexpr size_t kQueueOffset = 256;
 constexpr size_t kQueueBytes = 4096 * sizeof(unsigned);  // <= 512 tiles x 8 waves
 constexpr size_t kSubOffset = kQueueOffset + kQueueBytes;  // 8 class counters, 256 B apart
@@ -1427,7 +1497,13 @@ struct BarrierState {
   hipEvent_t chain = nullptr;  // end of the last launch (`last` or a trace event)
   hipStream_t last_stream = nullptr;
   bool used = false;
+  unsigned long long* eslots = nullptr;  // epoch-tagged partials, zeroed at creation
+  size_t eslot_bytes = 0;
+  unsigned long long* ecoef = nullptr;   // epoch-tagged coefficients, zeroed at creation
+  size_t ecoef_bytes = 0;
+  unsigned epoch = 0;                    // last epoch handed to a launch (< 2^31)
 };
+
 
 BarrierState* barrier_state() {
   static BarrierState states[64];
@@ -1438,8 +1514,7 @@ BarrierState* barrier_state() {
 
 template <class Tr, bool kGrad>
 hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
-                        const void* dy, void* out, const FinArgs& fin, float2* partial,
-                        float4* coef, hipStream_t stream) {
+                        const void* dy, void* out, const FinArgs& fin, hipStream_t stream) {
   BarrierState* bs = barrier_state();
   if (!bs) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lk(bs->mu);
@@ -1462,6 +1537,42 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
     if (e != hipSuccess) return e;
   }
   const bool recorded = cap != hipStreamCaptureStatusNone;
+  // Epoch-tagged values: partial slots for every (group, channel) and
+  // coefficient words for every channel of the largest fused plan (at most
+  // 2 workgroups per CU, each channel tile at most 256 channels wide and
+  // served by at least one workgroup, so G*C and C are both at most
+  // 512 * CUs), tagged with the launch's epoch, so a value from an earlier
+  // launch never matches.  Eager epochs stay below 2^31; at the wrap both
+  // regions are zeroed again.
+  if (!bs->eslots) {
+    const size_t slot_bytes = static_cast<size_t>(2 * DeviceCUs()) * 256 * 16;
+    const size_t coef_bytes = static_cast<size_t>(2 * DeviceCUs()) * 256 * 32;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, slot_bytes + coef_bytes);
+    if (e != hipSuccess) return e;
+    e = hipMemset(p, 0, slot_bytes + coef_bytes);
+    if (e != hipSuccess) {
+      (void)hipFree(p);
+      return e;
+    }
+    bs->eslots = static_cast<unsigned long long*>(p);
+    bs->eslot_bytes = slot_bytes;
+    bs->ecoef = reinterpret_cast<unsigned long long*>(static_cast<char*>(p) + slot_bytes);
+    bs->ecoef_bytes = coef_bytes;
+  }
+  if (fp.groups > kMaxEpochGroups ||
+      static_cast<size_t>(fp.groups) * g.c * 16 > bs->eslot_bytes ||
+      static_cast<size_t>(g.c) * 32 > bs->ecoef_bytes)
+    return hipErrorInvalidValue;  // excluded by make_fused_plan
+  unsigned epoch = 0;
+  if (!recorded) {
+    if (bs->epoch + 1 >= (1u << 31)) {
+      hipError_t e = hipMemsetAsync(bs->eslots, 0, bs->eslot_bytes + bs->ecoef_bytes, stream);
+      if (e != hipSuccess) return e;
+      bs->epoch = 0;
+    }
+    epoch = ++bs->epoch;
+  }
   unsigned long long* region =
       recorded ? reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(bs->counter) +
                                                        kStateBytes)
@@ -1481,21 +1592,23 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   fa.ct = fp.ct;
   fa.groups = fp.groups;
   fa.rows_per_g = fp.rows_per_g;
-  fa.partial = partial;
-  fa.coef = coef;
   fa.barrier = region;
   fa.base = recorded ? 0 : bs->base;
   fa.sub = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(region) + kSubOffset);
   for (int r = 0; r < 8; ++r) {
     const unsigned members = static_cast<unsigned>((fp.blocks + 7 - r) / 8);
     const unsigned sb = recorded ? 0u : bs->sub_base[r];
-    fa.sub_last[0][r] = sb + members - 1;
-    fa.sub_last[1][r] = sb + 2 * members - 1;
-    fa.sub_last[2][r] = sb + 3 * members - 1;
+    fa.sub_last[r] = sb + members - 1;
   }
   fa.timeout_flag = reinterpret_cast<unsigned*>(region + 1);
   fa.queues = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(region) + kQueueOffset);
   fa.reset_at_exit = recorded ? 1 : 0;
+  fa.eslots = bs->eslots;
+  fa.ecoef = bs->ecoef;
+  fa.epoch = epoch;
+  fa.epoch_dev = recorded ? reinterpret_cast<unsigned*>(reinterpret_cast<char*>(region) +
+                                                        kEpochOffset)
+                          : nullptr;
   const int ry = kFusedThreads >> fp.tx_shift;
   const int64_t nk_max = (fp.rows_per_g + ry - 1) / ry;  // rows of a thread
   const bool small = !kGrad && nk_max <= kSmallFwdRows;
@@ -1538,10 +1651,9 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   TraceCommit(tev);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // Per barrier (and per exit count, when chunks were handed out): each
-  // class counter gets one arrival per member, the global counter one per
-  // non-empty class.
-  const unsigned rounds = fa.dyn_rows > 0 ? 3u : 2u;
+  // Per exit count (when chunks were handed out): each class counter gets
+  // one arrival per member, the global counter one per non-empty class.
+  const unsigned rounds = fa.dyn_rows > 0 ? 1u : 0u;  // the exit arrival
   const unsigned long long classes = fp.blocks < 8 ? fp.blocks : 8;
   for (int r = 0; r < 8; ++r)
     bs->sub_base[r] += rounds * static_cast<unsigned>((fp.blocks + 7 - r) / 8);
@@ -1625,7 +1737,7 @@ hipError_t forward_t(const BnGeometry& g, const BnFwdArgs& a, void* ws,
   FusedPlan fp;
   if (a.is_training && p.vec > 1 && fused_enabled() &&
       make_fused_plan(g, p.vec, fused_blocks_per_cu<Tr, false>(), &fp)) {
-    return launch_fused<Tr, false>(fp, g, a.x, nullptr, a.y, fa, partial, coef,
+    return launch_fused<Tr, false>(fp, g, a.x, nullptr, a.y, fa,
                                                   stream);
   }
   if (a.is_training) {
@@ -1671,7 +1783,7 @@ hipError_t grad_t(const BnGeometry& g, const BnGradArgs& a, void* ws,
   FusedPlan fp;
   if (p.vec > 1 && fused_enabled() &&
       make_fused_plan(g, p.vec, fused_blocks_per_cu<Tr, true>(), &fp)) {
-    return launch_fused<Tr, true>(fp, g, a.x, a.dy, a.dx, fa, partial, coef,
+    return launch_fused<Tr, true>(fp, g, a.x, a.dy, a.dx, fa,
                                                   stream);
   }
   hipError_t e =

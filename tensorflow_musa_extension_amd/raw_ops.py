@@ -398,8 +398,9 @@ def trace_read():
 
 
 def fused_batch_norm_barrier_timed_out(reset=False):
-    """True if a fused BatchNorm launch on the current device gave up a grid
-    barrier wait (its outputs are then wrong); synchronizes the device."""
+    """True if a fused BatchNorm launch on the current device gave up a
+    grid-wide wait for other workgroups' values (its outputs are then wrong);
+    synchronizes the device."""
     lib = _lib.load()
     status = _lib.TFMA_Status()
     flag = ctypes.c_int32(0)

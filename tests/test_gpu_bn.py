@@ -317,3 +317,44 @@ def test_shape_errors(dev):
         ops.FusedBatchNormGradV3(torch.zeros((2, 3, 3, 5), **f32), x, torch.ones(4, **f32),
                                  torch.zeros(4, **f32), torch.ones(4, **f32),
                                  torch.zeros((), **f32))
+
+
+def test_fused_epochs_fresh_values(dev):
+    """Fused launches publish their partials and coefficients tagged with the
+    launch's epoch, in library-owned slots that later launches reuse.  Back-to-
+    back launches with no synchronization between them - same shape with other
+    data, and shapes whose (group, channel) slots and channel words overlap
+    differently - must each equal the same launch run alone, bit for bit, and
+    no poll may give up (a stale value taken for a fresh one would show as a
+    mismatch here)."""
+    torch.manual_seed(5)
+    eps = 1.001e-5
+    e = torch.empty(0, device=dev)
+    cases = []
+    for shape, dt in (((32, 14, 14, 256), torch.float16), ((32, 14, 14, 256), torch.float16),
+                      ((16, 7, 7, 512), torch.bfloat16), ((64, 28, 28, 64), torch.float32),
+                      ((8, 7, 7, 2048), torch.float16)):
+        c = shape[-1]
+        cases.append((torch.randn(shape, device=dev).to(dt), torch.randn(shape, device=dev).to(dt),
+                      torch.rand(c, device=dev) + 0.5, 0.1 * torch.randn(c, device=dev)))
+
+    def step(x, dy, scale, offset):
+        f = ops.FusedBatchNormV3(x, scale, offset, e, e, epsilon=eps)
+        g = ops.FusedBatchNormGradV3(dy, x, scale, f.reserve_space_1, f.reserve_space_2,
+                                     f.reserve_space_3, epsilon=eps)
+        assert ops.last_kernel_name() == "tfma_bn_grad_fused"
+        return [f.y, f.batch_mean, f.batch_variance, g.x_backprop, g.scale_backprop,
+                g.offset_backprop]
+
+    ops.fused_batch_norm_barrier_timed_out(reset=True)
+    want = []
+    for cs in cases:
+        want.append([t.clone() for t in step(*cs)])
+        torch.cuda.synchronize()
+    order = [0, 1, 0, 2, 3, 1, 4, 4, 0, 2, 1, 3]
+    got = [(k, step(*cases[k])) for k in order]
+    torch.cuda.synchronize()
+    assert not ops.fused_batch_norm_barrier_timed_out()
+    for k, outs in got:
+        for w, g in zip(want[k], outs):
+            assert torch.equal(w, g)
