@@ -1069,9 +1069,18 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   float4 cf[VEC];
   {
     // The tile's coefficients (4 words per channel, at most 1024 words: two
-    // per thread) are polled until tagged with this launch's epoch, then
-    // shared through `red`, free since phase 1's reduction (the first
-    // __syncthreads orders those reads before these writes).
+    // per thread, consecutive words to consecutive threads, so the
+    // cross-XCD loads stay coalesced) are polled until tagged with this
+    // launch's epoch, then shared through `red`, free since phase 1's
+    // reduction (the first __syncthreads below orders those reads before
+    // these writes).  LDS: component c of channel cl (= tx * VEC + j) at
+    // c * kW + cl + cl / VEC - a stride kW = 8 (mod 32) between components
+    // and one pad word per channel vector, so the writes (consecutive words)
+    // and the reads (lane tx at tx * (VEC + 1) + j) hit distinct banks.
+    constexpr int kW = VEC == 8 ? 296 : 168;  // >= 32 * (VEC + 1), = 8 mod 32
+    static_assert(kW >= 32 * (VEC + 1) && kW % 32 == 8, "coefficient layout");
+    static_assert(4 * kW * sizeof(float) <= sizeof(red), "coefficients fit in red");
+    float* const cs = reinterpret_cast<float*>(red);
     const uint64_t tag = etag;
     uint64_t v[2];
     int64_t wi[2];
@@ -1098,15 +1107,21 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
         }
       }
     }
-    float* const cs = reinterpret_cast<float*>(red);  // [width][4] of this tile
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      if (wi[i] >= 0) cs[wi[i]] = __builtin_bit_cast(float, static_cast<uint32_t>(v[i]));
+    for (int i = 0; i < 2; ++i) {
+      if (wi[i] >= 0) {
+        const int cl = static_cast<int>(wi[i] >> 2);
+        cs[(wi[i] & 3) * kW + cl + cl / VEC] = __builtin_bit_cast(float, static_cast<uint32_t>(v[i]));
+      }
+    }
     __syncthreads();
-    const float4* const cs4 = reinterpret_cast<const float4*>(cs);
+    const int cb = tx * (VEC + 1);
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) cf[j] = active ? cs4[tx * VEC + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < VEC; ++j)
+      cf[j] = active ? make_float4(cs[cb + j], cs[kW + cb + j], cs[2 * kW + cb + j],
+                                   cs[3 * kW + cb + j])
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   // Prefetched rows first, then the remaining streamed rows last-to-first.
   if (pre_a) {
