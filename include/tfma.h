@@ -108,6 +108,11 @@ int TFMA_GetDeviceCount(int* count, TFMA_Status* status);
  * reserve_space_3: 0-d FLOAT scalar, written with 0 (reference :59-62,
  * :100-104).  reserve_space_4/5 of the grad: FLOAT tensors of any length
  * (the reference allocates [C], :220-223), filled with zeros.
+ * The fused (persistent, NHWC training) path keeps the values its workgroups
+ * hand to each other - partial sums and per-channel coefficients, tagged
+ * with a per-launch epoch - in library-owned device memory (24 KB per CU,
+ * allocated and zeroed on the device's first fused launch: run one eagerly
+ * before capturing a graph); the caller's workspace serves the other paths.
  * ------------------------------------------------------------------------- */
 
 /* Scratch bytes FusedBatchNormV3 / FusedBatchNormGradV3 need for this x. */
