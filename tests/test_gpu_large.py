@@ -174,3 +174,42 @@ def test_bias_add_grad_f16_over_2_31(dev):
     got = to_np(out, "float16")
     ref = oracle.bias_add_grad(to_np(x, "float16"), "NHWC", "float16")
     assert_close(got, ref, "float16", 1e-2, "BiasAddGrad f16 > 2^31")
+
+
+@pytest.mark.parametrize("rows,kernel", [(15000, "fused"), (16384, "apply")])
+def test_batch_norm_wide_channels_group_span(dev, rows, kernel):
+    """FusedBatchNormV3 + GradV3 on [1, rows, 1, 65536] f16: 256 channel
+    tiles, so one row group of all rows per tile.  The fused kernel reads a
+    workgroup's rows through a buffer resource with 32-bit byte offsets; at
+    15000 rows the largest offset is ~2.0e9 (just below 2^31) and the fused
+    path runs, at 16384 rows the group's span reaches 2^31 bytes and the op
+    must take the split path instead.  Both: statistics against float64 sums
+    and every element of y and dx within 1 ulp of the float32 closed form from
+    the kernel's own statistics (tolerances as in the 2^31-element test)."""
+    _need(16)
+    c = 65536
+    shape = (1, rows, 1, c)
+    torch.manual_seed(15)
+    x = torch.randn(shape, device=dev, dtype=torch.float16).add_(0.5)
+    dy = torch.randn(shape, device=dev, dtype=torch.float16)
+    scale = torch.rand(c, device=dev) + 0.5
+    offset = 0.1 * torch.randn(c, device=dev)
+    e = torch.empty(0, device=dev)
+    eps = 1.001e-5
+    f = ops.FusedBatchNormV3(x, scale, offset, e, e, epsilon=eps)
+    assert ops.last_kernel_name() == f"tfma_bn_fwd_{kernel}"
+    s1 = _chunked_sums(x, c, lambda a: a, rows_per=1024)
+    s2 = _chunked_sums(x, c, lambda a: a * a, rows_per=1024)
+    mean = s1 / rows
+    var = s2 / rows - mean * mean
+    assert torch.allclose(f.reserve_space_1.double(), mean, rtol=0, atol=1e-5)
+    assert torch.allclose(f.reserve_space_2.double(), var, rtol=5e-5, atol=0)
+    mu, sig = f.reserve_space_1, f.reserve_space_2
+    assert bn_max_ulp(f.y, bn_fwd_ref32(x, mu, sig, scale, offset, eps, rows, c), rows, c,
+                      rows_per=2048) <= 1
+    g = ops.FusedBatchNormGradV3(dy, x, scale, mu, sig, f.reserve_space_3, epsilon=eps)
+    assert ops.last_kernel_name() == f"tfma_bn_grad_{kernel}"
+    sdy = _chunked_sums(dy, c, lambda a: a, rows_per=1024)
+    assert torch.allclose(g.offset_backprop.double(), sdy, rtol=1e-5, atol=5e-2)
+    ref = bn_grad_ref32(dy, x, scale, mu, sig, g.offset_backprop, g.scale_backprop, eps, rows, c)
+    assert bn_max_ulp(g.x_backprop, ref, rows, c, rows_per=2048) <= 1
