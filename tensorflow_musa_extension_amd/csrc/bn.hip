@@ -1579,6 +1579,16 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
       static_cast<size_t>(fp.groups) * g.c * 16 > bs->eslot_bytes ||
       static_cast<size_t>(g.c) * 32 > bs->ecoef_bytes)
     return hipErrorInvalidValue;  // excluded by make_fused_plan
+  unsigned long long* region =
+      recorded ? reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(bs->counter) +
+                                                       kStateBytes)
+               : bs->counter;
+  if (!recorded && bs->used && bs->last_stream != stream) {
+    hipError_t e = hipStreamWaitEvent(stream, bs->chain, 0);
+    if (e != hipSuccess) return e;
+  }
+  // The epoch, after the wait above: zeroing the regions at the wrap must
+  // follow the previous fused launch, which may be on another stream.
   unsigned epoch = 0;
   if (!recorded) {
     if (bs->epoch + 1 >= (1u << 31)) {
@@ -1587,14 +1597,6 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
       bs->epoch = 0;
     }
     epoch = ++bs->epoch;
-  }
-  unsigned long long* region =
-      recorded ? reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(bs->counter) +
-                                                       kStateBytes)
-               : bs->counter;
-  if (!recorded && bs->used && bs->last_stream != stream) {
-    hipError_t e = hipStreamWaitEvent(stream, bs->chain, 0);
-    if (e != hipSuccess) return e;
   }
   FusedArgs fa;
   fa.x = x;
