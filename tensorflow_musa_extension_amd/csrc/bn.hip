@@ -1574,6 +1574,11 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
     bs->eslot_bytes = slot_bytes;
     bs->ecoef = reinterpret_cast<unsigned long long*>(static_cast<char*>(p) + slot_bytes);
     bs->ecoef_bytes = coef_bytes;
+    // First eager epoch - 1 (TFMA_BN_EPOCH_START, default 0): a test starts
+    // just below the wrap to run launches across it.
+    const char* es = getenv("TFMA_BN_EPOCH_START");
+    const unsigned long long start = es ? strtoull(es, nullptr, 10) : 0ull;
+    bs->epoch = start < (1ull << 31) ? static_cast<unsigned>(start) : 0u;
   }
   if (fp.groups > kMaxEpochGroups ||
       static_cast<size_t>(fp.groups) * g.c * 16 > bs->eslot_bytes ||

@@ -358,3 +358,50 @@ def test_fused_epochs_fresh_values(dev):
     for k, outs in got:
         for w, g in zip(want[k], outs):
             assert torch.equal(w, g)
+
+
+_WRAP_SCRIPT = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+import tensorflow_musa_extension_amd as tfma
+ops = tfma.raw_ops
+dev = torch.device("cuda:0")
+torch.manual_seed(6)
+x = torch.randn(16, 14, 14, 256, device=dev).half()
+dy = torch.randn_like(x)
+scale = torch.rand(256, device=dev) + 0.5
+offset = 0.1 * torch.randn(256, device=dev)
+e = torch.empty(0, device=dev)
+outs = []
+for i in range(6):
+    f = ops.FusedBatchNormV3(x, scale, offset, e, e, epsilon=1e-3)
+    g = ops.FusedBatchNormGradV3(dy, x, scale, f.reserve_space_1, f.reserve_space_2,
+                                 f.reserve_space_3, epsilon=1e-3)
+    assert ops.last_kernel_name() == "tfma_bn_grad_fused"
+    outs.append([t.clone() for t in (f.y, f.batch_mean, f.batch_variance, g.x_backprop,
+                                     g.scale_backprop, g.offset_backprop)])
+torch.cuda.synchronize()
+assert not ops.fused_batch_norm_barrier_timed_out()
+for o in outs[1:]:
+    for a, b in zip(outs[0], o):
+        assert torch.equal(a, b)
+print("wrap ok")
+"""
+
+
+def test_fused_epoch_wrap(tmp_path):
+    """The eager epoch counter wraps below 2^31: the library zeroes its
+    epoch-tagged regions and starts again at 1.  A fresh process whose counter
+    starts 3 below the wrap (TFMA_BN_EPOCH_START) runs 12 fused launches across
+    it; every forward and grad must equal the first bit for bit."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = tmp_path / "wrap.py"
+    script.write_text(_WRAP_SCRIPT)
+    env = dict(os.environ, TFMA_BN_EPOCH_START=str(2**31 - 4))
+    r = subprocess.run([sys.executable, str(script), root], env=env, capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "wrap ok" in r.stdout
