@@ -21,7 +21,8 @@ roofline: the dominant kernel (tfma_bn_grad_fused: reads x, dy, writes dx,
 cpu_baseline: the TF-CPU restatement (oracle/, C + OpenMP) on the same
         BN workload (both dtypes, four shapes), repeated for >= 10 s on up to
         16 host cores.
-components: the other kernels (Adam, mixed-precision Adam, grouped Adam at
+components: cfg1 (FusedBatchNormV3 forward, f32 [32,56,56,64]) and the
+        other kernels (Adam, mixed-precision Adam, grouped Adam at
         the ResNet-50 and 1.31e9-parameter configs, the elementwise chains,
         ReluGrad, BiasAddGrad) at their config shapes, each rep timed with HIP
         events after a 1 GiB read that evicts the Infinity Cache (GB/s, % of
@@ -204,6 +205,19 @@ def components(torch, ops, dev):
                 "kernel_ms": round(kms, 4) if kms else None,
                 "kernel_GB/s": round(kgbps, 1) if kgbps else None,
                 "kernel_pct_peak": round(100 * kgbps / PEAK_GBPS, 1) if kgbps else None}
+
+    # cfg1: FusedBatchNormV3 training forward, NHWC f32 x[32,56,56,64]
+    # (the reference's CPU-runnable case; epsilon 1e-3), 2*s*E bytes.
+    x1 = torch.randn(32, 56, 56, 64, generator=gen, device=dev)
+    sc1 = torch.rand(64, generator=gen, device=dev) + 0.5
+    of1 = 0.1 * torch.randn(64, generator=gen, device=dev)
+    e1 = torch.empty(0, device=dev)
+    ws1 = torch.empty(ops.fused_batch_norm_workspace_bytes(x1), dtype=torch.uint8, device=dev)
+    bn1 = ops.bind(ops.FusedBatchNormV3, x1, sc1, of1, e1, e1, epsilon=1e-3, data_format="NHWC",
+                   is_training=True, workspace=ws1)
+    out["bn_fwd_f32_cfg1_32x56x56x64"] = rate([bn1], 8 * x1.numel(), x1.numel(),
+                                              "tfma_bn_fwd")
+    del x1, bn1, ws1
 
     n = 25_600_000
     var = 0.02 * torch.randn(n, generator=gen, device=dev)
