@@ -151,7 +151,8 @@ def bn_workload(torch, ops, dev):
 def time_calls(torch, calls, steps, warmup, flush=None):
     """ms per pass over `calls`.  With `flush` (a large device buffer), each
     pass is timed on its own after reading the buffer, so the 256 MB
-    Infinity Cache holds none of the op's data (the BASELINE.md protocol)."""
+    Infinity Cache holds none of the op's data (the cache is flushed between
+    reps: cfg1 and the smaller f16 shapes would otherwise fit in it)."""
     for _ in range(warmup):
         for c in calls:
             c()
