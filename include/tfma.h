@@ -350,15 +350,42 @@ void TFMA_FreeBuffer(void* buffer);
 int TFMA_TraceEnable(const char* name_substr, TFMA_Status* status);
 int TFMA_TraceRead(double* total_ms, int64_t* launches, TFMA_Status* status);
 
-/* Whether a fused BatchNorm launch on the current device gave up one of its
- * grid-wide waits - for another workgroup's partials or coefficients (the
- * bounded spin, ~0.5 s, ran out because the grid was not co-resident; that
- * launch's outputs are wrong).  *timed_out = 1 if so;
- * reset != 0 clears the flag.  Waits for the device to go idle
- * (hipDeviceSynchronize) before reading: a diagnostic, not for hot loops.
+/* The fused BatchNorm kernel assumes its workgroups (one or two per CU) are
+ * all resident at once; a wave waiting for another workgroup's partials or
+ * coefficients gives up after a bounded spin (~0.5 s), which only happens
+ * when another persistent kernel holds compute units the grid needs (another
+ * process's, or a graph replay overlapping an eager fused launch).  Such a
+ * launch writes NaN statistics and outputs for the channels concerned and
+ * stores its epoch in a host-visible word; the next FusedBatchNormV3 /
+ * FusedBatchNormGradV3 call on the device then returns TFMA_INTERNAL instead
+ * of launching (once per such launch; no device synchronization).
+ * This query: *timed_out = 1 if any fused launch on the current device gave
+ * up since the last reset; reset != 0 clears it.  Waits for the device to go
+ * idle (hipDeviceSynchronize) first: a diagnostic, not for hot loops.
  * No reference counterpart: the reference's BatchNorm kernels have no
  * grid-wide wait. */
 int TFMA_FusedBatchNormBarrierTimedOut(int32_t* timed_out, int32_t reset, TFMA_Status* status);
+
+/* Launch plan of the calling thread's last FusedBatchNormV3 /
+ * FusedBatchNormGradV3 call (for tests that check which path ran).
+ * fused = 1: the persistent kernel ran with `workgroups` workgroups over
+ * row_groups x channel_tiles; dynamic_rows > 0: each thread's lowest
+ * dynamic_rows streamed phase-3 rows were handed out in chunks of
+ * dynamic_chunk rows; register_rows / lds_rows: rows per thread kept on chip.
+ * fused = 0: the reduce / finalize / apply kernels ran.  No reference
+ * counterpart. */
+typedef struct TFMA_FusedBatchNormPlan {
+  int32_t fused;
+  int32_t workgroups;
+  int64_t row_groups;
+  int32_t channel_tiles;
+  int32_t dynamic_rows;
+  int32_t dynamic_chunk;
+  int32_t register_rows;
+  int32_t lds_rows;
+  int32_t reserved;
+} TFMA_FusedBatchNormPlan;
+int TFMA_FusedBatchNormLastPlan(TFMA_FusedBatchNormPlan* plan, TFMA_Status* status);
 
 /* Name of the last kernel this library launched on the calling thread (for
  * tests that check which path an op took). */

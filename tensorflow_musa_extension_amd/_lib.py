@@ -50,6 +50,14 @@ class TFMA_GraphRewriteStats(ctypes.Structure):
                 ("adam_grouped_nodes", ctypes.c_int32), ("adam_mixed", ctypes.c_int32)]
 
 
+class TFMA_FusedBatchNormPlan(ctypes.Structure):
+    _fields_ = [("fused", ctypes.c_int32), ("workgroups", ctypes.c_int32),
+                ("row_groups", ctypes.c_int64), ("channel_tiles", ctypes.c_int32),
+                ("dynamic_rows", ctypes.c_int32), ("dynamic_chunk", ctypes.c_int32),
+                ("register_rows", ctypes.c_int32), ("lds_rows", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
 LIB_NAME = "libtfma.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
@@ -94,6 +102,7 @@ SIGNATURES = {
     "TFMA_TraceRead": [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), _S],
     "TFMA_LastKernelName": [],
     "TFMA_FusedBatchNormBarrierTimedOut": [ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, _S],
+    "TFMA_FusedBatchNormLastPlan": [ctypes.POINTER(TFMA_FusedBatchNormPlan), _S],
     "TFMA_MemcpyHtoD": [_vp, _vp, _vp, ctypes.c_uint64, ctypes.c_int32, _S],
     "TFMA_MemcpyDtoH": [_vp, _vp, _vp, ctypes.c_uint64, ctypes.c_int32, _S],
     "TFMA_CreateStreamDependency": [_vp, _vp, _S],

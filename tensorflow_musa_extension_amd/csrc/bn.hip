@@ -624,7 +624,15 @@ __global__ __launch_bounds__(kThreads) void bn_nchw_apply_kernel(
 //    launch needs reset.
 // ---------------------------------------------------------------------------
 constexpr int kFusedThreads = 512;
-constexpr unsigned kSpinLimit = 1u << 24;  // ~0.5 s, then give up (flagged)
+// Polls of a cross-workgroup wait before it gives up (~0.5 s).  A wait can
+// only run out when the grid is not co-resident - another persistent kernel
+// (another process's, or a graph replay overlapping an eager launch) holds
+// CUs this grid's missing workgroups need.  The waiting wave then stops
+// waiting, poisons what it computes (the channel's statistics and
+// coefficients, hence its outputs, become NaN) and stores the launch's epoch
+// into a host-visible word; the host reports it as an error from the next
+// FusedBatchNorm call on the device (BnPendingGiveUp).
+constexpr unsigned kSpinLimit = 1u << 24;
 // Epoch-tagged partials: at most 8 row groups per lane of a finishing wave.
 constexpr int kEpochPerLane = 8;
 constexpr int64_t kMaxEpochGroups = 64 * kEpochPerLane;
@@ -680,7 +688,9 @@ struct FusedArgs {
   unsigned long long base;      // its value when this launch starts
   unsigned* sub;                // 8 arrival counters (workgroup id mod 8), 256 B apart
   unsigned sub_last[8];         // value class r's last exit arrival sees
-  unsigned* timeout_flag;
+  unsigned* gave_up;             // host-visible word: epoch of a launch whose wait ran out
+  unsigned spin_limit;          // polls before a wait gives up (kSpinLimit)
+  unsigned wait_xor;            // 0; a test hook flips an epoch bit no launch publishes
   unsigned* queues;             // [ct][wave] chunk counters, zero between launches
   int reset_at_exit;            // recorded into a graph: zero every counter at exit
   int dyn_rows;                 // streamed rows per thread handed out dynamically
@@ -840,6 +850,12 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
                                                     __HIP_MEMORY_SCOPE_AGENT) % 0x7fffffffu
                   : a.epoch;
   const uint64_t etag = static_cast<uint64_t>(epoch) << 32;
+  // The tag the waits look for: this launch's epoch (wait_xor is 0 except
+  // under the host's forced-give-up test hook).
+  const uint32_t wtag = epoch ^ a.wait_xor;
+  auto give_up = [&]() {
+    __hip_atomic_store(a.gave_up, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  };
 
   // ---- phase 1: partial statistics --------------------------------------
   float k[VEC], s1[VEC], s2[VEC];
@@ -999,7 +1015,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       // Lane l sums groups l, l + 64, ... (at most kMaxGroups / 64 of them):
       // all their slots are loaded at once, then the ones not yet tagged
       // with this launch's epoch are polled again.
-      const uint64_t tag = etag;
+      const uint64_t tag = static_cast<uint64_t>(wtag) << 32;
       uint64_t v1[kEpochPerLane], v2[kEpochPerLane];
 #pragma unroll
       for (int i = 0; i < kEpochPerLane; ++i) {
@@ -1011,14 +1027,16 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
         }
       }
       unsigned spins = 0;
+      bool lost = false;
       while (true) {
         bool ready = true;
 #pragma unroll
         for (int i = 0; i < kEpochPerLane; ++i)
           ready = ready && (v1[i] >> 32) == (tag >> 32) && (v2[i] >> 32) == (tag >> 32);
         if (ready) break;
-        if (++spins > kSpinLimit) {
-          __hip_atomic_store(a.timeout_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (++spins > a.spin_limit) {
+          lost = true;
+          give_up();
           break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -1037,6 +1055,9 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
           t2 += __builtin_bit_cast(float, static_cast<uint32_t>(v2[i]));
         }
       }
+      // A lane whose partials never arrived poisons the channel's sums (the
+      // wave sum below spreads the NaN to its statistics and coefficients).
+      if (lost) t1 = t2 = __builtin_nan("");
     }
     const double2 w = wave_sum(t1, t2);
     if (lane == 0) {
@@ -1084,7 +1105,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     static_assert(kW >= 32 * (VEC + 1) && kW % 32 == 8, "coefficient layout");
     static_assert(4 * kW * sizeof(float) <= sizeof(red), "coefficients fit in red");
     float* const cs = reinterpret_cast<float*>(red);
-    const uint64_t tag = etag;
+    const uint64_t tag = static_cast<uint64_t>(wtag) << 32;
     uint64_t v[2];
     int64_t wi[2];
 #pragma unroll
@@ -1097,8 +1118,13 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     }
     unsigned spins = 0;
     while ((v[0] >> 32) != (tag >> 32) || (v[1] >> 32) != (tag >> 32)) {
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(a.timeout_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (++spins > a.spin_limit) {
+        // Coefficients that never arrived are used as NaN (the tile's
+        // outputs for those channels become NaN).
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          if ((v[i] >> 32) != (tag >> 32)) v[i] = 0x7fc00000u;
+        give_up();
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -1508,7 +1534,7 @@ constexpr size_t kSubOffset = kQueueOffset + kQueueBytes;  // 8 class counters, 
 constexpr size_t kStateBytes = kSubOffset + 8 * 256;
 struct BarrierState {
   std::mutex mu;
-  unsigned long long* counter = nullptr;  // [0] arrivals, [1] timeout flag
+  unsigned long long* counter = nullptr;  // [0] arrivals
   unsigned long long base = 0;
   unsigned sub_base[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // class counters (mod 2^32)
   hipEvent_t last = nullptr;   // end of the last launch when it was not traced
@@ -1520,8 +1546,35 @@ struct BarrierState {
   unsigned long long* ecoef = nullptr;   // epoch-tagged coefficients, zeroed at creation
   size_t ecoef_bytes = 0;
   unsigned epoch = 0;                    // last epoch handed to a launch (< 2^31)
+  // Give-up word in pinned host memory (coherent, mapped): a launch whose
+  // wait ran out stores its epoch there; the host reads it without any
+  // device synchronization.  `reported`: the value last turned into an error.
+  volatile unsigned* gave_up_host = nullptr;
+  unsigned* gave_up_dev = nullptr;
+  unsigned reported = 0;
 };
 
+// Test hook (TFMA_BN_FORCE_GIVE_UP=1, read once): every eager fused launch
+// waits for an epoch no launch publishes, with a short spin limit, so each
+// wait gives up and the kernels still exit normally.
+bool force_give_up() {
+  static const bool on = [] {
+    const char* e = getenv("TFMA_BN_FORCE_GIVE_UP");
+    return e && e[0] == '1';
+  }();
+  return on;
+}
+
+
+// Plan of the calling thread's last FusedBatchNorm launch
+// (TFMA_FusedBatchNormLastPlan).
+thread_local TFMA_FusedBatchNormPlan t_last_plan{};
+
+void note_split_plan(const Plan& p) {
+  t_last_plan = TFMA_FusedBatchNormPlan{};
+  t_last_plan.row_groups = p.groups;
+  t_last_plan.channel_tiles = p.ct;
+}
 
 BarrierState* barrier_state() {
   static BarrierState states[64];
@@ -1548,6 +1601,20 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
       return e;
     }
     bs->counter = static_cast<unsigned long long*>(p);
+  }
+  if (!bs->gave_up_host) {
+    void* h = nullptr;
+    hipError_t e = hipHostMalloc(&h, 64, hipHostMallocCoherent | hipHostMallocMapped);
+    if (e != hipSuccess) return e;
+    *static_cast<volatile unsigned*>(h) = 0;
+    void* d = nullptr;
+    e = hipHostGetDevicePointer(&d, h, 0);
+    if (e != hipSuccess) {
+      (void)hipHostFree(h);
+      return e;
+    }
+    bs->gave_up_host = static_cast<volatile unsigned*>(h);
+    bs->gave_up_dev = static_cast<unsigned*>(d);
   }
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   {
@@ -1625,7 +1692,10 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
     const unsigned sb = recorded ? 0u : bs->sub_base[r];
     fa.sub_last[r] = sb + members - 1;
   }
-  fa.timeout_flag = reinterpret_cast<unsigned*>(region + 1);
+  fa.gave_up = bs->gave_up_dev;
+  const bool forced = force_give_up() && !recorded;
+  fa.spin_limit = forced ? 2000u : kSpinLimit;
+  fa.wait_xor = forced ? 0x40000000u : 0u;
   fa.queues = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(region) + kQueueOffset);
   fa.reset_at_exit = recorded ? 1 : 0;
   fa.eslots = bs->eslots;
@@ -1653,6 +1723,15 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   }
   fa.fin = fin;
   fa.fin.groups = fp.groups;
+  t_last_plan = TFMA_FusedBatchNormPlan{};
+  t_last_plan.fused = 1;
+  t_last_plan.workgroups = fp.blocks;
+  t_last_plan.row_groups = fp.groups;
+  t_last_plan.channel_tiles = fp.ct;
+  t_last_plan.dynamic_rows = fa.dyn_rows;
+  t_last_plan.dynamic_chunk = fa.dyn_chunk;
+  t_last_plan.register_rows = kr;
+  t_last_plan.lds_rows = fused_kl<Tr, kGrad>();
   const char* name = kGrad ? "tfma_bn_grad_fused" : "tfma_bn_fwd_fused";
   SetLastKernel(name);
   const void* kern = fused_kernel<Tr, kGrad>();
@@ -1696,21 +1775,29 @@ hipError_t BnBarrierTimedOut(bool reset, bool* timed_out) {
   BarrierState* bs = barrier_state();
   if (!bs) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lk(bs->mu);
-  if (!bs->counter) return hipSuccess;  // no fused launch on this device yet
-  hipError_t e = hipDeviceSynchronize();
-  for (int region = 0; region < 2 && e == hipSuccess; ++region) {
-    unsigned* fl = reinterpret_cast<unsigned*>(
-        reinterpret_cast<char*>(bs->counter) + region * kStateBytes + sizeof(unsigned long long));
-    unsigned flag = 0;
-    e = hipMemcpy(&flag, fl, sizeof(flag), hipMemcpyDeviceToHost);
-    if (e != hipSuccess) break;
-    *timed_out = *timed_out || flag != 0;
-    if (reset && flag) {
-      const unsigned zero = 0;
-      e = hipMemcpy(fl, &zero, sizeof(zero), hipMemcpyHostToDevice);
-    }
+  if (!bs->gave_up_host) return hipSuccess;  // no fused launch on this device yet
+  const hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return e;
+  *timed_out = *bs->gave_up_host != 0;
+  if (reset) {
+    *bs->gave_up_host = 0;
+    bs->reported = 0;
   }
-  return e;
+  return hipSuccess;
+}
+
+TFMA_FusedBatchNormPlan BnLastPlan() { return t_last_plan; }
+
+bool BnPendingGiveUp(unsigned* epoch) {
+  BarrierState* bs = barrier_state();
+  if (!bs) return false;
+  std::lock_guard<std::mutex> lk(bs->mu);
+  if (!bs->gave_up_host) return false;
+  const unsigned v = *bs->gave_up_host;
+  if (v == 0 || v == bs->reported) return false;
+  bs->reported = v;
+  *epoch = v;
+  return true;
 }
 
 namespace {
@@ -1765,6 +1852,7 @@ hipError_t forward_t(const BnGeometry& g, const BnFwdArgs& a, void* ws,
     return launch_fused<Tr, false>(fp, g, a.x, nullptr, a.y, fa,
                                                   stream);
   }
+  note_split_plan(p);
   if (a.is_training) {
     e = p.vec == 1 ? launch_reduce<Tr, 1, false>(p, g, a.x, nullptr, nullptr, partial, stream)
                    : launch_reduce<Tr, Tr::kVec, false>(p, g, a.x, nullptr, nullptr, partial, stream);
@@ -1811,6 +1899,7 @@ hipError_t grad_t(const BnGeometry& g, const BnGradArgs& a, void* ws,
     return launch_fused<Tr, true>(fp, g, a.x, a.dy, a.dx, fa,
                                                   stream);
   }
+  note_split_plan(p);
   hipError_t e =
       p.vec == 1 ? launch_reduce<Tr, 1, true>(p, g, a.x, a.dy, a.saved_mean, partial, stream)
                  : launch_reduce<Tr, Tr::kVec, true>(p, g, a.x, a.dy, a.saved_mean, partial, stream);

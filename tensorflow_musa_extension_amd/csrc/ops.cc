@@ -297,7 +297,9 @@ class AdamTableCache {
   static constexpr int kDevices = 64;
 
   // The cached device table equal to `t`, made ready on `stream`, or null.
-  // On success the caller launches and then calls mark_used().
+  // On success the slot is pinned (fill() will not reuse it) until the
+  // caller, after enqueuing its launch, calls mark_used(), which records the
+  // slot's use behind that launch and unpins it.
   const void* find(int dev, const std::vector<uint8_t>& t, hipStream_t stream, int* slot) {
     std::lock_guard<std::mutex> lk(mu_);
     if (dev < 0 || dev >= kDevices) return nullptr;
@@ -308,6 +310,7 @@ class AdamTableCache {
       if (s.fill_stream != stream && hipStreamWaitEvent(stream, s.ready, 0) != hipSuccess)
         return nullptr;
       s.tick = ++tick_;
+      ++s.pins;
       *slot = i;
       return s.dev;
     }
@@ -316,7 +319,9 @@ class AdamTableCache {
 
   void mark_used(int dev, int slot, hipStream_t stream) {
     std::lock_guard<std::mutex> lk(mu_);
-    (void)hipEventRecord(slots_[dev][slot].used, stream);
+    Slot& s = slots_[dev][slot];
+    (void)hipEventRecord(s.used, stream);
+    --s.pins;
   }
 
   // Keeps a copy of the table the caller has just uploaded to `ws` on
@@ -328,7 +333,9 @@ class AdamTableCache {
     int pick = -1;
     for (int i = 0; i < kSlots; ++i) {
       Slot& s = slots_[dev][i];
-      if (s.valid && hipEventQuery(s.used) != hipSuccess) continue;  // still in use
+      // Pinned by a call between find() and mark_used(), or still read by
+      // an enqueued launch.
+      if (s.pins > 0 || (s.valid && hipEventQuery(s.used) != hipSuccess)) continue;
       if (pick < 0 || !s.valid || (slots_[dev][pick].valid && s.tick < slots_[dev][pick].tick))
         pick = i;
       if (!s.valid) break;
@@ -369,6 +376,7 @@ class AdamTableCache {
     hipEvent_t used = nullptr;
     hipStream_t fill_stream = nullptr;
     uint64_t tick = 0;
+    int pins = 0;  // calls between find() and mark_used()
   };
   std::mutex mu_;
   Slot slots_[kDevices][kSlots];
@@ -552,11 +560,11 @@ int bias_add_impl(void* stream, const TFMA_Tensor* value, const TFMA_Tensor* bia
   if (!same_shape(value, output))
     return set_status(st, TFMA_INVALID_ARGUMENT, "%s: output shape %s != input shape %s",
                       name, shape_str(output).c_str(), shape_str(value).c_str());
-  const int64_t n = num_elements(value);
-  if (n == 0 || num_elements(bias) == 0) return ok(st);
   const int channel_dim = fmt == "NCHW" ? 1 : value->ndims - 1;
   if (bias->dims[0] != value->dims[channel_dim])
     return set_status(st, TFMA_INVALID_ARGUMENT, "Dimension mismatch in BiasAdd");
+  const int64_t n = num_elements(value);
+  if (n == 0) return ok(st);
   int64_t inner = 1;
   for (int d = channel_dim + 1; d < value->ndims; ++d) inner *= value->dims[d];
   if (!value->data || !bias->data || !output->data)
@@ -617,6 +625,24 @@ bool is_vec_f32(const TFMA_Tensor* t) {
   return valid_tensor(t) && t->ndims == 1 && t->dtype == TFMA_FLOAT;
 }
 
+// An earlier fused BatchNorm launch on this device that gave up a
+// grid-wide wait (its grid was not co-resident) wrote NaN statistics and
+// outputs for the channels concerned; the next BatchNorm call reports it,
+// once, as INTERNAL (the launch-failure code of the reference's ops,
+// musa_applyadam_op.cc:258-261) instead of launching.
+int check_bn_give_up(TFMA_Status* st) {
+  unsigned epoch = 0;
+  if (!BnPendingGiveUp(&epoch)) return TFMA_OK;
+  int dev = -1;
+  (void)hipGetDevice(&dev);
+  return set_status(st, TFMA_INTERNAL,
+                    "FusedBatchNorm: an earlier fused launch on device %d (epoch %u) gave up "
+                    "waiting for another workgroup's values because its grid was not "
+                    "co-resident (another persistent kernel held compute units); the "
+                    "statistics and outputs of the channels concerned were written as NaN",
+                    dev, epoch);
+}
+
 }  // namespace
 
 int DeviceCUs() {
@@ -666,6 +692,12 @@ int TFMA_FusedBatchNormBarrierTimedOut(int32_t* timed_out, int32_t reset,
     return set_status(status, TFMA_INTERNAL, "FusedBatchNorm barrier flag: %s",
                       hipGetErrorString(e));
   *timed_out = t ? 1 : 0;
+  return ok(status);
+}
+
+int TFMA_FusedBatchNormLastPlan(TFMA_FusedBatchNormPlan* plan, TFMA_Status* status) {
+  if (!plan) return set_status(status, TFMA_INVALID_ARGUMENT, "plan is null");
+  *plan = BnLastPlan();
   return ok(status);
 }
 
@@ -785,6 +817,7 @@ int TFMA_FusedBatchNormV3(void* stream, const TFMA_Tensor* x, const TFMA_Tensor*
   a.saved_mean = static_cast<float*>(reserve_space_1->data);
   a.saved_var = static_cast<float*>(reserve_space_2->data);
   a.reserve3 = r3;
+  if (const int rc = check_bn_give_up(status)) return rc;
   return hip_status(status, LaunchBnForward(t, g, a, workspace, workspace_bytes, s),
                     "FusedBatchNormV3");
 }
@@ -892,6 +925,7 @@ int TFMA_FusedBatchNormGradV3(void* stream, const TFMA_Tensor* y_backprop, const
   a.reserve4_n = n4;
   a.reserve5 = r5;
   a.reserve5_n = n5;
+  if (const int rc = check_bn_give_up(status)) return rc;
   return hip_status(status, LaunchBnGrad(t, g, a, workspace, workspace_bytes, s),
                     "FusedBatchNormGradV3");
 }
@@ -973,14 +1007,13 @@ int apply_adam(void* stream, TFMA_Tensor* var, TFMA_Tensor* m, TFMA_Tensor* v,
                const TFMA_Tensor* const* sc, const TFMA_Tensor* grad, int use_locking,
                int use_nesterov, bool mixed, const char* op, TFMA_Status* status) {
   int dt = 0, gdt = 0;
-  if (check_adam_triple(var, m, v, grad, mixed, &dt, &gdt, status) != TFMA_OK)
-    return status->code;
+  if (const int rc = check_adam_triple(var, m, v, grad, mixed, &dt, &gdt, status)) return rc;
   DType t, tg;
   if (!to_dtype(dt, &t) || !to_dtype(gdt, &tg))
     return set_status(status, TFMA_UNIMPLEMENTED, "%s: dtype %s is not supported", op,
                       dtype_name(dt));
   AdamScalars s;
-  if (check_adam_scalars(sc, dt, &s, t, status) != TFMA_OK) return status->code;
+  if (const int rc = check_adam_scalars(sc, dt, &s, t, status)) return rc;
   VarLocks locks;
   if (use_locking) {
     locks.add(var->data);
@@ -1063,11 +1096,10 @@ int TFMA_GroupedResourceApplyAdam(void* stream, int n, TFMA_Tensor* vars, TFMA_T
   int64_t chunks = 0;
   for (int i = 0; i < n; ++i) {
     int dt = 0, gdt = 0;
-    if (check_adam_triple(&vars[i], &ms[i], &vs[i], &grads[i], mixed, &dt, &gdt, status) !=
-        TFMA_OK) {
-      std::string msg = status->message;
-      return set_status(status, status->code, "tensor %d: %s", i, msg.c_str());
-    }
+    TFMA_Status inner;
+    if (const int rc = check_adam_triple(&vars[i], &ms[i], &vs[i], &grads[i], mixed, &dt, &gdt,
+                                         &inner))
+      return set_status(status, rc, "tensor %d: %s", i, inner.message);
     if (i == 0) {
       dt0 = dt;
       gdt0 = gdt;
@@ -1097,7 +1129,7 @@ int TFMA_GroupedResourceApplyAdam(void* stream, int n, TFMA_Tensor* vars, TFMA_T
                       "MusaGroupedResourceApplyAdam: dtype %s is not supported", dtype_name(dt0));
   const TFMA_Tensor* sc[6] = {beta1_power, beta2_power, lr, beta1, beta2, epsilon};
   AdamScalars s;
-  if (check_adam_scalars(sc, dt0, &s, t, status) != TFMA_OK) return status->code;
+  if (const int rc = check_adam_scalars(sc, dt0, &s, t, status)) return rc;
   size_t need = 0;
   TFMA_GroupedApplyAdamWorkspaceBytes(n, vars, &need, nullptr);
   if (!workspace || workspace_bytes < need)
@@ -1238,9 +1270,9 @@ int elem_size(int dt) {
 int TFMA_BiasAddGradWorkspaceBytes(const TFMA_Tensor* out_backprop, const char* data_format,
                                    size_t* bytes, TFMA_Status* status) {
   int64_t outer = 0, c = 0, inner = 0;
-  if (bias_grad_geometry(out_backprop, data_format, nullptr, &outer, &c, &inner, status) !=
-      TFMA_OK)
-    return status->code;
+  if (const int rc = bias_grad_geometry(out_backprop, data_format, nullptr, &outer, &c, &inner,
+                                        status))
+    return rc;
   if (!bytes) return set_status(status, TFMA_INVALID_ARGUMENT, "bytes is null");
   *bytes = (out_backprop->ndims < 2 || c == 0)
                ? 0
@@ -1253,9 +1285,9 @@ int TFMA_BiasAddGrad(void* stream, const TFMA_Tensor* out_backprop, const char* 
                      TFMA_Tensor* output, void* workspace, size_t workspace_bytes,
                      TFMA_Status* status) {
   int64_t outer = 0, c = 0, inner = 0;
-  if (bias_grad_geometry(out_backprop, data_format, output, &outer, &c, &inner, status) !=
-      TFMA_OK)
-    return status->code;
+  if (const int rc = bias_grad_geometry(out_backprop, data_format, output, &outer, &c, &inner,
+                                        status))
+    return rc;
   if (c == 0) return ok(status);
   if (!output->data) return set_status(status, TFMA_INVALID_ARGUMENT, "BiasAddGrad: null output");
   const int es = elem_size(out_backprop->dtype);

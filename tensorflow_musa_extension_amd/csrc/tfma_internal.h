@@ -183,8 +183,15 @@ struct BnGradArgs {
 hipError_t LaunchBnGrad(DType t, const BnGeometry& g, const BnGradArgs& a,
                         void* workspace, size_t workspace_bytes,
                         hipStream_t stream);
-// Reads (and with `reset` clears) the current device's barrier-timeout flag
-// after a device synchronize.
+// Reads (and with `reset` clears) the current device's give-up word after a
+// device synchronize.
 hipError_t BnBarrierTimedOut(bool reset, bool* timed_out);
+// Whether a fused launch on the current device gave up one of its waits and
+// has not been reported yet (no device synchronization: the kernel writes
+// the word to pinned host memory).  On true, *epoch is that launch's epoch
+// and the report is consumed.
+bool BnPendingGiveUp(unsigned* epoch);
+// Plan of the calling thread's last FusedBatchNorm launch.
+TFMA_FusedBatchNormPlan BnLastPlan();
 
 }  // namespace tfma

@@ -397,10 +397,24 @@ def trace_read():
     return ms.value, n.value
 
 
+def fused_batch_norm_last_plan():
+    """Launch plan of this thread's last FusedBatchNormV3 / GradV3 call, as a
+    dict: fused (persistent kernel ran), workgroups, row_groups,
+    channel_tiles, dynamic_rows / dynamic_chunk (phase-3 rows per thread
+    handed out in chunks), register_rows, lds_rows."""
+    lib = _lib.load()
+    status = _lib.TFMA_Status()
+    plan = _lib.TFMA_FusedBatchNormPlan()
+    lib.TFMA_FusedBatchNormLastPlan(ctypes.byref(plan), ctypes.byref(status))
+    raise_for_status(status)
+    return {name: getattr(plan, name) for name, _ in plan._fields_ if name != "reserved"}
+
+
 def fused_batch_norm_barrier_timed_out(reset=False):
     """True if a fused BatchNorm launch on the current device gave up a
-    grid-wide wait for other workgroups' values (its outputs are then wrong);
-    synchronizes the device."""
+    grid-wide wait for other workgroups' values since the last reset (its
+    outputs for the channels concerned are NaN, and the next BatchNorm call
+    raised InternalError); synchronizes the device."""
     lib = _lib.load()
     status = _lib.TFMA_Status()
     flag = ctypes.c_int32(0)

@@ -107,3 +107,17 @@ def bn_grad_ref32(dy, x, scale, mean, var, offset_bp, scale_bp, eps, rows, c):
     k2 = (k * k) * (scale_bp.double() / k.double() / rows).float()
     xv, dv = x.view(rows, c), dy.view(rows, c)
     return lambda r0, r1: gk * ((dv[r0:r1].float() - mean_dy) - (xv[r0:r1].float() - mean) * k2)
+
+
+def bn_scale_backprop_ref64(dy, x, mean, var, eps, rows, c, rows_per=1 << 20):
+    """scale_backprop from its definition, independent of the kernel's
+    gradient: rsqrt(var + eps) * sum over rows of dy * (x - mean), with the
+    mean and variance the gradient op was given, summed in float64 on the
+    device in chunks of rows_per rows."""
+    acc = torch.zeros(c, dtype=torch.float64, device=dy.device)
+    xv, dv = x.view(rows, c), dy.view(rows, c)
+    m = mean.double()
+    for r in range(0, rows, rows_per):
+        r1 = min(rows, r + rows_per)
+        acc += (dv[r:r1].double() * (xv[r:r1].double() - m)).sum(0)
+    return acc / torch.sqrt(var.double() + eps)

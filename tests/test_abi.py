@@ -255,6 +255,61 @@ def test_elementwise_validation():
     assert code == _lib.OK
 
 
+def test_bias_add_empty_bias_is_a_dimension_mismatch():
+    """An empty bias against a non-empty channel dimension is TF's dimension
+    error, not a silent success (the channel check runs before any shortcut
+    for empty tensors); an empty value with a matching bias is OK."""
+    code, msg = call("TFMA_BiasAdd", None, ref(T((2, 3))), ref(T((0,))), b"NHWC",
+                     ref(T((2, 3))))
+    assert code == _lib.INVALID_ARGUMENT and msg == "Dimension mismatch in BiasAdd"
+    code, msg = call("TFMA_MusaBiasAddRelu", None, ref(T((2, 3))), ref(T((0,))), b"NHWC",
+                     ref(T((2, 3))))
+    assert code == _lib.INVALID_ARGUMENT and msg == "Dimension mismatch in BiasAdd"
+    code, _ = call("TFMA_BiasAdd", None, ref(T((0, 3))), ref(T((3,))), b"NHWC", ref(T((0, 3))))
+    assert code == _lib.OK
+
+
+def test_invalid_input_with_null_status_returns_the_code():
+    """Every entry point accepts a NULL status: invalid input then returns
+    the error code instead of dereferencing the status."""
+    lib = _lib.load()
+    bufs, descs = scalars()
+    a, b = T((4, 3)), T((4, 2))
+    assert lib.TFMA_ResourceApplyAdam(None, ref(a), ref(b), ref(a), *[ref(d) for d in descs],
+                                      ref(a), 0, 0, None) == _lib.INVALID_ARGUMENT
+    assert lib.TFMA_ResourceApplyAdam(None, ref(T((4, 3), ptr=None)), ref(a), ref(a),
+                                      *[ref(d) for d in descs], ref(a), 0, 0,
+                                      None) == _lib.FAILED_PRECONDITION
+    bad = list(descs)
+    bad[2] = _lib.make_tensor(ctypes.addressof(bufs[2]), _lib.DT_FLOAT, (1,))
+    assert lib.TFMA_ResourceApplyAdam(None, ref(a), ref(a), ref(a), *[ref(d) for d in bad],
+                                      ref(a), 0, 0, None) == _lib.INVALID_ARGUMENT
+    n = 2
+    arr = lambda shapes: (_lib.TFMA_Tensor * n)(*[T(s) for s in shapes])
+    assert lib.TFMA_GroupedResourceApplyAdam(
+        None, n, arr([(4,), (5,)]), arr([(4,), (6,)]), arr([(4,), (5,)]), arr([(4,), (5,)]),
+        *[ref(d) for d in descs], 0, 0, ctypes.c_void_p(FAKE), 4096,
+        None) == _lib.INVALID_ARGUMENT
+    assert lib.TFMA_GroupedResourceApplyAdam(
+        None, n, arr([(4,), (5,)]), arr([(4,), (5,)]), arr([(4,), (5,)]), arr([(4,), (5,)]),
+        *[ref(d) for d in bad], 0, 0, ctypes.c_void_p(FAKE), 4096,
+        None) == _lib.INVALID_ARGUMENT
+    sz = ctypes.c_size_t(0)
+    assert lib.TFMA_BiasAddGradWorkspaceBytes(ref(T(())), b"NHWC", ctypes.byref(sz),
+                                              None) == _lib.INVALID_ARGUMENT
+    assert lib.TFMA_BiasAddGrad(None, ref(T((64, 7, 9))), b"NCDHW", ref(T((7,))),
+                                ctypes.c_void_p(FAKE), 1 << 20, None) == _lib.INVALID_ARGUMENT
+
+
+def test_fused_batch_norm_plan_query_without_device():
+    lib = _lib.load()
+    st = _lib.TFMA_Status()
+    plan = _lib.TFMA_FusedBatchNormPlan()
+    assert lib.TFMA_FusedBatchNormLastPlan(ctypes.byref(plan), ctypes.byref(st)) == _lib.OK
+    assert plan.fused == 0 and plan.workgroups == 0
+    assert lib.TFMA_FusedBatchNormLastPlan(None, ctypes.byref(st)) == _lib.INVALID_ARGUMENT
+
+
 def test_trace_api_without_device():
     st = _lib.TFMA_Status()
     lib = _lib.load()

@@ -13,8 +13,8 @@ import torch
 
 import tensorflow_musa_extension_amd as tfma
 from oracle import oracle
-from tests.helpers import (assert_close, bn_fwd_ref32, bn_grad_ref32, bn_max_ulp, gen,
-                           to_dev, to_np)
+from tests.helpers import (assert_close, bn_fwd_ref32, bn_grad_ref32, bn_max_ulp,
+                           bn_scale_backprop_ref64, gen, to_dev, to_np)
 
 pytestmark = pytest.mark.gpu
 ops = tfma.raw_ops
@@ -196,35 +196,66 @@ def test_constant_channel(dev):
     assert torch.all(fwd.batch_mean == 3.25)
 
 
-@pytest.mark.parametrize("shape", [(256, 7, 7, 2048), (256, 14, 14, 1024)])
+CFG2_SHAPES = [(256, 56, 56, 256), (256, 28, 28, 512), (256, 14, 14, 1024), (256, 7, 7, 2048)]
+
+
+@pytest.mark.parametrize("shape", CFG2_SHAPES)
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_cfg2_full_size(dev, shape, dtype):
-    """BASELINE cfg2 shapes at full size against the oracle (eps=1.001e-5)."""
-    rng = np.random.default_rng(0)
+    """BASELINE cfg2 at full size, every shape in both dtypes, against the
+    oracle (eps=1.001e-5): y and x_backprop to 1e-2, every statistic
+    (batch_mean, batch_variance, reserve spaces, scale_backprop,
+    offset_backprop) to 1e-5 - the outputs the reference's own test checks,
+    test/ops/fused_batchnorm_op_test.py:358-448.  The 56x56 and 28x28
+    gradients (and the 56x56 forward) hand part of phase 3 out dynamically;
+    the plan query shows that this path is the one compared here."""
+    rng = np.random.default_rng(zlib.crc32(repr((shape, dtype)).encode()))
     eps = 1.001e-5
     x, scale, offset, dy = _inputs(rng, shape, dtype, "NHWC")
-    fwd, grad = _run_fwd_grad(dev, x, scale, offset, dy, dtype, "NHWC", eps, poison=False)
+    print(f"cfg2 {shape} {dtype}: inputs ready", flush=True)
+    f = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    tx, tdy = to_dev(x, dtype, dev), to_dev(dy, dtype, dev)
+    e = torch.empty(0, device=dev)
+    fwd = ops.FusedBatchNormV3(tx, f(scale), f(offset), e, e, epsilon=eps)
+    fplan = ops.fused_batch_norm_last_plan()
+    grad = ops.FusedBatchNormGradV3(tdy, tx, f(scale), fwd.reserve_space_1,
+                                    fwd.reserve_space_2, fwd.reserve_space_3, epsilon=eps)
+    gplan = ops.fused_batch_norm_last_plan()
+    torch.cuda.synchronize()
+    assert fplan["fused"] == 1 and gplan["fused"] == 1
+    if shape[1] >= 28:
+        assert gplan["dynamic_rows"] > 0, gplan
+    if shape[1] == 56:
+        assert fplan["dynamic_rows"] > 0, fplan
+    del tx, tdy
     ry, rbm, rbv, rsm, rsv = oracle.bn_fwd(x, scale, offset, epsilon=eps, dtype=dtype)
-    rdx, rsb, rob = oracle.bn_grad(dy, x, scale, fwd.reserve_space_1.cpu().numpy(),
-                                   fwd.reserve_space_2.cpu().numpy(), epsilon=eps,
-                                   dtype=dtype)
     assert_close(to_np(fwd.y, dtype), ry, dtype, 1e-2, "y")
-    assert_close(fwd.batch_mean.cpu().numpy(), rbm, "float32", STAT_TOL, "batch_mean")
-    assert_close(fwd.batch_variance.cpu().numpy(), rbv, "float32", STAT_TOL, "batch_variance")
+    del ry
+    for name, got, want in (("batch_mean", fwd.batch_mean, rbm),
+                            ("batch_variance", fwd.batch_variance, rbv),
+                            ("reserve_space_1", fwd.reserve_space_1, rsm),
+                            ("reserve_space_2", fwd.reserve_space_2, rsv)):
+        assert_close(got.cpu().numpy(), want, "float32", STAT_TOL, name)
+    # The oracle's grad from its own statistics: the kernel's dx and
+    # scale_backprop are checked against values that share nothing with it.
+    rdx, rsb, rob = oracle.bn_grad(dy, x, scale, rsm, rsv, epsilon=eps, dtype=dtype)
     assert_close(to_np(grad.x_backprop, dtype), rdx, dtype, 1e-2, "x_backprop")
     assert_close(grad.scale_backprop.cpu().numpy(), rsb, "float32", STAT_TOL, "scale_backprop")
     assert_close(grad.offset_backprop.cpu().numpy(), rob, "float32", STAT_TOL, "offset_backprop")
 
 
-def test_largest_shape_invariants(dev):
-    """[256,56,56,256] f16 (cfg2's largest): size-independent properties.
-    Per channel: mean(y) = offset and var(y) = scale^2 var/(var+eps) (both
-    measured in float64 on the device); y and dx elementwise within 1 ulp of
-    the float32 closed form."""
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_largest_shape_invariants(dev, dtype):
+    """[256,56,56,256] (cfg2's largest) in f16 and bf16: size-independent
+    properties.  Per channel: mean(y) = offset and var(y) = scale^2
+    var/(var+eps) (both measured in float64 on the device); offset_backprop =
+    sum(dy) and scale_backprop = rsqrt(var+eps) * sum(dy*(x-mean)) against
+    float64 sums of the inputs; y and dx elementwise within 1 ulp of the
+    float32 closed form."""
     torch.manual_seed(0)
     shape = (256, 56, 56, 256)
-    x = torch.randn(shape, device=dev).half()
-    dy = torch.randn(shape, device=dev).half()
+    x = torch.randn(shape, device=dev).to(dtype)
+    dy = torch.randn(shape, device=dev).to(dtype)
     scale = torch.rand(256, device=dev) + 0.5
     offset = 0.1 * torch.randn(256, device=dev)
     e = torch.empty(0, device=dev)
@@ -239,17 +270,23 @@ def test_largest_shape_invariants(dev):
     assert torch.allclose(yd.mean(0), offset.double(), atol=2e-3)
     want_var = scale.double() ** 2 * var_ref / (var_ref + eps)
     assert torch.allclose(yd.var(0, unbiased=False), want_var, rtol=2e-3)
+    del yd
     grad = ops.FusedBatchNormGradV3(dy, x, scale, fwd.reserve_space_1, fwd.reserve_space_2,
                                     fwd.reserve_space_3, epsilon=eps)
+    assert ops.fused_batch_norm_last_plan()["dynamic_rows"] > 0
     dyd = dy.double().reshape(-1, 256)
     assert torch.allclose(grad.offset_backprop.double(), dyd.sum(0), rtol=1e-5, atol=1e-2)
+    del dyd
+    rows = xd.shape[0]
+    sbp = bn_scale_backprop_ref64(dy, x, fwd.reserve_space_1, fwd.reserve_space_2, eps, rows,
+                                  256)
+    assert torch.allclose(grad.scale_backprop.double(), sbp, rtol=1e-5, atol=1e-2)
     # Every element of y and dx within 1 ulp of the float32 closed form from
     # the kernel's own statistics, in its operation order.  (sum(dx) = 0 is
     # not a usable check for 16-bit dx: where scale*k is near a short binary
     # fraction, scale*k*dy falls on or halfway between f16 values and the
     # small mean terms bias every rounding the same way - TF-CPU's f16 output
     # does this too, with |sum(dx)| in the hundreds at this size.)
-    rows = xd.shape[0]
     mu, sig = fwd.reserve_space_1, fwd.reserve_space_2
     assert bn_max_ulp(fwd.y, bn_fwd_ref32(x, mu, sig, scale, offset, eps, rows, 256), rows,
                       256) <= 1
@@ -405,3 +442,74 @@ def test_fused_epoch_wrap(tmp_path):
                        text=True, timeout=240)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "wrap ok" in r.stdout
+
+
+_GIVE_UP_SCRIPT = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+import tensorflow_musa_extension_amd as tfma
+ops = tfma.raw_ops
+dev = torch.device("cuda:0")
+torch.manual_seed(8)
+x = torch.randn(16, 14, 14, 256, device=dev).half()
+dy = torch.randn_like(x)
+scale = torch.rand(256, device=dev) + 0.5
+offset = 0.1 * torch.randn(256, device=dev)
+e = torch.empty(0, device=dev)
+
+def fwd():
+    return ops.FusedBatchNormV3(x, scale, offset, e, e, epsilon=1e-3)
+
+def expect_internal(fn, what):
+    try:
+        fn()
+    except tfma.InternalError as err:
+        assert "gave up waiting" in str(err), str(err)
+        print(what, "InternalError:", str(err)[:80], flush=True)
+        return
+    raise AssertionError(what + ": no InternalError")
+
+f = fwd()
+assert ops.last_kernel_name() == "tfma_bn_fwd_fused"
+torch.cuda.synchronize()
+assert torch.isnan(f.y.float()).all() and torch.isnan(f.batch_mean).all()
+assert torch.isnan(f.batch_variance).all()
+# The launch that gave up is reported once, by the next call, which does not launch.
+expect_internal(fwd, "forward after forward")
+f2 = fwd()  # reported already: this one launches (and gives up again)
+torch.cuda.synchronize()
+assert ops.fused_batch_norm_barrier_timed_out()
+expect_internal(lambda: ops.FusedBatchNormGradV3(dy, x, scale, f2.reserve_space_1,
+                                                  f2.reserve_space_2, f2.reserve_space_3,
+                                                  epsilon=1e-3), "grad after forward")
+assert ops.fused_batch_norm_barrier_timed_out(reset=True)
+assert not ops.fused_batch_norm_barrier_timed_out()
+g = ops.FusedBatchNormGradV3(dy, x, scale, f.reserve_space_1, f.reserve_space_2,
+                             f.reserve_space_3, epsilon=1e-3)
+assert ops.last_kernel_name() == "tfma_bn_grad_fused"
+torch.cuda.synchronize()
+assert torch.isnan(g.x_backprop.float()).all() and torch.isnan(g.scale_backprop).all()
+expect_internal(fwd, "forward after grad")
+print("give-up ok", flush=True)
+"""
+
+
+def test_fused_give_up_is_an_error(tmp_path):
+    """A fused launch whose grid-wide wait gives up (forced from the host:
+    TFMA_BN_FORCE_GIVE_UP makes every eager fused launch wait, with a short
+    spin limit, for an epoch no launch publishes - every kernel still exits
+    normally) writes NaN statistics and outputs, and the next FusedBatchNorm
+    call on the device raises InternalError without launching, once per such
+    launch; the diagnostic reports it until reset.  Fresh process, since the
+    hook is read once."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = tmp_path / "give_up.py"
+    script.write_text(_GIVE_UP_SCRIPT)
+    env = dict(os.environ, TFMA_BN_FORCE_GIVE_UP="1")
+    r = subprocess.run([sys.executable, str(script), root], env=env, capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "give-up ok" in r.stdout

@@ -16,7 +16,7 @@ import torch
 import tensorflow_musa_extension_amd as tfma
 from oracle import oracle
 from tests.helpers import (assert_bitwise, assert_close, bn_fwd_ref32, bn_grad_ref32,
-                           bn_max_ulp, to_np)
+                           bn_max_ulp, bn_scale_backprop_ref64, to_np)
 
 pytestmark = pytest.mark.gpu
 ops = tfma.raw_ops
@@ -123,22 +123,25 @@ def _chunked_sums(t, c, fn, rows_per=1 << 20):
     return acc
 
 
-def test_batch_norm_f16_over_2_31(dev):
-    """FusedBatchNormV3 + GradV3 on [1, 8388640, 1, 256] f16 (2,147,491,840
-    elements, 2048 rows per thread in the fused kernel).  Statistics against
-    float64 sums taken on the device in chunks (mean 1e-5 absolute; variance
-    5e-5 relative - each thread sums 2048 rows in float32 before the float64
-    combine; sum(dy) 1e-5 relative + 5e-2).  Every element of y and dx within
-    1 ulp of the float32 closed form evaluated from the kernel's own
-    statistics in the kernel's operation order (the coefficients can differ
-    in their last float32 bit, which moves a rounding tie by one ulp)."""
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_batch_norm_over_2_31(dev, dtype):
+    """FusedBatchNormV3 + GradV3 on [1, 8388640, 1, 256] f16 and bf16
+    (2,147,491,840 elements, 2048 rows per thread in the fused kernel, whose
+    phase 3 hands rows out dynamically).  Statistics against float64 sums
+    taken on the device in chunks (mean 1e-5 absolute; variance 5e-5
+    relative - each thread sums 2048 rows in float32 before the float64
+    combine; sum(dy) and rsqrt(var+eps) * sum(dy*(x-mean)) 1e-5 relative +
+    5e-2).  Every element of y and dx within 1 ulp of the float32 closed form
+    evaluated from the kernel's own statistics in the kernel's operation
+    order (the coefficients can differ in their last float32 bit, which moves
+    a rounding tie by one ulp)."""
     _need(24)
     c, rows = 256, 8388640
     shape = (1, rows, 1, c)
     assert rows * c > BIG
     torch.manual_seed(14)
-    x = torch.randn(shape, device=dev, dtype=torch.float16).add_(0.5)
-    dy = torch.randn(shape, device=dev, dtype=torch.float16)
+    x = torch.randn(shape, device=dev, dtype=dtype).add_(0.5)
+    dy = torch.randn(shape, device=dev, dtype=dtype)
     scale = torch.rand(c, device=dev) + 0.5
     offset = 0.1 * torch.randn(c, device=dev)
     e = torch.empty(0, device=dev)
@@ -157,8 +160,11 @@ def test_batch_norm_f16_over_2_31(dev):
 
     g = ops.FusedBatchNormGradV3(dy, x, scale, mu, sig, f.reserve_space_3, epsilon=eps)
     assert ops.last_kernel_name() == "tfma_bn_grad_fused"
+    assert ops.fused_batch_norm_last_plan()["dynamic_rows"] > 0
     sdy = _chunked_sums(dy, c, lambda a: a)
     assert torch.allclose(g.offset_backprop.double(), sdy, rtol=1e-5, atol=5e-2)
+    sbp = bn_scale_backprop_ref64(dy, x, mu, sig, eps, rows, c)
+    assert torch.allclose(g.scale_backprop.double(), sbp, rtol=1e-5, atol=5e-2)
     ref = bn_grad_ref32(dy, x, scale, mu, sig, g.offset_backprop, g.scale_backprop, eps, rows, c)
     assert bn_max_ulp(g.x_backprop, ref, rows, c) <= 1
 
@@ -211,5 +217,7 @@ def test_batch_norm_wide_channels_group_span(dev, rows, kernel):
     assert ops.last_kernel_name() == f"tfma_bn_grad_{kernel}"
     sdy = _chunked_sums(dy, c, lambda a: a, rows_per=1024)
     assert torch.allclose(g.offset_backprop.double(), sdy, rtol=1e-5, atol=5e-2)
+    sbp = bn_scale_backprop_ref64(dy, x, mu, sig, eps, rows, c, rows_per=1024)
+    assert torch.allclose(g.scale_backprop.double(), sbp, rtol=1e-5, atol=5e-2)
     ref = bn_grad_ref32(dy, x, scale, mu, sig, g.offset_backprop, g.scale_backprop, eps, rows, c)
     assert bn_max_ulp(g.x_backprop, ref, rows, c, rows_per=2048) <= 1
