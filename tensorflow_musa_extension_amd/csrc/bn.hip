@@ -129,15 +129,36 @@ size_t coef_bytes(const BnGeometry& g) {
 
 // ---------------------------------------------------------------------------
 // Shift K of the forward's sums of (x - K) and (x - K)^2: the median of five
-// elements spread over the channel (its elements 0, n/4, n/2, 3n/4, n-1).
-// The variance sum((x-K)^2) - sum(x-K)^2 / n cancels in proportion to
-// ((mean - K) / std)^2, so K must sit near the mean: the channel's first
-// element would do unless it is an outlier (one at 1e3 among N(0,1) values
-// put the float32 statistics off by 1e-4); the median of five stays within a
-// few standard deviations unless three of the five are outliers.  A
-// non-finite median gives K = 0, so infinities and NaNs reach the sums as in
-// an unshifted sum.  Every kernel and the finals compute K with this
-// function from the same five elements, so they agree bit for bit.
+// elements spread over the channel (its elements 0, n/4, n/2, 3n/4, n-1),
+// truncated toward zero to a multiple of a power of two near 1/16 of the
+// samples' spread.  The variance sum((x-K)^2) - sum(x-K)^2 / n cancels in
+// proportion to ((mean - K) / std)^2, so K must sit near the mean: the
+// channel's first element would do unless it is an outlier (one at 1e3 among
+// N(0,1) values put the float32 statistics off by 1e-4); the median of five
+// stays within a few standard deviations unless three of the five are
+// outliers, and the truncation moves it by less than 1/16 of the spread.
+// The truncation keeps K on a grid no finer than the data's own: a median
+// near zero (|K| ~ 1e-3 among N(0,1) half values) carries bits far below the
+// data's quantum, every term x - K then carries those same bits, and the
+// float32 running sums round them the same way at every add - a bias that
+// put the mean of [256,56,56,256] half data off by 1e-7 (5e-5 of its largest
+// value); on the coarse grid the terms add exactly.  A non-finite median
+// gives K = 0, so infinities and NaNs reach the sums as in an unshifted sum.
+// Every kernel and the finals compute K with these functions from the same
+// five elements, so they agree bit for bit.
+__device__ inline float coarse_shift(float k, float spread) {
+  if (!(spread > 0.f) || !__builtin_isfinite(spread)) return k;
+  const int es = static_cast<int>((__builtin_bit_cast(uint32_t, spread) >> 23) & 0xffu);
+  uint32_t kb = __builtin_bit_cast(uint32_t, k);
+  int ek = static_cast<int>((kb >> 23) & 0xffu);
+  if (ek == 0) ek = 1;  // subnormal: same bit weights as exponent field 1
+  // Clear the mantissa bits worth less than 2^(es - 4 - 127).
+  const int drop = (es - 4) - ek + 23;
+  if (drop <= 0) return k;
+  if (drop >= 24) return __builtin_bit_cast(float, kb & 0x80000000u);
+  kb &= ~((1u << drop) - 1u);
+  return __builtin_bit_cast(float, kb);
+}
 // ---------------------------------------------------------------------------
 __device__ inline void cmp_swap(float& lo, float& hi) {
   const float a = fminf(lo, hi), b = fmaxf(lo, hi);
@@ -156,7 +177,7 @@ __device__ inline float shift_of(float (&v)[5]) {
   cmp_swap(v[1], v[4]);
   cmp_swap(v[1], v[3]);
   cmp_swap(v[1], v[2]);
-  return __builtin_isfinite(v[2]) ? v[2] : 0.f;
+  return __builtin_isfinite(v[2]) ? coarse_shift(v[2], v[3] - v[1]) : 0.f;
 }
 
 // The shifts of the VEC channels of five sample vectors (the fused kernel's
@@ -206,8 +227,10 @@ __device__ inline void shift_words<TF16>(const uint4 (&kw)[5], float (&k)[8]) {
     cmp_swap2(v[1][w], v[3][w]);
     cmp_swap2(v[1][w], v[2][w]);
     const float lo = static_cast<float>(v[2][w].x), hi = static_cast<float>(v[2][w].y);
-    k[2 * w] = __builtin_isfinite(lo) ? lo : 0.f;
-    k[2 * w + 1] = __builtin_isfinite(hi) ? hi : 0.f;
+    const float slo = static_cast<float>(v[3][w].x) - static_cast<float>(v[1][w].x);
+    const float shi = static_cast<float>(v[3][w].y) - static_cast<float>(v[1][w].y);
+    k[2 * w] = __builtin_isfinite(lo) ? coarse_shift(lo, slo) : 0.f;
+    k[2 * w + 1] = __builtin_isfinite(hi) ? coarse_shift(hi, shi) : 0.f;
   }
 }
 
@@ -656,7 +679,7 @@ constexpr int64_t kMaxEpochGroups = 64 * kEpochPerLane;
 // 2-3 more resident rows per type.
 template <class Tr> struct Resident {
   static constexpr bool kOpaqueFwd = false, kOpaqueGrad = true;
-  static constexpr int kRegFwd = 30, kRegGrad = 13, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kRegFwd = 29, kRegGrad = 13, kLdsFwd = 18, kLdsGrad = 9;
   static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 0, kPbFwd = 0, kPaGrad = 0, kPbGrad = 0;
 };

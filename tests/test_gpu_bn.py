@@ -251,7 +251,7 @@ def test_largest_shape_invariants(dev, dtype):
     var/(var+eps) (both measured in float64 on the device); offset_backprop =
     sum(dy) and scale_backprop = rsqrt(var+eps) * sum(dy*(x-mean)) against
     float64 sums of the inputs; y and dx elementwise within 1 ulp of the
-    float32 closed form."""
+    float32 closed form (or 1e-6: the float32 precision of its terms)."""
     torch.manual_seed(0)
     shape = (256, 56, 56, 256)
     x = torch.randn(shape, device=dev).to(dtype)
