@@ -254,6 +254,20 @@ int TFMA_BiasAddGrad(void* stream, const TFMA_Tensor* out_backprop, const char* 
                      TFMA_Tensor* output, void* workspace, size_t workspace_bytes,
                      TFMA_Status* status);
 
+/* Allocation-free BiasAddGrad.  No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same inputs, result and
+ * errors as TFMA_BiasAddGrad, but the per-group partials live in a static
+ * device array of the library (4 MiB per GPU, held until the process
+ * ends) instead of a caller workspace; the call allocates nothing.  An input
+ * whose partials need more (TFMA_BiasAddGradWorkspaceBytes > 4 MiB, i.e.
+ * more than about a million channels) is INVALID_ARGUMENT.  All calls on one
+ * GPU share that array: calls that overlap on one GPU (concurrent streams)
+ * race and must be serialized by the caller. */
+int TFMA_BiasAddGradNoAlloc(void* stream, const TFMA_Tensor* out_backprop,
+                            const char* data_format, TFMA_Tensor* output,
+                            TFMA_Status* status);
+
 /* Fused Relu(BiasAdd(value, bias)).  No live reference op: the reference
  * runs BiasAdd then Relu (musa_biasadd_op.cc:10-70, musa_relu_op.cc:10-62);
  * its only fused kernel, BiasAddReluKernel

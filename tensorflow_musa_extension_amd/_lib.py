@@ -92,6 +92,7 @@ SIGNATURES = {
     "TFMA_ReluGrad": [_vp, _T, _T, _T, _S],
     "TFMA_BiasAddGradWorkspaceBytes": [_T, _cs, ctypes.POINTER(_sz), _S],
     "TFMA_BiasAddGrad": [_vp, _T, _cs, _T, _vp, _sz, _S],
+    "TFMA_BiasAddGradNoAlloc": [_vp, _T, _cs, _T, _S],
     "TFMA_MusaBiasAddRelu": [_vp, _T, _T, _cs, _T, _S],
     "TFMA_MusaAddV2Relu": [_vp, _T, _T, _T, _S],
     "TFMA_MusaShiftedAffineMap": [_vp, _T, _T, _T, _T, _S],

@@ -15,6 +15,8 @@
 //   stage 2: per channel, the partials in group order, cast to T.
 // Every sum runs in a fixed order, so results are deterministic.  Memory:
 // one read of x (s*E bytes), partials of G*C accumulators.
+#include <mutex>
+
 #include "device_util.h"
 #include "tfma_internal.h"
 
@@ -277,7 +279,33 @@ size_t acc_bytes(int dt) {
   return (dt == TFMA_DOUBLE || dt == TFMA_INT64) ? 8 : 4;
 }
 
+// Scratch of the allocation-free BiasAddGrad: the per-group partials live in
+// this file-scope array instead of a caller workspace.  Each device holds its
+// own copy for the life of the process.  In host code `bag_scratch` names a
+// host-side stand-in, not device memory: kernels get the device address that
+// hipGetSymbolAddress returns for the current device (BiasAddGradScratch).
+static __device__ __align__(256) unsigned char bag_scratch[kBiasAddGradScratchBytes];
+
 }  // namespace
+
+hipError_t BiasAddGradScratch(void** ptr) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {nullptr};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(bag_scratch));
+    if (e != hipSuccess) return e;
+    addr[dev] = p;
+  }
+  *ptr = addr[dev];
+  return hipSuccess;
+}
 
 size_t BiasAddGradWorkspaceBytes(int dt, int64_t outer, int64_t c, int64_t inner, int esize) {
   const BagPlan p = make_bag_plan(outer, c, inner, esize, true);

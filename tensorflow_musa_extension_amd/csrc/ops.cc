@@ -1317,6 +1317,45 @@ int TFMA_BiasAddGrad(void* stream, const TFMA_Tensor* out_backprop, const char* 
                     "BiasAddGrad");
 }
 
+int TFMA_BiasAddGradNoAlloc(void* stream, const TFMA_Tensor* out_backprop,
+                            const char* data_format, TFMA_Tensor* output, TFMA_Status* status) {
+  int64_t outer = 0, c = 0, inner = 0;
+  if (const int rc = bias_grad_geometry(out_backprop, data_format, output, &outer, &c, &inner,
+                                        status))
+    return rc;
+  if (c == 0) return ok(status);
+  if (!output->data) return set_status(status, TFMA_INVALID_ARGUMENT, "BiasAddGrad: null output");
+  const int es = elem_size(out_backprop->dtype);
+  hipStream_t strm = as_stream(stream);
+  if (out_backprop->ndims == 1) {
+    if (!out_backprop->data)
+      return set_status(status, TFMA_INVALID_ARGUMENT, "BiasAddGrad: null input");
+    return hip_status(status,
+                      hipMemcpyAsync(output->data, out_backprop->data, static_cast<size_t>(c) * es,
+                                     hipMemcpyDeviceToDevice, strm),
+                      "BiasAddGrad");
+  }
+  if (outer == 0 || inner == 0)
+    return hip_status(status, LaunchZeroBytes(output->data, c * es, strm), "BiasAddGrad");
+  if (!out_backprop->data)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "BiasAddGrad: null input");
+  const size_t need = BiasAddGradWorkspaceBytes(out_backprop->dtype, outer, c, inner, es);
+  if (need > kBiasAddGradScratchBytes)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "BiasAddGradNoAlloc: this input needs %zu bytes of scratch, more than the "
+                      "library's static %zu bytes; use TFMA_BiasAddGrad with a workspace",
+                      need, kBiasAddGradScratchBytes);
+  void* scratch = nullptr;
+  const hipError_t e = BiasAddGradScratch(&scratch);
+  if (e != hipSuccess)
+    return set_status(status, TFMA_INTERNAL, "BiasAddGradNoAlloc: scratch address: %s",
+                      hipGetErrorString(e));
+  return hip_status(status,
+                    LaunchBiasAddGrad(out_backprop->dtype, out_backprop->data, outer, c, inner,
+                                      output->data, scratch, strm),
+                    "BiasAddGrad");
+}
+
 int TFMA_AddV2(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* y, TFMA_Tensor* z,
                TFMA_Status* status) {
   const TFMA_Tensor* ins[2] = {x, y};

@@ -87,6 +87,11 @@ hipError_t LaunchGroupedApplyAdam(DType t, DType tg, const AdamTensorEntry* dev_
 size_t BiasAddGradWorkspaceBytes(int dt, int64_t outer, int64_t c, int64_t inner, int esize);
 hipError_t LaunchBiasAddGrad(int dt, const void* x, int64_t outer, int64_t c, int64_t inner,
                              void* out, void* workspace, hipStream_t stream);
+// Allocation-free BiasAddGrad: device address, on the current device, of the
+// library's static scratch of kBiasAddGradScratchBytes (resolved with
+// hipGetSymbolAddress on the device's first call, then cached per device).
+constexpr size_t kBiasAddGradScratchBytes = size_t(4) << 20;
+hipError_t BiasAddGradScratch(void** ptr);
 // Zero-fills n bytes with a kernel (capturable, unlike a memset node).
 hipError_t LaunchZeroBytes(void* p, int64_t n, hipStream_t stream);
 

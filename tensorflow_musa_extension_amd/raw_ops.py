@@ -353,6 +353,16 @@ def BiasAddGrad(out_backprop, data_format="NHWC", out=None, workspace=None):
     return out
 
 
+def bias_add_grad_no_alloc(out_backprop, out, data_format="NHWC"):
+    """BiasAddGrad through the allocation-free entry point
+    (TFMA_BiasAddGradNoAlloc): the caller passes the output; the library's
+    static per-GPU scratch holds the partials, so nothing is allocated."""
+    dx, do = _desc(out_backprop, "out_backprop"), _desc(out, "output")
+    _call("TFMA_BiasAddGradNoAlloc", _stream(out_backprop), _ref(dx), _fmt(data_format),
+          _ref(do))
+    return out
+
+
 def AddV2(x, y, out=None):
     return _binary("TFMA_AddV2", x, y, out)
 
