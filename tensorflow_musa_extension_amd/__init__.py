@@ -9,7 +9,7 @@ libtfma.so binds to (both carry the soname libamdhip64.so.7).
 """
 import torch  # noqa: F401  (loads the process's HIP runtime)
 
-from . import _lib, errors, graph_rewrite, raw_ops, stream_executor  # noqa: F401
+from . import _lib, errors, graph_rewrite, raw_ops, stream_executor, tf_plugin  # noqa: F401
 from .errors import (FailedPreconditionError, InternalError,  # noqa: F401
                      InvalidArgumentError, OpError, UnimplementedError)
 
