@@ -5,7 +5,8 @@ Headline workload: FusedBatchNormV3 forward +
 FusedBatchNormGradV3, NHWC, is_training, epsilon 1.001e-5, at the four
 ResNet-50 stage shapes [256,56,56,256], [256,28,28,512], [256,14,14,1024],
 [256,7,7,2048], each in float16 and bfloat16 (float32 scale/offset/stats).
-One step = fwd + grad for all 8 (dtype, shape) pairs.  Inputs are synthetic
+One step = the 8 forwards, then the 8 grads in the same order (no grad finds
+its x still in the Infinity Cache from its forward).  Inputs are synthetic
 (x, dy ~ N(0,1); scale ~ U(0.5,1.5); offset ~ N(0,0.1)), resident in HBM
 before the timed region.
 
@@ -18,17 +19,25 @@ roofline: the dominant kernel (tfma_bn_grad_fused: reads x, dy, writes dx,
         of its launches in the last --trace-steps steps of the timed region
         (the events are the dispatch's own start/stop events; each costs
         ~5 us of idle GPU between kernels, so only those steps carry them).
-cpu_baseline: the TF-CPU restatement (oracle/, C + OpenMP) on the same
-        BN workload (both dtypes, four shapes), repeated for >= 10 s on up to
-        16 host cores.
-components: cfg1 (FusedBatchNormV3 forward, f32 [32,56,56,64]) and the
+cpu_baseline: the TF-CPU restatement (oracle/, C + OpenMP; TensorFlow is
+        not installed) on the same BN workload (both dtypes, four shapes),
+        repeated for >= 10 s on the box's CPU share (at most 16 threads;
+        lscpu model and os.cpu_count() reported), and under "components" the
+        same for Adam cfg3, a stated sample of cfg5 and the cfg4 chains.
+components: cfg1 (FusedBatchNormV3 forward, f32 [32,56,56,64]), BN on the
+        split path (NCHW training fwd and grad, NHWC inference), and the
         other kernels (Adam, mixed-precision Adam, grouped Adam at
         the ResNet-50 and 1.31e9-parameter configs, the elementwise chains,
         ReluGrad, BiasAddGrad) at their config shapes, each rep timed with HIP
         events after a 1 GiB read that evicts the Infinity Cache (GB/s, % of
         peak, Gelem/s), then the same reps again with events attached to the
         kernels' own dispatches (kernel_ms, kernel_GB/s, kernel_pct_peak: the
-        kernel's duration without the dispatch and event overhead).
+        kernel's duration without the dispatch and event overhead);
+        traffic_ratio = counter-measured HBM bytes per rep (committed
+        profiles/pmc_traffic_components.txt) / algorithmic bytes.
+--profile-components: each component once, then 3 times after a cache
+        flush, printing a PROFILE_MANIFEST line that attributes a rocprofv3
+        --pmc run's dispatches to components (no JSON line).
 host_path: pageable host<->device copies (256 MiB) through the library's
         staged path, beside the HIP runtime's own pageable copy and a pinned
         copy (the PCIe ceiling), in GB/s.
@@ -93,22 +102,25 @@ def parse():
     p.add_argument("--trace-steps", type=int, default=4,
                    help="timed steps (the last ones) whose launches of --trace carry timing "
                         "events; each such launch costs ~5 us of idle GPU between kernels")
+    p.add_argument("--profile-components", action="store_true",
+                   help="run each component 1 + 3 times (cache flushed before each) and print "
+                        "a PROFILE_MANIFEST line for attributing rocprofv3 counters; no JSON")
     p.add_argument("--calibrate", action="store_true",
                    help="also run a plain 256 MiB device copy (torch copy_) so a "
                         "rocprofv3 --pmc run can scale FETCH_SIZE/WRITE_SIZE")
     return p.parse_args()
 
 
-def read_traffic(kernel):
-    """Counter-derived HBM bytes per launch of `kernel` from the committed
-    rocprofv3 --pmc summary (profiles/pmc_traffic.txt, lines
-    "<kernel> hbm_bytes_per_launch=<N>"), or None."""
-    path = os.path.join(ROOT, "profiles", "pmc_traffic.txt")
+def read_traffic(key, summary="pmc_traffic.txt"):
+    """Counter-derived HBM bytes per launch (or per component rep) of `key`
+    from a committed rocprofv3 --pmc summary under profiles/ (lines
+    "<key> hbm_bytes_per_launch=<N>"), or None."""
+    path = os.path.join(ROOT, "profiles", summary)
     try:
         with open(path) as f:
             for line in f:
                 parts = line.split()
-                if len(parts) == 2 and parts[0] == kernel and parts[1].startswith(
+                if len(parts) == 2 and parts[0] == key and parts[1].startswith(
                         "hbm_bytes_per_launch="):
                     return int(parts[1].split("=", 1)[1])
     except (OSError, ValueError):
@@ -143,9 +155,12 @@ def bn_workload(torch, ops, dev):
             fwds.append(fwd)
             grads.append(grad)
             pairs.append((dt, shape, x.numel(), x.element_size()))
-    # A training step runs every forward, then the grads in reverse order, so
-    # a grad never finds its x still cache-warm from its own forward.
-    return fwds + grads[::-1], pairs
+    # A training step runs every forward, then every grad in the same order:
+    # the first grad's x was read by the first forward, with all the other
+    # forwards' 2.4 GB since, and each later grad's x has at least the
+    # earlier grads' traffic since its forward - more than the 256 MB
+    # Infinity Cache holds - so no grad finds its x cache-warm.
+    return fwds + grads, pairs
 
 
 def time_calls(torch, calls, steps, warmup, flush=None):
@@ -179,33 +194,21 @@ def time_calls(torch, calls, steps, warmup, flush=None):
     return sum(a.elapsed_time(b) for a, b in pairs) / steps
 
 
-def components(torch, ops, dev):
-    """Adam (cfg3), grouped Adam (cfg3b), elementwise chains (cfg4)."""
-    out = {}
+class Component:
+    """One measured component: `calls` (bound ops run in order per rep),
+    its algorithmic bytes and elements per rep, and the trace-name substring
+    of the library kernels it launches."""
+
+    def __init__(self, name, calls, nbytes, elems, kernel, reps=20, note=None):
+        self.name, self.calls, self.nbytes, self.elems = name, calls, nbytes, elems
+        self.kernel, self.reps, self.note = kernel, reps, note
+
+
+def component_groups(torch, ops, dev):
+    """Yields the components in groups; each group's tensors are freed
+    before the next is built (cfg5 alone holds 21 GB of state)."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
-    reps, warm = 20, 3
-    flush = torch.ones(1 << 28, device=dev)  # 1 GiB, read between reps
-
-    def rate(calls, nbytes, elems, kernel, reps_=reps):
-        """Wall time per call (HIP events around it, which includes the
-        dispatch and event overhead), then, in a second pass, the kernel time
-        per call from events attached to the library's own dispatches of
-        `kernel` (summed over its launches in the call)."""
-        ms = time_calls(torch, calls, reps_, warm, flush=flush)
-        gbps = nbytes / (ms / 1e3) / 1e9
-        ops.trace_enable(kernel)
-        time_calls(torch, calls, reps_, 0, flush=flush)
-        kms, launches = ops.trace_read()
-        ops.trace_enable(None)
-        kms = kms / reps_
-        kgbps = nbytes / (kms / 1e3) / 1e9 if kms else None
-        return {"ms": round(ms, 4), "GB/s": round(gbps, 1),
-                "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
-                "Gelem/s": round(elems / (ms / 1e3) / 1e9, 2),
-                "kernel_ms": round(kms, 4) if kms else None,
-                "kernel_GB/s": round(kgbps, 1) if kgbps else None,
-                "kernel_pct_peak": round(100 * kgbps / PEAK_GBPS, 1) if kgbps else None}
 
     # cfg1: FusedBatchNormV3 training forward, NHWC f32 x[32,56,56,64]
     # (the reference's CPU-runnable case; epsilon 1e-3), 2*s*E bytes.
@@ -216,9 +219,40 @@ def components(torch, ops, dev):
     ws1 = torch.empty(ops.fused_batch_norm_workspace_bytes(x1), dtype=torch.uint8, device=dev)
     bn1 = ops.bind(ops.FusedBatchNormV3, x1, sc1, of1, e1, e1, epsilon=1e-3, data_format="NHWC",
                    is_training=True, workspace=ws1)
-    out["bn_fwd_f32_cfg1_32x56x56x64"] = rate([bn1], 8 * x1.numel(), x1.numel(),
-                                              "tfma_bn_fwd")
+    yield [Component("bn_fwd_f32_cfg1_32x56x56x64", [bn1], 8 * x1.numel(), x1.numel(),
+                     "tfma_bn_fwd")]
     del x1, bn1, ws1
+
+    # BatchNorm on the 3-kernel split path (reduce, finalize, apply): NCHW
+    # training (fwd reads x twice: 3sE; grad reads x and dy twice: 5sE of
+    # traffic against the 2sE / 3sE algorithmic bytes) and NHWC inference
+    # (one read of x from running statistics: 2sE).
+    xn = torch.randn(256, 512, 28, 28, generator=gen, device=dev).half()
+    dyn = torch.randn(256, 512, 28, 28, generator=gen, device=dev).half()
+    scn = torch.rand(512, generator=gen, device=dev) + 0.5
+    ofn = 0.1 * torch.randn(512, generator=gen, device=dev)
+    wsn = torch.empty(ops.fused_batch_norm_workspace_bytes(xn, "NCHW"), dtype=torch.uint8,
+                      device=dev)
+    fn_ = ops.bind(ops.FusedBatchNormV3, xn, scn, ofn, e1, e1, epsilon=EPS, data_format="NCHW",
+                   is_training=True, workspace=wsn)
+    rn = fn_.result
+    gn = ops.bind(ops.FusedBatchNormGradV3, dyn, xn, scn, rn.reserve_space_1, rn.reserve_space_2,
+                  rn.reserve_space_3, epsilon=EPS, data_format="NCHW", is_training=True,
+                  workspace=wsn)
+    En = xn.numel()
+    xi = torch.randn(256, 56, 56, 256, generator=gen, device=dev).half()
+    rm = 0.1 * torch.randn(256, generator=gen, device=dev)
+    rv = torch.rand(256, generator=gen, device=dev) + 0.5
+    wsi = torch.empty(ops.fused_batch_norm_workspace_bytes(xi), dtype=torch.uint8, device=dev)
+    bi = ops.bind(ops.FusedBatchNormV3, xi, scn[:256].contiguous(), ofn[:256].contiguous(), rm,
+                  rv, epsilon=EPS, data_format="NHWC", is_training=False, workspace=wsi)
+    yield [Component("bn_fwd_f16_nchw_256x512x28x28", [fn_], 4 * En, En, "tfma_bn_fwd",
+                     note="split path, traffic 3sE"),
+           Component("bn_grad_f16_nchw_256x512x28x28", [gn], 6 * En, En, "tfma_bn_grad",
+                     note="split path, traffic 5sE"),
+           Component("bn_fwd_inference_f16_256x56x56x256", [bi], 4 * xi.numel(), xi.numel(),
+                     "tfma_bn_fwd", note="coefficients from running statistics, one pass")]
+    del xn, dyn, fn_, gn, wsn, xi, wsi, bi
 
     n = 25_600_000
     var = 0.02 * torch.randn(n, generator=gen, device=dev)
@@ -226,14 +260,10 @@ def components(torch, ops, dev):
     v = torch.zeros(n, device=dev)
     g = 1e-3 * torch.randn(n, generator=gen, device=dev)
     adam = ops.bind(ops.ResourceApplyAdam, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7, g)
-    out["adam_f32_25.6M"] = rate([adam], 28 * n, n, "tfma_adam_flat")
     # Mixed precision (fp32 state, bf16 grad): 24 B of state + 2 B of grad.
     gb = g.to(torch.bfloat16)
     mixed = ops.bind(ops.MusaResourceApplyAdamMixed, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999,
                      1e-7, gb)
-    out["adam_mixed_bf16grad_25.6M"] = rate([mixed], 26 * n, n, "tfma_adam_flat")
-    del gb
-
     shapes = resnet50_shapes()
     tv = [0.02 * torch.randn(s, generator=gen, device=dev) for s in shapes]
     tm = [torch.zeros(s, device=dev) for s in shapes]
@@ -242,9 +272,11 @@ def components(torch, ops, dev):
     total = sum(t.numel() for t in tv)
     grouped = ops.bind(ops.MusaGroupedResourceApplyAdam, tv, tm, tvv, tg, 0.9, 0.999, 1e-3, 0.9,
                        0.999, 1e-7)
-    out["grouped_adam_f32_resnet50_161"] = rate([grouped], 28 * total, total,
-                                                "tfma_adam_grouped")
-    del var, m, v, g, tv, tm, tvv, tg, grouped, adam, mixed
+    yield [Component("adam_f32_25.6M", [adam], 28 * n, n, "tfma_adam_flat"),
+           Component("adam_mixed_bf16grad_25.6M", [mixed], 26 * n, n, "tfma_adam_flat"),
+           Component("grouped_adam_f32_resnet50_161", [grouped], 28 * total, total,
+                     "tfma_adam_grouped")]
+    del var, m, v, g, gb, tv, tm, tvv, tg, grouped, adam, mixed
 
     # cfg5: 1.31B parameters in 145 tensors, 21 GB of state resident.
     shapes5 = cfg5_shapes()
@@ -255,8 +287,8 @@ def components(torch, ops, dev):
     total5 = sum(t.numel() for t in tv)
     grouped5 = ops.bind(ops.MusaGroupedResourceApplyAdam, tv, tm, tvv, tg, 0.9, 0.999, 1e-3,
                         0.9, 0.999, 1e-7)
-    out["grouped_adam_f32_cfg5_145"] = rate([grouped5], 28 * total5, total5,
-                                            "tfma_adam_grouped", reps_=10)
+    yield [Component("grouped_adam_f32_cfg5_145", [grouped5], 28 * total5, total5,
+                     "tfma_adam_grouped", reps=10)]
     del tv, tm, tvv, tg, grouped5
     torch.cuda.empty_cache()
 
@@ -265,33 +297,96 @@ def components(torch, ops, dev):
         x = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
         b = torch.randn(4096, generator=gen, device=dev).to(dt)
         E = x.numel()
-        out[f"bias_add_relu_{name}_8192x4096"] = rate([ops.bind(ops.MusaBiasAddRelu, x, b)],
-                                                      2 * s * E + s * 4096, E, "tfma_ew_add_relu")
-        out[f"add_v2_relu_{name}_8192x4096"] = rate([ops.bind(ops.MusaAddV2Relu, x, b)],
-                                                    2 * s * E + s * 4096, E, "tfma_ew_add_relu")
         a_full = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
         b_full = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
-        out[f"mul_add_full_{name}_8192x4096"] = rate(
-            [ops.bind(ops.MusaShiftedAffineMap, x, a_full, b_full)], 4 * s * E, E,
-            "tfma_ew_mul_add")
-        out[f"mul_add_row_{name}_8192x4096"] = rate(
-            [ops.bind(ops.MusaShiftedAffineMap, x, b, b)], 2 * s * E + 2 * s * 4096, E,
-            "tfma_ew_mul_add")
         xo = torch.randn(8191, 4095, generator=gen, device=dev).to(dt)
         bo = torch.randn(4095, generator=gen, device=dev).to(dt)
-        out[f"bias_add_relu_{name}_8191x4095"] = rate([ops.bind(ops.MusaBiasAddRelu, xo, bo)],
-                                                      2 * s * xo.numel() + s * 4095,
-                                                      xo.numel(), "tfma_ew_add_relu")
-        # The backward side of the chains: ReluGrad (2 reads, 1 write) and
-        # BiasAddGrad (one read of the gradient).
-        out[f"relu_grad_{name}_8192x4096"] = rate([ops.bind(ops.ReluGrad, a_full, x)], 3 * s * E,
-                                                  E, "tfma_ew_relu_grad")
-        out[f"bias_add_grad_{name}_8192x4096"] = rate([ops.bind(ops.BiasAddGrad, a_full)],
-                                                      s * E + s * 4096, E, "tfma_bias_add_grad")
+        yield [
+            Component(f"bias_add_relu_{name}_8192x4096", [ops.bind(ops.MusaBiasAddRelu, x, b)],
+                      2 * s * E + s * 4096, E, "tfma_ew_add_relu"),
+            Component(f"add_v2_relu_{name}_8192x4096", [ops.bind(ops.MusaAddV2Relu, x, b)],
+                      2 * s * E + s * 4096, E, "tfma_ew_add_relu"),
+            Component(f"mul_add_full_{name}_8192x4096",
+                      [ops.bind(ops.MusaShiftedAffineMap, x, a_full, b_full)], 4 * s * E, E,
+                      "tfma_ew_mul_add"),
+            Component(f"mul_add_row_{name}_8192x4096",
+                      [ops.bind(ops.MusaShiftedAffineMap, x, b, b)], 2 * s * E + 2 * s * 4096,
+                      E, "tfma_ew_mul_add"),
+            Component(f"bias_add_relu_{name}_8191x4095",
+                      [ops.bind(ops.MusaBiasAddRelu, xo, bo)], 2 * s * xo.numel() + s * 4095,
+                      xo.numel(), "tfma_ew_add_relu"),
+            # The backward side of the chains: ReluGrad (2 reads, 1 write)
+            # and BiasAddGrad (one read of the gradient).
+            Component(f"relu_grad_{name}_8192x4096", [ops.bind(ops.ReluGrad, a_full, x)],
+                      3 * s * E, E, "tfma_ew_relu_grad"),
+            Component(f"bias_add_grad_{name}_8192x4096", [ops.bind(ops.BiasAddGrad, a_full)],
+                      s * E + s * 4096, E, "tfma_bias_add_grad"),
+        ]
         del x, b, a_full, b_full, xo, bo
+
+
+def components(torch, ops, dev):
+    """Every component at its config shape: wall time per rep (HIP events
+    around it, dispatch included) after a 1 GiB read that evicts the
+    Infinity Cache, then the kernel time from events on the library's own
+    dispatches in a second pass."""
+    out = {}
+    warm = 3
+    flush = torch.ones(1 << 28, device=dev)  # 1 GiB, read between reps
+    for group in component_groups(torch, ops, dev):
+        for c in group:
+            ms = time_calls(torch, c.calls, c.reps, warm, flush=flush)
+            gbps = c.nbytes / (ms / 1e3) / 1e9
+            ops.trace_enable(c.kernel)
+            time_calls(torch, c.calls, c.reps, 0, flush=flush)
+            kms, _ = ops.trace_read()
+            ops.trace_enable(None)
+            kms = kms / c.reps
+            kgbps = c.nbytes / (kms / 1e3) / 1e9 if kms else None
+            r = {"ms": round(ms, 4), "GB/s": round(gbps, 1),
+                 "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
+                 "Gelem/s": round(c.elems / (ms / 1e3) / 1e9, 2),
+                 "kernel_ms": round(kms, 4) if kms else None,
+                 "kernel_GB/s": round(kgbps, 1) if kgbps else None,
+                 "kernel_pct_peak": round(100 * kgbps / PEAK_GBPS, 1) if kgbps else None}
+            traffic = read_traffic(c.name, "pmc_traffic_components.txt")
+            if traffic:
+                r["traffic_ratio"] = round(traffic / c.nbytes, 3)
+            if c.note:
+                r["note"] = c.note
+            out[c.name] = r
+        del group
     torch.cuda.synchronize()
     del flush
     return out
+
+
+def profile_components(torch, ops, dev, reps=3):
+    """Runs every component once to warm up, then `reps` times, each after
+    the 1 GiB cache flush, and prints one PROFILE_MANIFEST JSON line: per
+    component (in launch order) the library dispatches per rep, so a
+    rocprofv3 --pmc run of this command attributes its per-dispatch counters
+    to the components (the warm-up rep's dispatches come first)."""
+    manifest = []
+    flush = torch.ones(1 << 28, device=dev)
+    for group in component_groups(torch, ops, dev):
+        for c in group:
+            torch.cuda.synchronize()
+            ops.trace_enable("tfma_")
+            for call in c.calls:
+                call()
+            torch.cuda.synchronize()
+            _, launches = ops.trace_read()
+            ops.trace_enable(None)
+            for _ in range(reps):
+                flush.sum()
+                for call in c.calls:
+                    call()
+            torch.cuda.synchronize()
+            manifest.append({"name": c.name, "dispatches_per_rep": launches, "reps": reps,
+                             "warmup_reps": 1, "algorithmic_bytes": c.nbytes})
+        del group
+    print("PROFILE_MANIFEST " + json.dumps(manifest), flush=True)
 
 
 def host_path(torch, tfma, dev, mib=256, reps=5):
@@ -330,12 +425,56 @@ def host_path(torch, tfma, dev, mib=256, reps=5):
     return r
 
 
-def cpu_baseline(torch, dev, min_seconds=10.0):
-    """TF-CPU restatement (oracle, C + OpenMP on up to 16 host cores) on the
-    same workload: FusedBatchNormV3 + FusedBatchNormGradV3 over the four cfg2
-    shapes in float16 and bfloat16, repeated until at least `min_seconds` of
-    CPU time.  Inputs are drawn on the GPU and copied to host memory before
-    timing."""
+def cpu_model():
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def _host(torch, t):
+    """Device tensor -> numpy array (bfloat16 as uint16 bits)."""
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view("uint16")
+    return t.cpu().numpy()
+
+
+def _timed(fn, min_seconds):
+    """Runs fn() until at least min_seconds have passed; returns (calls,
+    seconds)."""
+    calls, secs = 0, 0.0
+    while calls == 0 or secs < min_seconds:
+        t = time.perf_counter()
+        fn()
+        secs += time.perf_counter() - t
+        calls += 1
+    return calls, secs
+
+
+def cpu_baseline(torch, dev, min_seconds=10.0, component_seconds=1.5):
+    """The TF-CPU restatement (oracle/: C + OpenMP, on the GPU box's CPU share
+    of at most 16 threads), timed on the host in the same run.  Headline: the
+    bench step's BN workload (FusedBatchNormV3 + GradV3 over the four cfg2
+    shapes in float16 and bfloat16) for at least `min_seconds`.  Components:
+    Adam cfg3 (25.6M f32, 10 steps), a sample of cfg5 (its [50304,2048]
+    embedding and the first layer's six tensors, 153M parameters - the
+    1.31B-parameter state would need 21 GB of host memory per pass), and the
+    cfg4 chains at [8192,4096], each for at least `component_seconds`.
+    Inputs are drawn on the GPU and copied to host memory before timing;
+    GB/s counts the same algorithmic bytes as the GPU figures."""
     import numpy as np
     sys.path.insert(0, ROOT)
     from oracle import oracle
@@ -348,13 +487,8 @@ def cpu_baseline(torch, dev, min_seconds=10.0):
         for tdt, name in ((torch.float16, "float16"), (torch.bfloat16, "bfloat16")):
             for shape in SHAPES:
                 c = shape[-1]
-                x = torch.randn(shape, generator=gen, device=dev).to(tdt)
-                dy = torch.randn(shape, generator=gen, device=dev).to(tdt)
-                if tdt == torch.bfloat16:
-                    x = x.view(torch.int16).cpu().numpy().view(np.uint16)
-                    dy = dy.view(torch.int16).cpu().numpy().view(np.uint16)
-                else:
-                    x, dy = x.cpu().numpy(), dy.cpu().numpy()
+                x = _host(torch, torch.randn(shape, generator=gen, device=dev).to(tdt))
+                dy = _host(torch, torch.randn(shape, generator=gen, device=dev).to(tdt))
                 scale = np.random.default_rng(0).uniform(0.5, 1.5, c).astype(np.float32)
                 offset = np.zeros(c, np.float32)
                 t = time.perf_counter()
@@ -365,10 +499,79 @@ def cpu_baseline(torch, dev, min_seconds=10.0):
                 del x, dy
         passes += 1
     gbps = total_bytes / secs / 1e9
+
+    comps = {}
+
+    def rate(name, nbytes, fn, sample):
+        calls, t = _timed(fn, component_seconds)
+        comps[name] = {"GB/s": round(nbytes * calls / t / 1e9, 3), "seconds": round(t, 2),
+                       "sample": sample}
+
+    # Adam cfg3: 10 steps with the step's beta powers.
+    n = 25_600_000
+    var = _host(torch, 0.02 * torch.randn(n, generator=gen, device=dev))
+    m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    g = _host(torch, 1e-3 * torch.randn(n, generator=gen, device=dev))
+
+    def ten_steps():
+        for t_ in range(1, 11):
+            oracle.adam(var, m, v, g, np.float32(0.9) ** t_, np.float32(0.999) ** t_, 1e-3, 0.9,
+                        0.999, 1e-7)
+
+    rate("adam_f32_25.6M", 10 * 28 * n, ten_steps, "10 steps (t = 1..10) of 25.6M f32")
+    del var, m, v, g
+    # cfg5 sample: the embedding and layer 0's six tensors.
+    shapes5 = cfg5_shapes()
+    sample = [shapes5[-1]] + shapes5[:6]
+    st = [[_host(torch, 0.02 * torch.randn(sh, generator=gen, device=dev)),
+           _host(torch, (1e-4 * torch.randn(sh, generator=gen, device=dev)).abs_()),
+           _host(torch, (1e-4 * torch.randn(sh, generator=gen, device=dev)).abs_()),
+           _host(torch, 1e-3 * torch.randn(sh, generator=gen, device=dev))] for sh in sample]
+    n5 = sum(a[0].size for a in st)
+
+    def cfg5_step():
+        for a in st:
+            oracle.adam(a[0], a[1], a[2], a[3], 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7)
+
+    rate("grouped_adam_f32_cfg5_145", 28 * n5, cfg5_step,
+         f"one step over {len(sample)} of the 145 tensors ({n5} parameters: the [50304,2048] "
+         "embedding and the first layer's six), repeated")
+    del st
+    # cfg4 chains.
+    for tdt, name, odt in ((torch.float32, "f32", "float32"), (torch.float16, "f16", "float16")):
+        es = 4 if tdt == torch.float32 else 2
+        x = _host(torch, torch.randn(8192, 4096, generator=gen, device=dev).to(tdt))
+        b = _host(torch, torch.randn(4096, generator=gen, device=dev).to(tdt))
+        a = _host(torch, torch.randn(8192, 4096, generator=gen, device=dev).to(tdt))
+        c = _host(torch, torch.randn(8192, 4096, generator=gen, device=dev).to(tdt))
+        E = x.size
+        rate(f"bias_add_relu_{name}_8192x4096", 2 * es * E + es * 4096,
+             lambda: oracle.bias_add(x, b, relu=True, dtype=odt), "one call, repeated")
+        rate(f"add_v2_relu_{name}_8192x4096", 2 * es * E + es * 4096,
+             lambda: oracle.eltwise("add_relu", [x, b], odt), "one call, repeated")
+        rate(f"mul_add_full_{name}_8192x4096", 4 * es * E,
+             lambda: oracle.eltwise("mul_add", [x, a, c], odt), "one call, repeated")
+        rate(f"mul_add_row_{name}_8192x4096", 2 * es * E + 2 * es * 4096,
+             lambda: oracle.eltwise("mul_add", [x, b, b], odt), "one call, repeated")
+        del x, b, a, c
     return {"value": round(gbps, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "label": "TF-CPU restatement, not TF (TensorFlow is not installed)",
+            "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
             "seconds": round(secs, 2),
             "sample": f"{passes} pass(es) of FusedBatchNormV3+GradV3 over the 4 cfg2 shapes in "
-                      "f16 and bf16 (the full bench step); algorithmic bytes / wall time"}
+                      "f16 and bf16 (the full bench step); algorithmic bytes / wall time",
+            "components": comps}
+
+
+def calibrate(torch, dev):
+    """Five plain 256 MiB device copies (torch copy_): the reference reads and
+    writes that scale a rocprofv3 --pmc run's FETCH_SIZE / WRITE_SIZE."""
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 def main():
@@ -385,6 +588,11 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.profile_components:
+        if args.calibrate:
+            calibrate(torch, dev)
+        profile_components(torch, ops, dev)
+        return
 
     calls, pairs = bn_workload(torch, ops, dev)
     bytes_per_step = sum(5 * s * e for _, _, e, s in pairs)
@@ -454,12 +662,7 @@ def main():
         "roofline": roofline,
     }
     if args.calibrate:
-        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        calibrate(torch, dev)
     if not args.no_components:
         result["components"] = components(torch, ops, dev)
         result["host_path"] = host_path(torch, tfma, dev)
