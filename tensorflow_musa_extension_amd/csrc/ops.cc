@@ -229,31 +229,33 @@ class PinnedRing {
   static constexpr size_t kSlotBytes = 1024 * 1024;
   static constexpr int kSlots = 16;
 
-  // Copies `bytes` from `src` to device `dst` on `stream`.
+  // Copies `bytes` from `src` to device `dst` on `stream`, in pieces of at
+  // most one slot (a table above 1 MiB - more than about 256M parameters of
+  // chunk map - takes several slots; only a table larger than the whole ring
+  // waits for its own earlier pieces to be copied).
   hipError_t upload(void* dst, const void* src, size_t bytes,
                     hipStream_t stream) {
     std::lock_guard<std::mutex> lk(mu_);
-    if (bytes > kSlotBytes) {
-      // Larger than a slot (> ~256M parameters of chunk map): synchronous copy.
-      hipError_t e = hipStreamSynchronize(stream);
-      if (e != hipSuccess) return e;
-      return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
-    }
     hipError_t e = ensure();
     if (e != hipSuccess) return e;
-    const int s = next_;
-    next_ = (next_ + 1) % kSlots;
-    if (used_[s]) {
-      e = hipEventSynchronize(events_[s]);
+    for (size_t off = 0; off < bytes; off += kSlotBytes) {
+      const size_t piece = std::min(kSlotBytes, bytes - off);
+      const int s = next_;
+      next_ = (next_ + 1) % kSlots;
+      if (used_[s]) {
+        e = hipEventSynchronize(events_[s]);
+        if (e != hipSuccess) return e;
+      }
+      char* slot = static_cast<char*>(host_) + s * kSlotBytes;
+      memcpy(slot, static_cast<const char*>(src) + off, piece);
+      e = hipMemcpyAsync(static_cast<char*>(dst) + off, slot, piece, hipMemcpyHostToDevice,
+                         stream);
       if (e != hipSuccess) return e;
+      e = hipEventRecord(events_[s], stream);
+      if (e != hipSuccess) return e;
+      used_[s] = true;
     }
-    char* slot = static_cast<char*>(host_) + s * kSlotBytes;
-    memcpy(slot, src, bytes);
-    e = hipMemcpyAsync(dst, slot, bytes, hipMemcpyHostToDevice, stream);
-    if (e != hipSuccess) return e;
-    e = hipEventRecord(events_[s], stream);
-    used_[s] = true;
-    return e;
+    return hipSuccess;
   }
 
  private:

@@ -277,6 +277,38 @@ def test_grouped_adam_cfg5_sampled(dev):
     torch.cuda.empty_cache()
 
 
+def test_grouped_tables_over_one_staging_slot(dev):
+    """24000 tiny tensors give a device table of about 1.2 MB, more than one
+    1 MiB pinned staging slot, so each call's table is copied in two pieces
+    through consecutive slots.  Nine calls, each with a different split of the
+    same buffers (so no call reuses a cached table), wrap the 16-slot ring;
+    every call must still match the oracle bit for bit."""
+    rng = np.random.default_rng(21)
+    n_tensors, n_calls = 24000, 9
+    sizes = [rng.integers(1, 65, n_tensors) for _ in range(n_calls)]
+    total = int(max(int(s.sum()) for s in sizes))
+    var = gen(rng, total, "float32", scale=0.02)
+    m = gen(rng, total, "float32", scale=1e-4)
+    v = np.abs(gen(rng, total, "float32", scale=1e-4))
+    tv, tm, tw = (to_dev(a, "float32", dev) for a in (var, m, v))
+    rv, rm, rw = var.copy(), m.copy(), v.copy()
+    for k in range(n_calls):
+        g = gen(rng, total, "float32", scale=1e-3)
+        tg = to_dev(g, "float32", dev)
+        cut = [int(s) for s in sizes[k]]
+        used = sum(cut)
+        parts = [list(torch.split(t[:used], cut)) for t in (tv, tm, tw, tg)]
+        ops.MusaGroupedResourceApplyAdam(*parts, 0.9, 0.999, LR, B1, B2, EPS)
+        oracle.adam(rv[:used], rm[:used], rw[:used], g[:used], _t_scalar(0.9, "float32"),
+                    _t_scalar(0.999, "float32"), _t_scalar(LR, "float32"),
+                    _t_scalar(B1, "float32"), _t_scalar(B2, "float32"),
+                    _t_scalar(EPS, "float32"))
+    torch.cuda.synchronize()
+    assert_bitwise(to_np(tv, "float32"), rv, "var")
+    assert_bitwise(to_np(tm, "float32"), rm, "m")
+    assert_bitwise(to_np(tw, "float32"), rw, "v")
+
+
 def test_grouped_repeated_steps_use_cached_table(dev):
     """The same tensors every step (as in training): the second and later
     calls run on the library's cached device table - on the caller's stream

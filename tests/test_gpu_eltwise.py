@@ -49,6 +49,7 @@ BCAST = [
     ((37, 3), (3,)),                # period shorter than a vector: wraps inside it
     ((9, 7, 11), (7, 1)),           # inner 11, period 7: incremental walk
     ((5, 1021), (1021,)),           # odd period, wrap in a few vectors
+    ((3, 8191), (8191,)),           # longest odd half period the padded LDS copy holds
     ((3, 9001), (9001,)),           # odd period too long for the LDS copy
     ((9000, 3), (9000, 1)),         # inner 3, long period: global walk
     ((4, 1, 5), (1, 3, 1)),         # neither operand full: strided path
