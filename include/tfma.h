@@ -385,7 +385,9 @@ int TFMA_FusedBatchNormBarrierTimedOut(int32_t* timed_out, int32_t reset, TFMA_S
  * fused = 1: the persistent kernel ran with `workgroups` workgroups over
  * row_groups x channel_tiles; dynamic_rows > 0: each thread's lowest
  * dynamic_rows streamed phase-3 rows were handed out in chunks of
- * dynamic_chunk rows; register_rows / lds_rows: rows per thread kept on chip.
+ * dynamic_chunk rows; register_rows / lds_rows: rows per thread kept on chip;
+ * slices > 1: each workgroup ran channel_tiles / slices tiles at a time, one
+ * whole two-phase pass per slice (1: all tiles at once).
  * fused = 0: the reduce / finalize / apply kernels ran.  No reference
  * counterpart. */
 typedef struct TFMA_FusedBatchNormPlan {
@@ -397,7 +399,7 @@ typedef struct TFMA_FusedBatchNormPlan {
   int32_t dynamic_chunk;
   int32_t register_rows;
   int32_t lds_rows;
-  int32_t reserved;
+  int32_t slices;
 } TFMA_FusedBatchNormPlan;
 int TFMA_FusedBatchNormLastPlan(TFMA_FusedBatchNormPlan* plan, TFMA_Status* status);
 

@@ -55,7 +55,7 @@ class TFMA_FusedBatchNormPlan(ctypes.Structure):
                 ("row_groups", ctypes.c_int64), ("channel_tiles", ctypes.c_int32),
                 ("dynamic_rows", ctypes.c_int32), ("dynamic_chunk", ctypes.c_int32),
                 ("register_rows", ctypes.c_int32), ("lds_rows", ctypes.c_int32),
-                ("reserved", ctypes.c_int32)]
+                ("slices", ctypes.c_int32)]
 
 
 LIB_NAME = "libtfma.so"

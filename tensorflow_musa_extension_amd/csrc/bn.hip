@@ -680,18 +680,21 @@ constexpr int64_t kMaxEpochGroups = 64 * kEpochPerLane;
 template <class Tr> struct Resident {
   static constexpr bool kOpaqueFwd = false, kOpaqueGrad = true;
   static constexpr int kRegFwd = 29, kRegGrad = 13, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kRegGradSliced = 11;
   static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 0, kPbFwd = 0, kPaGrad = 0, kPbGrad = 0;
 };
 template <> struct Resident<TF16> {
   static constexpr bool kOpaqueFwd = true, kOpaqueGrad = true;
   static constexpr int kRegFwd = 32, kRegGrad = 13, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kRegGradSliced = 12;
   static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 0, kPbFwd = 0, kPaGrad = 0, kPbGrad = 0;
 };
 template <> struct Resident<TBF16> {
   static constexpr bool kOpaqueFwd = false, kOpaqueGrad = true;
   static constexpr int kRegFwd = 32, kRegGrad = 11, kLdsFwd = 18, kLdsGrad = 9;
+  static constexpr int kRegGradSliced = 9;
   static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 0, kPbFwd = 0, kPaGrad = 0, kPbGrad = 0;
 };
@@ -704,7 +707,9 @@ struct FusedArgs {
   int c;
   int64_t cv;
   int tx_shift;
-  int ct;
+  int ct;                       // channel tiles
+  int ct_conc;                  // sliced kernel: tiles run at once (ct / slices)
+  int slices;                   // sliced kernel: tiles each workgroup runs in turn
   int64_t groups;
   int64_t rows_per_g;
   unsigned long long* barrier;  // device-wide exit-arrival counter
@@ -822,7 +827,7 @@ __device__ inline void st16(void* p, const uint4& v) {
   __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(p));
 }
 
-template <class Tr, bool kGrad, int KR, int KL>
+template <class Tr, bool kGrad, int KR, int KL, bool kSliced>
 __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs a) {
   using S = typename Tr::S;
   constexpr int VEC = Tr::kVec;
@@ -830,17 +835,53 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   constexpr int U = kGrad ? 4 : 8;  // streamed vectors per tensor in flight
   extern __shared__ uint4 lds_rows[];  // [KL][kIn][kFusedThreads]
   __shared__ float2 red[(kFusedThreads / 64) * 32 * VEC];  // [wave][tx * VEC + j]
-  const int tid = threadIdx.x;
+  constexpr int kWaves = kFusedThreads / 64;
+  // Channel tiles of this workgroup.  Unsliced: one, tile blockIdx % ct of
+  // row group blockIdx / ct.  Sliced: the workgroup owns row group
+  // blockIdx / ct_conc and runs the whole two-phase pass once per slice, on
+  // tile blockIdx % ct_conc + s * ct_conc in slice s, so a slice's rows fit
+  // (or nearly fit) in the resident registers and LDS and are not re-read.
+  const int nslices = kSliced ? a.slices : 1;
+  const int width = (1 << a.tx_shift) * VEC;  // channels of a tile
+
+  // This launch's epoch, in the upper half of the tag word (recorded
+  // launches: 2^31 + 1 + (device word mod 2^31 - 1)).
+  const unsigned epoch =
+      a.epoch_dev ? 0x80000001u + __hip_atomic_load(a.epoch_dev, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT) % 0x7fffffffu
+                  : a.epoch;
+  const uint64_t etag = static_cast<uint64_t>(epoch) << 32;
+  // The tag the waits look for: this launch's epoch (wait_xor is 0 except
+  // under the host's forced-give-up test hook).
+  const uint32_t wtag = epoch ^ a.wait_xor;
+  auto give_up = [&]() {
+    __hip_atomic_store(a.gave_up, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  };
+
+#pragma clang loop unroll(disable)
+  for (int sl = 0; sl < nslices; ++sl) {
+  int tid_v = threadIdx.x;
+  if constexpr (kSliced) asm volatile("" : "+v"(tid_v));
+  const int tid = tid_v;
   const int tx = tid & ((1 << a.tx_shift) - 1);
   const int ty = tid >> a.tx_shift;
   const int ry = kFusedThreads >> a.tx_shift;
-  const int ct = blockIdx.x % a.ct;
-  const int64_t g = blockIdx.x / a.ct;
-  const int64_t cvi = static_cast<int64_t>(ct) * (1 << a.tx_shift) + tx;
-  const bool active = cvi < a.cv;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int ct_conc = kSliced ? a.ct_conc : a.ct;
+  const int64_t g = blockIdx.x / ct_conc;
   const int64_t r0 = g * a.rows_per_g;
   int64_t r1 = r0 + a.rows_per_g;
   if (r1 > a.rows) r1 = a.rows;
+  const int ct = static_cast<int>(blockIdx.x % ct_conc) + sl * ct_conc;
+  // The channels whose finals this slice computes.
+  const int cs0 = sl * ct_conc * width;
+  const int cs1 = a.c < cs0 + ct_conc * width ? a.c : cs0 + ct_conc * width;
+  // The previous slice's reads of its coefficients from `red` come before
+  // this slice's phase-1 reduction writes it.
+  if (kSliced && sl > 0) __syncthreads();
+  const int64_t cvi = static_cast<int64_t>(ct) * (1 << a.tx_shift) + tx;
+  const bool active = cvi < a.cv;
   const int64_t nk = (active && r0 + ty < r1) ? (r1 - r0 - ty + ry - 1) / ry : 0;
   const int64_t c0 = active ? cvi * VEC : 0;
   const S* __restrict__ px = static_cast<const S*>(a.x) + c0;
@@ -866,20 +907,6 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     return lds_rows[(q2 * kIn + which) * kFusedThreads + tid];
   };
 
-  // This launch's epoch, in the upper half of the tag word (recorded
-  // launches: 2^31 + 1 + (device word mod 2^31 - 1)).
-  const unsigned epoch =
-      a.epoch_dev ? 0x80000001u + __hip_atomic_load(a.epoch_dev, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT) % 0x7fffffffu
-                  : a.epoch;
-  const uint64_t etag = static_cast<uint64_t>(epoch) << 32;
-  // The tag the waits look for: this launch's epoch (wait_xor is 0 except
-  // under the host's forced-give-up test hook).
-  const uint32_t wtag = epoch ^ a.wait_xor;
-  auto give_up = [&]() {
-    __hip_atomic_store(a.gave_up, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  };
-
   // ---- phase 1: partial statistics --------------------------------------
   float k[VEC], s1[VEC], s2[VEC];
 #pragma unroll
@@ -892,7 +919,6 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
 #pragma unroll
     for (int j = 0; j < VEC; ++j) k[j] = kGrad ? a.fin.mean_in[c0 + j] : 0.f;
   }
-  const int width = (1 << a.tx_shift) * VEC;  // channels of this tile
   // The shift samples: an inactive lane (px = x) reads channels 0..VEC-1 of
   // the same rows, in bounds, and its k is never used.
   uint4 kw[kGrad ? 1 : 5];
@@ -985,13 +1011,9 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       s2[j] += __shfl_xor(s2[j], off, 64);
     }
   }
-  {
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-    if (lane < (1 << a.tx_shift)) {
+  if (lane < (1 << a.tx_shift)) {
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) red[wave * width + lane * VEC + j] = make_float2(s1[j], s2[j]);
-    }
+    for (int j = 0; j < VEC; ++j) red[wave * width + lane * VEC + j] = make_float2(s1[j], s2[j]);
   }
   __syncthreads();
   if (tid < width && static_cast<int64_t>(ct) * width + tid < static_cast<int64_t>(a.cv) * VEC) {
@@ -1012,11 +1034,8 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   // partial loads of the others do not queue behind them.
   constexpr int PA = kGrad ? Resident<Tr>::kPaGrad : Resident<Tr>::kPaFwd;
   constexpr int PB = kGrad ? Resident<Tr>::kPbGrad : Resident<Tr>::kPbFwd;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  constexpr int kWaves = kFusedThreads / 64;
   const bool pre_a =
-      PA > 0 && static_cast<int>(blockIdx.x) + wave * static_cast<int>(gridDim.x) >= a.c;
+      PA > 0 && static_cast<int>(blockIdx.x) + wave * static_cast<int>(gridDim.x) >= cs1 - cs0;
   uint4 pax[PA > 0 ? PA : 1], pad[kGrad && PA > 0 ? PA : 1];
   if (pre_a) {
 #pragma unroll
@@ -1032,7 +1051,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   // Channel ch belongs to workgroup ch % gridDim.x; each wave of the
   // workgroup finishes one of its channels at a time, so all of a
   // workgroup's partial loads are in flight together.
-  for (int ch = blockIdx.x + wave * gridDim.x; ch < a.c; ch += kWaves * gridDim.x) {
+  for (int ch = cs0 + blockIdx.x + wave * gridDim.x; ch < cs1; ch += kWaves * gridDim.x) {
     double t1 = 0.0, t2 = 0.0;
     {
       // Lane l sums groups l, l + 64, ... (at most kMaxGroups / 64 of them):
@@ -1092,7 +1111,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
                      etag | __builtin_bit_cast(uint32_t, v4[i]));
     }
   }
-  zero_side_outputs<kGrad>(a.fin);
+  if (sl == 0) zero_side_outputs<kGrad>(a.fin);
 
   // Prefetch part B: the next rows, in flight while the tile's coefficients
   // are polled.
@@ -1266,8 +1285,8 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       int64_t o1 = o0 + a.rows_per_g;
       if (o1 > a.rows) o1 = a.rows;
       const int64_t onk = (active && o0 + ty < o1) ? (o1 - o0 - ty + ry - 1) / ry : 0;
-      const bool opre = PA > 0 && static_cast<int>(go * a.ct + ct) +
-                                          wave * static_cast<int>(gridDim.x) >= a.c;
+      const bool opre = PA > 0 && static_cast<int>(go * ct_conc + ct - sl * ct_conc) +
+                                          wave * static_cast<int>(gridDim.x) >= cs1 - cs0;
       int64_t qhi = onk - 1 - (opre ? PA : 0) - PB;  // owner's last streamed row
       if (qhi > qlo - 1) qhi = qlo - 1;              // owner's static rows end at qlo
       const int64_t qa = KR + KL + j * B;
@@ -1294,6 +1313,10 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       }
     }
   }
+
+  }  // slices
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
 
   // Exit (when chunks were handed out, and in a launch recorded into a
   // graph): counted in two levels - class counter, then the global counter -
@@ -1426,14 +1449,30 @@ constexpr int fused_kl() { return kGrad ? Resident<Tr>::kLdsGrad : Resident<Tr>:
 
 constexpr int64_t kSmallFwdRows = 64;
 
-template <class Tr, bool kGrad, int KR = fused_kr<Tr, kGrad>()>
+template <class Tr, bool kGrad, int KR = fused_kr<Tr, kGrad>(), bool kSliced = false>
 const void* fused_kernel() {
-  return reinterpret_cast<const void*>(&bn_fused_nhwc_kernel<Tr, kGrad, KR, fused_kl<Tr, kGrad>()>);
+  return reinterpret_cast<const void*>(
+      &bn_fused_nhwc_kernel<Tr, kGrad, KR, fused_kl<Tr, kGrad>(), kSliced>);
 }
 
 template <class Tr, bool kGrad>
 size_t fused_smem() {
   return static_cast<size_t>(fused_kl<Tr, kGrad>()) * (kGrad ? 2 : 1) * kFusedThreads * 16;
+}
+
+// The sliced grad kernel (the slice loop costs registers: kRegGradSliced is
+// the largest spill-free count).
+template <class Tr>
+const void* sliced_kernel() {
+  return fused_kernel<Tr, true, Resident<Tr>::kRegGradSliced, true>();
+}
+
+// Per device: the sliced kernel has the unsliced kernel's occupancy (set by
+// fused_blocks_per_cu).
+template <class Tr, bool kGrad>
+bool* sliced_ok() {
+  static bool ok[64] = {false};
+  return ok;
 }
 
 // Co-resident workgroups per CU for the fused kernel (0 if it cannot run).
@@ -1443,7 +1482,7 @@ int fused_blocks_per_cu() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   if (cached[dev] == 0) {
-    int nb = 0;
+    int nb = 0, sliced_ns = 0;
     hipError_t e = hipFuncSetAttribute(fused_kernel<Tr, kGrad>(),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        static_cast<int>(fused_smem<Tr, kGrad>()));
@@ -1453,11 +1492,20 @@ int fused_blocks_per_cu() {
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 static_cast<int>(fused_smem<Tr, kGrad>()));
     }
+    if constexpr (kGrad) {  // the sliced grad: same LDS, and it must fit as often
+      if (e == hipSuccess)
+        e = hipFuncSetAttribute(sliced_kernel<Tr>(), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(fused_smem<Tr, kGrad>()));
+      if (e == hipSuccess)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&sliced_ns, sliced_kernel<Tr>(),
+                                                         kFusedThreads, fused_smem<Tr, kGrad>());
+    }
     if (e == hipSuccess)
       e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fused_kernel<Tr, kGrad>(),
                                                        kFusedThreads, fused_smem<Tr, kGrad>());
     if (e != hipSuccess || nb < 1) nb = -1;
     cached[dev] = nb > 2 ? 2 : nb;
+    sliced_ok<Tr, kGrad>()[dev] = nb >= 1 && sliced_ns >= cached[dev];
   }
   return cached[dev];
 }
@@ -1465,6 +1513,8 @@ int fused_blocks_per_cu() {
 struct FusedPlan {
   int tx_shift;
   int ct;
+  int ct_conc = 0;  // tiles in flight at once (= ct unless sliced)
+  int slices = 1;   // > 1: each workgroup runs ct / ct_conc tiles in turn
   int64_t cv;
   int64_t groups;
   int64_t rows_per_g;
@@ -1511,8 +1561,88 @@ bool make_fused_plan(const BnGeometry& g, int vec, int blocks_per_cu, FusedPlan*
     return false;
   fp->groups = (g.rows + fp->rows_per_g - 1) / fp->rows_per_g;
   fp->blocks = static_cast<int>(fp->groups * fp->ct);
+  fp->ct_conc = fp->ct;
+  fp->slices = 1;
   fp->dyn_rows = 0;
   fp->dyn_chunk = 1;
+  return true;
+}
+
+// Sliced plan: tiles of 2^tx_shift channel vectors, ct_conc of them in
+// flight, each workgroup running ct / ct_conc of them in turn (one row group
+// of all blocks / ct_conc per workgroup).
+bool make_sliced_plan(const BnGeometry& g, int vec, int blocks_per_cu, int tx_shift, int ct_conc,
+                      FusedPlan* fp) {
+  if (!g.nhwc || blocks_per_cu < 1 || g.c % vec != 0 || tx_shift < 0 || tx_shift > 5 ||
+      ct_conc < 1)
+    return false;
+  fp->cv = g.c / vec;
+  fp->tx_shift = tx_shift;
+  const int tx = 1 << tx_shift;
+  const int64_t tiles = (fp->cv + tx - 1) / tx;
+  if (tiles < 2 || tiles % ct_conc != 0 || tiles / ct_conc < 2) return false;
+  fp->ct = static_cast<int>(tiles);
+  fp->ct_conc = ct_conc;
+  fp->slices = static_cast<int>(tiles / ct_conc);
+  const int64_t max_blocks = static_cast<int64_t>(blocks_per_cu) * DeviceCUs();
+  int64_t groups = max_blocks / ct_conc;
+  if (groups < 1) return false;
+  const int ry = kFusedThreads / tx;
+  const int64_t max_groups = (g.rows + ry - 1) / ry;
+  if (groups > max_groups) groups = max_groups;
+  if (groups > fused_group_bound()) groups = fused_group_bound();
+  if (groups > kMaxEpochGroups) groups = kMaxEpochGroups;
+  // The epoch-tagged partial slots hold at most 512 * CUs (group, channel)
+  // values.
+  if (groups * g.c > 512 * static_cast<int64_t>(DeviceCUs())) return false;
+  fp->rows_per_g = (g.rows + groups - 1) / groups;
+  const int64_t esz = 16 / vec;
+  if ((fp->rows_per_g + 64 * static_cast<int64_t>(ry)) * g.c * esz >= (int64_t{1} << 31))
+    return false;
+  fp->groups = (g.rows + fp->rows_per_g - 1) / fp->rows_per_g;
+  fp->blocks = static_cast<int>(fp->groups * ct_conc);
+  fp->dyn_rows = 0;
+  fp->dyn_chunk = 1;
+  return true;
+}
+
+// Rows per thread of the unsliced grad plan from which the grad is sliced.
+constexpr int64_t kSliceMinRows = 128;
+
+// The fused plan of an NHWC op.  A gradient whose unsliced plan leaves each
+// thread kSliceMinRows rows or more (x + dy several times what the grid
+// holds on chip; cfg2's 256x56x56x256) runs sliced: tiles of 8 channel
+// vectors (128-byte row segments, the narrowest that read whole cache
+// lines), every workgroup running all of them in turn, so each slice's
+// phase-3 re-read is 55 % of its x + dy instead of 89 % of the whole
+// (measured: 333 -> 305 us f16, 343 -> 313 us bf16 at 256x56x56x256; at
+// 256x28x28x512, 98 rows, no slicing was faster; sliced forwards were
+// never faster - a slice's read-only phase 1 and write-only phase 3 stream
+// slower than the unsliced phase 3, which reads and writes at once).
+// TFMA_BN_SLICE_TW (read per call, for tests and measurements): 0 never
+// slices; 8, 16 or 32 slices every grad that has such a plan, with tiles of
+// that many vectors.
+template <class Tr, bool kGrad>
+bool choose_fused_plan(const BnGeometry& g, int vec, FusedPlan* fp) {
+  const int bpc = fused_blocks_per_cu<Tr, kGrad>();
+  if (!make_fused_plan(g, vec, bpc, fp)) return false;
+  if constexpr (kGrad) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !sliced_ok<Tr, kGrad>()[dev])
+      return true;
+    const char* o = getenv("TFMA_BN_SLICE_TW");
+    int tw = o ? atoi(o) : -1;
+    if (tw == 0) return true;
+    if (tw != 8 && tw != 16 && tw != 32) {
+      const int ry = kFusedThreads >> fp->tx_shift;
+      if ((fp->rows_per_g + ry - 1) / ry < kSliceMinRows) return true;
+      tw = 8;
+    }
+    FusedPlan sp;
+    if (make_sliced_plan(g, vec, bpc, tw == 8 ? 3 : (tw == 16 ? 4 : 5), 1, &sp) &&
+        sp.slices <= 8)
+      *fp = sp;
+  }
   return true;
 }
 
@@ -1705,6 +1835,8 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   fa.cv = fp.cv;
   fa.tx_shift = fp.tx_shift;
   fa.ct = fp.ct;
+  fa.ct_conc = fp.ct_conc;
+  fa.slices = fp.slices;
   fa.groups = fp.groups;
   fa.rows_per_g = fp.rows_per_g;
   fa.barrier = region;
@@ -1729,8 +1861,12 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
                           : nullptr;
   const int ry = kFusedThreads >> fp.tx_shift;
   const int64_t nk_max = (fp.rows_per_g + ry - 1) / ry;  // rows of a thread
+  const bool sliced = kGrad && fp.slices > 1;
   const bool small = !kGrad && nk_max <= kSmallFwdRows;
-  const int kr = small ? Resident<Tr>::kRegFwdSmall : fused_kr<Tr, kGrad>();
+  int kr = small ? Resident<Tr>::kRegFwdSmall : fused_kr<Tr, kGrad>();
+  if constexpr (kGrad) {
+    if (sliced) kr = Resident<Tr>::kRegGradSliced;
+  }
   {
     FusedPlan fd = fp;
     constexpr int kPre = kGrad ? Resident<Tr>::kPaGrad + Resident<Tr>::kPbGrad
@@ -1755,9 +1891,13 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   t_last_plan.dynamic_chunk = fa.dyn_chunk;
   t_last_plan.register_rows = kr;
   t_last_plan.lds_rows = fused_kl<Tr, kGrad>();
+  t_last_plan.slices = fp.slices;
   const char* name = kGrad ? "tfma_bn_grad_fused" : "tfma_bn_fwd_fused";
   SetLastKernel(name);
   const void* kern = fused_kernel<Tr, kGrad>();
+  if constexpr (kGrad) {
+    if (sliced) kern = sliced_kernel<Tr>();
+  }
   if constexpr (!kGrad) {
     if (small) kern = fused_kernel<Tr, kGrad, Resident<Tr>::kRegFwdSmall>();
   }
@@ -1871,7 +2011,7 @@ hipError_t forward_t(const BnGeometry& g, const BnFwdArgs& a, void* ws,
   hipError_t e;
   FusedPlan fp;
   if (a.is_training && p.vec > 1 && fused_enabled() &&
-      make_fused_plan(g, p.vec, fused_blocks_per_cu<Tr, false>(), &fp)) {
+      choose_fused_plan<Tr, false>(g, p.vec, &fp)) {
     return launch_fused<Tr, false>(fp, g, a.x, nullptr, a.y, fa,
                                                   stream);
   }
@@ -1918,7 +2058,7 @@ hipError_t grad_t(const BnGeometry& g, const BnGradArgs& a, void* ws,
   fa.is_training = a.is_training;
   FusedPlan fp;
   if (p.vec > 1 && fused_enabled() &&
-      make_fused_plan(g, p.vec, fused_blocks_per_cu<Tr, true>(), &fp)) {
+      choose_fused_plan<Tr, true>(g, p.vec, &fp)) {
     return launch_fused<Tr, true>(fp, g, a.x, a.dy, a.dx, fa,
                                                   stream);
   }

@@ -417,7 +417,7 @@ def fused_batch_norm_last_plan():
     plan = _lib.TFMA_FusedBatchNormPlan()
     lib.TFMA_FusedBatchNormLastPlan(ctypes.byref(plan), ctypes.byref(status))
     raise_for_status(status)
-    return {name: getattr(plan, name) for name, _ in plan._fields_ if name != "reserved"}
+    return {name: getattr(plan, name) for name, _ in plan._fields_}
 
 
 def fused_batch_norm_barrier_timed_out(reset=False):

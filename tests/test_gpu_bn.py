@@ -106,6 +106,49 @@ def test_fwd_grad_matches_oracle(dev, shape, dtype, data_format):
     assert torch.all(grad.reserve_space_4 == 0) and torch.all(grad.reserve_space_5 == 0)
 
 
+SLICED_CASES = [
+    ((4, 9, 11, 256), "float16"),
+    ((4, 9, 11, 256), "bfloat16"),
+    ((3, 7, 13, 128), "float32"),
+    ((6, 5, 7, 200), "float16"),   # 25 vectors: a last tile with one active vector
+    ((2, 3, 3, 512), "bfloat16"),  # fewer rows than a workgroup pass: empty groups
+]
+
+
+@pytest.mark.parametrize("tw", [8, 16, 32])
+@pytest.mark.parametrize("is_training", [True, False])
+@pytest.mark.parametrize("shape,dtype", SLICED_CASES)
+def test_sliced_grad_matches_oracle(dev, monkeypatch, shape, dtype, tw, is_training):
+    """The sliced fused gradient (each workgroup runs the whole two-phase pass
+    once per channel tile of tw vectors), forced at small shapes, against the
+    oracle; the plan query shows how many slices ran."""
+    monkeypatch.setenv("TFMA_BN_SLICE_TW", str(tw))
+    rng = np.random.default_rng(zlib.crc32(repr((shape, dtype, tw)).encode()))
+    eps = 1e-3
+    c = shape[-1]
+    x, scale, offset, dy = _inputs(rng, shape, dtype, "NHWC")
+    mean = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    var = rng.uniform(0.5, 2.0, c).astype(np.float32)
+    fwd, grad = _run_fwd_grad(dev, x, scale, offset, dy, dtype, "NHWC", eps, mean=mean,
+                              var=var, is_training=is_training)
+    plan = ops.fused_batch_norm_last_plan()
+    vec = 4 if dtype == "float32" else 8
+    tiles = -(-(c // vec) // tw)
+    assert plan["fused"] == 1
+    if tiles >= 2:
+        assert plan["slices"] == tiles and plan["channel_tiles"] == tiles, plan
+    else:
+        assert plan["slices"] == 1, plan
+    sm = fwd.reserve_space_1.cpu().numpy() if is_training else mean
+    sv = fwd.reserve_space_2.cpu().numpy() if is_training else var
+    rdx, rsb, rob = oracle.bn_grad(dy, x, scale, sm, sv, epsilon=eps, dtype=dtype,
+                                   is_training=is_training)
+    assert_close(to_np(grad.x_backprop, dtype), rdx, dtype, ACT_TOL[dtype], "x_backprop")
+    assert_close(grad.scale_backprop.cpu().numpy(), rsb, "float32", STAT_TOL, "scale_backprop")
+    assert_close(grad.offset_backprop.cpu().numpy(), rob, "float32", STAT_TOL, "offset_backprop")
+    assert torch.all(grad.reserve_space_4 == 0) and torch.all(grad.reserve_space_5 == 0)
+
+
 def test_large_mean_statistics(dev):
     """|mean| >> std: the shifted sums must not cancel (variance to 1e-5)."""
     rng = np.random.default_rng(7)
@@ -206,9 +249,10 @@ def test_cfg2_full_size(dev, shape, dtype):
     oracle (eps=1.001e-5): y and x_backprop to 1e-2, every statistic
     (batch_mean, batch_variance, reserve spaces, scale_backprop,
     offset_backprop) to 1e-5 - the outputs the reference's own test checks,
-    test/ops/fused_batchnorm_op_test.py:358-448.  The 56x56 and 28x28
-    gradients (and the 56x56 forward) hand part of phase 3 out dynamically;
-    the plan query shows that this path is the one compared here."""
+    test/ops/fused_batchnorm_op_test.py:358-448.  The 56x56 gradient runs
+    sliced (4 slices of 64 channels); the 28x28 gradient and the 56x56
+    forward hand part of phase 3 out dynamically; the plan query shows that
+    these paths are the ones compared here."""
     rng = np.random.default_rng(zlib.crc32(repr((shape, dtype)).encode()))
     eps = 1.001e-5
     x, scale, offset, dy = _inputs(rng, shape, dtype, "NHWC")
@@ -223,10 +267,11 @@ def test_cfg2_full_size(dev, shape, dtype):
     gplan = ops.fused_batch_norm_last_plan()
     torch.cuda.synchronize()
     assert fplan["fused"] == 1 and gplan["fused"] == 1
-    if shape[1] >= 28:
-        assert gplan["dynamic_rows"] > 0, gplan
     if shape[1] == 56:
+        assert gplan["slices"] == 4, gplan
         assert fplan["dynamic_rows"] > 0, fplan
+    elif shape[1] == 28:
+        assert gplan["dynamic_rows"] > 0 and gplan["slices"] == 1, gplan
     del tx, tdy
     ry, rbm, rbv, rsm, rsv = oracle.bn_fwd(x, scale, offset, epsilon=eps, dtype=dtype)
     assert_close(to_np(fwd.y, dtype), ry, dtype, 1e-2, "y")
@@ -273,7 +318,7 @@ def test_largest_shape_invariants(dev, dtype):
     del yd
     grad = ops.FusedBatchNormGradV3(dy, x, scale, fwd.reserve_space_1, fwd.reserve_space_2,
                                     fwd.reserve_space_3, epsilon=eps)
-    assert ops.fused_batch_norm_last_plan()["dynamic_rows"] > 0
+    assert ops.fused_batch_norm_last_plan()["slices"] == 4
     dyd = dy.double().reshape(-1, 256)
     assert torch.allclose(grad.offset_backprop.double(), dyd.sum(0), rtol=1e-5, atol=1e-2)
     del dyd

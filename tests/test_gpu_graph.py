@@ -49,9 +49,14 @@ def _state(d):
 
 # (16,14,14,256): every row resident, no dynamic chunks.  (128,56,56,256):
 # the grad hands out phase-3 chunks, so the recorded launch zeroes the chunk
-# counters as well as the barrier counters at exit.
-@pytest.mark.parametrize("shape", [(16, 14, 14, 256), (128, 56, 56, 256)])
-def test_recorded_training_step_replays(dev, shape):
+# counters as well as the barrier counters at exit; with slice_tw 8 the grad
+# runs sliced (4 slices of 64 channels, eager and recorded).
+@pytest.mark.parametrize("shape,slice_tw", [((16, 14, 14, 256), None),
+                                            ((128, 56, 56, 256), None),
+                                            ((128, 56, 56, 256), 8)])
+def test_recorded_training_step_replays(dev, monkeypatch, shape, slice_tw):
+    if slice_tw is not None:
+        monkeypatch.setenv("TFMA_BN_SLICE_TW", str(slice_tw))
     d = _inputs(dev, shape, seed=31)
     other = _inputs(dev, (8, 7, 7, 512), seed=32)
     e = torch.empty(0, device=dev)
@@ -59,6 +64,8 @@ def test_recorded_training_step_replays(dev, shape):
     eager = []
     for _ in range(3):
         eager.append([t.clone() for t in _step(d)] + _state(d))
+        if slice_tw is not None:
+            assert ops.fused_batch_norm_last_plan()["slices"] == 4
     other_ref = ops.FusedBatchNormV3(other["x"], other["scale"], other["offset"], e, e,
                                      epsilon=EPS).y.clone()
     torch.cuda.synchronize()

@@ -126,8 +126,9 @@ def _chunked_sums(t, c, fn, rows_per=1 << 20):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_batch_norm_over_2_31(dev, dtype):
     """FusedBatchNormV3 + GradV3 on [1, 8388640, 1, 256] f16 and bf16
-    (2,147,491,840 elements, 2048 rows per thread in the fused kernel, whose
-    phase 3 hands rows out dynamically).  Statistics against float64 sums
+    (2,147,491,840 elements; the forward's fused kernel has 2048 rows per
+    thread, the gradient runs in 4 slices of 64 channels with 512 rows per
+    thread per slice, and both hand phase-3 rows out dynamically).  Statistics against float64 sums
     taken on the device in chunks (mean 1e-5 absolute; variance 5e-5
     relative - each thread sums 2048 rows in float32 before the float64
     combine; sum(dy) and rsqrt(var+eps) * sum(dy*(x-mean)) 1e-5 relative +
@@ -161,7 +162,8 @@ def test_batch_norm_over_2_31(dev, dtype):
 
     g = ops.FusedBatchNormGradV3(dy, x, scale, mu, sig, f.reserve_space_3, epsilon=eps)
     assert ops.last_kernel_name() == "tfma_bn_grad_fused"
-    assert ops.fused_batch_norm_last_plan()["dynamic_rows"] > 0
+    plan = ops.fused_batch_norm_last_plan()
+    assert plan["slices"] == 4 and plan["dynamic_rows"] > 0, plan
     sdy = _chunked_sums(dy, c, lambda a: a)
     assert torch.allclose(g.offset_backprop.double(), sdy, rtol=1e-5, atol=5e-2)
     sbp = bn_scale_backprop_ref64(dy, x, mu, sig, eps, rows, c)
