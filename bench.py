@@ -223,10 +223,11 @@ def component_groups(torch, ops, dev):
                      "tfma_bn_fwd")]
     del x1, bn1, ws1
 
-    # BatchNorm on the 3-kernel split path (reduce, finalize, apply): NCHW
-    # training (fwd reads x twice: 3sE; grad reads x and dy twice: 5sE of
-    # traffic against the 2sE / 3sE algorithmic bytes) and NHWC inference
-    # (one read of x from running statistics: 2sE).
+    # BatchNorm off the NHWC fused path: NCHW training with at least one
+    # channel per CU (one workgroup per channel: 2sE / 3sE algorithmic bytes,
+    # plus re-reads of what a workgroup cannot hold on chip) and NHWC
+    # inference (one apply kernel, coefficients from the running statistics:
+    # 2sE).
     xn = torch.randn(256, 512, 28, 28, generator=gen, device=dev).half()
     dyn = torch.randn(256, 512, 28, 28, generator=gen, device=dev).half()
     scn = torch.rand(512, generator=gen, device=dev) + 0.5
@@ -247,11 +248,11 @@ def component_groups(torch, ops, dev):
     bi = ops.bind(ops.FusedBatchNormV3, xi, scn[:256].contiguous(), ofn[:256].contiguous(), rm,
                   rv, epsilon=EPS, data_format="NHWC", is_training=False, workspace=wsi)
     yield [Component("bn_fwd_f16_nchw_256x512x28x28", [fn_], 4 * En, En, "tfma_bn_fwd",
-                     note="split path, traffic 3sE"),
+                     note="one workgroup per channel"),
            Component("bn_grad_f16_nchw_256x512x28x28", [gn], 6 * En, En, "tfma_bn_grad",
-                     note="split path, traffic 5sE"),
+                     note="one workgroup per channel"),
            Component("bn_fwd_inference_f16_256x56x56x256", [bi], 4 * xi.numel(), xi.numel(),
-                     "tfma_bn_fwd", note="coefficients from running statistics, one pass")]
+                     "tfma_bn_infer", note="coefficients from running statistics, one kernel")]
     del xn, dyn, fn_, gn, wsn, xi, wsi, bi
 
     n = 25_600_000

@@ -388,6 +388,8 @@ int TFMA_FusedBatchNormBarrierTimedOut(int32_t* timed_out, int32_t reset, TFMA_S
  * dynamic_chunk rows; register_rows / lds_rows: rows per thread kept on chip;
  * slices > 1: each workgroup ran channel_tiles / slices tiles at a time, one
  * whole two-phase pass per slice (1: all tiles at once).
+ * fused = 2: the NCHW kernel with one workgroup per channel ran
+ * (workgroups = channel_tiles = C).
  * fused = 0: the reduce / finalize / apply kernels ran.  No reference
  * counterpart. */
 typedef struct TFMA_FusedBatchNormPlan {

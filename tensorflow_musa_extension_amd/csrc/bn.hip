@@ -512,18 +512,25 @@ __global__ __launch_bounds__(kFinThreads) void bn_finalize_kernel(
 }
 
 // Inference-mode forward coefficients from the running statistics.
-__global__ void bn_infer_coef_kernel(FinArgs a, float4* __restrict__ coef) {
-  const int ch = blockIdx.x * blockDim.x + threadIdx.x;
-  if (ch == 0 && a.reserve3) a.reserve3[0] = 0.f;
-  if (ch >= a.c) return;
-  const float mu = a.mean_in[ch];
-  const float var = a.var_in[ch];
-  const float inv = 1.0f / __builtin_sqrtf(var + a.eps);
-  a.batch_mean[ch] = mu;
-  a.batch_var[ch] = var;
-  a.saved_mean[ch] = mu;
-  a.saved_var[ch] = var;
-  coef[ch] = make_float4(mu, inv * a.scale[ch], a.offset[ch], 0.f);
+// Inference forward: the statistics outputs are the running mean and
+// variance, and each apply thread forms its channels' coefficients itself
+// (no coefficient kernel, no second launch).  infer_stats: the statistics
+// outputs, spread over the whole grid (lid, nthreads: the calling thread's
+// linear index in it and its size).
+__device__ inline float4 infer_coef(const FinArgs& a, int64_t ch) {
+  const float inv = 1.0f / __builtin_sqrtf(a.var_in[ch] + a.eps);
+  return make_float4(a.mean_in[ch], inv * a.scale[ch], a.offset[ch], 0.f);
+}
+__device__ inline void infer_stats(const FinArgs& a, int64_t lid, int64_t nthreads) {
+  if (lid == 0 && a.reserve3) a.reserve3[0] = 0.f;
+  for (int64_t ch = lid; ch < a.c; ch += nthreads) {
+    const float mu = a.mean_in[ch];
+    const float var = a.var_in[ch];
+    a.batch_mean[ch] = mu;
+    a.batch_var[ch] = var;
+    a.saved_mean[ch] = mu;
+    a.saved_var[ch] = var;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -541,13 +548,17 @@ __device__ inline typename Tr::S apply_one(typename Tr::S xs, typename Tr::S ds,
   }
 }
 
-template <class Tr, int VEC, bool kGrad>
+template <class Tr, int VEC, bool kGrad, bool kInfer>
 __global__ __launch_bounds__(kThreads) void bn_nhwc_apply_kernel(
     const typename Tr::S* __restrict__ x, const typename Tr::S* __restrict__ dy,
     typename Tr::S* __restrict__ out, const float4* __restrict__ coef,
     int64_t rows, int c, int64_t cv, int tx_shift, int64_t rows_per_g,
-    int64_t groups) {
+    int64_t groups, FinArgs fa) {
   using S = typename Tr::S;
+  if constexpr (kInfer)
+    infer_stats(fa, (static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x) * kThreads +
+                        threadIdx.x,
+                static_cast<int64_t>(gridDim.x) * gridDim.y * kThreads);
   const int tx = threadIdx.x & ((1 << tx_shift) - 1);
   const int ty = threadIdx.x >> tx_shift;
   const int ry = kThreads >> tx_shift;
@@ -560,7 +571,7 @@ __global__ __launch_bounds__(kThreads) void bn_nhwc_apply_kernel(
   const int64_t c0 = cvi * VEC;
   float4 cf[VEC];
 #pragma unroll
-  for (int j = 0; j < VEC; ++j) cf[j] = coef[c0 + j];
+  for (int j = 0; j < VEC; ++j) cf[j] = kInfer ? infer_coef(fa, c0 + j) : coef[c0 + j];
   if (r0 + ty >= r1) return;
   const int64_t nr = (r1 - r0 - ty + ry - 1) / ry;  // rows of this thread
   const S* __restrict__ px = x + c0;
@@ -600,17 +611,23 @@ __global__ __launch_bounds__(kThreads) void bn_nhwc_apply_kernel(
 
 // NCHW apply: flat over vectors (plane % VEC == 0 keeps a vector inside one
 // (image, channel) plane); channel = (i / plane) % C.  Reverse order.
-template <class Tr, int VEC, bool kGrad>
+template <class Tr, int VEC, bool kGrad, bool kInfer>
 __global__ __launch_bounds__(kThreads) void bn_nchw_apply_kernel(
     const typename Tr::S* __restrict__ x, const typename Tr::S* __restrict__ dy,
     typename Tr::S* __restrict__ out, const float4* __restrict__ coef,
-    int64_t nvec, int64_t pv, int c) {
+    int64_t nvec, int64_t pv, int c, FinArgs fa) {
   using S = typename Tr::S;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-  for (int64_t i = nvec - 1 - (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x);
-       i >= 0; i -= stride) {
+  const int64_t lid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if constexpr (kInfer) infer_stats(fa, lid, stride);
+  int last = -1;
+  float4 cf = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int64_t i = nvec - 1 - lid; i >= 0; i -= stride) {
     const int ch = static_cast<int>((i / pv) % c);
-    const float4 cf = coef[ch];
+    if (kInfer ? ch != last : true) {
+      cf = kInfer ? infer_coef(fa, ch) : coef[ch];
+      last = ch;
+    }
     S xv[VEC], dv[VEC], ov[VEC];
     vload<S, VEC>(x + i * VEC, xv);
     if constexpr (kGrad) vload<S, VEC>(dy + i * VEC, dv);
@@ -1369,6 +1386,239 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
 }
 
 // ---------------------------------------------------------------------------
+// 5. NCHW, one channel per workgroup: workgroup ch sums, finishes and applies
+//    channel ch alone, so no value crosses workgroups - no waits, no
+//    co-residency assumption, any number of workgroups in flight.  The
+//    channel's vectors (its N planes, 16 bytes each, plane % VEC == 0) are
+//    dealt to the 512 threads in turn: vector i = tid + q * 512 of the
+//    channel is the thread's row q.  As in the NHWC kernel, a thread's first
+//    KR rows stay in VGPRs, the next KL in LDS, the rest are re-read in
+//    phase 3 (last-to-first, from the Infinity Cache when they are still
+//    there).  All loads go through one buffer resource over the channel's
+//    span of the tensor (the host keeps the tensor below 2^31 bytes): a row
+//    past the channel's last vector lies past the span, reads zeros and
+//    makes no memory request, so no load needs a branch.
+// ---------------------------------------------------------------------------
+struct NchwArgs {
+  const void* x;
+  const void* dy;
+  void* out;
+  int64_t n;      // images
+  int c;          // channels
+  int64_t plane;  // elements per (image, channel) plane
+  int64_t pv;     // 16-byte vectors per plane
+  FinArgs fin;
+};
+
+// Register rows per thread (the largest spill-free counts; LDS rows as in the
+// NHWC kernel).
+template <class Tr> struct OwnedRows { static constexpr int kFwd = 30, kGrad = 16; };
+template <> struct OwnedRows<TF16> { static constexpr int kFwd = 30, kGrad = 17; };
+template <> struct OwnedRows<TBF16> { static constexpr int kFwd = 31, kGrad = 15; };
+
+template <class Tr, bool kGrad, int KR, int KL>
+__global__ __launch_bounds__(kFusedThreads) void bn_nchw_owned_kernel(NchwArgs a) {
+  using S = typename Tr::S;
+  constexpr int VEC = Tr::kVec;
+  constexpr int kIn = kGrad ? 2 : 1;
+  constexpr int U = kGrad ? 4 : 8;  // streamed vectors per tensor in flight
+  constexpr int kWaves = kFusedThreads / 64;
+  extern __shared__ uint4 lds_rows[];  // [KL][kIn][kFusedThreads]
+  __shared__ double red[2][kWaves];
+  __shared__ float cfs[4];
+  const int tid = threadIdx.x;
+  const int ch = blockIdx.x;
+  const int64_t nv = a.n * a.pv;  // vectors of the channel
+  const int64_t nk = tid < nv ? (nv - tid + kFusedThreads - 1) / kFusedThreads : 0;
+  // Byte offset of this thread's row q from the channel's first plane:
+  // img * c * plane * s + v * 16 for channel vector (img, v).  Rows advance
+  // by kFusedThreads vectors: dimg images and dv vectors (with carry).
+  const uint32_t img_b = static_cast<uint32_t>(a.c * a.plane * static_cast<int64_t>(sizeof(S)));
+  const uint32_t dimg = static_cast<uint32_t>(kFusedThreads / a.pv);
+  const uint32_t dv = static_cast<uint32_t>(kFusedThreads % a.pv);
+  const uint32_t pv = static_cast<uint32_t>(a.pv);
+  uint32_t img0 = static_cast<uint32_t>(tid / a.pv), v0 = static_cast<uint32_t>(tid % a.pv);
+  auto step = [&](uint32_t& img, uint32_t& v) {
+    v += dv;
+    const bool carry = v >= pv;
+    v = carry ? v - pv : v;
+    img += dimg + (carry ? 1u : 0u);
+  };
+  auto off_of = [&](uint32_t img, uint32_t v) { return img * img_b + v * 16u; };
+  const int64_t chan0 = static_cast<int64_t>(ch) * a.plane;  // element offset of plane (0, ch)
+  const int64_t span = ((a.n - 1) * a.c * a.plane + a.plane) * static_cast<int64_t>(sizeof(S));
+  const auto rx = rows_rsrc(static_cast<const S*>(a.x) + chan0, span);
+  const auto rd = rows_rsrc(kGrad ? static_cast<const S*>(a.dy) + chan0 : a.x, span);
+  char* const obase = reinterpret_cast<char*>(static_cast<S*>(a.out) + chan0);
+  auto lds = [&](int q2, int which) -> uint4& {
+    return lds_rows[(q2 * kIn + which) * kFusedThreads + tid];
+  };
+
+  // ---- phase 1: the channel's sums ----------------------------------------
+  const float kk = kGrad ? a.fin.mean_in[ch]
+                         : chan_shift<Tr>(static_cast<const S*>(a.x), ch, a.n * a.plane, a.c,
+                                          a.plane);
+  float k[VEC], s1[VEC], s2[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    k[j] = kk;
+    s1[j] = 0.f;
+    s2[j] = 0.f;
+  }
+  uint4 xr[KR];
+  uint4 dr[kGrad ? KR : 1];
+  uint4 xl[KL];
+  uint4 dl[kGrad ? KL : 1];
+  uint32_t img = img0, v = v0;
+#pragma unroll
+  for (int q = 0; q < KR; ++q) {
+    const uint32_t o = off_of(img, v);
+    xr[q] = bld16(rx, o);
+    if constexpr (kGrad) dr[q] = bld16(rd, o);
+    step(img, v);
+  }
+#pragma unroll
+  for (int q = 0; q < KL; ++q) {
+    const uint32_t o = off_of(img, v);
+    xl[q] = bld16(rx, o);
+    if constexpr (kGrad) dl[q] = bld16(rd, o);
+    step(img, v);
+  }
+  const uint32_t img_s = img, v_s = v;  // first streamed row
+#pragma unroll
+  for (int q = 0; q < KR; ++q) {
+    if (q < nk) accum_words<Tr, kGrad>(xr[q], dr[kGrad ? q : 0], k, s1, s2);
+    if constexpr (kGrad ? Resident<Tr>::kOpaqueGrad : Resident<Tr>::kOpaqueFwd) {
+      asm volatile("" : "+v"(xr[q].x), "+v"(xr[q].y), "+v"(xr[q].z), "+v"(xr[q].w));
+      if constexpr (kGrad)
+        asm volatile("" : "+v"(dr[q].x), "+v"(dr[q].y), "+v"(dr[q].z), "+v"(dr[q].w));
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < KL; ++q) {
+    lds(q, 0) = xl[q];
+    if constexpr (kGrad) lds(q, kGrad ? 1 : 0) = dl[kGrad ? q : 0];
+  }
+#pragma unroll 2
+  for (int q = 0; q < KL; ++q) {
+    if (KR + q < nk) {
+      const uint4 xw = lds(q, 0);
+      const uint4 dw = kGrad ? lds(q, kGrad ? 1 : 0) : xw;
+      accum_words<Tr, kGrad>(xw, dw, k, s1, s2);
+    }
+  }
+  // Streamed rows, U in flight (rows past nk read zeros and are not summed).
+  for (int64_t q = KR + KL; q < nk; q += U) {
+    uint4 xw[U], dw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t o = off_of(img, v);
+      xw[u] = bld16(rx, o);
+      if constexpr (kGrad) dw[u] = bld16(rd, o);
+      step(img, v);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (q + u < nk) accum_words<Tr, kGrad>(xw[u], dw[u], k, s1, s2);
+  }
+  // The workgroup's sums: per thread in float, then in double across the
+  // threads in a fixed order (wave shuffles, then the waves in order).
+  float ta = 0.f, tb = 0.f;
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    ta += s1[j];
+    tb += s2[j];
+  }
+  const double2 w = wave_sum(static_cast<double>(ta), static_cast<double>(tb));
+  const int wave = tid >> 6;
+  if ((tid & 63) == 0) {
+    red[0][wave] = w.x;
+    red[1][wave] = w.y;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    double t1 = 0.0, t2 = 0.0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+      t1 += red[0][i];
+      t2 += red[1][i];
+    }
+    const float4 cf = finish_channel<Tr, kGrad>(a.fin, ch, t1, t2);
+    cfs[0] = cf.x;
+    cfs[1] = cf.y;
+    cfs[2] = cf.z;
+    cfs[3] = cf.w;
+  }
+  zero_side_outputs<kGrad>(a.fin);
+  __syncthreads();
+  const float4 cone = make_float4(cfs[0], cfs[1], cfs[2], cfs[3]);
+  float4 cf[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) cf[j] = cone;
+
+  // ---- phase 3: outputs ----------------------------------------------------
+  // Streamed rows last-to-first: walk forward to find the last row's
+  // position, then step backwards.
+#pragma unroll
+  for (int r = 0; r < KR; ++r) {
+    asm volatile("" : "+v"(xr[r].x), "+v"(xr[r].y), "+v"(xr[r].z), "+v"(xr[r].w));
+    if constexpr (kGrad)
+      asm volatile("" : "+v"(dr[r].x), "+v"(dr[r].y), "+v"(dr[r].z), "+v"(dr[r].w));
+  }
+  if (nk > KR + KL) {
+    // Row nk - 1's position: (nk - 1 - (KR + KL)) steps past the first
+    // streamed row.
+    const uint64_t steps = static_cast<uint64_t>(nk - 1 - (KR + KL));
+    const uint64_t vv = v_s + steps * dv;
+    uint32_t bimg = img_s + static_cast<uint32_t>(steps * dimg + vv / pv);
+    uint32_t bv = static_cast<uint32_t>(vv % pv);
+    auto back = [&](uint32_t& im, uint32_t& vi) {
+      const bool borrow = vi < dv;
+      vi = borrow ? vi + pv - dv : vi - dv;
+      im -= dimg + (borrow ? 1u : 0u);
+    };
+    int64_t q = nk - 1;
+    for (; q >= KR + KL + U - 1; q -= U) {
+      uint4 xw[U], dw[U];
+      uint32_t os[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        os[u] = off_of(bimg, bv);
+        xw[u] = bld16_last(rx, os[u]);
+        if constexpr (kGrad) dw[u] = bld16_last(rd, os[u]);
+        back(bimg, bv);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) st16(obase + os[u], apply_words<Tr, kGrad>(xw[u], dw[u], cf));
+    }
+    for (; q >= KR + KL; --q) {
+      const uint32_t o = off_of(bimg, bv);
+      const uint4 xw = bld16_last(rx, o);
+      uint4 dw = xw;
+      if constexpr (kGrad) dw = bld16_last(rd, o);
+      st16(obase + o, apply_words<Tr, kGrad>(xw, dw, cf));
+      back(bimg, bv);
+    }
+  }
+  img = img0;
+  v = v0;
+#pragma unroll
+  for (int r = 0; r < KR; ++r) {
+    if (r < nk) st16(obase + off_of(img, v), apply_words<Tr, kGrad>(xr[r], dr[kGrad ? r : 0], cf));
+    step(img, v);
+  }
+#pragma unroll 2
+  for (int q2 = 0; q2 < KL; ++q2) {
+    if (KR + q2 < nk) {
+      const uint4 xw = lds(q2, 0);
+      const uint4 dw = kGrad ? lds(q2, kGrad ? 1 : 0) : xw;
+      st16(obase + off_of(img, v), apply_words<Tr, kGrad>(xw, dw, cf));
+    }
+    step(img, v);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host drivers.
 // ---------------------------------------------------------------------------
 template <class Tr, int VEC, bool kGrad>
@@ -1394,27 +1644,32 @@ hipError_t launch_reduce(const Plan& p, const BnGeometry& g, const void* x,
   return hipGetLastError();
 }
 
-template <class Tr, int VEC, bool kGrad>
+// kInfer: the inference forward (coefficients from fa's running statistics,
+// statistics outputs written by the same launch; coef unused).
+template <class Tr, int VEC, bool kGrad, bool kInfer = false>
 hipError_t launch_apply(const Plan& p, const BnGeometry& g, const void* x,
                         const void* dy, void* out, const float4* coef,
-                        hipStream_t stream) {
+                        hipStream_t stream, const FinArgs& fa = FinArgs{}) {
   using S = typename Tr::S;
   if (p.nhwc) {
-    TFMA_LAUNCH(kGrad ? "tfma_bn_grad_apply" : "tfma_bn_fwd_apply", (bn_nhwc_apply_kernel<Tr, VEC, kGrad>),
+    TFMA_LAUNCH(kInfer ? "tfma_bn_infer_apply" : (kGrad ? "tfma_bn_grad_apply" : "tfma_bn_fwd_apply"),
+                       (bn_nhwc_apply_kernel<Tr, VEC, kGrad, kInfer>),
                        dim3(p.ct, p.groups), dim3(kThreads), 0, stream,
                        static_cast<const S*>(x), static_cast<const S*>(dy),
                        static_cast<S*>(out), coef, g.rows, static_cast<int>(g.c),
-                       p.cv, p.tx_shift, p.rows_per_g, p.groups);
+                       p.cv, p.tx_shift, p.rows_per_g, p.groups, fa);
   } else {
     const int64_t nvec = g.n * g.c * p.cv;
     int64_t blocks = (nvec + kThreads * 4 - 1) / (kThreads * 4);
     const int64_t maxb = static_cast<int64_t>(DeviceCUs()) * 16;
     if (blocks > maxb) blocks = maxb;
     if (blocks < 1) blocks = 1;
-    TFMA_LAUNCH(kGrad ? "tfma_bn_grad_apply_nchw" : "tfma_bn_fwd_apply_nchw", (bn_nchw_apply_kernel<Tr, VEC, kGrad>), dim3(blocks),
+    TFMA_LAUNCH(kInfer ? "tfma_bn_infer_apply_nchw"
+                       : (kGrad ? "tfma_bn_grad_apply_nchw" : "tfma_bn_fwd_apply_nchw"),
+                (bn_nchw_apply_kernel<Tr, VEC, kGrad, kInfer>), dim3(blocks),
                        dim3(kThreads), 0, stream, static_cast<const S*>(x),
                        static_cast<const S*>(dy), static_cast<S*>(out), coef,
-                       nvec, p.cv, static_cast<int>(g.c));
+                       nvec, p.cv, static_cast<int>(g.c), fa);
   }
   return hipGetLastError();
 }
@@ -1976,6 +2231,59 @@ size_t partial_region_bytes(DType t, const BnGeometry& g) {
   return r > f ? r : f;
 }
 
+// The channel-per-workgroup NCHW kernel: training, 16-byte plane vectors, at
+// least one channel per CU (fewer channels leave CUs idle: the split path's
+// reduce spreads every channel over many workgroups), and offsets that fit
+// the kernel's 32-bit buffer offsets (rows up to 16 images past the tensor's
+// end).  TFMA_BN_NCHW_OWNED=0 (read per call) keeps the split path.
+bool nchw_owned_ok(const BnGeometry& g, int vec, int elem) {
+  if (g.nhwc || vec <= 1 || g.c < DeviceCUs()) return false;
+  const char* e = getenv("TFMA_BN_NCHW_OWNED");
+  if (e && e[0] == '0') return false;
+  const int64_t plane = g.h * g.w;
+  return plane % vec == 0 && (g.n + 16) * g.c * plane * elem < (int64_t{1} << 31);
+}
+
+template <class Tr, bool kGrad>
+hipError_t launch_nchw_owned(const BnGeometry& g, const void* x, const void* dy, void* out,
+                             const FinArgs& fin, hipStream_t stream) {
+  constexpr int KR = kGrad ? OwnedRows<Tr>::kGrad : OwnedRows<Tr>::kFwd;
+  constexpr int KL = fused_kl<Tr, kGrad>();
+  const auto kern = &bn_nchw_owned_kernel<Tr, kGrad, KR, KL>;
+  const size_t smem = static_cast<size_t>(KL) * (kGrad ? 2 : 1) * kFusedThreads * 16;
+  static bool attr_set[64] = {false};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  if (!attr_set[dev]) {
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
+    if (e != hipSuccess) return e;
+    attr_set[dev] = true;
+  }
+  NchwArgs na;
+  na.x = x;
+  na.dy = dy;
+  na.out = out;
+  na.n = g.n;
+  na.c = static_cast<int>(g.c);
+  na.plane = g.h * g.w;
+  na.pv = na.plane / Tr::kVec;
+  na.fin = fin;
+  t_last_plan = TFMA_FusedBatchNormPlan{};
+  t_last_plan.fused = 2;
+  t_last_plan.workgroups = static_cast<int32_t>(g.c);
+  t_last_plan.row_groups = 1;
+  t_last_plan.channel_tiles = static_cast<int32_t>(g.c);
+  t_last_plan.register_rows = KR;
+  t_last_plan.lds_rows = KL;
+  t_last_plan.slices = 1;
+  TFMA_LAUNCH(kGrad ? "tfma_bn_grad_nchw_owned" : "tfma_bn_fwd_nchw_owned", kern,
+              dim3(static_cast<unsigned>(g.c)), dim3(kFusedThreads), smem, stream, na);
+  return hipGetLastError();
+}
+
 bool ptr_aligned(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
 }
@@ -2010,22 +2318,23 @@ hipError_t forward_t(const BnGeometry& g, const BnFwdArgs& a, void* ws,
   fa.is_training = a.is_training;
   hipError_t e;
   FusedPlan fp;
+  if (a.is_training && nchw_owned_ok(g, p.vec, sizeof(typename Tr::S)))
+    return launch_nchw_owned<Tr, false>(g, a.x, nullptr, a.y, fa, stream);
   if (a.is_training && p.vec > 1 && fused_enabled() &&
       choose_fused_plan<Tr, false>(g, p.vec, &fp)) {
     return launch_fused<Tr, false>(fp, g, a.x, nullptr, a.y, fa,
                                                   stream);
   }
   note_split_plan(p);
-  if (a.is_training) {
-    e = p.vec == 1 ? launch_reduce<Tr, 1, false>(p, g, a.x, nullptr, nullptr, partial, stream)
-                   : launch_reduce<Tr, Tr::kVec, false>(p, g, a.x, nullptr, nullptr, partial, stream);
-    if (e != hipSuccess) return e;
-    e = launch_finalize<Tr, false>(p, fa, partial, coef, stream);
-  } else {
-    TFMA_LAUNCH("tfma_bn_infer_coef", bn_infer_coef_kernel, dim3((g.c + 255) / 256), dim3(256),
-                       0, stream, fa, coef);
-    e = hipGetLastError();
-  }
+  if (!a.is_training)
+    return p.vec == 1
+               ? launch_apply<Tr, 1, false, true>(p, g, a.x, nullptr, a.y, nullptr, stream, fa)
+               : launch_apply<Tr, Tr::kVec, false, true>(p, g, a.x, nullptr, a.y, nullptr, stream,
+                                                        fa);
+  e = p.vec == 1 ? launch_reduce<Tr, 1, false>(p, g, a.x, nullptr, nullptr, partial, stream)
+                 : launch_reduce<Tr, Tr::kVec, false>(p, g, a.x, nullptr, nullptr, partial, stream);
+  if (e != hipSuccess) return e;
+  e = launch_finalize<Tr, false>(p, fa, partial, coef, stream);
   if (e != hipSuccess) return e;
   return p.vec == 1 ? launch_apply<Tr, 1, false>(p, g, a.x, nullptr, a.y, coef, stream)
                     : launch_apply<Tr, Tr::kVec, false>(p, g, a.x, nullptr, a.y, coef, stream);
@@ -2057,6 +2366,8 @@ hipError_t grad_t(const BnGeometry& g, const BnGradArgs& a, void* ws,
   fa.reserve5_n = a.reserve5 ? a.reserve5_n : 0;
   fa.is_training = a.is_training;
   FusedPlan fp;
+  if (nchw_owned_ok(g, p.vec, sizeof(typename Tr::S)))
+    return launch_nchw_owned<Tr, true>(g, a.x, a.dy, a.dx, fa, stream);
   if (p.vec > 1 && fused_enabled() &&
       choose_fused_plan<Tr, true>(g, p.vec, &fp)) {
     return launch_fused<Tr, true>(fp, g, a.x, a.dy, a.dx, fa,

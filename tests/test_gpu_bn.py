@@ -149,6 +149,70 @@ def test_sliced_grad_matches_oracle(dev, monkeypatch, shape, dtype, tw, is_train
     assert torch.all(grad.reserve_space_4 == 0) and torch.all(grad.reserve_space_5 == 0)
 
 
+OWNED_CASES = [
+    ((4, 256, 7, 8), "float16"),      # 28 vectors per channel: most threads idle
+    ((64, 256, 28, 28), "bfloat16"),  # every row on chip
+    ((32, 512, 14, 14), "float32"),   # two channels per CU
+    ((8, 300, 12, 12), "float16"),    # C not a multiple of the CU count
+    ((2, 256, 64, 72), "float16"),    # a plane of 576 vectors: rows step within planes
+    ((64, 256, 32, 56), "bfloat16"),  # grad rows past registers + LDS: streamed
+    ((256, 256, 28, 28), "float16"),  # forward rows streamed too
+]
+
+
+@pytest.mark.parametrize("shape,dtype", OWNED_CASES)
+def test_nchw_owned_matches_oracle(dev, shape, dtype):
+    """NCHW training with at least one channel per CU runs the
+    channel-per-workgroup kernel (plan fused = 2) forward and backward;
+    against the oracle like the split path."""
+    if shape[1] < torch.cuda.get_device_properties(dev).multi_processor_count:
+        pytest.skip("fewer channels than CUs: split path")
+    rng = np.random.default_rng(zlib.crc32(repr((shape, dtype, "owned")).encode()))
+    eps = 1e-3
+    x, scale, offset, dy = _inputs(rng, shape, dtype, "NCHW", loc=0.5)
+    fwd, grad = _run_fwd_grad(dev, x, scale, offset, dy, dtype, "NCHW", eps)
+    plan = ops.fused_batch_norm_last_plan()
+    assert plan["fused"] == 2 and plan["workgroups"] == shape[1], plan
+    ry, rbm, rbv, rsm, rsv = oracle.bn_fwd(x, scale, offset, epsilon=eps, data_format="NCHW",
+                                          dtype=dtype)
+    assert_close(to_np(fwd.y, dtype), ry, dtype, ACT_TOL[dtype], "y")
+    for name, got, ref in (("batch_mean", fwd.batch_mean, rbm),
+                           ("batch_variance", fwd.batch_variance, rbv),
+                           ("reserve_space_1", fwd.reserve_space_1, rsm),
+                           ("reserve_space_2", fwd.reserve_space_2, rsv)):
+        assert_close(got.cpu().numpy(), ref, "float32", STAT_TOL, name)
+    rdx, rsb, rob = oracle.bn_grad(dy, x, scale, fwd.reserve_space_1.cpu().numpy(),
+                                   fwd.reserve_space_2.cpu().numpy(), epsilon=eps,
+                                   data_format="NCHW", dtype=dtype)
+    assert_close(to_np(grad.x_backprop, dtype), rdx, dtype, ACT_TOL[dtype], "x_backprop")
+    assert_close(grad.scale_backprop.cpu().numpy(), rsb, "float32", STAT_TOL, "scale_backprop")
+    assert_close(grad.offset_backprop.cpu().numpy(), rob, "float32", STAT_TOL, "offset_backprop")
+    assert torch.all(grad.reserve_space_4 == 0) and torch.all(grad.reserve_space_5 == 0)
+
+
+def test_nchw_owned_equals_split_path(dev, monkeypatch):
+    """The channel-per-workgroup kernel and the split path (forced with
+    TFMA_BN_NCHW_OWNED=0) agree: statistics to 1e-5 of their largest value
+    (the float32 partial sums of the two are taken in different orders, and
+    sums such as offset_backprop cancel), outputs within one ulp of their
+    largest value."""
+    rng = np.random.default_rng(5)
+    shape, dtype = (32, 256, 28, 28), "float16"
+    x, scale, offset, dy = _inputs(rng, shape, dtype, "NCHW")
+    f1, g1 = _run_fwd_grad(dev, x, scale, offset, dy, dtype, "NCHW", 1e-3)
+    assert ops.fused_batch_norm_last_plan()["fused"] == 2
+    monkeypatch.setenv("TFMA_BN_NCHW_OWNED", "0")
+    f2, g2 = _run_fwd_grad(dev, x, scale, offset, dy, dtype, "NCHW", 1e-3)
+    assert ops.fused_batch_norm_last_plan()["fused"] == 0
+    for name, a, b in (("mean", f1.reserve_space_1, f2.reserve_space_1),
+                       ("variance", f1.reserve_space_2, f2.reserve_space_2),
+                       ("scale_backprop", g1.scale_backprop, g2.scale_backprop),
+                       ("offset_backprop", g1.offset_backprop, g2.offset_backprop)):
+        assert_close(a.cpu().numpy(), b.cpu().numpy(), "float32", STAT_TOL, name)
+    for a, b in ((f1.y, f2.y), (g1.x_backprop, g2.x_backprop)):
+        assert (a.float() - b.float()).abs().max().item() <= 2 ** -9 * max(1.0, b.float().abs().max().item())
+
+
 def test_large_mean_statistics(dev):
     """|mean| >> std: the shifted sums must not cancel (variance to 1e-5)."""
     rng = np.random.default_rng(7)
