@@ -82,3 +82,39 @@ def test_bias_add_grad_unaligned_view(dev):
     torch.cuda.synchronize()
     assert_close(out.cpu().numpy(), oracle.bias_add_grad(x.cpu().numpy(), "NHWC", "float32"),
                  "float32", 1e-5, "unaligned")
+
+
+def test_bias_add_grad_two_streams(dev):
+    """Forty calls alternating between two streams, each with its own input
+    and workspace: every result matches its run on one stream bit for bit."""
+    xs = [torch.randn(2048 + 64 * k, 1024, device=dev).half() for k in range(40)]
+    want = [ops.BiasAddGrad(x) for x in xs]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    for s in (s1, s2):
+        s.wait_stream(torch.cuda.current_stream(dev))
+    got = []
+    for k, x in enumerate(xs):
+        with torch.cuda.stream(s1 if k % 2 else s2):
+            got.append(ops.BiasAddGrad(x))
+    torch.cuda.synchronize()
+    for k, (a, b) in enumerate(zip(got, want)):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), k
+
+
+def test_bias_add_grad_captured_equals_eager(dev):
+    """Recorded into a graph (stream capture), BiasAddGrad's replays give the
+    eager bits, with eager calls between the replays."""
+    x = torch.randn(4096, 2048, device=dev).half()
+    eager = ops.BiasAddGrad(x)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = ops.BiasAddGrad(x)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
+        again = ops.BiasAddGrad(x)
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int16), eager.view(torch.int16))
