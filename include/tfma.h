@@ -198,7 +198,10 @@ int TFMA_MusaResourceApplyAdamMixed(void* stream, TFMA_Tensor* var, TFMA_Tensor*
  * uploads it on the stream, so the workspace must stay allocated until the
  * launch has run.  The library also keeps device copies of the last few
  * tables per device: a call with the same tensors as an earlier one uploads
- * nothing and leaves the workspace untouched. */
+ * nothing and leaves the workspace untouched.  Recorded into a graph (stream
+ * capture), the call puts the table in the kernel arguments instead (64
+ * tensors per launch), so every replay updates the tensors of the recorded
+ * call; the workspace is then not used. */
 int TFMA_GroupedApplyAdamWorkspaceBytes(int n, const TFMA_Tensor* vars,
                                         size_t* bytes, TFMA_Status* status);
 

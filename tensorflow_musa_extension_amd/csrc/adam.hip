@@ -183,6 +183,35 @@ __global__ __launch_bounds__(kThreads) void adam_grouped_kernel(
                                 static_cast<const SG*>(e.grad) + start, len, p);
 }
 
+// Grouped variant for launches recorded into a graph: the table travels in
+// the kernel arguments, which a recorded launch keeps by value (a device
+// table staged per call could have changed by the time a replay reads it).
+// Workgroup b finds its tensor by a binary search over the chunk prefix sums,
+// read from the kernarg segment through its pointer (indexing the by-value
+// argument would copy it to scratch).
+template <class Tr, class Tg, bool kNesterov, bool kStream>
+__global__ __launch_bounds__(kThreads) void adam_grouped_args_kernel(
+    AdamArgTable tab, AdamP<typename Tr::C> p) {
+  using S = typename Tr::S;
+  using SG = typename Tg::S;
+  (void)tab;
+  const AdamArgTable* t = (const AdamArgTable*)__builtin_amdgcn_kernarg_segment_ptr();
+  const int64_t b = blockIdx.x;
+  int lo = 0, hi = t->count - 1;  // the last tensor whose first chunk is <= b
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (t->first_chunk[mid] <= b) lo = mid;
+    else hi = mid - 1;
+  }
+  const int64_t start = (b - t->first_chunk[lo]) * kGroupedAdamChunk;
+  int64_t len = t->n[lo] - start;
+  if (len > kGroupedAdamChunk) len = kGroupedAdamChunk;
+  adam_range<Tr, Tg, kNesterov, kStream>(static_cast<S*>(t->var[lo]) + start,
+                                         static_cast<S*>(t->m[lo]) + start,
+                                         static_cast<S*>(t->v[lo]) + start,
+                                         static_cast<const SG*>(t->grad[lo]) + start, len, p);
+}
+
 template <class Tr>
 AdamP<typename Tr::C> make_params(const AdamScalars& s) {
   using C = typename Tr::C;
@@ -234,7 +263,66 @@ hipError_t launch_grouped(const AdamTensorEntry* table, int n_tensors,
   return hipGetLastError();
 }
 
+// The table in kernel arguments, kArgTableTensors tensors per launch.
+template <class Tr, class Tg, bool kNesterov>
+hipError_t launch_grouped_args(const AdamTensorEntry* entries, int n_tensors,
+                               const AdamScalars& s, hipStream_t stream) {
+  const auto p = make_params<Tr>(s);
+  for (int i0 = 0; i0 < n_tensors; i0 += kArgTableTensors) {
+    const int cnt = n_tensors - i0 < kArgTableTensors ? n_tensors - i0 : kArgTableTensors;
+    AdamArgTable t{};
+    int64_t chunks = 0;
+    for (int k = 0; k < cnt; ++k) {
+      const AdamTensorEntry& e = entries[i0 + k];
+      t.first_chunk[k] = chunks;
+      t.var[k] = e.var;
+      t.m[k] = e.m;
+      t.v[k] = e.v;
+      t.grad[k] = e.grad;
+      t.n[k] = e.n;
+      chunks += (e.n + kGroupedAdamChunk - 1) / kGroupedAdamChunk;
+    }
+    t.first_chunk[cnt] = chunks;
+    t.count = cnt;
+    if (chunks == 0) continue;
+    if (chunks * kGroupedAdamChunk >= kStreamElems)
+      TFMA_LAUNCH("tfma_adam_grouped", (adam_grouped_args_kernel<Tr, Tg, kNesterov, true>),
+                  dim3(chunks), dim3(kThreads), 0, stream, t, p);
+    else
+      TFMA_LAUNCH("tfma_adam_grouped", (adam_grouped_args_kernel<Tr, Tg, kNesterov, false>),
+                  dim3(chunks), dim3(kThreads), 0, stream, t, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 }  // namespace
+
+hipError_t LaunchGroupedApplyAdamArgs(DType t, DType tg, const AdamTensorEntry* entries,
+                                      int n_tensors, const AdamScalars& s, bool nesterov,
+                                      hipStream_t stream) {
+  if (n_tensors <= 0) return hipSuccess;
+#define TFMA_GADAM_ARGS(TR, TG)                                                        \
+  return nesterov ? launch_grouped_args<TR, TG, true>(entries, n_tensors, s, stream)  \
+                  : launch_grouped_args<TR, TG, false>(entries, n_tensors, s, stream);
+  if (tg != t) {
+    if (t != DType::kF32) return hipErrorInvalidValue;
+    switch (tg) {
+      case DType::kF16: TFMA_GADAM_ARGS(TF32, TF16)
+      case DType::kBF16: TFMA_GADAM_ARGS(TF32, TBF16)
+      default: return hipErrorInvalidValue;
+    }
+  }
+  switch (t) {
+    case DType::kF32: TFMA_GADAM_ARGS(TF32, TF32)
+    case DType::kF16: TFMA_GADAM_ARGS(TF16, TF16)
+    case DType::kBF16: TFMA_GADAM_ARGS(TBF16, TBF16)
+    case DType::kF64: TFMA_GADAM_ARGS(TF64, TF64)
+  }
+#undef TFMA_GADAM_ARGS
+  return hipErrorInvalidValue;
+}
 
 hipError_t LaunchApplyAdam(DType t, DType tg, void* var, void* m, void* v,
                            const void* grad, int64_t n, const AdamScalars& s,

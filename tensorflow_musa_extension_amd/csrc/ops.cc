@@ -1138,16 +1138,15 @@ int TFMA_GroupedResourceApplyAdam(void* stream, int n, TFMA_Tensor* vars, TFMA_T
     return set_status(status, TFMA_INVALID_ARGUMENT,
                       "MusaGroupedResourceApplyAdam: workspace of %zu bytes required, got %zu",
                       need, workspace ? workspace_bytes : size_t(0));
-  if (!table.empty()) {
-    // The tensor table is staged per call (a pinned ring slot or a cached
-    // device copy, both reused by later calls), so a graph replay would read
-    // a table that has since changed.
+  // Recorded into a graph, the table travels in the kernel arguments: the
+  // staged device table (a pinned ring slot or a cached copy, both reused by
+  // later calls) could have changed by the time a replay reads it.
+  bool recorded = false;
+  {
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(as_stream(stream), &cap) == hipSuccess &&
-        cap != hipStreamCaptureStatusNone)
-      return set_status(status, TFMA_UNIMPLEMENTED,
-                        "MusaGroupedResourceApplyAdam cannot be recorded into a graph: its tensor "
-                        "table is staged per call; use ResourceApplyAdam per tensor there");
+    const hipError_t ce = hipStreamIsCapturing(as_stream(stream), &cap);
+    if (ce != hipSuccess) return hip_status(status, ce, "MusaGroupedResourceApplyAdam");
+    recorded = cap != hipStreamCaptureStatusNone;
   }
   VarLocks locks;
   if (use_locking) {
@@ -1159,6 +1158,11 @@ int TFMA_GroupedResourceApplyAdam(void* stream, int n, TFMA_Tensor* vars, TFMA_T
     locks.lock();
   }
   if (table.empty()) return ok(status);
+  if (recorded)
+    return hip_status(status,
+                      LaunchGroupedApplyAdamArgs(t, tg, table.data(), static_cast<int>(table.size()),
+                                                 s, use_nesterov != 0, as_stream(stream)),
+                      "MusaGroupedResourceApplyAdam");
   // Blob: entries, then the tensor index of every chunk.
   std::vector<uint8_t> blob(grouped_table_bytes(static_cast<int>(table.size()), chunks));
   memcpy(blob.data(), table.data(), table.size() * sizeof(AdamTensorEntry));

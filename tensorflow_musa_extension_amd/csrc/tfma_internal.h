@@ -76,6 +76,22 @@ struct AdamTensorEntry {
 };
 constexpr int64_t kGroupedAdamChunk = 8192;  // elements per workgroup chunk
 
+// The tensor table in kernel arguments (launches recorded into a graph):
+// kArgTableTensors tensors per launch, 3.1 KB of arguments.
+constexpr int kArgTableTensors = 64;
+struct AdamArgTable {
+  int64_t first_chunk[kArgTableTensors + 1];  // chunk prefix sums; [count] = total
+  void* var[kArgTableTensors];
+  void* m[kArgTableTensors];
+  void* v[kArgTableTensors];
+  const void* grad[kArgTableTensors];
+  int64_t n[kArgTableTensors];
+  int32_t count;
+};
+hipError_t LaunchGroupedApplyAdamArgs(DType t, DType tg, const AdamTensorEntry* entries,
+                                      int n_tensors, const AdamScalars& s, bool nesterov,
+                                      hipStream_t stream);
+
 hipError_t LaunchGroupedApplyAdam(DType t, DType tg, const AdamTensorEntry* dev_table,
                                   int n_tensors, int64_t total_chunks,
                                   const AdamScalars& s, bool nesterov,

@@ -3,10 +3,12 @@ and replayed.  Every replay must equal the eager run of the same iteration
 bit for bit; replays are separated by eager work (other fused BatchNorm
 launches, which use the eager barrier counters) and synchronizations, as a
 training loop would run them."""
+import numpy as np
 import pytest
 import torch
 
 import tensorflow_musa_extension_amd as tfma
+from oracle import oracle
 
 pytestmark = pytest.mark.gpu
 ops = tfma.raw_ops
@@ -89,15 +91,38 @@ def test_recorded_training_step_replays(dev, monkeypatch, shape, slice_tw):
     assert not ops.fused_batch_norm_barrier_timed_out()
 
 
-def test_grouped_adam_refuses_capture(dev):
-    vs = [torch.zeros(1000, device=dev) for _ in range(3)]
-    ms = [torch.zeros(1000, device=dev) for _ in range(3)]
-    vvs = [torch.zeros(1000, device=dev) for _ in range(3)]
-    gs = [torch.ones(1000, device=dev) for _ in range(3)]
-    ops.MusaGroupedResourceApplyAdam(vs, ms, vvs, gs, 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7)
+@pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
+def test_grouped_adam_recorded_replays(dev, gdtype):
+    """MusaGroupedResourceApplyAdam recorded into a graph (its tensor table
+    travels in the kernel arguments: 100 tensors, two launches) and replayed
+    three times, with eager grouped calls on other tensors between the
+    replays: every replay applies one Adam step, bit for bit the oracle's."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(41)
+    sizes = [1 + (37 * k) % 5000 for k in range(100)]
+    vars_ = [0.02 * torch.randn(n, generator=g, device=dev) for n in sizes]
+    ms = [torch.zeros(n, device=dev) for n in sizes]
+    vs = [torch.zeros(n, device=dev) for n in sizes]
+    grads = [(1e-3 * torch.randn(n, generator=g, device=dev)).to(gdtype) for n in sizes]
+    refs = [[t.cpu().numpy().copy() for t in (v, m, w)] for v, m, w in zip(vars_, ms, vs)]
+    other = [torch.randn(4096, device=dev) for _ in range(3)]
+    om = [torch.zeros(4096, device=dev) for _ in range(3)]
+    ov = [torch.zeros(4096, device=dev) for _ in range(3)]
+    og = [torch.randn(4096, device=dev) for _ in range(3)]
+    b1p, b2p, lr, b1, b2, eps = 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7
+    f32 = lambda x: float(np.float32(x))
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with pytest.raises(tfma.UnimplementedError, match="cannot be recorded into a graph"):
-        with torch.cuda.graph(graph):
-            ops.MusaGroupedResourceApplyAdam(vs, ms, vvs, gs, 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7)
+    with torch.cuda.graph(graph):
+        ops.MusaGroupedResourceApplyAdam(vars_, ms, vs, grads, b1p, b2p, lr, b1, b2, eps)
     torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+        ops.MusaGroupedResourceApplyAdam(other, om, ov, og, b1p, b2p, lr, b1, b2, eps)
+        torch.cuda.synchronize()
+        for (rv, rm, rw), gt in zip(refs, grads):
+            gn = gt.float().cpu().numpy()
+            oracle.adam(rv, rm, rw, gn, f32(b1p), f32(b2p), f32(lr), f32(b1), f32(b2), f32(eps))
+    for i, (v, m, w) in enumerate(zip(vars_, ms, vs)):
+        for name, t, r in (("var", v, refs[i][0]), ("m", m, refs[i][1]), ("v", w, refs[i][2])):
+            assert np.array_equal(t.cpu().numpy().view(np.uint32), r.view(np.uint32)), (i, name)
