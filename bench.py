@@ -564,6 +564,37 @@ def cpu_baseline(torch, dev, min_seconds=10.0, component_seconds=1.5):
             "components": comps}
 
 
+def stream_copy_ceiling(torch, ops, dev, sizes=(268435456, 1 << 30, 8 << 30), reps=5):
+    """The measured stream-copy ceiling (informational; every percentage is
+    against 8 TB/s): a plain streaming copy (the library's TFMA_StreamCopy,
+    16-byte non-temporal loads and stores) of each size, each rep after the
+    1 GiB read that evicts the Infinity Cache; read+write bytes per second,
+    median of `reps`."""
+    flush = torch.ones(1 << 28, device=dev)
+    sink = torch.empty((), device=dev)
+    out = {}
+    for nbytes in sizes:
+        src = torch.ones(nbytes // 4, device=dev)
+        dst = torch.empty_like(src)
+        ops.stream_copy(dst, src)
+        ts = []
+        for _ in range(reps):
+            torch.sum(flush, dim=0, out=sink)
+            a, b = _events(torch)
+            a.record()
+            ops.stream_copy(dst, src)
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        ts.sort()
+        out[f"{nbytes >> 20}MiB"] = round(2 * nbytes / (ts[len(ts) // 2] / 1e3) / 1e9, 1)
+        del src, dst
+    torch.cuda.empty_cache()
+    return {"GB/s": out, "note": "informational: read+write bytes of a plain 16-byte "
+            "non-temporal streaming copy, Infinity Cache flushed; percentages are against "
+            f"{PEAK_GBPS:.0f} GB/s"}
+
+
 def calibrate(torch, dev):
     """Five plain 256 MiB device copies (torch copy_): the reference reads and
     writes that scale a rocprofv3 --pmc run's FETCH_SIZE / WRITE_SIZE."""
@@ -665,6 +696,7 @@ def main():
     if args.calibrate:
         calibrate(torch, dev)
     if not args.no_components:
+        result["stream_copy_ceiling"] = stream_copy_ceiling(torch, ops, dev)
         result["components"] = components(torch, ops, dev)
         result["host_path"] = host_path(torch, tfma, dev)
     if not args.no_cpu:

@@ -367,6 +367,14 @@ void TFMA_FreeBuffer(void* buffer);
 int TFMA_TraceEnable(const char* name_substr, TFMA_Status* status);
 int TFMA_TraceRead(double* total_ms, int64_t* launches, TFMA_Status* status);
 
+/* Device-to-device copy of `bytes` (a multiple of 16; both pointers 16-byte
+ * aligned, else INVALID_ARGUMENT) by a plain streaming kernel: 16-byte
+ * non-temporal loads and stores, grid-stride.  A measuring stick, not an op:
+ * bench.py reports its rate as the stream-copy ceiling the kernels' rates sit
+ * beside.  No reference counterpart. */
+int TFMA_StreamCopy(void* stream, void* dst, const void* src, uint64_t bytes,
+                    TFMA_Status* status);
+
 /* The fused BatchNorm kernel assumes its workgroups (one or two per CU) are
  * all resident at once; a wave waiting for another workgroup's partials or
  * coefficients gives up after a bounded spin (~0.5 s), which only happens

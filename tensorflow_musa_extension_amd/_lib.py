@@ -101,6 +101,7 @@ SIGNATURES = {
     "TFMA_FreeBuffer": [_vp],
     "TFMA_TraceEnable": [_cs, _S],
     "TFMA_TraceRead": [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), _S],
+    "TFMA_StreamCopy": [_vp, _vp, _vp, ctypes.c_uint64, _S],
     "TFMA_LastKernelName": [],
     "TFMA_FusedBatchNormBarrierTimedOut": [ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, _S],
     "TFMA_FusedBatchNormLastPlan": [ctypes.POINTER(TFMA_FusedBatchNormPlan), _S],

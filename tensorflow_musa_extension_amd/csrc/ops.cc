@@ -677,6 +677,21 @@ extern "C" {
 
 const char* TFMA_Version(void) { return "tfma 0.1 gfx950"; }
 
+int TFMA_StreamCopy(void* stream, void* dst, const void* src, uint64_t bytes,
+                    TFMA_Status* status) {
+  if (bytes == 0) return ok(status);
+  if (!dst || !src)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "StreamCopy: null pointer");
+  if (bytes % 16 != 0 || (reinterpret_cast<uintptr_t>(dst) & 15) != 0 ||
+      (reinterpret_cast<uintptr_t>(src) & 15) != 0)
+    return set_status(status, TFMA_INVALID_ARGUMENT,
+                      "StreamCopy: bytes (%llu) and both pointers must be 16-byte multiples",
+                      static_cast<unsigned long long>(bytes));
+  return hip_status(status,
+                    LaunchStreamCopy(dst, src, static_cast<int64_t>(bytes), as_stream(stream)),
+                    "StreamCopy");
+}
+
 int TFMA_GetDeviceCount(int* count, TFMA_Status* status) {
   if (!count) return set_status(status, TFMA_INVALID_ARGUMENT, "count is null");
   int n = 0;

@@ -110,6 +110,9 @@ constexpr size_t kBiasAddGradScratchBytes = size_t(4) << 20;
 hipError_t BiasAddGradScratch(void** ptr);
 // Zero-fills n bytes with a kernel (capturable, unlike a memset node).
 hipError_t LaunchZeroBytes(void* p, int64_t n, hipStream_t stream);
+// 16-byte non-temporal streaming copy (bytes a multiple of 16, both pointers
+// 16-byte aligned): the measured ceiling bench.py reports.
+hipError_t LaunchStreamCopy(void* dst, const void* src, int64_t bytes, hipStream_t stream);
 
 // ---------------------------------------------------------------------------
 // Elementwise

@@ -390,6 +390,18 @@ def MusaShiftedAffineMap(data_left, mask, sliced_var_right, out=None):
 # ---------------------------------------------------------------------------
 # Tracing
 # ---------------------------------------------------------------------------
+def stream_copy(dst, src):
+    """dst <- src (same byte count, a multiple of 16, 16-byte aligned) through
+    the library's streaming-copy kernel (TFMA_StreamCopy): the measuring stick
+    for the stream-copy ceiling, not an op."""
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nbytes:
+        raise ValueError("stream_copy: dst and src differ in size")
+    _call("TFMA_StreamCopy", _stream(src), ctypes.c_void_p(dst.data_ptr()),
+          ctypes.c_void_p(src.data_ptr()), nbytes)
+    return dst
+
+
 def trace_enable(name_substr):
     lib = _lib.load()
     status = _lib.TFMA_Status()

@@ -135,3 +135,15 @@ def test_staging_pool_reuses_blocks(dev):
     assert blocks <= 32 and allocs == blocks
     assert reuses >= 40 * 2 - 32
     assert pending == 0
+
+
+def test_stream_copy(dev):
+    """TFMA_StreamCopy (the bench's measuring stick) copies exactly, and
+    rejects sizes and pointers that are not 16-byte multiples."""
+    src = torch.randint(0, 2**31 - 1, ((64 << 20) // 4 + 12,), dtype=torch.int32, device=dev)
+    dst = torch.zeros_like(src)
+    tfma.raw_ops.stream_copy(dst, src)
+    torch.cuda.synchronize()
+    assert torch.equal(dst, src)
+    with pytest.raises(tfma.InvalidArgumentError, match="16-byte"):
+        tfma.raw_ops.stream_copy(dst[1:5], src[1:5])
