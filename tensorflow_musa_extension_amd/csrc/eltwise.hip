@@ -34,7 +34,10 @@ constexpr int kThreads = 256;
 enum Kind : int {
   kFullK = 0, kScalarK = 1, kRowK = 2, kChanK = 3, kRowOddK = 4, kGatherK = 5, kGatherGlobalK = 6
 };
-constexpr uint32_t kStageBytes = 20480;  // per staged operand (periods up to 8192 half, 4096 float with the pad)
+// Per staged operand: the padded copy (periods up to 8191 half, 4095 float)
+// and 16 bytes the half gather may read past its end (never used).
+constexpr uint32_t kStageBytes = 20496;
+constexpr uint32_t kStageSlack = 16;
 constexpr bool staged_kind(int k) { return k == kRowOddK || k == kGatherK; }
 
 // LDS slot of element e of a staged odd-period row operand.  Consecutive
@@ -109,8 +112,29 @@ __device__ inline void fetch(const Operand& o, const S* p, uint32_t i0, S (&out)
     // p is the padded LDS copy (odd_slot).
     uint32_t idx = i0 - o.div_period.div(i0) * o.period;
     if (idx + V <= o.period) {  // no wrap: consecutive elements from one base
+      if constexpr (sizeof(S) == 2 && V == 8) {
+        // Eight halves from the five 32-bit words that cover them (word d of
+        // the copy sits at d + d / 4: one pad word per four), realigned by
+        // one funnel shift per output word - 0 or 16 bits by idx's parity.
+        // (Eight 16-bit reads with their own slot arithmetic made the kernel
+        // issue-bound.)  For an even idx the fifth word is read and unused.
+        const uint32_t* pw = reinterpret_cast<const uint32_t*>(p);
+        const uint32_t d0 = idx >> 1;
+        uint32_t w[5];
 #pragma unroll
-      for (int j = 0; j < V; ++j) out[j] = p[odd_slot<sizeof(S)>(idx + j)];
+        for (int k = 0; k < 5; ++k) {
+          const uint32_t d = d0 + k;
+          w[k] = pw[d + (d >> 2)];
+        }
+        const uint32_t sh = (idx & 1u) << 4;
+        uint32_t ow[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ow[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
+        __builtin_memcpy(out, ow, 16);
+      } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j) out[j] = p[odd_slot<sizeof(S)>(idx + j)];
+      }
     } else {
 #pragma unroll
       for (int j = 0; j < V; ++j) {
@@ -323,7 +347,7 @@ Operand make_operand(const BcastOperand& o, int elem_bytes, int V,
         r.kind = kRowK;
       } else if (o.inner % V == 0) {
         r.kind = kChanK;
-      } else if (o.inner == 1 ? odd_stage_bytes(r.period, elem_bytes) > kStageBytes
+      } else if (o.inner == 1 ? odd_stage_bytes(r.period, elem_bytes) + kStageSlack > kStageBytes
                               : o.period * elem_bytes > kStageBytes) {
         r.kind = kGatherGlobalK;
       } else if (o.inner == 1) {
@@ -362,7 +386,7 @@ void launch_vec(const Operand& ob, const Operand& oc, const typename Tr::S* a,
   // workgroups keep that copy cheap.
   constexpr int kEs = sizeof(typename Tr::S);
   const size_t lds = sc ? (sb ? 2 : 1) * kStageBytes
-                        : (sb ? (KB == kRowOddK ? odd_stage_bytes(ob.period, kEs)
+                        : (sb ? (KB == kRowOddK ? odd_stage_bytes(ob.period, kEs) + kStageSlack
                                                 : ob.period * kEs)
                               : 0);
   int64_t blocks = grid_for(n / V, U);
