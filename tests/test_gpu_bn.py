@@ -599,6 +599,16 @@ assert ops.last_kernel_name() == "tfma_bn_grad_fused"
 torch.cuda.synchronize()
 assert torch.isnan(g.x_backprop.float()).all() and torch.isnan(g.scale_backprop).all()
 expect_internal(fwd, "forward after grad")
+# A sliced gradient (forced: 4 slices of 64 channels, two waits per slice)
+# gives up the same way.
+import os
+os.environ["TFMA_BN_SLICE_TW"] = "8"
+gs = ops.FusedBatchNormGradV3(dy, x, scale, f.reserve_space_1, f.reserve_space_2,
+                              f.reserve_space_3, epsilon=1e-3)
+assert ops.fused_batch_norm_last_plan()["slices"] == 4
+torch.cuda.synchronize()
+assert torch.isnan(gs.x_backprop.float()).all() and torch.isnan(gs.scale_backprop).all()
+expect_internal(fwd, "forward after sliced grad")
 print("give-up ok", flush=True)
 """
 
