@@ -422,16 +422,63 @@ struct FinArgs {
   bool is_training;
 };
 
-// Final statistics and apply coefficients of channel ch from the double
-// sums s1, s2 over all of the channel's elements; writes the op's per-channel
-// outputs and returns the coefficients {mean, a, b, c2} for apply_one().
+// The per-channel inputs finish_channel() needs besides the sums, loaded
+// where they are used (FinLoad) or all at once ahead of the sums (FinIn,
+// from fin_inputs()), so a caller can issue the loads before it waits for
+// the sums and their latency overlaps the wait (the forward's shift K
+// re-reads five elements of x).
+template <class Tr>
+struct FinLoad {
+  const FinArgs& a;
+  int ch;
+  __device__ float kshift() const {
+    return chan_shift<Tr>(static_cast<const typename Tr::S*>(a.x), ch, a.n, a.c, a.k_stride);
+  }
+  __device__ float scale() const { return a.scale[ch]; }
+  __device__ float offset() const { return a.offset[ch]; }
+  __device__ float mean_in() const { return a.mean_in[ch]; }
+  __device__ float var_in() const { return a.var_in[ch]; }
+};
+
+struct FinIn {
+  float k, sc, of, mi, vi;  // shift (forward), scale, offset (forward), mean_in, var_in
+  __device__ float kshift() const { return k; }
+  __device__ float scale() const { return sc; }
+  __device__ float offset() const { return of; }
+  __device__ float mean_in() const { return mi; }
+  __device__ float var_in() const { return vi; }
+};
+
+// FinIn of channel ch; kshift = the forward's shift K (unused by the grad).
+// mean_in and var_in are read by the grad, and by a forward whose
+// exponential_avg_factor is not 1 (only then are they given).
 template <class Tr, bool kGrad>
-__device__ inline float4 finish_channel(const FinArgs& a, int ch, double s1, double s2) {
+__device__ inline FinIn fin_inputs(const FinArgs& a, int ch, float kshift) {
+  FinIn p{kshift, 0.f, 0.f, 0.f, 0.f};
+  if (kGrad || a.f != 1.0f) {
+    p.mi = a.mean_in[ch];
+    p.vi = a.var_in[ch];
+  }
+  p.sc = a.scale[ch];
+  if constexpr (!kGrad) p.of = a.offset[ch];
+  return p;
+}
+
+template <class Tr, bool kGrad>
+__device__ inline FinIn fin_inputs(const FinArgs& a, int ch) {
+  return fin_inputs<Tr, kGrad>(a, ch, kGrad ? 0.f : FinLoad<Tr>{a, ch}.kshift());
+}
+
+// Final statistics and apply coefficients of channel ch from the double
+// sums s1, s2 over all of the channel's elements and its inputs p (FinIn or
+// FinLoad); writes the op's per-channel outputs and returns the coefficients
+// {mean, a, b, c2} for apply_one().
+template <class Tr, bool kGrad, class In>
+__device__ inline float4 finish_channel(const FinArgs& a, int ch, double s1, double s2,
+                                        const In& p) {
   const double n = static_cast<double>(a.n);
   if constexpr (!kGrad) {
-    const float kshift =
-        chan_shift<Tr>(static_cast<const typename Tr::S*>(a.x), ch, a.n, a.c, a.k_stride);
-    const double mean = static_cast<double>(kshift) + s1 / n;
+    const double mean = static_cast<double>(p.kshift()) + s1 / n;
     double m2 = s2 - s1 * s1 / n;
     if (m2 < 0.0) m2 = 0.0;
     const float mean_f = static_cast<float>(mean);
@@ -446,24 +493,29 @@ __device__ inline float4 finish_channel(const FinArgs& a, int ch, double s1, dou
       a.batch_var[ch] = var_f * adj;
     } else {
       const float omf = 1.0f - a.f;
-      a.batch_mean[ch] = a.mean_in[ch] * omf + mean_f * a.f;
-      a.batch_var[ch] = a.var_in[ch] * omf + (var_f * adj) * a.f;
+      a.batch_mean[ch] = p.mean_in() * omf + mean_f * a.f;
+      a.batch_var[ch] = p.var_in() * omf + (var_f * adj) * a.f;
     }
     const float inv = 1.0f / __builtin_sqrtf(var_f + a.eps);
-    return make_float4(mean_f, inv * a.scale[ch], a.offset[ch], 0.f);
+    return make_float4(mean_f, inv * p.scale(), p.offset(), 0.f);
   } else {
-    const float mu = a.mean_in[ch];
-    const float k = 1.0f / __builtin_sqrtf(a.var_in[ch] + a.eps);
+    const float mu = p.mean_in();
+    const float k = 1.0f / __builtin_sqrtf(p.var_in() + a.eps);
     a.offset_bp[ch] = static_cast<float>(s1);
     a.scale_bp[ch] = static_cast<float>(s2 * static_cast<double>(k));
     if (a.is_training) {
       const float mean_dy = static_cast<float>(s1 / n);
       const float mean_dyxc = static_cast<float>(s2 / n);
-      return make_float4(mu, a.scale[ch] * k, mean_dy, (k * k) * mean_dyxc);
+      return make_float4(mu, p.scale() * k, mean_dy, (k * k) * mean_dyxc);
     } else {
-      return make_float4(mu, a.scale[ch] * k, 0.f, 0.f);
+      return make_float4(mu, p.scale() * k, 0.f, 0.f);
     }
   }
+}
+
+template <class Tr, bool kGrad>
+__device__ inline float4 finish_channel(const FinArgs& a, int ch, double s1, double s2) {
+  return finish_channel<Tr, kGrad>(a, ch, s1, s2, FinLoad<Tr>{a, ch});
 }
 
 // Zero-filled side outputs (reserve_space_3 of the forward, reserve_space_4/5
@@ -1069,6 +1121,8 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   // workgroup finishes one of its channels at a time, so all of a
   // workgroup's partial loads are in flight together.
   for (int ch = cs0 + blockIdx.x + wave * gridDim.x; ch < cs1; ch += kWaves * gridDim.x) {
+    // The channel's other inputs, in flight while its partials are polled.
+    const FinIn fin_in = fin_inputs<Tr, kGrad>(a.fin, ch);
     double t1 = 0.0, t2 = 0.0;
     {
       // Lane l sums groups l, l + 64, ... (at most kMaxGroups / 64 of them):
@@ -1120,7 +1174,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     }
     const double2 w = wave_sum(t1, t2);
     if (lane == 0) {
-      const float4 cfc = finish_channel<Tr, kGrad>(a.fin, ch, w.x, w.y);
+      const float4 cfc = finish_channel<Tr, kGrad>(a.fin, ch, w.x, w.y, fin_in);
       const float v4[4] = {cfc.x, cfc.y, cfc.z, cfc.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -1521,6 +1575,11 @@ __global__ __launch_bounds__(kFusedThreads) void bn_nchw_owned_kernel(NchwArgs a
     for (int u = 0; u < U; ++u)
       if (q + u < nk) accum_words<Tr, kGrad>(xw[u], dw[u], k, s1, s2);
   }
+  // The forward's other inputs (K is kk; scale, offset in flight during the
+  // reduction below).  The grad loads its inputs after the reduction: loaded
+  // here, they cost the grad kernels registers they do not have.
+  FinIn fin_in{};
+  if constexpr (!kGrad) fin_in = fin_inputs<Tr, kGrad>(a.fin, ch, kk);
   // The workgroup's sums: per thread in float, then in double across the
   // threads in a fixed order (wave shuffles, then the waves in order).
   float ta = 0.f, tb = 0.f;
@@ -1543,7 +1602,11 @@ __global__ __launch_bounds__(kFusedThreads) void bn_nchw_owned_kernel(NchwArgs a
       t1 += red[0][i];
       t2 += red[1][i];
     }
-    const float4 cf = finish_channel<Tr, kGrad>(a.fin, ch, t1, t2);
+    float4 cf;
+    if constexpr (kGrad)
+      cf = finish_channel<Tr, kGrad>(a.fin, ch, t1, t2);
+    else
+      cf = finish_channel<Tr, kGrad>(a.fin, ch, t1, t2, fin_in);
     cfs[0] = cf.x;
     cfs[1] = cf.y;
     cfs[2] = cf.z;
