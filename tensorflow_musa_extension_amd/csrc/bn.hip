@@ -1003,15 +1003,19 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   uint4 dr[kGrad ? KR : 1];
   uint4 xl[KL];
   uint4 dl[kGrad ? KL : 1];
+  // These rows are never read from memory again (phase 3 takes them from
+  // registers and LDS), so their loads are non-temporal: they leave the
+  // Infinity Cache to the streamed rows that phase 3 re-reads (measured: the
+  // 16-op cfg2 step 1.825 -> 1.802 ms, the 56x56 grads 3 % faster).
 #pragma unroll
   for (int q = 0; q < KR; ++q) {
-    xr[q] = bld16(rx, roff(q));
-    if constexpr (kGrad) dr[q] = bld16(rd, roff(q));
+    xr[q] = bld16_last(rx, roff(q));
+    if constexpr (kGrad) dr[q] = bld16_last(rd, roff(q));
   }
 #pragma unroll
   for (int q = 0; q < KL; ++q) {
-    xl[q] = bld16(rx, roff(KR + q));
-    if constexpr (kGrad) dl[q] = bld16(rd, roff(KR + q));
+    xl[q] = bld16_last(rx, roff(KR + q));
+    if constexpr (kGrad) dl[q] = bld16_last(rd, roff(KR + q));
   }
   if constexpr (!kGrad) shift_words<Tr>(kw, k);
   // After its phase-1 use a register row is made opaque, so the compiler
