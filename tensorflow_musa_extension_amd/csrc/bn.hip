@@ -896,6 +896,186 @@ __device__ inline void st16(void* p, const uint4& v) {
   __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(p));
 }
 
+// Phase-1 end of a channel tile: the threads' partial sums, summed over the
+// row lanes of each wave with shuffles, then over the waves through LDS
+// (`red`), published as one epoch-tagged pair of words per channel.
+template <int VEC>
+__device__ __forceinline__ void publish_partials(const FusedArgs& a, float2* red,
+                                                 float (&s1)[VEC], float (&s2)[VEC], int tid,
+                                                 int width, int ct, int64_t g, uint64_t etag) {
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    if (off < (1 << a.tx_shift)) break;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      s1[j] += __shfl_xor(s1[j], off, 64);
+      s2[j] += __shfl_xor(s2[j], off, 64);
+    }
+  }
+  if (lane < (1 << a.tx_shift)) {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) red[wave * width + lane * VEC + j] = make_float2(s1[j], s2[j]);
+  }
+  __syncthreads();
+  if (tid < width && static_cast<int64_t>(ct) * width + tid < static_cast<int64_t>(a.cv) * VEC) {
+    float sa = 0.f, sb = 0.f;
+#pragma unroll
+    for (int w = 0; w < kFusedThreads / 64; ++w) {
+      const float2 v = red[w * width + tid];
+      sa += v.x;
+      sb += v.y;
+    }
+    const int64_t slot = g * a.c + static_cast<int64_t>(ct) * width + tid;
+    store_shared(a.eslots + 2 * slot, etag | __builtin_bit_cast(uint32_t, sa));
+    store_shared(a.eslots + 2 * slot + 1, etag | __builtin_bit_cast(uint32_t, sb));
+  }
+}
+
+// Phase 2 for channels [cs0, cs1): channel ch is finished by wave
+// (ch - cs0) / gridDim.x of workgroup (ch - cs0) % gridDim.x, one channel
+// at a time per wave, so all of a workgroup's partial loads are in flight
+// together.  A wait that runs out stores the launch's epoch into the
+// host-visible give-up word and poisons the channel.
+template <class Tr, bool kGrad>
+__device__ __forceinline__ void finish_channels(const FusedArgs& a, int cs0, int cs1, int wave,
+                                                int lane, uint32_t wtag, uint64_t etag,
+                                                unsigned epoch) {
+  constexpr int kWaves = kFusedThreads / 64;
+  auto give_up = [&]() {
+    __hip_atomic_store(a.gave_up, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  };
+  for (int ch = cs0 + blockIdx.x + wave * gridDim.x; ch < cs1; ch += kWaves * gridDim.x) {
+    // The channel's other inputs, in flight while its partials are polled.
+    const FinIn fin_in = fin_inputs<Tr, kGrad>(a.fin, ch);
+    double t1 = 0.0, t2 = 0.0;
+    {
+      // Lane l sums groups l, l + 64, ... (at most kMaxGroups / 64 of them):
+      // all their slots are loaded at once, then the ones not yet tagged
+      // with this launch's epoch are polled again.
+      const uint64_t tag = static_cast<uint64_t>(wtag) << 32;
+      uint64_t v1[kEpochPerLane], v2[kEpochPerLane];
+#pragma unroll
+      for (int i = 0; i < kEpochPerLane; ++i) {
+        const int64_t gg = lane + 64 * i;
+        v1[i] = v2[i] = tag;
+        if (gg < a.groups) {
+          v1[i] = load_shared(a.eslots + 2 * (gg * a.c + ch));
+          v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
+        }
+      }
+      unsigned spins = 0;
+      bool lost = false;
+      while (true) {
+        bool ready = true;
+#pragma unroll
+        for (int i = 0; i < kEpochPerLane; ++i)
+          ready = ready && (v1[i] >> 32) == (tag >> 32) && (v2[i] >> 32) == (tag >> 32);
+        if (ready) break;
+        if (++spins > a.spin_limit) {
+          lost = true;
+          give_up();
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < kEpochPerLane; ++i) {
+          const int64_t gg = lane + 64 * i;
+          if ((v1[i] >> 32) != (tag >> 32)) v1[i] = load_shared(a.eslots + 2 * (gg * a.c + ch));
+          if ((v2[i] >> 32) != (tag >> 32))
+            v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kEpochPerLane; ++i) {
+        if (lane + 64 * i < a.groups) {
+          t1 += __builtin_bit_cast(float, static_cast<uint32_t>(v1[i]));
+          t2 += __builtin_bit_cast(float, static_cast<uint32_t>(v2[i]));
+        }
+      }
+      // A lane whose partials never arrived poisons the channel's sums (the
+      // wave sum below spreads the NaN to its statistics and coefficients).
+      if (lost) t1 = t2 = __builtin_nan("");
+    }
+    const double2 w = wave_sum(t1, t2);
+    if (lane == 0) {
+      const float4 cfc = finish_channel<Tr, kGrad>(a.fin, ch, w.x, w.y, fin_in);
+      const float v4[4] = {cfc.x, cfc.y, cfc.z, cfc.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        store_shared(a.ecoef + 4 * static_cast<int64_t>(ch) + i,
+                     etag | __builtin_bit_cast(uint32_t, v4[i]));
+    }
+  }
+}
+
+// The coefficients of channel tile ct (4 words per channel, at most 1024
+// words: two per thread, consecutive words to consecutive threads, so the
+// cross-XCD loads stay coalesced), polled until tagged with this launch's
+// epoch, then shared through `red`, free since phase 1's reduction (the
+// first __syncthreads below orders those reads before these writes).  LDS:
+// component c of channel cl (= tx * VEC + j) at c * kW + cl + cl / VEC - a
+// stride kW = 8 (mod 32) between components and one pad word per channel
+// vector, so the writes (consecutive words) and the reads (lane tx at
+// tx * (VEC + 1) + j) hit distinct banks.  Coefficients that never arrive
+// are used as NaN.
+template <class Tr>
+__device__ __forceinline__ void tile_coefs(const FusedArgs& a, float2* red, int tid, int tx, int ct,
+                                           int width, bool active, uint32_t wtag, unsigned epoch,
+                                           float4 (&cf)[Tr::kVec]) {
+  constexpr int VEC = Tr::kVec;
+  constexpr int kW = VEC == 8 ? 296 : 168;  // >= 32 * (VEC + 1), = 8 mod 32
+  static_assert(kW >= 32 * (VEC + 1) && kW % 32 == 8, "coefficient layout");
+  static_assert(4 * kW * sizeof(float) <= (kFusedThreads / 64) * 32 * VEC * sizeof(float2),
+                "coefficients fit in red");
+  float* const cs = reinterpret_cast<float*>(red);
+  const uint64_t tag = static_cast<uint64_t>(wtag) << 32;
+  uint64_t v[2];
+  int64_t wi[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    wi[i] = tid + kFusedThreads * i;
+    const int64_t chn = static_cast<int64_t>(ct) * width + (wi[i] >> 2);
+    const bool need = (wi[i] >> 2) < width && chn < a.c;
+    v[i] = need ? load_shared(a.ecoef + 4 * chn + (wi[i] & 3)) : tag;
+    if (!need) wi[i] = -1;
+  }
+  unsigned spins = 0;
+  while ((v[0] >> 32) != (tag >> 32) || (v[1] >> 32) != (tag >> 32)) {
+    if (++spins > a.spin_limit) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if ((v[i] >> 32) != (tag >> 32)) v[i] = 0x7fc00000u;
+      __hip_atomic_store(a.gave_up, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if ((v[i] >> 32) != (tag >> 32)) {
+        const int64_t chn = static_cast<int64_t>(ct) * width + (wi[i] >> 2);
+        v[i] = load_shared(a.ecoef + 4 * chn + (wi[i] & 3));
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (wi[i] >= 0) {
+      const int cl = static_cast<int>(wi[i] >> 2);
+      cs[(wi[i] & 3) * kW + cl + cl / VEC] = __builtin_bit_cast(float, static_cast<uint32_t>(v[i]));
+    }
+  }
+  __syncthreads();
+  const int cb = tx * (VEC + 1);
+#pragma unroll
+  for (int j = 0; j < VEC; ++j)
+    cf[j] = active ? make_float4(cs[cb + j], cs[kW + cb + j], cs[2 * kW + cb + j],
+                                 cs[3 * kW + cb + j])
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
 template <class Tr, bool kGrad, int KR, int KL, bool kSliced>
 __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs a) {
   using S = typename Tr::S;
@@ -923,9 +1103,6 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   // The tag the waits look for: this launch's epoch (wait_xor is 0 except
   // under the host's forced-give-up test hook).
   const uint32_t wtag = epoch ^ a.wait_xor;
-  auto give_up = [&]() {
-    __hip_atomic_store(a.gave_up, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  };
 
 #pragma clang loop unroll(disable)
   for (int sl = 0; sl < nslices; ++sl) {
@@ -1072,35 +1249,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     for (int u = 0; u < U; ++u)
       if (q + u < nk) accum_words<Tr, kGrad>(xw[u], dw[u], k, s1, s2);
   }
-  // Workgroup partial per channel: sum the row lanes of each wave with
-  // shuffles, then the waves through LDS, then one coherent store per
-  // channel.
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    if (off < (1 << a.tx_shift)) break;
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      s1[j] += __shfl_xor(s1[j], off, 64);
-      s2[j] += __shfl_xor(s2[j], off, 64);
-    }
-  }
-  if (lane < (1 << a.tx_shift)) {
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) red[wave * width + lane * VEC + j] = make_float2(s1[j], s2[j]);
-  }
-  __syncthreads();
-  if (tid < width && static_cast<int64_t>(ct) * width + tid < static_cast<int64_t>(a.cv) * VEC) {
-    float sa = 0.f, sb = 0.f;
-#pragma unroll
-    for (int w = 0; w < kFusedThreads / 64; ++w) {
-      const float2 v = red[w * width + tid];
-      sa += v.x;
-      sb += v.y;
-    }
-    const int64_t slot = g * a.c + static_cast<int64_t>(ct) * width + tid;
-    store_shared(a.eslots + 2 * slot, etag | __builtin_bit_cast(uint32_t, sa));
-    store_shared(a.eslots + 2 * slot + 1, etag | __builtin_bit_cast(uint32_t, sb));
-  }
+  publish_partials<VEC>(a, red, s1, s2, tid, width, ct, g, etag);
 
   // Phase-3 prefetch, part A: the last streamed rows (phase 3 runs
   // last-to-first), loaded by the waves that have no phase-2 channel so the
@@ -1121,71 +1270,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   const int64_t qb = nk - 1 - (pre_a ? PA : 0);  // first row of part B
 
   // ---- phase 2: per-channel finals ---------------------------------------
-  // Channel ch belongs to workgroup ch % gridDim.x; each wave of the
-  // workgroup finishes one of its channels at a time, so all of a
-  // workgroup's partial loads are in flight together.
-  for (int ch = cs0 + blockIdx.x + wave * gridDim.x; ch < cs1; ch += kWaves * gridDim.x) {
-    // The channel's other inputs, in flight while its partials are polled.
-    const FinIn fin_in = fin_inputs<Tr, kGrad>(a.fin, ch);
-    double t1 = 0.0, t2 = 0.0;
-    {
-      // Lane l sums groups l, l + 64, ... (at most kMaxGroups / 64 of them):
-      // all their slots are loaded at once, then the ones not yet tagged
-      // with this launch's epoch are polled again.
-      const uint64_t tag = static_cast<uint64_t>(wtag) << 32;
-      uint64_t v1[kEpochPerLane], v2[kEpochPerLane];
-#pragma unroll
-      for (int i = 0; i < kEpochPerLane; ++i) {
-        const int64_t gg = lane + 64 * i;
-        v1[i] = v2[i] = tag;
-        if (gg < a.groups) {
-          v1[i] = load_shared(a.eslots + 2 * (gg * a.c + ch));
-          v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
-        }
-      }
-      unsigned spins = 0;
-      bool lost = false;
-      while (true) {
-        bool ready = true;
-#pragma unroll
-        for (int i = 0; i < kEpochPerLane; ++i)
-          ready = ready && (v1[i] >> 32) == (tag >> 32) && (v2[i] >> 32) == (tag >> 32);
-        if (ready) break;
-        if (++spins > a.spin_limit) {
-          lost = true;
-          give_up();
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-        for (int i = 0; i < kEpochPerLane; ++i) {
-          const int64_t gg = lane + 64 * i;
-          if ((v1[i] >> 32) != (tag >> 32)) v1[i] = load_shared(a.eslots + 2 * (gg * a.c + ch));
-          if ((v2[i] >> 32) != (tag >> 32))
-            v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < kEpochPerLane; ++i) {
-        if (lane + 64 * i < a.groups) {
-          t1 += __builtin_bit_cast(float, static_cast<uint32_t>(v1[i]));
-          t2 += __builtin_bit_cast(float, static_cast<uint32_t>(v2[i]));
-        }
-      }
-      // A lane whose partials never arrived poisons the channel's sums (the
-      // wave sum below spreads the NaN to its statistics and coefficients).
-      if (lost) t1 = t2 = __builtin_nan("");
-    }
-    const double2 w = wave_sum(t1, t2);
-    if (lane == 0) {
-      const float4 cfc = finish_channel<Tr, kGrad>(a.fin, ch, w.x, w.y, fin_in);
-      const float v4[4] = {cfc.x, cfc.y, cfc.z, cfc.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        store_shared(a.ecoef + 4 * static_cast<int64_t>(ch) + i,
-                     etag | __builtin_bit_cast(uint32_t, v4[i]));
-    }
-  }
+  finish_channels<Tr, kGrad>(a, cs0, cs1, wave, lane, wtag, etag, epoch);
   if (sl == 0) zero_side_outputs<kGrad>(a.fin);
 
   // Prefetch part B: the next rows, in flight while the tile's coefficients
@@ -1208,67 +1293,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       asm volatile("" : "+v"(dr[r].x), "+v"(dr[r].y), "+v"(dr[r].z), "+v"(dr[r].w));
   }
   float4 cf[VEC];
-  {
-    // The tile's coefficients (4 words per channel, at most 1024 words: two
-    // per thread, consecutive words to consecutive threads, so the
-    // cross-XCD loads stay coalesced) are polled until tagged with this
-    // launch's epoch, then shared through `red`, free since phase 1's
-    // reduction (the first __syncthreads below orders those reads before
-    // these writes).  LDS: component c of channel cl (= tx * VEC + j) at
-    // c * kW + cl + cl / VEC - a stride kW = 8 (mod 32) between components
-    // and one pad word per channel vector, so the writes (consecutive words)
-    // and the reads (lane tx at tx * (VEC + 1) + j) hit distinct banks.
-    constexpr int kW = VEC == 8 ? 296 : 168;  // >= 32 * (VEC + 1), = 8 mod 32
-    static_assert(kW >= 32 * (VEC + 1) && kW % 32 == 8, "coefficient layout");
-    static_assert(4 * kW * sizeof(float) <= sizeof(red), "coefficients fit in red");
-    float* const cs = reinterpret_cast<float*>(red);
-    const uint64_t tag = static_cast<uint64_t>(wtag) << 32;
-    uint64_t v[2];
-    int64_t wi[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      wi[i] = tid + kFusedThreads * i;
-      const int64_t chn = static_cast<int64_t>(ct) * width + (wi[i] >> 2);
-      const bool need = (wi[i] >> 2) < width && chn < a.c;
-      v[i] = need ? load_shared(a.ecoef + 4 * chn + (wi[i] & 3)) : tag;
-      if (!need) wi[i] = -1;
-    }
-    unsigned spins = 0;
-    while ((v[0] >> 32) != (tag >> 32) || (v[1] >> 32) != (tag >> 32)) {
-      if (++spins > a.spin_limit) {
-        // Coefficients that never arrived are used as NaN (the tile's
-        // outputs for those channels become NaN).
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-          if ((v[i] >> 32) != (tag >> 32)) v[i] = 0x7fc00000u;
-        give_up();
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        if ((v[i] >> 32) != (tag >> 32)) {
-          const int64_t chn = static_cast<int64_t>(ct) * width + (wi[i] >> 2);
-          v[i] = load_shared(a.ecoef + 4 * chn + (wi[i] & 3));
-        }
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      if (wi[i] >= 0) {
-        const int cl = static_cast<int>(wi[i] >> 2);
-        cs[(wi[i] & 3) * kW + cl + cl / VEC] = __builtin_bit_cast(float, static_cast<uint32_t>(v[i]));
-      }
-    }
-    __syncthreads();
-    const int cb = tx * (VEC + 1);
-#pragma unroll
-    for (int j = 0; j < VEC; ++j)
-      cf[j] = active ? make_float4(cs[cb + j], cs[kW + cb + j], cs[2 * kW + cb + j],
-                                   cs[3 * kW + cb + j])
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  tile_coefs<Tr>(a, red, tid, tx, ct, width, active, wtag, epoch, cf);
   // Prefetched rows first, then the remaining streamed rows last-to-first.
   if (pre_a) {
 #pragma unroll
