@@ -150,8 +150,15 @@ int TFMA_FusedBatchNormGradV3(
  * (musa_ext/kernels/training/musa_apply_sparse_adam_kernel.mu:140-169).
  *
  * var, m, v: the variables' device tensors, updated in place; grad: device
- * tensor; all the same shape and dtype T in {FLOAT, HALF, BFLOAT16, DOUBLE}.
- * beta1_power .. epsilon: 0-d HOST tensors of dtype T (HostMemory inputs).
+ * tensor; all the same shape and dtype T in {FLOAT, HALF, BFLOAT16, DOUBLE,
+ * INT32, INT64}.  beta1_power .. epsilon: 0-d HOST tensors of dtype T
+ * (HostMemory inputs).  Floating T: TF-CPU's update in T.  Integer T: the
+ * reference's generic op chain (:224-246, 300-408) in T with two's-complement
+ * wrap - alpha from the scalars in double, converted to T (truncation; T's
+ * minimum for NaN or out of range), m = m*b1 + g*(1-b1),
+ * v = v*b2 + (g*g)*(1-b2), var -= (m / (isqrt(v) + eps)) * alpha with the
+ * exact integer square root (0 for v <= 0) and truncating division
+ * (x / 0 = 0, MIN / -1 = MIN); use_nesterov has no integer form.
  * A NULL var/m/v data pointer with a non-empty shape is an uninitialised
  * variable (FAILED_PRECONDITION).  use_locking serialises calls that touch
  * the same var/m/v memory through this library (locks taken in address

@@ -6,6 +6,12 @@ The product (tensorflow_musa_extension_amd) never imports this module.
 
 Arrays are numpy; bfloat16 data is carried as uint16 bit patterns with
 dtype="bfloat16" passed explicitly.
+
+adam_int (integer ResourceApplyAdam, numpy) restates the reference's generic
+op chain; its integer square root and division are closed muDNN operations
+in the reference, so for those two steps parity with the reference is
+unpinned (the oracle fixes one definition, pinned against an independent
+big-integer restatement and a closed form in tests/test_oracle.py).
 """
 import ctypes
 import os
@@ -181,6 +187,67 @@ def adam_mixed(var, m, v, grad, beta1_power, beta2_power, lr, beta1, beta2, epsi
     g32 = np.ascontiguousarray(to_f32(grad, grad_dtype), dtype=np.float32)
     adam(var, m, v, g32, beta1_power, beta2_power, lr, beta1, beta2, epsilon,
          use_nesterov=use_nesterov, dtype="float32")
+
+
+def _int_alpha(beta1_power, beta2_power, lr, dtype):
+    """The reference's alpha for integer T: computed in double from the T
+    scalars, lr when beta1_power is within 1e-10 of 1
+    (musa_ext/kernels/training/musa_applyadam_op.cc:231-246), then
+    static_cast<T> as its x86-64 host converts: truncation toward zero, T's
+    minimum for NaN or out-of-range values."""
+    import math
+    b1p, b2p, lrd = float(int(beta1_power)), float(int(beta2_power)), float(int(lr))
+    omb1p = 1.0 - b1p
+    if abs(omb1p) < 1e-10:
+        a = lrd
+    else:
+        r = 1.0 - b2p
+        a = lrd * math.sqrt(r) / omb1p if r >= 0 else float("nan")
+    info = np.iinfo(dtype)
+    if not (a == a) or not (-2.0 ** (info.bits - 1) <= math.trunc(a) < 2.0 ** (info.bits - 1)):
+        return int(info.min)
+    return int(math.trunc(a))
+
+
+def adam_int(var, m, v, grad, beta1_power, beta2_power, lr, beta1, beta2, epsilon):
+    """ResourceApplyAdam for int32 / int64 var, m, v, grad (in place): the
+    reference's generic op chain (musa_ext/kernels/training/
+    musa_applyadam_op.cc:300-408), each step in T with two's-complement
+    wrap: m = m*beta1 + grad*(1-beta1); v = v*beta2 + (grad*grad)*(1-beta2);
+    var -= (m / (sqrt(v) + epsilon)) * alpha.  The square root and the
+    division are closed muDNN integer ops in the reference; here sqrt is the
+    exact integer square root (0 for v <= 0) and the division truncates
+    toward zero, 0 for a zero divisor, MIN / -1 = MIN (the definition the
+    library implements; parity with muDNN unpinned)."""
+    dt = var.dtype
+    if dt not in (np.int32, np.int64):
+        raise ValueError("int32 or int64 arrays")
+    t = lambda x: np.array(int(x), dtype=np.int64).astype(dt)  # wraps like static_cast<T>
+    b1, b2, eps = t(beta1), t(beta2), t(epsilon)
+    one = np.array(1, dtype=dt)
+    with np.errstate(over="ignore"):
+        omb1, omb2 = one - b1, one - b2
+        alpha = np.array(_int_alpha(beta1_power, beta2_power, lr, dt), dtype=dt)
+        g = grad.astype(dt, copy=False)
+        mn = m * b1 + g * omb1
+        vn = v * b2 + (g * g) * omb2
+        # exact integer square root
+        pos = vn > 0
+        u = np.where(pos, vn, 0).astype(np.uint64)
+        r = np.floor(np.sqrt(u.astype(np.float64))).astype(np.uint64)
+        for _ in range(4):
+            r = np.where(r * r > u, r - np.uint64(1), r)
+            r = np.where((r + np.uint64(1)) * (r + np.uint64(1)) <= u, r + np.uint64(1), r)
+        root = r.astype(dt)
+        d = root + eps
+        # truncating division; 0 for d == 0, -a for d == -1 (MIN / -1 wraps)
+        safe = np.where((d == 0) | (d == -1), one, d)
+        rem = np.fmod(mn, safe)
+        q = (mn - rem) // safe
+        q = np.where(d == 0, np.zeros_like(q), np.where(d == -1, np.zeros_like(mn) - mn, q))
+        var -= q * alpha
+    m[...] = mn
+    v[...] = vn
 
 
 def bias_add_grad(x, data_format="NHWC", dtype="float32"):

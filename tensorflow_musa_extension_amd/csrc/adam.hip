@@ -27,6 +27,8 @@
 #include "device_util.h"
 #include "tfma_internal.h"
 
+#include <type_traits>
+
 namespace tfma {
 namespace {
 
@@ -212,6 +214,61 @@ __global__ __launch_bounds__(kThreads) void adam_grouped_args_kernel(
                                          static_cast<const SG*>(t->grad[lo]) + start, len, p);
 }
 
+// Integer state (int32 / int64): the reference's generic op chain for T
+// (musa_applyadam_op.cc:300-408), each step one operation in T:
+//   m = m * beta1 + grad * (1 - beta1)
+//   v = v * beta2 + (grad * grad) * (1 - beta2)
+//   var = var - (m / (sqrt(v) + epsilon)) * alpha
+// Multiplies, adds and subtracts wrap (two's complement).  The reference
+// runs the square root and the division through the closed muDNN library,
+// whose integer semantics are not published; here the square root is the
+// exact integer square root (0 for v <= 0) and the division truncates
+// toward zero, with 0 for a zero divisor and MIN / -1 = MIN.  The chain has
+// no Nesterov form (the reference's ignores use_nesterov).
+template <typename T>
+struct IntOps {
+  using U = typename std::make_unsigned<T>::type;
+  __device__ static T add(T a, T b) { return static_cast<T>(static_cast<U>(a) + static_cast<U>(b)); }
+  __device__ static T sub(T a, T b) { return static_cast<T>(static_cast<U>(a) - static_cast<U>(b)); }
+  __device__ static T mul(T a, T b) { return static_cast<T>(static_cast<U>(a) * static_cast<U>(b)); }
+  __device__ static T div(T a, T b) {
+    if (b == 0) return 0;
+    if (b == -1) return sub(0, a);
+    return a / b;
+  }
+  __device__ static T sqrt(T v) {
+    if (v <= 0) return 0;
+    const uint64_t u = static_cast<uint64_t>(v);
+    // The double root is within one of the integer root; s * s and
+    // (s + 1) * (s + 1) fit in 64 bits for any v < 2^63.
+    uint64_t r = static_cast<uint64_t>(__builtin_sqrt(static_cast<double>(v)));
+    while (r * r > u) --r;
+    while ((r + 1) * (r + 1) <= u) ++r;
+    return static_cast<T>(r);
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void adam_int_kernel(T* __restrict__ var, T* __restrict__ m,
+                                                           T* __restrict__ v,
+                                                           const T* __restrict__ g, int64_t n,
+                                                           IntAdamScalars s) {
+  using O = IntOps<T>;
+  const T b1 = static_cast<T>(s.beta1), b2 = static_cast<T>(s.beta2);
+  const T omb1 = static_cast<T>(s.omb1), omb2 = static_cast<T>(s.omb2);
+  const T eps = static_cast<T>(s.eps), alpha = static_cast<T>(s.alpha);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
+    const T gi = g[i];
+    const T mi = O::add(O::mul(m[i], b1), O::mul(gi, omb1));
+    const T vi = O::add(O::mul(v[i], b2), O::mul(O::mul(gi, gi), omb2));
+    const T upd = O::mul(O::div(mi, O::add(O::sqrt(vi), eps)), alpha);
+    var[i] = O::sub(var[i], upd);
+    m[i] = mi;
+    v[i] = vi;
+  }
+}
+
 template <class Tr>
 AdamP<typename Tr::C> make_params(const AdamScalars& s) {
   using C = typename Tr::C;
@@ -347,6 +404,23 @@ hipError_t LaunchApplyAdam(DType t, DType tg, void* var, void* m, void* v,
   }
 #undef TFMA_ADAM_CASE
   return hipErrorInvalidValue;
+}
+
+hipError_t LaunchApplyAdamInt(bool is64, void* var, void* m, void* v, const void* grad,
+                              int64_t n, const IntAdamScalars& s, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  int64_t blocks = (n + kThreads - 1) / kThreads;
+  const int64_t cap = static_cast<int64_t>(DeviceCUs()) * 8;
+  if (blocks > cap) blocks = cap;
+  if (is64)
+    TFMA_LAUNCH("tfma_adam_int", adam_int_kernel<int64_t>, dim3(blocks), dim3(kThreads), 0,
+                stream, static_cast<int64_t*>(var), static_cast<int64_t*>(m),
+                static_cast<int64_t*>(v), static_cast<const int64_t*>(grad), n, s);
+  else
+    TFMA_LAUNCH("tfma_adam_int", adam_int_kernel<int32_t>, dim3(blocks), dim3(kThreads), 0,
+                stream, static_cast<int32_t*>(var), static_cast<int32_t*>(m),
+                static_cast<int32_t*>(v), static_cast<const int32_t*>(grad), n, s);
+  return hipGetLastError();
 }
 
 hipError_t LaunchGroupedApplyAdam(DType t, DType tg, const AdamTensorEntry* dev_table,

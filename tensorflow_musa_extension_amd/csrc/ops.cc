@@ -5,6 +5,9 @@
 // where it defines them and TensorFlow's CPU kernels otherwise.
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <stdint.h>
+
+#include <cmath>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -1020,11 +1023,77 @@ int check_adam_triple(const TFMA_Tensor* var, const TFMA_Tensor* m, const TFMA_T
   return TFMA_OK;
 }
 
+// The double -> T conversion of the reference's static_cast<T>(alpha_val)
+// as its x86-64 host performs it: truncation toward zero, and the "integer
+// indefinite" value (T's minimum) for NaN or a value outside T's range.
+int64_t host_double_to_int(double d, bool is64) {
+  const double lim = is64 ? 9223372036854775808.0 : 2147483648.0;
+  const int64_t minv = is64 ? INT64_MIN : INT32_MIN;
+  if (!(d > -lim - 1.0 && d < lim)) return minv;
+  const double t = std::trunc(d);
+  if (t < -lim || t >= lim) return minv;
+  return static_cast<int64_t>(t);
+}
+
+int64_t wrap_to(int64_t x, bool is64) {
+  return is64 ? x : static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(x)));
+}
+
+// int32 / int64 ResourceApplyAdam, registered by the reference
+// (musa_applyadam_op.cc:645-682) and run there through its generic op chain:
+// alpha in double from the scalars, with lr when beta1_power is within 1e-10
+// of 1 (:231-246), converted to T; 1 - beta in T (:310-316).
+int apply_adam_int(void* stream, TFMA_Tensor* var, TFMA_Tensor* m, TFMA_Tensor* v,
+                   const TFMA_Tensor* const* sc, const TFMA_Tensor* grad, int dt,
+                   int use_locking, TFMA_Status* status) {
+  static const char* names[6] = {"beta1_power", "beta2_power", "lr", "beta1", "beta2", "epsilon"};
+  const bool is64 = dt == TFMA_INT64;
+  int64_t val[6];
+  for (int i = 0; i < 6; ++i) {
+    if (!valid_tensor(sc[i]) || !sc[i]->data)
+      return set_status(status, TFMA_INVALID_ARGUMENT, "%s is missing", names[i]);
+    if (sc[i]->ndims != 0)
+      return set_status(status, TFMA_INVALID_ARGUMENT, "%s is not a scalar: %s", names[i],
+                        shape_str(sc[i]).c_str());
+    if (sc[i]->dtype != dt)
+      return set_status(status, TFMA_INVALID_ARGUMENT, "%s has dtype %s, expected %s", names[i],
+                        dtype_name(sc[i]->dtype), dtype_name(dt));
+    val[i] = is64 ? *static_cast<const int64_t*>(sc[i]->data)
+                  : static_cast<int64_t>(*static_cast<const int32_t*>(sc[i]->data));
+  }
+  const double b1p = static_cast<double>(val[0]), b2p = static_cast<double>(val[1]);
+  const double lr = static_cast<double>(val[2]);
+  const double omb1p = 1.0 - b1p;
+  const double alpha = std::abs(omb1p) < 1e-10 ? lr : lr * std::sqrt(1.0 - b2p) / omb1p;
+  IntAdamScalars s;
+  s.alpha = host_double_to_int(alpha, is64);
+  s.beta1 = val[3];
+  s.beta2 = val[4];
+  s.eps = val[5];
+  s.omb1 = wrap_to(static_cast<int64_t>(1ull - static_cast<uint64_t>(val[3])), is64);
+  s.omb2 = wrap_to(static_cast<int64_t>(1ull - static_cast<uint64_t>(val[4])), is64);
+  VarLocks locks;
+  if (use_locking) {
+    locks.add(var->data);
+    locks.add(m->data);
+    locks.add(v->data);
+    locks.lock();
+  }
+  const int64_t n = num_elements(var);
+  if (n == 0) return ok(status);
+  return hip_status(status,
+                    LaunchApplyAdamInt(is64, var->data, m->data, v->data, grad->data, n, s,
+                                       as_stream(stream)),
+                    "ResourceApplyAdam");
+}
+
 int apply_adam(void* stream, TFMA_Tensor* var, TFMA_Tensor* m, TFMA_Tensor* v,
                const TFMA_Tensor* const* sc, const TFMA_Tensor* grad, int use_locking,
                int use_nesterov, bool mixed, const char* op, TFMA_Status* status) {
   int dt = 0, gdt = 0;
   if (const int rc = check_adam_triple(var, m, v, grad, mixed, &dt, &gdt, status)) return rc;
+  if (!mixed && (dt == TFMA_INT32 || dt == TFMA_INT64))
+    return apply_adam_int(stream, var, m, v, sc, grad, dt, use_locking, status);
   DType t, tg;
   if (!to_dtype(dt, &t) || !to_dtype(gdt, &tg))
     return set_status(status, TFMA_UNIMPLEMENTED, "%s: dtype %s is not supported", op,

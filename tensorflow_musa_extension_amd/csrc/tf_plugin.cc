@@ -1378,6 +1378,11 @@ std::vector<KernelSpec> kernel_specs() {
                   {"vars", "ms", "vs", "beta1_power", "beta2_power", "lr", "beta1", "beta2",
                    "epsilon"}});
   }
+  // Integer state: the reference registers ResourceApplyAdam (only) for
+  // int64 and int32 too (musa_applyadam_op.cc:675-676).
+  for (TF_DataType t : {TF_INT64, TF_INT32})
+    ks.push_back({"ResourceApplyAdam", adam_create, adam_compute<false>,
+                  delete_kernel<AdamKernel>, {{"T", t}}, adam_host});
   for (TF_DataType g : {TF_HALF, TF_BFLOAT16})
     ks.push_back({"MusaGroupedResourceApplyAdam", adam_create, grouped_adam_compute,
                   delete_kernel<AdamKernel>, {{"T", TF_FLOAT}, {"Tgrad", g}},

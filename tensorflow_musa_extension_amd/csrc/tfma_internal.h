@@ -65,6 +65,15 @@ hipError_t LaunchApplyAdam(DType t, DType tg, void* var, void* m, void* v,
                            const void* grad, int64_t n, const AdamScalars& s,
                            bool nesterov, hipStream_t stream);
 
+// Integer ResourceApplyAdam (int32 / int64 var, m, v and grad): the
+// reference's generic op chain in T; the scalars as T values (alpha already
+// converted from the double the reference computes, 1 - beta in T).
+struct IntAdamScalars {
+  int64_t alpha, beta1, beta2, eps, omb1, omb2;
+};
+hipError_t LaunchApplyAdamInt(bool is64, void* var, void* m, void* v, const void* grad,
+                              int64_t n, const IntAdamScalars& s, hipStream_t stream);
+
 // One entry of the grouped-Adam tensor table (device memory).
 struct AdamTensorEntry {
   void* var;

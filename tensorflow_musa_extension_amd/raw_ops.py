@@ -209,7 +209,9 @@ def host_scalar(value, dtype):
     """A 0-d host tensor of `dtype` (TF HostMemory scalar) kept alive by the
     returned pair (buffer, descriptor)."""
     if isinstance(value, torch.Tensor):
-        value = float(value.detach().cpu().double())
+        value = value.detach().cpu().reshape(()).item()
+    if not dtype.is_floating_point:
+        value = int(value)
     buf = torch.tensor([value], dtype=dtype)
     desc = _lib.make_tensor(buf.data_ptr(), _TORCH_TO_TF[dtype], ())
     return buf, desc

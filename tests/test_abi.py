@@ -139,9 +139,17 @@ def test_adam_validation():
     bad[2] = _lib.make_tensor(ctypes.addressof(bufs[2]), _lib.DT_FLOAT, (1,))
     code, msg = adam(a, a, a, a, bad)
     assert code == _lib.INVALID_ARGUMENT and msg == "lr is not a scalar: [1]"
-    code, msg = adam(T((4, 3), _lib.DT_INT32), T((4, 3), _lib.DT_INT32),
-                     T((4, 3), _lib.DT_INT32), T((4, 3), _lib.DT_INT32), descs)
-    assert code == _lib.UNIMPLEMENTED
+    # int32 / int64 state (the reference registers both): the scalars must be
+    # of the state's type; an empty update succeeds without a device.
+    i32 = lambda shape=(4, 3): T(shape, _lib.DT_INT32)
+    code, msg = adam(i32(), i32(), i32(), i32(), descs)
+    assert code == _lib.INVALID_ARGUMENT and msg == "beta1_power has dtype float, expected int32"
+    ibufs = [(ctypes.c_int32 * 1)(v) for v in (1, 1, 3, 0, 0, 1)]
+    idescs = [_lib.make_tensor(ctypes.addressof(b), _lib.DT_INT32, ()) for b in ibufs]
+    code, msg = adam(i32((0, 3)), i32((0, 3)), i32((0, 3)), i32((0, 3)), idescs)
+    assert code == _lib.OK, msg
+    code, msg = adam(i32(), i32(), i32(), T((4, 3), _lib.DT_INT64), idescs)
+    assert code == _lib.INVALID_ARGUMENT
 
 
 def test_adam_mixed_validation():

@@ -340,3 +340,39 @@ def test_grouped_repeated_steps_use_cached_table(dev):
     for i, (v, m, w) in enumerate(zip(vars_, ms, vs)):
         for name, t, r in (("var", v, refs[i][0]), ("m", m, refs[i][1]), ("v", w, refs[i][2])):
             assert_bitwise(to_np(t, "float32"), r, f"tensor {i} {name}")
+
+
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
+def test_adam_int_matches_oracle(dev, dtype):
+    """int32 / int64 ResourceApplyAdam (the reference's integer registrations,
+    musa_applyadam_op.cc:645-676, which run its generic op chain in T)
+    bitwise against the oracle's integer chain: three steps under every
+    alpha regime (beta1_power 1 -> lr, a NaN alpha -> T's minimum, one out of
+    T's range), with products that wrap, v <= 0, zero divisors and MIN / -1.
+    The integer square root and division are this build's definition (the
+    reference's are closed muDNN ops)."""
+    npdt = np.int32 if dtype == torch.int32 else np.int64
+    info = np.iinfo(npdt)
+    rng = np.random.default_rng(info.bits + 7)
+    n = 100003
+    full = lambda: rng.integers(info.min, info.max, n, dtype=npdt, endpoint=True)
+    var0, m0, v0 = full(), full(), full()
+    half = n // 2
+    for a in (var0, m0, v0):
+        a[:half] = rng.integers(-5000, 5000, half)
+    v0[:64] = np.arange(-32, 32)
+    m0[64:96] = info.min
+    scalars = [(3, 1, 9, 2, 3, 1), (1, 0, 11, 1, 1, -1), (2, 5, 7, 0, 1, 0),
+               (2, -3, info.max, 3, 2, 2), (0, 0, 3, 0, 0, -1), (-3, -8, -6, 7, -2, 5)]
+    for sc in scalars:
+        tv, tm, tvv = (torch.from_numpy(a.copy()).to(dev) for a in (var0, m0, v0))
+        rv, rm, rvv = var0.copy(), m0.copy(), v0.copy()
+        for step in range(3):
+            g = full()
+            g[:half] = rng.integers(-300, 300, half)
+            ops.ResourceApplyAdam(tv, tm, tvv, *sc, torch.from_numpy(g).to(dev))
+            assert ops.last_kernel_name() == "tfma_adam_int"
+            oracle.adam_int(rv, rm, rvv, g, *sc)
+        torch.cuda.synchronize()
+        for name, got, want in (("var", tv, rv), ("m", tm, rm), ("v", tvv, rvv)):
+            np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=f"{name} {sc}")

@@ -280,6 +280,25 @@ def test_resource_apply_adam(plugin, use_locking):
     k.free()
 
 
+def test_resource_apply_adam_int64(plugin):
+    """ResourceApplyAdam with int64 state through the adapter's integer
+    registration: host int64 scalars, bitwise equal to the oracle's integer
+    chain."""
+    p = plugin
+    rng = np.random.default_rng(14)
+    n = 50_001
+    var, m, v, g = (rng.integers(-10_000, 10_000, n).astype(np.int64) for _ in range(4))
+    dvar, dm, dv, dg = (torch.from_numpy(a.copy()).cuda() for a in (var, m, v, g))
+    sc = [np.array(x, np.int64) for x in (3, 1, 9, 2, 3, 1)]
+    k = p.run("ResourceApplyAdam", {"T": "int64"},
+              [T(dvar, "var"), T(dm, "var"), T(dv, "var")] + [H(s, "int64") for s in sc] + [T(dg)],
+              dict(use_locking=False, use_nesterov=False))
+    oracle.adam_int(var, m, v, g, *[int(s) for s in sc])
+    for got, want in ((dvar, var), (dm, m), (dv, v)):
+        np.testing.assert_array_equal(got.cpu().numpy(), want)
+    k.free()
+
+
 def test_mixed_and_grouped_adam(plugin):
     p = plugin
     rng = np.random.default_rng(5)

@@ -362,6 +362,86 @@ def test_adam_other_dtypes_vs_f64(dtype, tol):
 # ---------------------------------------------------------------------------
 # Elementwise
 # ---------------------------------------------------------------------------
+# ---------------------------------------------------------------------------
+# Integer ResourceApplyAdam (the reference's int32 / int64 registration)
+# ---------------------------------------------------------------------------
+def _adam_int_python(var, m, v, g, b1p, b2p, lr, b1, b2, eps, bits):
+    """Element by element with Python integers reduced modulo 2**bits,
+    math.isqrt and sign-magnitude truncating division - an implementation
+    independent of the oracle's numpy wrap and fmod arithmetic."""
+    import math
+    half, mod = 1 << (bits - 1), 1 << bits
+    w = lambda x: (x + half) % mod - half
+    if abs(1.0 - float(b1p)) < 1e-10:
+        a = float(lr)
+    elif 1.0 - float(b2p) < 0:
+        a = float("nan")
+    else:
+        a = float(lr) * math.sqrt(1.0 - float(b2p)) / (1.0 - float(b1p))
+    alpha = -half if (a != a or not (-half <= math.trunc(a) < half)) else math.trunc(a)
+    b1, b2, eps = w(b1), w(b2), w(eps)
+    out = []
+    for x, mi, vi, gi in zip(var.tolist(), m.tolist(), v.tolist(), g.tolist()):
+        mi = w(w(mi * b1) + w(gi * w(1 - b1)))
+        vi = w(w(vi * b2) + w(w(gi * gi) * w(1 - b2)))
+        d = w((math.isqrt(vi) if vi > 0 else 0) + eps)
+        if d == 0:
+            q = 0
+        else:
+            q = abs(mi) // abs(d)
+            q = w(-q if (mi < 0) != (d < 0) else q)
+        out.append((w(x - w(q * alpha)), mi, vi))
+    return [np.array(c, dtype=var.dtype) for c in zip(*out)]
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+def test_adam_int_matches_python_integers(dtype):
+    """The oracle's integer chain against a big-integer restatement, on random
+    values and on the edge cases: products that wrap, v <= 0 (root 0), a zero
+    divisor (epsilon = -root), MIN / -1, and every alpha regime (beta1_power
+    1 -> lr; beta2_power > 1 -> NaN -> MIN; an alpha outside T's range)."""
+    info = np.iinfo(dtype)
+    bits = info.bits
+    rng = np.random.default_rng(bits)
+    n = 4000
+    var = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+    m = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+    v = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+    g = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+    small = slice(0, n // 2)  # half the elements small enough not to wrap
+    for a in (var, m, v, g):
+        a[small] = rng.integers(-1000, 1000, n // 2)
+    v[:64] = np.arange(-32, 32)
+    m[64:80] = info.min
+    scalars = [
+        (3, 1, 9, 2, 3, 1), (0, 0, 5, 0, 0, 0), (1, 0, 11, 1, 1, -1), (2, 5, 7, 0, 1, 0),
+        (4, 0, info.max, 3, 2, 2), (2, -3, info.max, 3, 2, 2), (-3, -8, -6, 7, -2, 5),
+        (0, 0, 3, 0, 0, -1),
+    ]
+    for sc in scalars:
+        xs, ms, vs = var.copy(), m.copy(), v.copy()
+        oracle.adam_int(xs, ms, vs, g, *sc)
+        ex, em, ev = _adam_int_python(var, m, v, g, *sc, bits)
+        np.testing.assert_array_equal(ms, em, err_msg=str(sc))
+        np.testing.assert_array_equal(vs, ev, err_msg=str(sc))
+        np.testing.assert_array_equal(xs, ex, err_msg=str(sc))
+
+
+def test_adam_int_closed_form():
+    """beta1 = beta2 = 0 and epsilon = 0: m = grad, v = grad^2, the root is
+    |grad| and the update is sign(grad) * alpha with alpha = trunc(lr *
+    sqrt(1 - beta2_power) / (1 - beta1_power)); here lr = 10,
+    beta1_power = -1, beta2_power = -3 -> alpha = trunc(10 * 2 / 2) = 10."""
+    g = np.array([5, -7, 0, 1, -1, 123456], dtype=np.int64)
+    var = np.full(6, 100, dtype=np.int64)
+    m = np.zeros(6, dtype=np.int64)
+    v = np.zeros(6, dtype=np.int64)
+    oracle.adam_int(var, m, v, g, -1, -3, 10, 0, 0, 0)
+    np.testing.assert_array_equal(m, g)
+    np.testing.assert_array_equal(v, g * g)
+    np.testing.assert_array_equal(var, 100 - 10 * np.sign(g))
+
+
 def test_relu_reference_known_answers():
     """test/ops/relu_op_test.py:45-96 literal [-2,-1,0,1,2]."""
     x = np.array([-2.0, -1.0, 0.0, 1.0, 2.0], np.float32)

@@ -134,13 +134,16 @@ def test_batch_norm_registrations(h):
 
 def test_adam_registrations_host_memory(h):
     """ResourceApplyAdam: var, m, v handles and the six scalars in host
-    memory (musa_applyadam_op.cc:645-658); ApplyAdam: the scalars
-    (:660-669); MusaResourceApplyAdamMixed: float/half/bfloat16 gradients
-    (musa_applyadam_mixed_op.cc:285-300)."""
+    memory, for float, double, half, bfloat16, int64 and int32
+    (musa_applyadam_op.cc:645-676); ApplyAdam: the scalars, floating types
+    only (:660-681); MusaResourceApplyAdamMixed: float/half/bfloat16
+    gradients (musa_applyadam_mixed_op.cc:285-300)."""
     scal = ["beta1_power", "beta2_power", "lr", "beta1", "beta2", "epsilon"]
     regs = _reg(h, "ResourceApplyAdam")
     assert {_types(k)["T"] for k in regs} == {th.DT[t] for t in ("float", "half", "bfloat16",
-                                                                 "double")}
+                                                                 "double", "int32", "int64")}
+    assert {_types(k)["T"] for k in _reg(h, "ApplyAdam")} == {
+        th.DT[t] for t in ("float", "half", "bfloat16", "double")}
     for k in regs:
         assert k["host_memory"] == ["var", "m", "v"] + scal
     for k in _reg(h, "ApplyAdam"):
