@@ -283,9 +283,15 @@ class PinnedRing {
   int next_ = 0;
 };
 
-PinnedRing& pinned_ring() {
-  static PinnedRing* r = new PinnedRing();
-  return *r;
+// One ring per device: its events belong to the device that was current
+// when they were created, and are recorded on that device's streams only.
+PinnedRing* pinned_ring(int dev) {
+  static PinnedRing* rings[64] = {nullptr};
+  static std::mutex mu;
+  if (dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lk(mu);
+  if (!rings[dev]) rings[dev] = new PinnedRing();
+  return rings[dev];
 }
 
 // ---------------------------------------------------------------------------
@@ -312,7 +318,9 @@ class AdamTableCache {
       Slot& s = slots_[dev][i];
       if (!s.valid || s.host.size() != t.size() || memcmp(s.host.data(), t.data(), t.size()) != 0)
         continue;
-      if (s.fill_stream != stream && hipStreamWaitEvent(stream, s.ready, 0) != hipSuccess)
+      // The copy that filled the slot may still be in flight (on any stream:
+      // a stream handle can be recycled after its stream is destroyed).
+      if (hipEventQuery(s.ready) != hipSuccess && hipStreamWaitEvent(stream, s.ready, 0) != hipSuccess)
         return nullptr;
       s.tick = ++tick_;
       ++s.pins;
@@ -325,7 +333,13 @@ class AdamTableCache {
   void mark_used(int dev, int slot, hipStream_t stream) {
     std::lock_guard<std::mutex> lk(mu_);
     Slot& s = slots_[dev][slot];
+    // `used` completes only after every launch that reads the slot: a use
+    // still pending on another stream is chained in before the record (the
+    // launch itself, already enqueued, does not wait for it).
+    if (s.used_stream != stream && hipEventQuery(s.used) == hipErrorNotReady)
+      (void)hipStreamWaitEvent(stream, s.used, 0);
     (void)hipEventRecord(s.used, stream);
+    s.used_stream = stream;
     --s.pins;
   }
 
@@ -366,7 +380,7 @@ class AdamTableCache {
     if (hipEventRecord(s.ready, stream) != hipSuccess) return;
     if (hipEventRecord(s.used, stream) != hipSuccess) return;
     s.host = t;
-    s.fill_stream = stream;
+    s.used_stream = stream;
     s.tick = ++tick_;
     s.valid = true;
   }
@@ -379,7 +393,7 @@ class AdamTableCache {
     size_t cap = 0;
     hipEvent_t ready = nullptr;
     hipEvent_t used = nullptr;
-    hipStream_t fill_stream = nullptr;
+    hipStream_t used_stream = nullptr;  // stream of the last record of `used`
     uint64_t tick = 0;
     int pins = 0;  // calls between find() and mark_used()
   };
@@ -1267,7 +1281,10 @@ int TFMA_GroupedResourceApplyAdam(void* stream, int n, TFMA_Tensor* vars, TFMA_T
     cache.mark_used(dev, slot, strm);
     return hip_status(status, e, "MusaGroupedResourceApplyAdam");
   }
-  hipError_t e = pinned_ring().upload(workspace, blob.data(), blob.size(), strm);
+  PinnedRing* ring = pinned_ring(dev);
+  if (!ring)
+    return set_status(status, TFMA_INTERNAL, "MusaGroupedResourceApplyAdam: no current device");
+  hipError_t e = ring->upload(workspace, blob.data(), blob.size(), strm);
   if (e != hipSuccess) return hip_status(status, e, "MusaGroupedResourceApplyAdam table upload");
   e = LaunchGroupedApplyAdam(t, tg, static_cast<const AdamTensorEntry*>(workspace),
                              static_cast<int>(table.size()), chunks, s, use_nesterov != 0,

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -22,7 +23,7 @@ struct Pending {
 
 struct TraceState {
   std::mutex mu;
-  bool enabled = false;
+  std::atomic<bool> enabled{false};  // read without the mutex on every launch
   std::string substr;
   std::vector<Pending> pending;
   std::vector<hipEvent_t> pool;
@@ -72,7 +73,7 @@ void SetLastKernel(const char* kernel_name) { t_last_kernel = kernel_name; }
 TraceEvents TraceTake(const char* kernel_name) {
   TraceEvents ev;
   TraceState& s = state();
-  if (!s.enabled) return ev;
+  if (!s.enabled.load(std::memory_order_relaxed)) return ev;
   std::lock_guard<std::mutex> lk(s.mu);
   if (!s.enabled || strstr(kernel_name, s.substr.c_str()) == nullptr) return ev;
   ev.start = take_event(s);
