@@ -750,6 +750,7 @@ template <class Tr> struct Resident {
   static constexpr bool kOpaqueFwd = false, kOpaqueGrad = true;
   static constexpr int kRegFwd = 29, kRegGrad = 13, kLdsFwd = 18, kLdsGrad = 9;
   static constexpr int kRegGradSliced = 11;
+  static constexpr int kRegGradOverlap = 14;
   static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 0, kPbFwd = 0, kPaGrad = 0, kPbGrad = 0;
 };
@@ -757,6 +758,7 @@ template <> struct Resident<TF16> {
   static constexpr bool kOpaqueFwd = true, kOpaqueGrad = true;
   static constexpr int kRegFwd = 32, kRegGrad = 13, kLdsFwd = 18, kLdsGrad = 9;
   static constexpr int kRegGradSliced = 12;
+  static constexpr int kRegGradOverlap = 12;
   static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 0, kPbFwd = 0, kPaGrad = 0, kPbGrad = 0;
 };
@@ -764,6 +766,7 @@ template <> struct Resident<TBF16> {
   static constexpr bool kOpaqueFwd = false, kOpaqueGrad = true;
   static constexpr int kRegFwd = 32, kRegGrad = 11, kLdsFwd = 18, kLdsGrad = 9;
   static constexpr int kRegGradSliced = 9;
+  static constexpr int kRegGradOverlap = 11;
   static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 0, kPbFwd = 0, kPaGrad = 0, kPbGrad = 0;
 };
@@ -899,12 +902,11 @@ __device__ inline void st16(void* p, const uint4& v) {
 // Phase-1 end of a channel tile: the threads' partial sums, summed over the
 // row lanes of each wave with shuffles, then over the waves through LDS
 // (`red`), published as one epoch-tagged pair of words per channel.
+// Sums s1, s2 over the row lanes of each wave (shuffles); lanes
+// 0 .. 2^tx_shift - 1 of the wave then hold the wave's sums of their channels.
 template <int VEC>
-__device__ __forceinline__ void publish_partials(const FusedArgs& a, float2* red,
-                                                 float (&s1)[VEC], float (&s2)[VEC], int tid,
-                                                 int width, int ct, int64_t g, uint64_t etag) {
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
+__device__ __forceinline__ void wave_row_sums(const FusedArgs& a, float (&s1)[VEC],
+                                              float (&s2)[VEC]) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     if (off < (1 << a.tx_shift)) break;
@@ -914,9 +916,29 @@ __device__ __forceinline__ void publish_partials(const FusedArgs& a, float2* red
       s2[j] += __shfl_xor(s2[j], off, 64);
     }
   }
+}
+
+// `stash` (optional): per-wave sums of earlier rows of the same tile, in the
+// layout the row lanes write `red` in, added to the wave's sums first.
+template <int VEC>
+__device__ __forceinline__ void publish_partials(const FusedArgs& a, float2* red,
+                                                 float (&s1)[VEC], float (&s2)[VEC], int tid,
+                                                 int width, int ct, int64_t g, uint64_t etag,
+                                                 const float2* stash = nullptr) {
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  wave_row_sums<VEC>(a, s1, s2);
   if (lane < (1 << a.tx_shift)) {
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) red[wave * width + lane * VEC + j] = make_float2(s1[j], s2[j]);
+    for (int j = 0; j < VEC; ++j) {
+      float2 v = make_float2(s1[j], s2[j]);
+      if (stash) {
+        const float2 e = stash[wave * width + lane * VEC + j];
+        v.x += e.x;
+        v.y += e.y;
+      }
+      red[wave * width + lane * VEC + j] = v;
+    }
   }
   __syncthreads();
   if (tid < width && static_cast<int64_t>(ct) * width + tid < static_cast<int64_t>(a.cv) * VEC) {
@@ -1469,6 +1491,301 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
 }
 
 // ---------------------------------------------------------------------------
+// 4b. Sliced gradient with the hand-offs hidden (NHWC, tiles of 8 channel
+//     vectors, every workgroup one row group running the slices in turn).
+//     After publishing slice s's partials, a workgroup does not wait idle
+//     for slice s's coefficients: it first reads the streamed (not resident)
+//     rows of slice s + 1 - their x and dy need no storage, only their sums,
+//     which each wave keeps in an LDS stash - then takes slice s's
+//     coefficients, writes slice s's outputs (re-reading its streamed rows),
+//     loads slice s + 1's resident rows into the freed registers and LDS,
+//     and publishes slice s + 1's partials (resident rows plus the stash).
+//     Only the last slice's hand-off is a wait.  Registers in use are those
+//     of the plain sliced pass: the stash takes the place of the next
+//     slice's sums while phase 3 runs.
+// ---------------------------------------------------------------------------
+// The stash (per wave and channel, in `red`'s partial layout) sits past the
+// regions publish_partials (8 waves x width float2) and tile_coefs (4 x kW
+// floats) use, both below 8 KB (16-bit) / 4 KB (float) for 8-vector tiles.
+// A copy of a row's words that the compiler cannot see through.
+__device__ inline uint4 opaque_words(uint4 w) {
+  asm volatile("" : "+v"(w.x), "+v"(w.y), "+v"(w.z), "+v"(w.w));
+  return w;
+}
+
+template <int VEC>
+constexpr int stash_offset() { return VEC == 8 ? 1024 : 512; }  // float2 units
+
+template <class Tr, int KR, int KL>
+__global__ __launch_bounds__(kFusedThreads) void bn_sliced_grad_kernel(FusedArgs a) {
+  using S = typename Tr::S;
+  constexpr int VEC = Tr::kVec;
+  constexpr int U = 4;   // streamed vectors per tensor in flight, phase 1
+  constexpr int U3 = 6;  // and phase 3
+  extern __shared__ uint4 lds_rows[];  // [KL][2][kFusedThreads]
+  __shared__ float2 red[(kFusedThreads / 64) * 32 * VEC];
+  static_assert(stash_offset<VEC>() + (kFusedThreads / 64) * 8 * VEC <=
+                    (kFusedThreads / 64) * 32 * VEC, "stash fits in red");
+  float2* const stash = red + stash_offset<VEC>();
+  const int nslices = a.slices;
+  const int width = (1 << a.tx_shift) * VEC;  // channels of a slice
+  const unsigned epoch =
+      a.epoch_dev ? 0x80000001u + __hip_atomic_load(a.epoch_dev, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT) % 0x7fffffffu
+                  : a.epoch;
+  const uint64_t etag = static_cast<uint64_t>(epoch) << 32;
+  const uint32_t wtag = epoch ^ a.wait_xor;
+  const int ry = kFusedThreads >> a.tx_shift;
+  const int64_t g = blockIdx.x;  // one row group per workgroup, every slice
+  const int64_t r0 = g * a.rows_per_g;
+  int64_t r1 = r0 + a.rows_per_g;
+  if (r1 > a.rows) r1 = a.rows;
+  const int64_t gbytes = (r1 - r0) * a.c * static_cast<int64_t>(sizeof(S));
+  const auto rx = rows_rsrc(static_cast<const S*>(a.x) + r0 * a.c, gbytes);
+  const auto rd = rows_rsrc(static_cast<const S*>(a.dy) + r0 * a.c, gbytes);
+  const uint32_t rstride_b =
+      static_cast<uint32_t>(static_cast<int64_t>(ry) * a.c * static_cast<int64_t>(sizeof(S)));
+  const int64_t rstride = static_cast<int64_t>(ry) * a.c;
+
+  // Per-lane geometry of slice s for thread tid (tid is an opaque copy of
+  // threadIdx.x made in each slice, so none of this stays live across the
+  // slice loop).
+  struct Lane {
+    int tx, ty;
+    bool active;
+    int64_t nk, c0;
+    uint32_t off;  // byte offset of row 0 in the group's buffer resources
+  };
+  auto lane_of = [&](int tid, int s) {
+    Lane l;
+    l.tx = tid & ((1 << a.tx_shift) - 1);
+    l.ty = tid >> a.tx_shift;
+    const int64_t cvi = static_cast<int64_t>(s) * (1 << a.tx_shift) + l.tx;
+    l.active = cvi < a.cv;
+    l.nk = l.active && r0 + l.ty < r1 ? (r1 - r0 - l.ty + ry - 1) / ry : 0;
+    l.c0 = l.active ? cvi * VEC : 0;
+    l.off = l.active ? static_cast<uint32_t>((l.ty * static_cast<int64_t>(a.c) + l.c0) *
+                                             static_cast<int64_t>(sizeof(S)))
+                     : kOutOfRange;
+    return l;
+  };
+  auto opaque_tid = []() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+  };
+  auto load_k = [&](const Lane& l, float (&k)[VEC]) {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) k[j] = l.active ? a.fin.mean_in[l.c0 + j] : 0.f;
+  };
+  auto lds = [&](int tid, int q2, int which) -> uint4& {
+    return lds_rows[(q2 * 2 + which) * kFusedThreads + tid];
+  };
+  // Streamed rows [KR + KL, nk) of lane l, accumulated.  Plain loads: phase
+  // 3 re-reads these lines, and finding them in the Infinity Cache matters
+  // (non-temporal loads here made the 56x56 grads 325 us instead of 285-289).
+  auto stream_accum = [&](const Lane& l, const float (&k)[VEC], float (&s1)[VEC],
+                          float (&s2)[VEC]) {
+    const S* px = static_cast<const S*>(a.x) + (r0 + l.ty) * a.c + l.c0;
+    const S* pd = static_cast<const S*>(a.dy) + (r0 + l.ty) * a.c + l.c0;
+    int64_t q = KR + KL;
+    for (; q + U <= l.nk; q += U) {
+      uint4 xw[U], dw[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        xw[u] = ld16(px + (q + u) * rstride);
+        dw[u] = ld16(pd + (q + u) * rstride);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) accum_words<Tr, true>(xw[u], dw[u], k, s1, s2);
+    }
+    if (q < l.nk) {
+      uint4 xw[U], dw[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t o = l.off + static_cast<uint32_t>(q + u) * rstride_b;
+        xw[u] = bld16(rx, o);
+        dw[u] = bld16(rd, o);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (q + u < l.nk) accum_words<Tr, true>(xw[u], dw[u], k, s1, s2);
+    }
+  };
+  // Resident rows of lane l: KR into registers, KL into LDS, all loads in
+  // flight before any is used (never re-read from memory: non-temporal),
+  // then accumulated.
+  uint4 xr[KR], dr[KR];
+  auto resident_accum = [&](int tid, const Lane& l, const float (&k)[VEC], float (&s1)[VEC],
+                            float (&s2)[VEC]) {
+    uint4 xl[KL], dl[KL];
+#pragma unroll
+    for (int q = 0; q < KR; ++q) {
+      const uint32_t o = l.off + static_cast<uint32_t>(q) * rstride_b;
+      xr[q] = bld16_last(rx, o);
+      dr[q] = bld16_last(rd, o);
+    }
+#pragma unroll
+    for (int q = 0; q < KL; ++q) {
+      const uint32_t o = l.off + static_cast<uint32_t>(KR + q) * rstride_b;
+      xl[q] = bld16_last(rx, o);
+      dl[q] = bld16_last(rd, o);
+    }
+    // Register rows are only ever used through opaque copies: rows loaded
+    // here and used as 16-bit values in the next slice's phase 3 were
+    // otherwise split into their halves at the load, both pieces live
+    // across the hand-off (8 registers per row instead of 4; it spilled).
+#pragma unroll
+    for (int q = 0; q < KR; ++q)
+      if (q < l.nk) accum_words<Tr, true>(opaque_words(xr[q]), opaque_words(dr[q]), k, s1, s2);
+#pragma unroll
+    for (int q = 0; q < KL; ++q) {
+      lds(tid, q, 0) = xl[q];
+      lds(tid, q, 1) = dl[q];
+    }
+#pragma unroll 2
+    for (int q = 0; q < KL; ++q) {
+      if (KR + q < l.nk) accum_words<Tr, true>(lds(tid, q, 0), lds(tid, q, 1), k, s1, s2);
+    }
+  };
+
+  // Slice 0: the whole phase 1, then its partials.
+  {
+    const int tid = opaque_tid();
+    const Lane l = lane_of(tid, 0);
+    float k[VEC], s1[VEC], s2[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) s1[j] = s2[j] = 0.f;
+    load_k(l, k);
+    resident_accum(tid, l, k, s1, s2);
+    stream_accum(l, k, s1, s2);
+    publish_partials<VEC>(a, red, s1, s2, tid, width, 0, g, etag);
+  }
+
+#pragma clang loop unroll(disable)
+  for (int sl = 0; sl < nslices; ++sl) {
+    const int tid = opaque_tid();
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const Lane l = lane_of(tid, sl);
+    const int cs0 = sl * width;
+    const int cs1 = a.c < cs0 + width ? a.c : cs0 + width;
+    // ---- phase 2 of slice sl ----
+    finish_channels<Tr, true>(a, cs0, cs1, wave, lane, wtag, etag, epoch);
+    if (sl == 0) zero_side_outputs<true>(a.fin);
+    const bool more = sl + 1 < nslices;
+    // ---- while slice sl's coefficients are pending: the streamed rows of
+    // slice sl + 1, summed into the stash ----
+    if (more) {
+      const Lane ln = lane_of(tid, sl + 1);
+      float k[VEC], s1[VEC], s2[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) s1[j] = s2[j] = 0.f;
+      load_k(ln, k);
+      stream_accum(ln, k, s1, s2);
+      wave_row_sums<VEC>(a, s1, s2);
+      if (lane < (1 << a.tx_shift)) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j)
+          stash[wave * width + lane * VEC + j] = make_float2(s1[j], s2[j]);
+      }
+    }
+    // ---- phase 3 of slice sl ----
+    float4 cf[VEC];
+    tile_coefs<Tr>(a, red, tid, l.tx, sl, width, l.active, wtag, epoch, cf);
+    {
+      const S* px = static_cast<const S*>(a.x) + (r0 + l.ty) * a.c + l.c0;
+      const S* pd = static_cast<const S*>(a.dy) + (r0 + l.ty) * a.c + l.c0;
+      S* po = static_cast<S*>(a.out) + (r0 + l.ty) * a.c + l.c0;
+      const int64_t qlo = KR + KL;
+      int64_t q = l.nk - 1;
+      for (; q >= qlo + U3 - 1; q -= U3) {
+        uint4 xw[U3], dw[U3];
+#pragma unroll
+        for (int u = 0; u < U3; ++u) {
+          xw[u] = ld16_last(px + (q - u) * rstride);
+          dw[u] = ld16_last(pd + (q - u) * rstride);
+        }
+#pragma unroll
+        for (int u = 0; u < U3; ++u)
+          st16(po + (q - u) * rstride, apply_words<Tr, true>(xw[u], dw[u], cf));
+      }
+      if (q >= qlo) {  // fewer than U3 rows left: loads issued together
+        uint4 xw[U3], dw[U3];
+#pragma unroll
+        for (int u = 0; u < U3; ++u) {
+          const uint32_t o = q - u >= qlo ? l.off + static_cast<uint32_t>(q - u) * rstride_b
+                                          : kOutOfRange;
+          xw[u] = bld16_last(rx, o);
+          dw[u] = bld16_last(rd, o);
+        }
+#pragma unroll
+        for (int u = 0; u < U3; ++u)
+          if (q - u >= qlo) st16(po + (q - u) * rstride, apply_words<Tr, true>(xw[u], dw[u], cf));
+      }
+#pragma unroll 2
+      for (int q2 = 0; q2 < KL; ++q2) {
+        if (KR + q2 < l.nk)
+          st16(po + (KR + q2) * rstride,
+               apply_words<Tr, true>(lds(tid, q2, 0), lds(tid, q2, 1), cf));
+      }
+#pragma unroll
+      for (int r = 0; r < KR; ++r)
+        if (r < l.nk)
+          st16(po + r * rstride, apply_words<Tr, true>(opaque_words(xr[r]), opaque_words(dr[r]), cf));
+    }
+    // ---- phase 1 of slice sl + 1: its resident rows, then its partials ----
+    if (more) {
+      const Lane ln = lane_of(tid, sl + 1);
+      float k[VEC], s1[VEC], s2[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) s1[j] = s2[j] = 0.f;
+      load_k(ln, k);
+      resident_accum(tid, ln, k, s1, s2);
+      // Every thread has read slice sl's coefficients out of `red` before
+      // the reduction below writes it.
+      __syncthreads();
+      publish_partials<VEC>(a, red, s1, s2, tid, width, sl + 1, g, etag, stash);
+    }
+  }
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  // Exit of a launch recorded into a graph: counted in two levels; the
+  // workgroup completing the count zeroes the counters and advances the
+  // replays' epoch word (as in bn_fused_nhwc_kernel, which documents the
+  // orderings).
+  if (a.reset_at_exit) {
+    __syncthreads();
+    if (wave == 0) {
+      unsigned done = 0;
+      if (lane == 0) {
+        const unsigned r = blockIdx.x & 7;
+        unsigned last = a.sub_last[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) last = r == static_cast<unsigned>(i) ? a.sub_last[i] : last;
+        const unsigned old =
+            __hip_atomic_fetch_add(a.sub + 64 * r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == last) {
+          const unsigned long long gg =
+              __hip_atomic_fetch_add(a.barrier, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          done = gg == a.base + barrier_classes() - 1;
+        }
+      }
+      if (__builtin_amdgcn_readfirstlane(done)) {
+        if (lane < 8)
+          __hip_atomic_store(a.sub + 64 * lane, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) {
+          __hip_atomic_store(a.barrier, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (a.epoch_dev)
+            __hip_atomic_store(a.epoch_dev, (epoch - 0x80000001u + 1u) % 0x7fffffffu,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 5. NCHW, one channel per workgroup: workgroup ch sums, finishes and applies
 //    channel ch alone, so no value crosses workgroups - no waits, no
 //    co-residency assumption, any number of workgroups in flight.  The
@@ -1814,6 +2131,21 @@ const void* sliced_kernel() {
   return fused_kernel<Tr, true, Resident<Tr>::kRegGradSliced, true>();
 }
 
+// The sliced grad that hides its slices' hand-offs (8-vector tiles, no
+// dynamic tail): the plain sliced kernel's residency.
+template <class Tr>
+const void* sliced_overlap_kernel() {
+  return reinterpret_cast<const void*>(
+      &bn_sliced_grad_kernel<Tr, Resident<Tr>::kRegGradOverlap, Resident<Tr>::kLdsGrad>);
+}
+
+// TFMA_BN_SLICED_OVERLAP=0 (read per call, for tests and measurements):
+// sliced grads run the plain sliced kernel.
+bool sliced_overlap_enabled() {
+  const char* e = getenv("TFMA_BN_SLICED_OVERLAP");
+  return !(e && e[0] == '0');
+}
+
 // Per device: the sliced kernel has the unsliced kernel's occupancy (set by
 // fused_blocks_per_cu).
 template <class Tr, bool kGrad>
@@ -1839,13 +2171,22 @@ int fused_blocks_per_cu() {
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 static_cast<int>(fused_smem<Tr, kGrad>()));
     }
-    if constexpr (kGrad) {  // the sliced grad: same LDS, and it must fit as often
+    if constexpr (kGrad) {  // the sliced grads: same LDS, and they must fit as often
+      int overlap_ns = 0;
       if (e == hipSuccess)
         e = hipFuncSetAttribute(sliced_kernel<Tr>(), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 static_cast<int>(fused_smem<Tr, kGrad>()));
       if (e == hipSuccess)
         e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&sliced_ns, sliced_kernel<Tr>(),
                                                          kFusedThreads, fused_smem<Tr, kGrad>());
+      if (e == hipSuccess)
+        e = hipFuncSetAttribute(sliced_overlap_kernel<Tr>(),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(fused_smem<Tr, kGrad>()));
+      if (e == hipSuccess)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&overlap_ns, sliced_overlap_kernel<Tr>(),
+                                                         kFusedThreads, fused_smem<Tr, kGrad>());
+      if (overlap_ns < sliced_ns) sliced_ns = overlap_ns;
     }
     if (e == hipSuccess)
       e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fused_kernel<Tr, kGrad>(),
@@ -2243,7 +2584,13 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   SetLastKernel(name);
   const void* kern = fused_kernel<Tr, kGrad>();
   if constexpr (kGrad) {
-    if (sliced) kern = sliced_kernel<Tr>();
+    if (sliced) {
+      kern = sliced_kernel<Tr>();
+      // Tiles of 8 vectors (the stash layout) and no dynamic tail: the
+      // kernel that hides the slices' hand-offs.
+      if (fp.tx_shift == 3 && fp.ct_conc == 1 && fa.dyn_rows == 0 && sliced_overlap_enabled())
+        kern = sliced_overlap_kernel<Tr>();
+    }
   }
   if constexpr (!kGrad) {
     if (small) kern = fused_kernel<Tr, kGrad, Resident<Tr>::kRegFwdSmall>();

@@ -149,6 +149,45 @@ def test_sliced_grad_matches_oracle(dev, monkeypatch, shape, dtype, tw, is_train
     assert torch.all(grad.reserve_space_4 == 0) and torch.all(grad.reserve_space_5 == 0)
 
 
+@pytest.mark.parametrize("shape,dtype", [((64, 56, 56, 256), "float16"),
+                                         ((64, 56, 56, 256), "bfloat16"),
+                                         ((32, 28, 28, 128), "float32"),
+                                         ((6, 5, 7, 200), "float16")])
+def test_sliced_overlap_equals_plain_sliced(dev, monkeypatch, shape, dtype):
+    """The sliced gradient that reads the next slice's streamed rows while a
+    slice's coefficients are pending, against the plain sliced pass
+    (TFMA_BN_SLICED_OVERLAP=0), both forced to 8-vector tiles: the same
+    slices, so scale_backprop and offset_backprop within 1e-5 of their
+    largest value (the streamed rows' sums are added in a different order)
+    and x_backprop within one ulp of its largest value; both against the
+    oracle as well."""
+    monkeypatch.setenv("TFMA_BN_SLICE_TW", "8")
+    rng = np.random.default_rng(zlib.crc32(repr((shape, dtype, "overlap")).encode()))
+    eps = 1e-3
+    x, scale, offset, dy = _inputs(rng, shape, dtype, "NHWC", loc=0.5)
+    outs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("TFMA_BN_SLICED_OVERLAP", mode)
+        fwd, grad = _run_fwd_grad(dev, x, scale, offset, dy, dtype, "NHWC", eps)
+        plan = ops.fused_batch_norm_last_plan()
+        vec = 4 if dtype == "float32" else 8
+        assert plan["slices"] == -(-(shape[-1] // vec) // 8), plan
+        outs[mode] = (fwd, grad)
+    (fa, ga), (fb, gb) = outs["1"], outs["0"]
+    for name in ("scale_backprop", "offset_backprop"):
+        a, b = getattr(ga, name).cpu().numpy(), getattr(gb, name).cpu().numpy()
+        assert np.max(np.abs(a - b)) <= 1e-5 * np.max(np.abs(b)), name
+    da, db = to_np(ga.x_backprop, dtype).astype(np.float64), to_np(gb.x_backprop, dtype).astype(np.float64)
+    big = np.max(np.abs(db))
+    ulp = {"float32": 2.0 ** -23, "float16": 2.0 ** -10, "bfloat16": 2.0 ** -7}[dtype]
+    assert np.max(np.abs(da - db)) <= ulp * 2.0 ** np.ceil(np.log2(big)), "x_backprop"
+    rdx, rsb, rob = oracle.bn_grad(dy, x, scale, fa.reserve_space_1.cpu().numpy(),
+                                   fa.reserve_space_2.cpu().numpy(), epsilon=eps, dtype=dtype)
+    assert_close(to_np(ga.x_backprop, dtype), rdx, dtype, ACT_TOL[dtype], "x_backprop")
+    assert_close(ga.scale_backprop.cpu().numpy(), rsb, "float32", STAT_TOL, "scale_backprop")
+    assert_close(ga.offset_backprop.cpu().numpy(), rob, "float32", STAT_TOL, "offset_backprop")
+
+
 OWNED_CASES = [
     ((4, 256, 7, 8), "float16"),      # 28 vectors per channel: most threads idle
     ((64, 256, 28, 28), "bfloat16"),  # every row on chip
