@@ -918,27 +918,48 @@ __device__ __forceinline__ void wave_row_sums(const FusedArgs& a, float (&s1)[VE
   }
 }
 
-// `stash` (optional): per-wave sums of earlier rows of the same tile, in the
-// layout the row lanes write `red` in, added to the wave's sums first.
+// The workgroup's sums of its threads' s1, s2 per channel of the tile, for
+// thread tid < width (channel tid), through `red`: wave sums by shuffles,
+// then the waves in a fixed order.  Every thread calls it (two barriers);
+// `red` must be free on entry.
+template <int VEC>
+__device__ __forceinline__ float2 workgroup_sums(const FusedArgs& a, float2* red,
+                                                float (&s1)[VEC], float (&s2)[VEC], int tid,
+                                                int width) {
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  wave_row_sums<VEC>(a, s1, s2);
+  __syncthreads();
+  if (lane < (1 << a.tx_shift)) {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) red[wave * width + lane * VEC + j] = make_float2(s1[j], s2[j]);
+  }
+  __syncthreads();
+  float2 r = make_float2(0.f, 0.f);
+  if (tid < width) {
+#pragma unroll
+    for (int w = 0; w < kFusedThreads / 64; ++w) {
+      const float2 v = red[w * width + tid];
+      r.x += v.x;
+      r.y += v.y;
+    }
+  }
+  return r;
+}
+
+// `pend` (thread tid < width, channel tid of the tile): sums of earlier rows
+// of the workgroup for that channel, added last.
 template <int VEC>
 __device__ __forceinline__ void publish_partials(const FusedArgs& a, float2* red,
                                                  float (&s1)[VEC], float (&s2)[VEC], int tid,
                                                  int width, int ct, int64_t g, uint64_t etag,
-                                                 const float2* stash = nullptr) {
+                                                 float2 pend = make_float2(0.f, 0.f)) {
   const int wave = tid >> 6;
   const int lane = tid & 63;
   wave_row_sums<VEC>(a, s1, s2);
   if (lane < (1 << a.tx_shift)) {
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      float2 v = make_float2(s1[j], s2[j]);
-      if (stash) {
-        const float2 e = stash[wave * width + lane * VEC + j];
-        v.x += e.x;
-        v.y += e.y;
-      }
-      red[wave * width + lane * VEC + j] = v;
-    }
+    for (int j = 0; j < VEC; ++j) red[wave * width + lane * VEC + j] = make_float2(s1[j], s2[j]);
   }
   __syncthreads();
   if (tid < width && static_cast<int64_t>(ct) * width + tid < static_cast<int64_t>(a.cv) * VEC) {
@@ -949,6 +970,8 @@ __device__ __forceinline__ void publish_partials(const FusedArgs& a, float2* red
       sa += v.x;
       sb += v.y;
     }
+    sa += pend.x;
+    sb += pend.y;
     const int64_t slot = g * a.c + static_cast<int64_t>(ct) * width + tid;
     store_shared(a.eslots + 2 * slot, etag | __builtin_bit_cast(uint32_t, sa));
     store_shared(a.eslots + 2 * slot + 1, etag | __builtin_bit_cast(uint32_t, sb));
@@ -1491,30 +1514,24 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
 }
 
 // ---------------------------------------------------------------------------
-// 4b. Sliced gradient with the hand-offs hidden (NHWC, tiles of 8 channel
-//     vectors, every workgroup one row group running the slices in turn).
+// 4b. Sliced gradient with the hand-offs hidden (NHWC, every workgroup one
+//     row group running the channel tiles - slices - in turn).
 //     After publishing slice s's partials, a workgroup does not wait idle
 //     for slice s's coefficients: it first reads the streamed (not resident)
 //     rows of slice s + 1 - their x and dy need no storage, only their sums,
-//     which each wave keeps in an LDS stash - then takes slice s's
+//     which the workgroup reduces per channel into one register pair of the
+//     thread owning the channel (`pend`) - then takes slice s's
 //     coefficients, writes slice s's outputs (re-reading its streamed rows),
 //     loads slice s + 1's resident rows into the freed registers and LDS,
-//     and publishes slice s + 1's partials (resident rows plus the stash).
+//     and publishes slice s + 1's partials (resident rows, then `pend`).
 //     Only the last slice's hand-off is a wait.  Registers in use are those
-//     of the plain sliced pass: the stash takes the place of the next
-//     slice's sums while phase 3 runs.
+//     of the plain sliced pass plus `pend`.
 // ---------------------------------------------------------------------------
-// The stash (per wave and channel, in `red`'s partial layout) sits past the
-// regions publish_partials (8 waves x width float2) and tile_coefs (4 x kW
-// floats) use, both below 8 KB (16-bit) / 4 KB (float) for 8-vector tiles.
 // A copy of a row's words that the compiler cannot see through.
 __device__ inline uint4 opaque_words(uint4 w) {
   asm volatile("" : "+v"(w.x), "+v"(w.y), "+v"(w.z), "+v"(w.w));
   return w;
 }
-
-template <int VEC>
-constexpr int stash_offset() { return VEC == 8 ? 1024 : 512; }  // float2 units
 
 template <class Tr, int KR, int KL>
 __global__ __launch_bounds__(kFusedThreads) void bn_sliced_grad_kernel(FusedArgs a) {
@@ -1524,9 +1541,6 @@ __global__ __launch_bounds__(kFusedThreads) void bn_sliced_grad_kernel(FusedArgs
   constexpr int U3 = 6;  // and phase 3
   extern __shared__ uint4 lds_rows[];  // [KL][2][kFusedThreads]
   __shared__ float2 red[(kFusedThreads / 64) * 32 * VEC];
-  static_assert(stash_offset<VEC>() + (kFusedThreads / 64) * 8 * VEC <=
-                    (kFusedThreads / 64) * 32 * VEC, "stash fits in red");
-  float2* const stash = red + stash_offset<VEC>();
   const int nslices = a.slices;
   const int width = (1 << a.tx_shift) * VEC;  // channels of a slice
   const unsigned epoch =
@@ -1675,7 +1689,8 @@ __global__ __launch_bounds__(kFusedThreads) void bn_sliced_grad_kernel(FusedArgs
     if (sl == 0) zero_side_outputs<true>(a.fin);
     const bool more = sl + 1 < nslices;
     // ---- while slice sl's coefficients are pending: the streamed rows of
-    // slice sl + 1, summed into the stash ----
+    // slice sl + 1, summed per channel into `pend` ----
+    float2 pend = make_float2(0.f, 0.f);
     if (more) {
       const Lane ln = lane_of(tid, sl + 1);
       float k[VEC], s1[VEC], s2[VEC];
@@ -1683,12 +1698,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_sliced_grad_kernel(FusedArgs
       for (int j = 0; j < VEC; ++j) s1[j] = s2[j] = 0.f;
       load_k(ln, k);
       stream_accum(ln, k, s1, s2);
-      wave_row_sums<VEC>(a, s1, s2);
-      if (lane < (1 << a.tx_shift)) {
-#pragma unroll
-        for (int j = 0; j < VEC; ++j)
-          stash[wave * width + lane * VEC + j] = make_float2(s1[j], s2[j]);
-      }
+      pend = workgroup_sums<VEC>(a, red, s1, s2, tid, width);
     }
     // ---- phase 3 of slice sl ----
     float4 cf[VEC];
@@ -1745,7 +1755,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_sliced_grad_kernel(FusedArgs
       // Every thread has read slice sl's coefficients out of `red` before
       // the reduction below writes it.
       __syncthreads();
-      publish_partials<VEC>(a, red, s1, s2, tid, width, sl + 1, g, etag, stash);
+      publish_partials<VEC>(a, red, s1, s2, tid, width, sl + 1, g, etag, pend);
     }
   }
   const int wave = threadIdx.x >> 6;
@@ -2294,19 +2304,22 @@ bool make_sliced_plan(const BnGeometry& g, int vec, int blocks_per_cu, int tx_sh
   return true;
 }
 
-// Rows per thread of the unsliced grad plan from which the grad is sliced.
-constexpr int64_t kSliceMinRows = 128;
+// A gradient is sliced when the x + dy rows its unsliced plan re-reads in
+// phase 3 exceed kGradSliceAbove (more than the 256 MB Infinity Cache keeps
+// for the re-read), into the fewest slices whose re-read stays below
+// kGradSliceStreamMax.
+constexpr int64_t kGradSliceAbove = int64_t(192) << 20;
+constexpr int64_t kGradSliceStreamMax = int64_t(128) << 20;
 
-// The fused plan of an NHWC op.  A gradient whose unsliced plan leaves each
-// thread kSliceMinRows rows or more (x + dy several times what the grid
-// holds on chip; cfg2's 256x56x56x256) runs sliced: tiles of 8 channel
+// The fused plan of an NHWC op.  A gradient whose unsliced plan re-reads more
+// x + dy in phase 3 than the Infinity Cache keeps for it runs sliced: every
+// workgroup runs the two-phase pass once per channel tile in turn, with the
+// widest tiles (fewest slices and hand-offs) whose per-slice re-read stays
+// below kGradSliceStreamMax - cfg2's 256x56x56x256 in 4 slices of 8
 // vectors (128-byte row segments, the narrowest that read whole cache
-// lines), every workgroup running all of them in turn, so each slice's
-// phase-3 re-read is 55 % of its x + dy instead of 89 % of the whole
-// (measured: 333 -> 305 us f16, 343 -> 313 us bf16 at 256x56x56x256; at
-// 256x28x28x512, 98 rows, no slicing was faster; sliced forwards were
-// never faster - a slice's read-only phase 1 and write-only phase 3 stream
-// slower than the unsliced phase 3, which reads and writes at once).
+// lines), 256x28x28x512 in 2 of 32.  Forwards are not sliced (measured
+// slower: a slice's read-only phase 1 and write-only phase 3 stream slower
+// than the unsliced phase 3, which reads and writes at once).
 // TFMA_BN_SLICE_TW (read per call, for tests and measurements): 0 never
 // slices; 8, 16 or 32 slices every grad that has such a plan, with tiles of
 // that many vectors.
@@ -2321,15 +2334,33 @@ bool choose_fused_plan(const BnGeometry& g, int vec, FusedPlan* fp) {
     const char* o = getenv("TFMA_BN_SLICE_TW");
     int tw = o ? atoi(o) : -1;
     if (tw == 0) return true;
-    if (tw != 8 && tw != 16 && tw != 32) {
-      const int ry = kFusedThreads >> fp->tx_shift;
-      if ((fp->rows_per_g + ry - 1) / ry < kSliceMinRows) return true;
-      tw = 8;
+    if (tw == 8 || tw == 16 || tw == 32) {
+      FusedPlan sp;
+      if (make_sliced_plan(g, vec, bpc, tw == 8 ? 3 : (tw == 16 ? 4 : 5), 1, &sp) &&
+          sp.slices <= 8)
+        *fp = sp;
+      return true;
     }
-    FusedPlan sp;
-    if (make_sliced_plan(g, vec, bpc, tw == 8 ? 3 : (tw == 16 ? 4 : 5), 1, &sp) &&
-        sp.slices <= 8)
+    // x + dy rows that phase 3 re-reads (those not held on chip), in bytes.
+    constexpr int kRes = Resident<Tr>::kRegGradOverlap + Resident<Tr>::kLdsGrad;
+    const int64_t threads = static_cast<int64_t>(fp->blocks) * kFusedThreads;
+    auto streamed_bytes = [&](const FusedPlan& p) {
+      const int ry = kFusedThreads >> p.tx_shift;
+      const int64_t nk = (p.rows_per_g + ry - 1) / ry;
+      return (nk > kRes ? nk - kRes : 0) * 32 * threads;
+    };
+    if (streamed_bytes(*fp) <= kGradSliceAbove) return true;
+    for (int shift = 5; shift >= 3; --shift) {
+      FusedPlan sp;
+      if (!make_sliced_plan(g, vec, bpc, shift, 1, &sp) || sp.slices > 8) continue;
+      if (streamed_bytes(sp) > kGradSliceStreamMax) continue;
       *fp = sp;
+      return true;
+    }
+    // Too large for any slice to keep its re-read in the cache: the
+    // narrowest tiles (fewest rows on chip to re-read per slice).
+    FusedPlan sp;
+    if (make_sliced_plan(g, vec, bpc, 3, 1, &sp) && sp.slices <= 8) *fp = sp;
   }
   return true;
 }
@@ -2586,11 +2617,11 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   if constexpr (kGrad) {
     if (sliced) {
       kern = sliced_kernel<Tr>();
-      // Tiles of 8 vectors (the stash's layout; 16-vector tiles measured no
-      // gain at 28x28 and a loss at 56x56) and no dynamic tail: the kernel
-      // that hides the slices' hand-offs.
-      if (fp.tx_shift == 3 && fp.ct_conc == 1 && fa.dyn_rows == 0 && sliced_overlap_enabled())
+      // No dynamic tail: the kernel that hides the slices' hand-offs.
+      if (fp.ct_conc == 1 && fa.dyn_rows == 0 && sliced_overlap_enabled()) {
         kern = sliced_overlap_kernel<Tr>();
+        t_last_plan.register_rows = Resident<Tr>::kRegGradOverlap;
+      }
     }
   }
   if constexpr (!kGrad) {

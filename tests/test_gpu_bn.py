@@ -149,20 +149,22 @@ def test_sliced_grad_matches_oracle(dev, monkeypatch, shape, dtype, tw, is_train
     assert torch.all(grad.reserve_space_4 == 0) and torch.all(grad.reserve_space_5 == 0)
 
 
-@pytest.mark.parametrize("shape,dtype", [((64, 56, 56, 256), "float16"),
-                                         ((64, 56, 56, 256), "bfloat16"),
-                                         ((32, 28, 28, 128), "float32"),
-                                         ((6, 5, 7, 200), "float16")])
-def test_sliced_overlap_equals_plain_sliced(dev, monkeypatch, shape, dtype):
+@pytest.mark.parametrize("shape,dtype,tw", [((64, 56, 56, 256), "float16", 8),
+                                            ((64, 56, 56, 256), "bfloat16", 8),
+                                            ((32, 28, 28, 128), "float32", 8),
+                                            ((6, 5, 7, 200), "float16", 8),
+                                            ((64, 28, 28, 512), "bfloat16", 32),
+                                            ((16, 28, 28, 512), "float32", 16)])
+def test_sliced_overlap_equals_plain_sliced(dev, monkeypatch, shape, dtype, tw):
     """The sliced gradient that reads the next slice's streamed rows while a
     slice's coefficients are pending, against the plain sliced pass
-    (TFMA_BN_SLICED_OVERLAP=0), both forced to 8-vector tiles: the same
+    (TFMA_BN_SLICED_OVERLAP=0), both forced to tw-vector tiles: the same
     slices, so scale_backprop and offset_backprop within 1e-5 of their
     largest value (the streamed rows' sums are added in a different order)
     and x_backprop within one ulp of its largest value; both against the
     oracle as well."""
-    monkeypatch.setenv("TFMA_BN_SLICE_TW", "8")
-    rng = np.random.default_rng(zlib.crc32(repr((shape, dtype, "overlap")).encode()))
+    monkeypatch.setenv("TFMA_BN_SLICE_TW", str(tw))
+    rng = np.random.default_rng(zlib.crc32(repr((shape, dtype, tw, "overlap")).encode()))
     eps = 1e-3
     x, scale, offset, dy = _inputs(rng, shape, dtype, "NHWC", loc=0.5)
     outs = {}
@@ -171,7 +173,7 @@ def test_sliced_overlap_equals_plain_sliced(dev, monkeypatch, shape, dtype):
         fwd, grad = _run_fwd_grad(dev, x, scale, offset, dy, dtype, "NHWC", eps)
         plan = ops.fused_batch_norm_last_plan()
         vec = 4 if dtype == "float32" else 8
-        assert plan["slices"] == -(-(shape[-1] // vec) // 8), plan
+        assert plan["slices"] == -(-(shape[-1] // vec) // tw), plan
         outs[mode] = (fwd, grad)
     (fa, ga), (fb, gb) = outs["1"], outs["0"]
     for name in ("scale_backprop", "offset_backprop"):
@@ -353,9 +355,10 @@ def test_cfg2_full_size(dev, shape, dtype):
     (batch_mean, batch_variance, reserve spaces, scale_backprop,
     offset_backprop) to 1e-5 - the outputs the reference's own test checks,
     test/ops/fused_batchnorm_op_test.py:358-448.  The 56x56 gradient runs
-    sliced (4 slices of 64 channels); the 28x28 gradient and the 56x56
-    forward hand part of phase 3 out dynamically; the plan query shows that
-    these paths are the ones compared here."""
+    in 4 slices of 64 channels and the 28x28 gradient in 2 of 256 (both
+    hiding their slices' hand-offs); the 56x56 forward hands part of phase 3
+    out dynamically; the plan query shows that these paths are the ones
+    compared here."""
     rng = np.random.default_rng(zlib.crc32(repr((shape, dtype)).encode()))
     eps = 1.001e-5
     x, scale, offset, dy = _inputs(rng, shape, dtype, "NHWC")
@@ -371,10 +374,12 @@ def test_cfg2_full_size(dev, shape, dtype):
     torch.cuda.synchronize()
     assert fplan["fused"] == 1 and gplan["fused"] == 1
     if shape[1] == 56:
-        assert gplan["slices"] == 4, gplan
+        assert gplan["slices"] == 4 and gplan["dynamic_rows"] == 0, gplan
         assert fplan["dynamic_rows"] > 0, fplan
     elif shape[1] == 28:
-        assert gplan["dynamic_rows"] > 0 and gplan["slices"] == 1, gplan
+        assert gplan["slices"] == 2 and gplan["dynamic_rows"] == 0, gplan
+    else:
+        assert gplan["slices"] == 1, gplan
     del tx, tdy
     ry, rbm, rbv, rsm, rsv = oracle.bn_fwd(x, scale, offset, epsilon=eps, dtype=dtype)
     assert_close(to_np(fwd.y, dtype), ry, dtype, 1e-2, "y")

@@ -49,14 +49,16 @@ def _state(d):
     return [d["var"].clone(), d["m"].clone(), d["v"].clone()]
 
 
-# (16,14,14,256): every row resident, no dynamic chunks.  (128,56,56,256):
-# the grad hands out phase-3 chunks, so the recorded launch zeroes the chunk
-# counters as well as the barrier counters at exit; with slice_tw 8 the grad
-# runs sliced (4 slices of 64 channels, eager and recorded).
-@pytest.mark.parametrize("shape,slice_tw", [((16, 14, 14, 256), None),
-                                            ((128, 56, 56, 256), None),
-                                            ((128, 56, 56, 256), 8)])
-def test_recorded_training_step_replays(dev, monkeypatch, shape, slice_tw):
+# (16,14,14,256): every row resident, no dynamic chunks.  (128,56,56,256)
+# unsliced (TFMA_BN_SLICE_TW=0): the grad hands out phase-3 chunks, so the
+# recorded launch zeroes the chunk counters as well as the barrier counters
+# at exit; left to the host, the grad runs in 2 slices of 128 channels
+# (hand-offs hidden); with slice_tw 8 in 4 slices of 64 channels.
+@pytest.mark.parametrize("shape,slice_tw,slices", [((16, 14, 14, 256), None, 1),
+                                                   ((128, 56, 56, 256), 0, 1),
+                                                   ((128, 56, 56, 256), None, 2),
+                                                   ((128, 56, 56, 256), 8, 4)])
+def test_recorded_training_step_replays(dev, monkeypatch, shape, slice_tw, slices):
     if slice_tw is not None:
         monkeypatch.setenv("TFMA_BN_SLICE_TW", str(slice_tw))
     d = _inputs(dev, shape, seed=31)
@@ -66,8 +68,10 @@ def test_recorded_training_step_replays(dev, monkeypatch, shape, slice_tw):
     eager = []
     for _ in range(3):
         eager.append([t.clone() for t in _step(d)] + _state(d))
-        if slice_tw is not None:
-            assert ops.fused_batch_norm_last_plan()["slices"] == 4
+        plan = ops.fused_batch_norm_last_plan()
+        assert plan["slices"] == slices, plan
+        if slice_tw == 0 and shape[1] == 56:
+            assert plan["dynamic_rows"] > 0, plan
     other_ref = ops.FusedBatchNormV3(other["x"], other["scale"], other["offset"], e, e,
                                      epsilon=EPS).y.clone()
     torch.cuda.synchronize()
