@@ -2321,8 +2321,8 @@ constexpr int64_t kGradSliceStreamMax = int64_t(128) << 20;
 // slower: a slice's read-only phase 1 and write-only phase 3 stream slower
 // than the unsliced phase 3, which reads and writes at once).
 // TFMA_BN_SLICE_TW (read per call, for tests and measurements): 0 never
-// slices; 8, 16 or 32 slices every grad that has such a plan, with tiles of
-// that many vectors.
+// slices; 4, 8, 16 or 32 slices every grad that has such a plan, with tiles
+// of that many vectors.
 template <class Tr, bool kGrad>
 bool choose_fused_plan(const BnGeometry& g, int vec, FusedPlan* fp) {
   const int bpc = fused_blocks_per_cu<Tr, kGrad>();
@@ -2334,9 +2334,9 @@ bool choose_fused_plan(const BnGeometry& g, int vec, FusedPlan* fp) {
     const char* o = getenv("TFMA_BN_SLICE_TW");
     int tw = o ? atoi(o) : -1;
     if (tw == 0) return true;
-    if (tw == 8 || tw == 16 || tw == 32) {
+    if (tw == 4 || tw == 8 || tw == 16 || tw == 32) {
       FusedPlan sp;
-      if (make_sliced_plan(g, vec, bpc, tw == 8 ? 3 : (tw == 16 ? 4 : 5), 1, &sp) &&
+      if (make_sliced_plan(g, vec, bpc, __builtin_ctz(tw), 1, &sp) &&
           sp.slices <= 8)
         *fp = sp;
       return true;
