@@ -24,44 +24,58 @@ namespace {
 constexpr int kThreads = 256;
 
 // kRowOddK: a row operand (inner extent 1) whose period is not a multiple of
-// the vector width - one modulo per vector, then consecutive elements with a
-// wrap at the period.  kGatherK: anything else - one division per vector,
-// then an incremental walk of (index, position within the inner extent).
-// Both read the operand's `period` values from a copy in LDS that each
-// workgroup makes first (per-element gathers from global memory are limited
-// by the L1's request rate, not by bytes); kGatherGlobalK is the same walk
-// from global memory, for periods larger than the LDS copy allows.
+// the vector width - one modulo per vector, then one 16-byte read from the
+// operand's shifted copies in LDS (odd_len below).  kGatherK: anything else -
+// one division per vector, then an incremental walk of (index, position
+// within the inner extent) over a copy of the operand's `period` values in
+// LDS.  Each workgroup makes its copies first (per-element gathers from
+// global memory are limited by the L1's request rate, not by bytes);
+// kGatherGlobalK is the same walk from global memory, for periods larger
+// than the LDS copies allow.
 enum Kind : int {
   kFullK = 0, kScalarK = 1, kRowK = 2, kChanK = 3, kRowOddK = 4, kGatherK = 5, kGatherGlobalK = 6
 };
-// Per staged operand: the padded copy (periods up to 8191 half, 4095 float)
-// and 16 bytes the half gather may read past its end (never used).
-constexpr uint32_t kStageBytes = 20496;
-constexpr uint32_t kStageSlack = 16;
 constexpr bool staged_kind(int k) { return k == kRowOddK || k == kGatherK; }
 
-// LDS slot of element e of a staged odd-period row operand.  Consecutive
-// lanes read elements 16 bytes apart (one vector each), which puts every
-// lane of a wave on the same few banks; one pad word after every 16 bytes
-// makes the lane stride 20 bytes (5 words, coprime with the bank count), so
-// those reads are conflict-free (measured: 2.8 conflicts per LDS access
-// without the pad on [8191,4095]).  8-byte elements are stored unpadded.
-template <int ES>
-__host__ __device__ constexpr uint32_t odd_slot(uint32_t e) {
-  return ES == 2 ? e + ((e >> 3) << 1) : (ES == 4 ? e + (e >> 2) : e);
+// A staged odd-period row operand is held as V = 16 / es copies of
+// odd_len(period, es) positions each, copy s holding element
+// (k + s) mod period at position k.  The vector of V elements that starts at
+// element idx is then the 16 bytes at position idx - s of copy
+// s = idx mod V: 16-byte aligned whatever idx is, one ds_read_b128, no wrap
+// at the period's end.  (A single copy needed five 32-bit reads and four
+// funnel shifts per half vector, and an element loop where a vector wraps.)
+// Consecutive lanes read consecutive 16-byte spans of one copy.  Copy s
+// sits at odd_slot(s) * odd_len: copies 1 .. V - 1 first, copy 0 last, with
+// kOddGuard more positions, from which copies 1 .. V - 1 are built.
+__host__ __device__ constexpr uint32_t odd_copies(int es) { return 16u / es; }
+constexpr uint32_t kOddGuard = 16;
+// Positions per copy: at least period + V - 1, a multiple of V (so every
+// copy starts 16-byte aligned).
+__host__ __device__ constexpr uint32_t odd_len(uint32_t period, int es) {
+  return (period + 2 * (16 / es) - 2) / (16 / es) * (16 / es);
 }
-// Bytes of the padded LDS copy of a period-element odd row operand.
+__host__ __device__ constexpr uint32_t odd_slot(uint32_t s, int es) {
+  return (s - 1) & (odd_copies(es) - 1);
+}
 __host__ __device__ constexpr uint32_t odd_stage_bytes(uint32_t period, int es) {
-  return period == 0 ? 0
-                     : ((es == 2 ? odd_slot<2>(period - 1)
-                                 : es == 4 ? odd_slot<4>(period - 1) : period - 1) + 1) * es;
+  return period == 0 ? 0 : (odd_copies(es) * odd_len(period, es) + kOddGuard) * es;
 }
+// LDS budget per staged operand: the shifted copies of periods up to 4095
+// elements (65696 bytes for half), the plain copy of kGatherK periods up to
+// 20496 bytes.
+constexpr uint32_t kOddStageBytes = 65696;
+constexpr uint32_t kGatherStageBytes = 20496;
+__host__ __device__ constexpr uint32_t stage_bytes(int kind, uint32_t period, int es) {
+  return kind == kRowOddK ? odd_stage_bytes(period, es) : (kind == kGatherK ? period * es : 0);
+}
+__host__ __device__ constexpr uint32_t round16(uint32_t b) { return (b + 15u) & ~15u; }
 
 struct Operand {
   const void* p;
   int kind;
   uint32_t period;
   uint32_t inner;
+  uint32_t olen;  // kRowOddK: odd_len(period, element bytes)
   FastDiv div_inner;
   FastDiv div_period;
 };
@@ -92,7 +106,12 @@ __device__ inline void fetch(const Operand& o, const S* p, uint32_t i0, S (&out)
       case kScalarK: fetch<kScalarK, S, V>(o, p, i0, out); break;
       case kRowK: fetch<kRowK, S, V>(o, p, i0, out); break;
       case kChanK: fetch<kChanK, S, V>(o, p, i0, out); break;
-      case kRowOddK: fetch<kRowOddK, S, V>(o, p, i0, out); break;
+      case kRowOddK:  // only classified for 16-byte vectors
+        if constexpr (V * sizeof(S) == 16) {
+          fetch<kRowOddK, S, V>(o, p, i0, out);
+          break;
+        }
+        [[fallthrough]];
       default: fetch<kGatherK, S, V>(o, p, i0, out); break;
     }
   } else if constexpr (K == kFullK) {
@@ -109,39 +128,13 @@ __device__ inline void fetch(const Operand& o, const S* p, uint32_t i0, S (&out)
 #pragma unroll
     for (int j = 0; j < V; ++j) out[j] = s;
   } else if constexpr (K == kRowOddK) {
-    // p is the padded LDS copy (odd_slot).
-    uint32_t idx = i0 - o.div_period.div(i0) * o.period;
-    if (idx + V <= o.period) {  // no wrap: consecutive elements from one base
-      if constexpr (sizeof(S) == 2 && V == 8) {
-        // Eight halves from the five 32-bit words that cover them (word d of
-        // the copy sits at d + d / 4: one pad word per four), realigned by
-        // one funnel shift per output word - 0 or 16 bits by idx's parity.
-        // (Eight 16-bit reads with their own slot arithmetic made the kernel
-        // issue-bound.)  For an even idx the fifth word is read and unused.
-        const uint32_t* pw = reinterpret_cast<const uint32_t*>(p);
-        const uint32_t d0 = idx >> 1;
-        uint32_t w[5];
-#pragma unroll
-        for (int k = 0; k < 5; ++k) {
-          const uint32_t d = d0 + k;
-          w[k] = pw[d + (d >> 2)];
-        }
-        const uint32_t sh = (idx & 1u) << 4;
-        uint32_t ow[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) ow[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
-        __builtin_memcpy(out, ow, 16);
-      } else {
-#pragma unroll
-        for (int j = 0; j < V; ++j) out[j] = p[odd_slot<sizeof(S)>(idx + j)];
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        out[j] = p[odd_slot<sizeof(S)>(idx)];
-        idx = idx + 1 == o.period ? 0 : idx + 1;
-      }
-    }
+    // p is the shifted copies (odd_len).
+    static_assert(V * sizeof(S) == 16 && V == odd_copies(sizeof(S)), "one 16-byte read");
+    const uint32_t idx = i0 - o.div_period.div(i0) * o.period;
+    const uint32_t sh = idx & (V - 1);
+    const uint4 w = *static_cast<const uint4*>(
+        __builtin_assume_aligned(p + odd_slot(sh, sizeof(S)) * o.olen + (idx - sh), 16));
+    __builtin_memcpy(out, &w, 16);
   } else {
     const uint32_t q = o.div_inner.div(i0);
     uint32_t r = i0 - q * o.inner;
@@ -153,6 +146,95 @@ __device__ inline void fetch(const Operand& o, const S* p, uint32_t i0, S (&out)
       r = next ? 0 : r;
       idx = next ? (idx + 1 == o.period ? 0 : idx + 1) : idx;
     }
+  }
+}
+
+// The 16 bytes of V elements p[e .. e + V - 1] of an LDS array at any
+// element e: halves as the five 32-bit words that cover them, realigned by
+// one funnel shift per word (0 or 16 bits by e's parity; reads elements up
+// to e + 9), wider elements directly.
+template <typename S>
+__device__ inline uint4 lds_window(const S* p, uint32_t e) {
+  constexpr int V = 16 / sizeof(S);
+  uint4 r;
+  if constexpr (sizeof(S) == 2) {
+    const uint32_t* pw = reinterpret_cast<const uint32_t*>(p);
+    const uint32_t d0 = e >> 1;
+    uint32_t w[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) w[k] = pw[d0 + k];
+    const uint32_t sh = (e & 1u) << 4;
+    r = make_uint4(__builtin_amdgcn_alignbit(w[1], w[0], sh),
+                   __builtin_amdgcn_alignbit(w[2], w[1], sh),
+                   __builtin_amdgcn_alignbit(w[3], w[2], sh),
+                   __builtin_amdgcn_alignbit(w[4], w[3], sh));
+  } else {
+    S v[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = p[e + j];
+    __builtin_memcpy(&r, v, 16);
+  }
+  return r;
+}
+
+// Per thread, the positions of copy 0 and the vectors of each other copy
+// staged (odd_len is at most kOddStageBytes / 16 for every element size).
+constexpr uint32_t kOddStageLoads = (kOddStageBytes / 16 + kOddGuard + kThreads - 1) / kThreads;
+template <typename S>
+constexpr uint32_t odd_stage_vecs() {
+  return (kOddStageBytes / 16 / (16 / sizeof(S)) + kThreads - 1) / kThreads;
+}
+
+// A workgroup's LDS copy of a staged operand (src: its values in global
+// memory).  kRowOddK: copy 0 (odd_len + kOddGuard positions) element by
+// element from global memory, then copies 1 .. V - 1 a 16-byte vector at a
+// time from copy 0 (lds_window), every load of a thread issued before the
+// first is used.  Indices past the end are clamped, not branched around
+// (the clamped store writes the value its position holds anyway): a load
+// whose only use sat in a branch left the compiler's wait analysis treating
+// its register as pending in the streaming loop, which then waited for each
+// load before issuing the next.  kGatherK: the plain copy.
+template <int K, typename S>
+__device__ inline void stage(const Operand& o, const S* src, S* dst) {
+  if constexpr (K == kRowOddK) {
+    constexpr uint32_t V = odd_copies(sizeof(S));
+    const uint32_t len = o.olen;
+    S* const c0 = dst + (V - 1) * len;
+    const uint32_t ext = len + kOddGuard;
+    S v0[kOddStageLoads];
+#pragma unroll
+    for (uint32_t r = 0; r < kOddStageLoads; ++r) {
+      uint32_t k = threadIdx.x + r * kThreads;
+      k = k < ext ? k : ext - 1;
+      v0[r] = src[k - o.div_period.div(k) * o.period];
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < kOddStageLoads; ++r) {
+      const uint32_t k = threadIdx.x + r * kThreads;
+      c0[k < ext ? k : ext - 1] = v0[r];
+    }
+    __syncthreads();
+    // Copy sh, vector kv: elements kv * V + sh .. kv * V + sh + V - 1 of
+    // copy 0 (lds_window reads up to 9 past them: within the guard).
+    const uint32_t nvec = len / V;
+#pragma unroll
+    for (uint32_t sh = 1; sh < V; ++sh) {
+      uint4 w[odd_stage_vecs<S>()];
+      uint32_t kv[odd_stage_vecs<S>()];
+#pragma unroll
+      for (uint32_t r = 0; r < odd_stage_vecs<S>(); ++r) {
+        kv[r] = threadIdx.x + r * kThreads;
+        kv[r] = kv[r] < nvec ? kv[r] : nvec - 1;
+        w[r] = lds_window(c0, kv[r] * V + sh);
+      }
+#pragma unroll
+      for (uint32_t r = 0; r < odd_stage_vecs<S>(); ++r)
+        *static_cast<uint4*>(__builtin_assume_aligned(dst + (sh - 1) * len + kv[r] * V, 16)) =
+            w[r];
+    }
+  } else {
+#pragma unroll 4
+    for (uint32_t k = threadIdx.x; k < o.period; k += kThreads) dst[k] = src[k];
   }
 }
 
@@ -201,14 +283,14 @@ __global__ __launch_bounds__(kThreads) void ew_flat_kernel(
   const S* pc = static_cast<const S*>(c.p);
   if constexpr (kArity >= 2 && staged_kind(KB)) {
     S* l = reinterpret_cast<S*>(ew_lds);
-    for (uint32_t k = threadIdx.x; k < b.period; k += kThreads)
-      l[KB == kRowOddK ? odd_slot<sizeof(S)>(k) : k] = pb[k];
+    stage<KB>(b, pb, l);
     pb = l;
   }
   if constexpr (kArity >= 3 && staged_kind(KC)) {
-    S* l = reinterpret_cast<S*>(ew_lds + (staged_kind(KB) ? kStageBytes : 0));
-    for (uint32_t k = threadIdx.x; k < c.period; k += kThreads)
-      l[KC == kRowOddK ? odd_slot<sizeof(S)>(k) : k] = pc[k];
+    const uint32_t off =
+        kArity >= 2 && staged_kind(KB) ? round16(stage_bytes(KB, b.period, sizeof(S))) : 0;
+    S* l = reinterpret_cast<S*>(ew_lds + off);
+    stage<KC>(c, pc, l);
     pc = l;
   }
   if constexpr ((kArity >= 2 && staged_kind(KB)) || (kArity >= 3 && staged_kind(KC)))
@@ -323,6 +405,7 @@ Operand make_operand(const BcastOperand& o, int elem_bytes, int V,
   r.p = o.data;
   r.period = 1;
   r.inner = 1;
+  r.olen = 0;
   const bool aligned = (reinterpret_cast<uintptr_t>(o.data) & 15) == 0;
   switch (o.mode) {
     case BcastMode::kFull:
@@ -347,11 +430,12 @@ Operand make_operand(const BcastOperand& o, int elem_bytes, int V,
         r.kind = kRowK;
       } else if (o.inner % V == 0) {
         r.kind = kChanK;
-      } else if (o.inner == 1 ? odd_stage_bytes(r.period, elem_bytes) + kStageSlack > kStageBytes
-                              : o.period * elem_bytes > kStageBytes) {
+      } else if (o.inner == 1 ? odd_stage_bytes(r.period, elem_bytes) > kOddStageBytes
+                              : o.period * elem_bytes > kGatherStageBytes) {
         r.kind = kGatherGlobalK;
       } else if (o.inner == 1) {
         r.kind = kRowOddK;
+        r.olen = odd_len(r.period, elem_bytes);
       } else {
         r.kind = kGatherK;
       }
@@ -385,10 +469,23 @@ void launch_vec(const Operand& ob, const Operand& oc, const typename Tr::S* a,
   // A staged workgroup copies the operand once; fewer, longer-lived
   // workgroups keep that copy cheap.
   constexpr int kEs = sizeof(typename Tr::S);
-  const size_t lds = sc ? (sb ? 2 : 1) * kStageBytes
-                        : (sb ? (KB == kRowOddK ? odd_stage_bytes(ob.period, kEs) + kStageSlack
-                                                : ob.period * kEs)
-                              : 0);
+  const uint32_t lds_b = sb ? stage_bytes(KB, ob.period, kEs) : 0;
+  const size_t lds = sc ? round16(lds_b) + stage_bytes(KC, oc.period, kEs) : lds_b;
+  // Two staged operands may need more than the 64 KB a launch gets by default
+  // (a failure here is left for the caller's hipGetLastError).
+  if (lds > 65536) {
+    static bool raised[64] = {false};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
+    if (!raised[dev]) {
+      constexpr int kMaxLds = static_cast<int>(round16(kOddStageBytes) + kOddStageBytes);
+      if (hipFuncSetAttribute(
+              reinterpret_cast<const void*>(&ew_flat_kernel<Tr, OP, V, U, KB, KC, 0>),
+              hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds) != hipSuccess)
+        return;
+      raised[dev] = true;
+    }
+  }
   int64_t blocks = grid_for(n / V, U);
   const int64_t cap = static_cast<int64_t>(DeviceCUs()) * 4;
   if ((sb || sc) && blocks > cap) blocks = cap;
