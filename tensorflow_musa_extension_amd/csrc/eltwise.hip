@@ -37,17 +37,19 @@ enum Kind : int {
 };
 constexpr bool staged_kind(int k) { return k == kRowOddK || k == kGatherK; }
 
-// A staged odd-period row operand is held as V = 16 / es copies of
-// odd_len(period, es) positions each, copy s holding element
-// (k + s) mod period at position k.  The vector of V elements that starts at
-// element idx is then the 16 bytes at position idx - s of copy
-// s = idx mod V: 16-byte aligned whatever idx is, one ds_read_b128, no wrap
-// at the period's end.  (A single copy needed five 32-bit reads and four
-// funnel shifts per half vector, and an element loop where a vector wraps.)
-// Consecutive lanes read consecutive 16-byte spans of one copy.  Copy s
-// sits at odd_slot(s) * odd_len: copies 1 .. V - 1 first, copy 0 last, with
-// kOddGuard more positions, from which copies 1 .. V - 1 are built.
-__host__ __device__ constexpr uint32_t odd_copies(int es) { return 16u / es; }
+// A staged odd-period row operand is held as odd_copies(es) = 8 / es copies
+// (one for 8-byte elements) of odd_len(period, es) positions each, copy s
+// holding element (k + s) mod period at position k.  The vector of
+// V = 16 / es elements that starts at element idx is then the 16 bytes at
+// position idx - s of copy s = idx mod odd_copies: 8-byte aligned whatever
+// idx is, one ds_read2_b64, no wrap at the period's end.  (A single copy
+// needed five 32-bit reads and four funnel shifts per half vector, and an
+// element loop where a vector wraps; V copies, for 16-byte aligned reads,
+// measured no faster and take twice the LDS.)  Consecutive lanes read
+// consecutive 16-byte spans of one copy.  Copy s sits at odd_slot(s) *
+// odd_len: copies 1 .. odd_copies - 1 first, copy 0 last, with kOddGuard
+// more positions, from which the other copies are built.
+__host__ __device__ constexpr uint32_t odd_copies(int es) { return es >= 8 ? 1u : 8u / es; }
 constexpr uint32_t kOddGuard = 16;
 // Positions per copy: at least period + V - 1, a multiple of V (so every
 // copy starts 16-byte aligned).
@@ -60,8 +62,8 @@ __host__ __device__ constexpr uint32_t odd_slot(uint32_t s, int es) {
 __host__ __device__ constexpr uint32_t odd_stage_bytes(uint32_t period, int es) {
   return period == 0 ? 0 : (odd_copies(es) * odd_len(period, es) + kOddGuard) * es;
 }
-// LDS budget per staged operand: the shifted copies of periods up to 4095
-// elements (65696 bytes for half), the plain copy of kGatherK periods up to
+// LDS budget per staged operand: the shifted copies of periods up to 8191
+// elements (65632 bytes for half), the plain copy of kGatherK periods up to
 // 20496 bytes.
 constexpr uint32_t kOddStageBytes = 65696;
 constexpr uint32_t kGatherStageBytes = 20496;
@@ -129,11 +131,13 @@ __device__ inline void fetch(const Operand& o, const S* p, uint32_t i0, S (&out)
     for (int j = 0; j < V; ++j) out[j] = s;
   } else if constexpr (K == kRowOddK) {
     // p is the shifted copies (odd_len).
-    static_assert(V * sizeof(S) == 16 && V == odd_copies(sizeof(S)), "one 16-byte read");
+    constexpr uint32_t kC = odd_copies(sizeof(S));
+    static_assert(V * sizeof(S) == 16 && V % kC == 0, "one 16-byte read");
     const uint32_t idx = i0 - o.div_period.div(i0) * o.period;
-    const uint32_t sh = idx & (V - 1);
-    const uint4 w = *static_cast<const uint4*>(
-        __builtin_assume_aligned(p + odd_slot(sh, sizeof(S)) * o.olen + (idx - sh), 16));
+    const uint32_t sh = idx & (kC - 1);
+    const uint2* q = static_cast<const uint2*>(
+        __builtin_assume_aligned(p + odd_slot(sh, sizeof(S)) * o.olen + (idx - sh), 8));
+    const uint4 w = make_uint4(q[0].x, q[0].y, q[1].x, q[1].y);
     __builtin_memcpy(out, &w, 16);
   } else {
     const uint32_t q = o.div_inner.div(i0);
@@ -178,16 +182,23 @@ __device__ inline uint4 lds_window(const S* p, uint32_t e) {
 }
 
 // Per thread, the positions of copy 0 and the vectors of each other copy
-// staged (odd_len is at most kOddStageBytes / 16 for every element size).
-constexpr uint32_t kOddStageLoads = (kOddStageBytes / 16 + kOddGuard + kThreads - 1) / kThreads;
+// staged (odd_len is at most kOddStageBytes / (odd_copies * es)).
+template <typename S>
+constexpr uint32_t odd_max_len() {
+  return kOddStageBytes / (odd_copies(sizeof(S)) * sizeof(S));
+}
+template <typename S>
+constexpr uint32_t odd_stage_loads() {
+  return (odd_max_len<S>() + kOddGuard + kThreads - 1) / kThreads;
+}
 template <typename S>
 constexpr uint32_t odd_stage_vecs() {
-  return (kOddStageBytes / 16 / (16 / sizeof(S)) + kThreads - 1) / kThreads;
+  return (odd_max_len<S>() / (16 / sizeof(S)) + kThreads - 1) / kThreads;
 }
 
 // A workgroup's LDS copy of a staged operand (src: its values in global
 // memory).  kRowOddK: copy 0 (odd_len + kOddGuard positions) element by
-// element from global memory, then copies 1 .. V - 1 a 16-byte vector at a
+// element from global memory, then the other copies a 16-byte vector at a
 // time from copy 0 (lds_window), every load of a thread issued before the
 // first is used.  Indices past the end are clamped, not branched around
 // (the clamped store writes the value its position holds anyway): a load
@@ -197,19 +208,21 @@ constexpr uint32_t odd_stage_vecs() {
 template <int K, typename S>
 __device__ inline void stage(const Operand& o, const S* src, S* dst) {
   if constexpr (K == kRowOddK) {
-    constexpr uint32_t V = odd_copies(sizeof(S));
+    constexpr uint32_t V = 16 / sizeof(S);
+    constexpr uint32_t kC = odd_copies(sizeof(S));
+    constexpr uint32_t kLoads = odd_stage_loads<S>();
     const uint32_t len = o.olen;
-    S* const c0 = dst + (V - 1) * len;
+    S* const c0 = dst + (kC - 1) * len;
     const uint32_t ext = len + kOddGuard;
-    S v0[kOddStageLoads];
+    S v0[kLoads];
 #pragma unroll
-    for (uint32_t r = 0; r < kOddStageLoads; ++r) {
+    for (uint32_t r = 0; r < kLoads; ++r) {
       uint32_t k = threadIdx.x + r * kThreads;
       k = k < ext ? k : ext - 1;
       v0[r] = src[k - o.div_period.div(k) * o.period];
     }
 #pragma unroll
-    for (uint32_t r = 0; r < kOddStageLoads; ++r) {
+    for (uint32_t r = 0; r < kLoads; ++r) {
       const uint32_t k = threadIdx.x + r * kThreads;
       c0[k < ext ? k : ext - 1] = v0[r];
     }
@@ -218,7 +231,7 @@ __device__ inline void stage(const Operand& o, const S* src, S* dst) {
     // copy 0 (lds_window reads up to 9 past them: within the guard).
     const uint32_t nvec = len / V;
 #pragma unroll
-    for (uint32_t sh = 1; sh < V; ++sh) {
+    for (uint32_t sh = 1; sh < kC; ++sh) {
       uint4 w[odd_stage_vecs<S>()];
       uint32_t kv[odd_stage_vecs<S>()];
 #pragma unroll
