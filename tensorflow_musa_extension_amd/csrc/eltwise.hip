@@ -36,36 +36,35 @@ enum Kind : int {
   kFullK = 0, kScalarK = 1, kRowK = 2, kChanK = 3, kRowOddK = 4, kGatherK = 5, kGatherGlobalK = 6
 };
 constexpr bool staged_kind(int k) { return k == kRowOddK || k == kGatherK; }
+// Vectors of `a` per thread a staging kernel loads before its staging
+// completes; staged kinds are launched only where every thread has them.
+constexpr int kStagedPre = 8;
 
 // A staged odd-period row operand is held as odd_copies(es) = 8 / es copies
 // (one for 8-byte elements) of odd_len(period, es) positions each, copy s
-// holding element (k + s) mod period at position k.  The vector of
-// V = 16 / es elements that starts at element idx is then the 16 bytes at
-// position idx - s of copy s = idx mod odd_copies: 8-byte aligned whatever
-// idx is, one ds_read2_b64, no wrap at the period's end.  (A single copy
-// needed five 32-bit reads and four funnel shifts per half vector, and an
-// element loop where a vector wraps; V copies, for 16-byte aligned reads,
-// measured no faster and take twice the LDS.)  Consecutive lanes read
-// consecutive 16-byte spans of one copy.  Copy s sits at odd_slot(s) *
-// odd_len: copies 1 .. odd_copies - 1 first, copy 0 last, with kOddGuard
-// more positions, from which the other copies are built.
+// at s * odd_len holding element (k + s) mod period at position k.  The
+// vector of V = 16 / es elements that starts at element idx is then the 16
+// bytes at position idx - s of copy s = idx mod odd_copies: 8-byte aligned
+// whatever idx is, one ds_read2_b64, no wrap at the period's end.  (A
+// single copy needed five 32-bit reads and four funnel shifts per half
+// vector, and an element loop where a vector wraps; V copies, for 16-byte
+// aligned reads, measured no faster and take twice the LDS.)  Consecutive
+// lanes read consecutive 16-byte spans of one copy.
 __host__ __device__ constexpr uint32_t odd_copies(int es) { return es >= 8 ? 1u : 8u / es; }
-constexpr uint32_t kOddGuard = 16;
 // Positions per copy: at least period + V - 1, a multiple of V (so every
 // copy starts 16-byte aligned).
 __host__ __device__ constexpr uint32_t odd_len(uint32_t period, int es) {
   return (period + 2 * (16 / es) - 2) / (16 / es) * (16 / es);
 }
-__host__ __device__ constexpr uint32_t odd_slot(uint32_t s, int es) {
-  return (s - 1) & (odd_copies(es) - 1);
-}
+// The copies and one 16-byte slot after them that takes the staging's
+// stores of positions no copy has (stored there instead of branched around).
 __host__ __device__ constexpr uint32_t odd_stage_bytes(uint32_t period, int es) {
-  return period == 0 ? 0 : (odd_copies(es) * odd_len(period, es) + kOddGuard) * es;
+  return period == 0 ? 0 : odd_copies(es) * odd_len(period, es) * es + 16;
 }
-// LDS budget per staged operand: the shifted copies of periods up to 8191
-// elements (65632 bytes for half), the plain copy of kGatherK periods up to
-// 20496 bytes.
-constexpr uint32_t kOddStageBytes = 65696;
+// LDS budget per staged operand: the shifted copies of periods up to 4095
+// elements (32848 bytes for half; a thread then stages at most 17 elements),
+// the plain copy of kGatherK periods up to 20496 bytes.
+constexpr uint32_t kOddStageBytes = 32848;
 constexpr uint32_t kGatherStageBytes = 20496;
 __host__ __device__ constexpr uint32_t stage_bytes(int kind, uint32_t period, int es) {
   return kind == kRowOddK ? odd_stage_bytes(period, es) : (kind == kGatherK ? period * es : 0);
@@ -136,7 +135,7 @@ __device__ inline void fetch(const Operand& o, const S* p, uint32_t i0, S (&out)
     const uint32_t idx = i0 - o.div_period.div(i0) * o.period;
     const uint32_t sh = idx & (kC - 1);
     const uint2* q = static_cast<const uint2*>(
-        __builtin_assume_aligned(p + odd_slot(sh, sizeof(S)) * o.olen + (idx - sh), 8));
+        __builtin_assume_aligned(p + sh * o.olen + (idx - sh), 8));
     const uint4 w = make_uint4(q[0].x, q[0].y, q[1].x, q[1].y);
     __builtin_memcpy(out, &w, 16);
   } else {
@@ -153,103 +152,65 @@ __device__ inline void fetch(const Operand& o, const S* p, uint32_t i0, S (&out)
   }
 }
 
-// The 16 bytes of V elements p[e .. e + V - 1] of an LDS array at any
-// element e: halves as the five 32-bit words that cover them, realigned by
-// one funnel shift per word (0 or 16 bits by e's parity; reads elements up
-// to e + 9), wider elements directly.
-template <typename S>
-__device__ inline uint4 lds_window(const S* p, uint32_t e) {
-  constexpr int V = 16 / sizeof(S);
-  uint4 r;
-  if constexpr (sizeof(S) == 2) {
-    const uint32_t* pw = reinterpret_cast<const uint32_t*>(p);
-    const uint32_t d0 = e >> 1;
-    uint32_t w[5];
-#pragma unroll
-    for (int k = 0; k < 5; ++k) w[k] = pw[d0 + k];
-    const uint32_t sh = (e & 1u) << 4;
-    r = make_uint4(__builtin_amdgcn_alignbit(w[1], w[0], sh),
-                   __builtin_amdgcn_alignbit(w[2], w[1], sh),
-                   __builtin_amdgcn_alignbit(w[3], w[2], sh),
-                   __builtin_amdgcn_alignbit(w[4], w[3], sh));
-  } else {
-    S v[V];
-#pragma unroll
-    for (int j = 0; j < V; ++j) v[j] = p[e + j];
-    __builtin_memcpy(&r, v, 16);
-  }
-  return r;
-}
-
-// Per thread, the positions of copy 0 and the vectors of each other copy
-// staged (odd_len is at most kOddStageBytes / (odd_copies * es)).
-template <typename S>
-constexpr uint32_t odd_max_len() {
-  return kOddStageBytes / (odd_copies(sizeof(S)) * sizeof(S));
-}
+// Elements of the extended period a thread stages (odd_len is at most
+// kOddStageBytes / (odd_copies * es); copy s needs odd_len + s positions).
 template <typename S>
 constexpr uint32_t odd_stage_loads() {
-  return (odd_max_len<S>() + kOddGuard + kThreads - 1) / kThreads;
-}
-template <typename S>
-constexpr uint32_t odd_stage_vecs() {
-  return (odd_max_len<S>() / (16 / sizeof(S)) + kThreads - 1) / kThreads;
+  constexpr uint32_t kC = odd_copies(sizeof(S));
+  return ((kOddStageBytes - 16) / (kC * sizeof(S)) + kC - 1 + kThreads - 1) / kThreads;
 }
 
 // A workgroup's LDS copy of a staged operand (src: its values in global
-// memory).  kRowOddK: copy 0 (odd_len + kOddGuard positions) element by
-// element from global memory, then the other copies a 16-byte vector at a
-// time from copy 0 (lds_window), every load of a thread issued before the
-// first is used.  Indices past the end are clamped, not branched around
-// (the clamped store writes the value its position holds anyway): a load
-// whose only use sat in a branch left the compiler's wait analysis treating
-// its register as pending in the streaming loop, which then waited for each
-// load before issuing the next.  kGatherK: the plain copy.
+// memory), in two steps so that the kernel can issue its first loads of `a`
+// between them: issue() starts the global loads, commit() writes LDS (the
+// kernel's __syncthreads follows).  kGatherK: the plain copy, in commit().
 template <int K, typename S>
-__device__ inline void stage(const Operand& o, const S* src, S* dst) {
-  if constexpr (K == kRowOddK) {
-    constexpr uint32_t V = 16 / sizeof(S);
-    constexpr uint32_t kC = odd_copies(sizeof(S));
-    constexpr uint32_t kLoads = odd_stage_loads<S>();
-    const uint32_t len = o.olen;
-    S* const c0 = dst + (kC - 1) * len;
-    const uint32_t ext = len + kOddGuard;
-    S v0[kLoads];
+struct Stage {
+  __device__ void issue(const Operand&, const S*) {}
+  __device__ void commit(const Operand& o, const S* src, S* dst) {
+#pragma unroll 4
+    for (uint32_t k = threadIdx.x; k < o.period; k += kThreads) dst[k] = src[k];
+  }
+};
+
+// kRowOddK: element t of the extended period (element t mod period, for
+// t < odd_len + copies - 1) is loaded once, by thread t mod kThreads, all of
+// a thread's loads issued before the first is used, and stored straight
+// into every copy s at position t - s (a third of the time of loading copy
+// 0 and building the others from it with 16-byte LDS windows).  No load
+// or store sits in a branch: load indices past the end are clamped, and a
+// position no copy has is stored to the spare slot after the copies.  (A load whose use
+// sat in a branch left the compiler's wait analysis treating its register
+// as pending in the streaming loop, which then waited for each load before
+// issuing the next; and loads in branches make it wait for every
+// outstanding load, the kernel's prefetch of `a` included.)
+template <typename S>
+struct Stage<kRowOddK, S> {
+  static constexpr uint32_t kLoads = odd_stage_loads<S>();
+  S v0[kLoads];
+  __device__ void issue(const Operand& o, const S* src) {
+    const uint32_t ext = o.olen + odd_copies(sizeof(S)) - 1;
 #pragma unroll
     for (uint32_t r = 0; r < kLoads; ++r) {
       uint32_t k = threadIdx.x + r * kThreads;
       k = k < ext ? k : ext - 1;
       v0[r] = src[k - o.div_period.div(k) * o.period];
     }
+  }
+  __device__ void commit(const Operand& o, const S*, S* dst) {
+    constexpr uint32_t kC = odd_copies(sizeof(S));
+    const uint32_t len = o.olen;
 #pragma unroll
     for (uint32_t r = 0; r < kLoads; ++r) {
-      const uint32_t k = threadIdx.x + r * kThreads;
-      c0[k < ext ? k : ext - 1] = v0[r];
-    }
-    __syncthreads();
-    // Copy sh, vector kv: elements kv * V + sh .. kv * V + sh + V - 1 of
-    // copy 0 (lds_window reads up to 9 past them: within the guard).
-    const uint32_t nvec = len / V;
+      const uint32_t t = threadIdx.x + r * kThreads;
 #pragma unroll
-    for (uint32_t sh = 1; sh < kC; ++sh) {
-      uint4 w[odd_stage_vecs<S>()];
-      uint32_t kv[odd_stage_vecs<S>()];
-#pragma unroll
-      for (uint32_t r = 0; r < odd_stage_vecs<S>(); ++r) {
-        kv[r] = threadIdx.x + r * kThreads;
-        kv[r] = kv[r] < nvec ? kv[r] : nvec - 1;
-        w[r] = lds_window(c0, kv[r] * V + sh);
+      for (uint32_t sh = 0; sh < kC; ++sh) {
+        const bool in = t >= sh && t - sh < len;
+        dst[in ? sh * len + (t - sh) : kC * len] = v0[r];
       }
-#pragma unroll
-      for (uint32_t r = 0; r < odd_stage_vecs<S>(); ++r)
-        *static_cast<uint4*>(__builtin_assume_aligned(dst + (sh - 1) * len + kv[r] * V, 16)) =
-            w[r];
     }
-  } else {
-#pragma unroll 4
-    for (uint32_t k = threadIdx.x; k < o.period; k += kThreads) dst[k] = src[k];
   }
-}
+};
 
 template <class Tr, EwOp OP>
 __device__ inline typename Tr::S ew_apply(typename Tr::S a, typename Tr::S b,
@@ -294,24 +255,65 @@ __global__ __launch_bounds__(kThreads) void ew_flat_kernel(
   extern __shared__ __align__(16) unsigned char ew_lds[];
   const S* pb = static_cast<const S*>(b.p);
   const S* pc = static_cast<const S*>(c.p);
-  if constexpr (kArity >= 2 && staged_kind(KB)) {
-    S* l = reinterpret_cast<S*>(ew_lds);
-    stage<KB>(b, pb, l);
-    pb = l;
-  }
-  if constexpr (kArity >= 3 && staged_kind(KC)) {
-    const uint32_t off =
-        kArity >= 2 && staged_kind(KB) ? round16(stage_bytes(KB, b.period, sizeof(S))) : 0;
-    S* l = reinterpret_cast<S*>(ew_lds + off);
-    stage<KC>(c, pc, l);
-    pc = l;
-  }
-  if constexpr ((kArity >= 2 && staged_kind(KB)) || (kArity >= 3 && staged_kind(KC)))
-    __syncthreads();
   const uint32_t nv = n / V;
   const uint32_t stride = gridDim.x * kThreads;
   const uint32_t tid = blockIdx.x * kThreads + threadIdx.x;
+  // A kernel that stages an operand issues the staging loads, then its
+  // first kStagedPre vectors of `a`, then completes the staging: those
+  // vectors stream in meanwhile instead of the memory system idling while
+  // every workgroup stages (the staging of a [4095] half operand takes
+  // ~2.5 us).  Loads complete in order, so the staging waits only for its
+  // own - which needs straight-line code: no load of the prologue sits in a
+  // branch.  The host launches staged kinds only with
+  // nv >= kStagedPre * stride (stage_grid), so every prefetched vector
+  // exists; the indices are clamped all the same.
+  constexpr bool kSB = kArity >= 2 && staged_kind(KB);
+  constexpr bool kSC = kArity >= 3 && staged_kind(KC);
+  constexpr int kPre = (kSB || kSC) ? kStagedPre : 1;
+  [[maybe_unused]] Stage<KB, S> stb;
+  [[maybe_unused]] Stage<KC, S> stc;
+  if constexpr (kSB) stb.issue(b, pb);
+  if constexpr (kSC) stc.issue(c, pc);
+  [[maybe_unused]] S ap[kPre][V];
+  if constexpr (kSB || kSC) {
+#pragma unroll
+    for (int q = 0; q < kPre; ++q) {
+      const uint32_t iq = tid + q * stride < nv ? tid + q * stride : nv - 1;
+      vload_sel<(NT >= 1), S, V>(a + iq * V, ap[q]);
+    }
+    // Keep the scheduler from sinking these loads below the staging's first
+    // waits (it interleaved them with the LDS stores, after the first
+    // staging load had returned).
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (kSB) {
+    S* l = reinterpret_cast<S*>(ew_lds);
+    stb.commit(b, pb, l);
+    pb = l;
+  }
+  if constexpr (kSC) {
+    const uint32_t off = kSB ? round16(stage_bytes(KB, b.period, sizeof(S))) : 0;
+    S* l = reinterpret_cast<S*>(ew_lds + off);
+    stc.commit(c, pc, l);
+    pc = l;
+  }
   uint32_t i = tid;
+  if constexpr (kSB || kSC) {
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kPre; ++q) {
+      const uint32_t iq = tid + q * stride < nv ? tid + q * stride : nv - 1;
+      S bv[V], cv[V], ov[V];
+      if constexpr (kArity >= 2) fetch<KB, S, V, NT>(b, pb, iq * V, bv);
+      if constexpr (kArity >= 3) fetch<KC, S, V, NT>(c, pc, iq * V, cv);
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        ov[j] = ew_apply<Tr, OP>(ap[q][j], kArity >= 2 ? bv[j] : S(0),
+                                 kArity >= 3 ? cv[j] : S(0));
+      if (tid + q * stride < nv) vstore_sel<(NT == 2), S, V>(out + iq * V, ov);
+    }
+    i += kPre * stride;
+  }
   for (; i + (UNROLL - 1) * stride < nv; i += UNROLL * stride) {
     S av[UNROLL][V], bv[UNROLL][V], cv[UNROLL][V];
 #pragma unroll
@@ -471,6 +473,14 @@ constexpr bool streams(int k) {
   return k == kFullK || k == kScalarK || k == kRowK || k == kChanK;
 }
 
+// Grid of a staging kernel: at most `blocks`, and few enough that every
+// thread has kStagedPre vectors (the kernel's prologue loads them
+// unconditionally).  launch_ew stages only where nv >= kStagedPre * kThreads.
+int64_t stage_grid(int64_t nv, int64_t blocks) {
+  const int64_t most = nv / (static_cast<int64_t>(kThreads) * kStagedPre);
+  return blocks < most ? blocks : (most > 0 ? most : 1);
+}
+
 // Vector-path launch with the operand kinds as compile-time parameters.
 template <class Tr, EwOp OP, int KB, int KC>
 void launch_vec(const Operand& ob, const Operand& oc, const typename Tr::S* a,
@@ -500,8 +510,7 @@ void launch_vec(const Operand& ob, const Operand& oc, const typename Tr::S* a,
     }
   }
   int64_t blocks = grid_for(n / V, U);
-  const int64_t cap = static_cast<int64_t>(DeviceCUs()) * 4;
-  if ((sb || sc) && blocks > cap) blocks = cap;
+  if (sb || sc) blocks = stage_grid(n / V, blocks);
   if constexpr (streams(KB) && streams(KC)) {
     if (nt == 2) {
       TFMA_LAUNCH(op_kernel_name(OP), (ew_flat_kernel<Tr, OP, V, U, KB, KC, 2>), dim3(blocks),
@@ -567,6 +576,12 @@ hipError_t launch_ew(int64_t n, const BcastOperand& a, const BcastOperand& b,
   Operand oc = kArity >= 3 ? make_operand(c, sizeof(S), V, &vec_ok)
                            : make_operand(a, sizeof(S), V, &vec_ok);
   const uint32_t n32 = static_cast<uint32_t>(n);
+  // Too few vectors for a staging kernel's prologue: walk such operands in
+  // global memory instead.
+  if (n / V < static_cast<int64_t>(kThreads) * kStagedPre) {
+    if (staged_kind(ob.kind)) ob.kind = kGatherGlobalK;
+    if (staged_kind(oc.kind)) oc.kind = kGatherGlobalK;
+  }
   if (vec_ok) {
     pick_kb<Tr, OP>(ob, oc, static_cast<const S*>(a.data), static_cast<S*>(out), n32,
                     stream_mode(n * static_cast<int64_t>(sizeof(S))), stream);

@@ -51,6 +51,8 @@ BCAST = [
     ((5, 1021), (1021,)),           # odd period, wrap in a few vectors
     ((3, 8191), (8191,)),           # longest odd half period the padded LDS copy holds
     ((3, 9001), (9001,)),           # odd period too long for the LDS copy
+    ((2048, 33), (33,)),            # short odd period, staged shifted copies
+    ((8192, 3), (3,)),              # period shorter than a vector, staged
     ((9000, 3), (9000, 1)),         # inner 3, long period: global walk
     ((4, 1, 5), (1, 3, 1)),         # neither operand full: strided path
     ((2, 3, 4, 8), (3, 1, 8)),      # two broadcast runs: strided path
@@ -78,6 +80,7 @@ MULADD = [
     ((8191, 4095), (4095,), (4095,)),
     ((5, 7), (5, 7), ()),
     ((5, 1, 7), (1, 3, 1), (3, 7)),               # strided path
+    ((1024, 1021), (1021,), (1021,)),             # two staged odd-period operands
 ]
 
 
