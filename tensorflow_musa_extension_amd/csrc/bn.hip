@@ -629,14 +629,18 @@ __global__ __launch_bounds__(kThreads) void bn_nhwc_apply_kernel(
   const S* __restrict__ px = x + c0;
   const S* __restrict__ pd = kGrad ? dy + c0 : nullptr;
   S* __restrict__ po = out + c0;
-  // Walk this thread's rows last-to-first.
+  // Walk this thread's rows last-to-first.  The inference forward reads x
+  // once: non-temporal loads, which leave the Infinity Cache to the output
+  // (measured, [256,56,56,256] f16 kernel time: 69.8 -> 79.3 % of 8 TB/s;
+  // non-temporal stores as well 62.8 %, stores alone 61.9 %).  The split
+  // training path re-reads lines its reduce kernel just read: plain loads.
   int64_t k = nr - 1;
   for (; k >= kUnroll - 1; k -= kUnroll) {
     S xv[kUnroll][VEC], dv[kUnroll][VEC];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t r = r0 + ty + (k - u) * ry;
-      vload<S, VEC>(px + r * c, xv[u]);
+      vload_sel<kInfer, S, VEC>(px + r * c, xv[u]);
       if constexpr (kGrad) vload<S, VEC>(pd + r * c, dv[u]);
     }
 #pragma unroll
@@ -652,7 +656,7 @@ __global__ __launch_bounds__(kThreads) void bn_nhwc_apply_kernel(
   for (; k >= 0; --k) {
     const int64_t r = r0 + ty + k * ry;
     S xv[VEC], dv[VEC], ov[VEC];
-    vload<S, VEC>(px + r * c, xv);
+    vload_sel<kInfer, S, VEC>(px + r * c, xv);
     if constexpr (kGrad) vload<S, VEC>(pd + r * c, dv);
 #pragma unroll
     for (int j = 0; j < VEC; ++j)
