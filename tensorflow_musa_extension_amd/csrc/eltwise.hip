@@ -459,14 +459,23 @@ Operand make_operand(const BcastOperand& o, int elem_bytes, int V,
   return r;
 }
 
-// Cache mode by output size (measured on MI355X, f32 BiasAdd+Relu with the
-// Infinity Cache flushed between reps): plain accesses are 5-10 % faster up
-// to 2^26 elements; at 2^27 non-temporal loads of the full operands are
-// 13 % faster; from 2^28 on non-temporal loads of every operand and
-// non-temporal stores 5-7 % faster than plain.  Only the kinds
-// that stream (full, scalar, row, channel) have the non-temporal variants.
-int stream_mode(int64_t out_bytes) {
-  return out_bytes >= (int64_t(1) << 30) ? 2 : (out_bytes >= (int64_t(1) << 29) ? 1 : 0);
+// Cache mode by size (measured on MI355X with the Infinity Cache flushed
+// between reps).  By output size, f32 BiasAdd+Relu: plain accesses are
+// 5-10 % faster up to 2^26 elements; at 2^27 non-temporal loads of the full
+// operands are 13 % faster; from 2^28 on non-temporal loads of every
+// operand and non-temporal stores 5-7 % faster than plain.  By the bytes of
+// full-size inputs: from 192 MiB non-temporal loads (cfg4 Mul+Add with full
+// a and b, kernel time: f32 74.8 -> 81.3 %, f16 74.2 -> 78.3 % of 8 TB/s;
+// ReluGrad f32 79.7 -> 80.9 %; at 128 MiB, f16 ReluGrad, plain loads are
+// 2 points faster).  Only the kinds that stream (full, scalar, row,
+// channel) have the non-temporal variants.  TFMA_EW_NT (read per call, for
+// measurements): 0, 1 or 2 forces the mode.
+int stream_mode(int64_t out_bytes, int64_t full_in_bytes) {
+  const char* e = getenv("TFMA_EW_NT");
+  if (e && e[0] >= '0' && e[0] <= '2' && e[1] == 0) return e[0] - '0';
+  if (out_bytes >= (int64_t(1) << 30)) return 2;
+  if (out_bytes >= (int64_t(1) << 29) || full_in_bytes >= (int64_t(192) << 20)) return 1;
+  return 0;
 }
 
 constexpr bool streams(int k) {
@@ -576,6 +585,9 @@ hipError_t launch_ew(int64_t n, const BcastOperand& a, const BcastOperand& b,
   Operand oc = kArity >= 3 ? make_operand(c, sizeof(S), V, &vec_ok)
                            : make_operand(a, sizeof(S), V, &vec_ok);
   const uint32_t n32 = static_cast<uint32_t>(n);
+  int64_t full_in = n * static_cast<int64_t>(sizeof(S));  // a
+  if (kArity >= 2 && b.mode == BcastMode::kFull) full_in += n * static_cast<int64_t>(sizeof(S));
+  if (kArity >= 3 && c.mode == BcastMode::kFull) full_in += n * static_cast<int64_t>(sizeof(S));
   // Too few vectors for a staging kernel's prologue: walk such operands in
   // global memory instead.
   if (n / V < static_cast<int64_t>(kThreads) * kStagedPre) {
@@ -584,7 +596,7 @@ hipError_t launch_ew(int64_t n, const BcastOperand& a, const BcastOperand& b,
   }
   if (vec_ok) {
     pick_kb<Tr, OP>(ob, oc, static_cast<const S*>(a.data), static_cast<S*>(out), n32,
-                    stream_mode(n * static_cast<int64_t>(sizeof(S))), stream);
+                    stream_mode(n * static_cast<int64_t>(sizeof(S)), full_in), stream);
   } else {
     // Re-classify for V = 1 (rows and channels become per-element gathers).
     bool dummy = true;
