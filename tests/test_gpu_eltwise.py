@@ -49,8 +49,8 @@ BCAST = [
     ((37, 3), (3,)),                # period shorter than a vector: wraps inside it
     ((9, 7, 11), (7, 1)),           # inner 11, period 7: incremental walk
     ((5, 1021), (1021,)),           # odd period, wrap in a few vectors
-    ((3, 8191), (8191,)),           # longest odd half period the padded LDS copy holds
-    ((3, 9001), (9001,)),           # odd period too long for the LDS copy
+    ((3, 8191), (8191,)),           # odd period longer than the staged copies hold: global walk
+    ((3, 9001), (9001,)),           # longer odd period, few vectors: global walk
     ((2048, 33), (33,)),            # short odd period, staged shifted copies
     ((8192, 3), (3,)),              # period shorter than a vector, staged
     ((9000, 3), (9000, 1)),         # inner 3, long period: global walk
