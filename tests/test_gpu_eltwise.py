@@ -54,6 +54,7 @@ BCAST = [
     ((2048, 33), (33,)),            # short odd period, staged shifted copies
     ((8192, 3), (3,)),              # period shorter than a vector, staged
     ((9000, 3), (9000, 1)),         # inner 3, long period: global walk
+    ((64, 37, 33), (37, 1)),        # inner 33, period 37: staged walk
     ((4, 1, 5), (1, 3, 1)),         # neither operand full: strided path
     ((2, 3, 4, 8), (3, 1, 8)),      # two broadcast runs: strided path
     ((0, 4), (4,)),                 # empty
