@@ -225,9 +225,9 @@ def component_groups(torch, ops, dev):
 
     # BatchNorm off the NHWC fused path: NCHW training with at least one
     # channel per CU (one workgroup per channel: 2sE / 3sE algorithmic bytes,
-    # plus re-reads of what a workgroup cannot hold on chip) and NHWC
-    # inference (one apply kernel, coefficients from the running statistics:
-    # 2sE).
+    # plus re-reads of what a workgroup cannot hold on chip) and inference,
+    # NHWC and NCHW (one apply kernel, coefficients from the running
+    # statistics: 2sE).
     xn = torch.randn(256, 512, 28, 28, generator=gen, device=dev).half()
     dyn = torch.randn(256, 512, 28, 28, generator=gen, device=dev).half()
     scn = torch.rand(512, generator=gen, device=dev) + 0.5
@@ -247,13 +247,19 @@ def component_groups(torch, ops, dev):
     wsi = torch.empty(ops.fused_batch_norm_workspace_bytes(xi), dtype=torch.uint8, device=dev)
     bi = ops.bind(ops.FusedBatchNormV3, xi, scn[:256].contiguous(), ofn[:256].contiguous(), rm,
                   rv, epsilon=EPS, data_format="NHWC", is_training=False, workspace=wsi)
+    rmn = 0.1 * torch.randn(512, generator=gen, device=dev)
+    rvn = torch.rand(512, generator=gen, device=dev) + 0.5
+    bin_ = ops.bind(ops.FusedBatchNormV3, xn, scn, ofn, rmn, rvn, epsilon=EPS, data_format="NCHW",
+                    is_training=False, workspace=wsn)
     yield [Component("bn_fwd_f16_nchw_256x512x28x28", [fn_], 4 * En, En, "tfma_bn_fwd",
                      note="one workgroup per channel"),
            Component("bn_grad_f16_nchw_256x512x28x28", [gn], 6 * En, En, "tfma_bn_grad",
                      note="one workgroup per channel"),
            Component("bn_fwd_inference_f16_256x56x56x256", [bi], 4 * xi.numel(), xi.numel(),
-                     "tfma_bn_infer", note="coefficients from running statistics, one kernel")]
-    del xn, dyn, fn_, gn, wsn, xi, wsi, bi
+                     "tfma_bn_infer", note="coefficients from running statistics, one kernel"),
+           Component("bn_fwd_inference_f16_nchw_256x512x28x28", [bin_], 4 * En, En,
+                     "tfma_bn_infer", note="NCHW, coefficients from running statistics, one kernel")]
+    del xn, dyn, fn_, gn, wsn, xi, wsi, bi, bin_
 
     n = 25_600_000
     var = 0.02 * torch.randn(n, generator=gen, device=dev)
