@@ -52,6 +52,8 @@ BCAST = [
     ((3, 8191), (8191,)),           # odd period longer than the staged copies hold: global walk
     ((3, 9001), (9001,)),           # longer odd period, few vectors: global walk
     ((2048, 33), (33,)),            # short odd period, staged shifted copies
+    ((221, 37), (37,)),             # f32: 2044 vectors, just below the staging minimum
+    ((222, 37), (37,)),             # f32: 2053 vectors, staged by a single workgroup
     ((8192, 3), (3,)),              # period shorter than a vector, staged
     ((9000, 3), (9000, 1)),         # inner 3, long period: global walk
     ((64, 37, 33), (37, 1)),        # inner 33, period 37: staged walk
