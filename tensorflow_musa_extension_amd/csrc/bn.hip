@@ -678,8 +678,24 @@ __global__ __launch_bounds__(kThreads) void bn_nchw_apply_kernel(
   if constexpr (kInfer) infer_stats(fa, lid, stride);
   int last = -1;
   float4 cf = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int64_t i = nvec - 1 - lid; i >= 0; i -= stride) {
-    const int ch = static_cast<int>((i / pv) % c);
+  // Vector i = q * pv + r of channel q mod c.  One division at the start,
+  // then each step back by `stride` vectors updates (r, ch) by subtraction
+  // with a borrow (a 64-bit division and modulo per vector made this kernel
+  // issue 58k VALU instructions per MB).
+  const int64_t i0 = nvec - 1 - lid;
+  const int64_t q0 = i0 >= 0 ? i0 / pv : 0;
+  int64_t r = i0 >= 0 ? i0 - q0 * pv : 0;
+  int64_t chv = q0 % c;
+  const int64_t dq = stride / pv;
+  const int64_t dr = stride - dq * pv;
+  const int64_t dch = dq % c;
+  for (int64_t i = i0; i >= 0; i -= stride) {
+    const int ch = static_cast<int>(chv);
+    r -= dr;
+    const int64_t borrow = r < 0 ? 1 : 0;
+    r += borrow * pv;
+    chv -= dch + borrow;  // dch + borrow <= c: at most one wrap
+    chv += chv < 0 ? c : 0;
     if (kInfer ? ch != last : true) {
       cf = kInfer ? infer_coef(fa, ch) : coef[ch];
       last = ch;
