@@ -28,11 +28,19 @@ components: cfg1 (FusedBatchNormV3 forward, f32 [32,56,56,64]), BN on the
         split path (NCHW training fwd and grad, NHWC inference), and the
         other kernels (Adam, mixed-precision Adam, grouped Adam at
         the ResNet-50 and 1.31e9-parameter configs, the elementwise chains,
-        ReluGrad, BiasAddGrad) at their config shapes, each rep timed with HIP
-        events after a 1 GiB read that evicts the Infinity Cache (GB/s, % of
-        peak, Gelem/s), then the same reps again with events attached to the
-        kernels' own dispatches (kernel_ms, kernel_GB/s, kernel_pct_peak: the
-        kernel's duration without the dispatch and event overhead);
+        ReluGrad, BiasAddGrad) at their config shapes, each of 20 reps timed
+        with HIP events after a 1 GiB read that evicts the Infinity Cache
+        (median ms with min / max; GB/s, % of peak, Gelem/s from the median),
+        then the same reps again with events attached to the kernels' own
+        dispatches (kernel_ms, kernel_GB/s, kernel_pct_peak: the kernel's
+        mean duration without the dispatch and event overhead).  The flushed
+        figure stops the clock with the op's output possibly still dirty in
+        the Infinity Cache; "sustained" (Adam, grouped Adam, the elementwise
+        chains, ReluGrad, BiasAddGrad) is the rate of back-to-back calls
+        cycling over rotating buffer sets of >= 1 GiB in total, so every call
+        also pays the write-back of the ones before it (median / min / max
+        of 20 timings of >= 4 calls each).  above_copy_ceiling flags a
+        flushed rate above the measured stream-copy ceiling.
         traffic_ratio = counter-measured HBM bytes per rep (committed
         profiles/pmc_traffic_components.txt) / algorithmic bytes.
 --profile-components: each component once, then 3 times after a cache
@@ -164,10 +172,12 @@ def bn_workload(torch, ops, dev):
 
 
 def time_calls(torch, calls, steps, warmup, flush=None):
-    """ms per pass over `calls`.  With `flush` (a large device buffer), each
-    pass is timed on its own after reading the buffer, so the 256 MB
-    Infinity Cache holds none of the op's data (the cache is flushed between
-    reps: cfg1 and the smaller f16 shapes would otherwise fit in it)."""
+    """ms per pass over `calls`.  Without `flush`: the mean over `steps`
+    back-to-back passes under one event pair.  With `flush` (a large device
+    buffer): a sorted list of `steps` per-pass times, each pass timed on its
+    own after reading the buffer, so the 256 MB Infinity Cache holds none of
+    the op's data (cfg1 and the smaller f16 shapes would otherwise fit in
+    it)."""
     for _ in range(warmup):
         for c in calls:
             c()
@@ -191,7 +201,48 @@ def time_calls(torch, calls, steps, warmup, flush=None):
         t1.record()
         pairs.append((t0, t1))
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in pairs) / steps
+    return sorted(a.elapsed_time(b) for a, b in pairs)
+
+
+def median(xs):
+    xs = sorted(xs)
+    k = len(xs)
+    return xs[k // 2] if k % 2 else 0.5 * (xs[k // 2 - 1] + xs[k // 2])
+
+
+SUSTAIN_BYTES = 1 << 30  # rotating buffer sets add up to at least this much
+
+
+def time_sustained(torch, c, reps=20):
+    """Sustained rate of a component: k back-to-back calls under one event
+    pair, cycling over n distinct buffer sets (its own calls and n - 1 more
+    from c.make()) with n * bytes >= 1 GiB, so by the time a set comes round
+    again more than the 256 MB Infinity Cache has streamed through, and each
+    call pays for the write-back of the dirty lines the calls before it left
+    (the flushed per-call figure leaves its own output's write-back to the
+    next flush).  `reps` such timings back to back; returns (sorted ms per
+    call, n, k)."""
+    n = max(1, min(16, -(-SUSTAIN_BYTES // c.nbytes)))
+    sets = [c.calls] + [c.make() for _ in range(n - 1)]
+    k = max(n, 4)
+    seq = [sets[i % n] for i in range(k)]
+    for calls in seq:  # one warm pass over every set
+        for call in calls:
+            call()
+    torch.cuda.synchronize()
+    pairs = []
+    for _ in range(reps):
+        t0, t1 = _events(torch)
+        t0.record()
+        for calls in seq:
+            for call in calls:
+                call()
+        t1.record()
+        pairs.append((t0, t1))
+    torch.cuda.synchronize()
+    ms = sorted(a.elapsed_time(b) / k for a, b in pairs)
+    del sets, seq
+    return ms, n, k
 
 
 class Component:
@@ -199,9 +250,12 @@ class Component:
     its algorithmic bytes and elements per rep, and the trace-name substring
     of the library kernels it launches."""
 
-    def __init__(self, name, calls, nbytes, elems, kernel, reps=20, note=None):
+    def __init__(self, name, calls, nbytes, elems, kernel, reps=20, note=None, make=None):
         self.name, self.calls, self.nbytes, self.elems = name, calls, nbytes, elems
         self.kernel, self.reps, self.note = kernel, reps, note
+        # make(): the same calls on a fresh set of buffers (for the sustained
+        # rate over rotating buffer sets); None: no sustained figure.
+        self.make = make
 
 
 def component_groups(torch, ops, dev):
@@ -262,30 +316,42 @@ def component_groups(torch, ops, dev):
     del xn, dyn, fn_, gn, wsn, xi, wsi, bi, bin_
 
     n = 25_600_000
-    var = 0.02 * torch.randn(n, generator=gen, device=dev)
-    m = torch.zeros(n, device=dev)
-    v = torch.zeros(n, device=dev)
-    g = 1e-3 * torch.randn(n, generator=gen, device=dev)
-    adam = ops.bind(ops.ResourceApplyAdam, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7, g)
-    # Mixed precision (fp32 state, bf16 grad): 24 B of state + 2 B of grad.
-    gb = g.to(torch.bfloat16)
-    mixed = ops.bind(ops.MusaResourceApplyAdamMixed, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999,
-                     1e-7, gb)
     shapes = resnet50_shapes()
-    tv = [0.02 * torch.randn(s, generator=gen, device=dev) for s in shapes]
-    tm = [torch.zeros(s, device=dev) for s in shapes]
-    tvv = [torch.zeros(s, device=dev) for s in shapes]
-    tg = [1e-3 * torch.randn(s, generator=gen, device=dev) for s in shapes]
-    total = sum(t.numel() for t in tv)
-    grouped = ops.bind(ops.MusaGroupedResourceApplyAdam, tv, tm, tvv, tg, 0.9, 0.999, 1e-3, 0.9,
-                       0.999, 1e-7)
-    yield [Component("adam_f32_25.6M", [adam], 28 * n, n, "tfma_adam_flat"),
-           Component("adam_mixed_bf16grad_25.6M", [mixed], 26 * n, n, "tfma_adam_flat"),
-           Component("grouped_adam_f32_resnet50_161", [grouped], 28 * total, total,
-                     "tfma_adam_grouped")]
-    del var, m, v, g, gb, tv, tm, tvv, tg, grouped, adam, mixed
 
-    # cfg5: 1.31B parameters in 145 tensors, 21 GB of state resident.
+    def adam_set():
+        var = 0.02 * torch.randn(n, generator=gen, device=dev)
+        m = torch.zeros(n, device=dev)
+        v = torch.zeros(n, device=dev)
+        g = 1e-3 * torch.randn(n, generator=gen, device=dev)
+        return [ops.bind(ops.ResourceApplyAdam, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7,
+                         g)]
+
+    def mixed_set():
+        # Mixed precision (fp32 state, bf16 grad): 24 B of state + 2 B of grad.
+        var = 0.02 * torch.randn(n, generator=gen, device=dev)
+        m = torch.zeros(n, device=dev)
+        v = torch.zeros(n, device=dev)
+        gb = (1e-3 * torch.randn(n, generator=gen, device=dev)).to(torch.bfloat16)
+        return [ops.bind(ops.MusaResourceApplyAdamMixed, var, m, v, 0.9, 0.999, 1e-3, 0.9, 0.999,
+                         1e-7, gb)]
+
+    def grouped_set():
+        tv = [0.02 * torch.randn(s, generator=gen, device=dev) for s in shapes]
+        tm = [torch.zeros(s, device=dev) for s in shapes]
+        tvv = [torch.zeros(s, device=dev) for s in shapes]
+        tg = [1e-3 * torch.randn(s, generator=gen, device=dev) for s in shapes]
+        return [ops.bind(ops.MusaGroupedResourceApplyAdam, tv, tm, tvv, tg, 0.9, 0.999, 1e-3,
+                         0.9, 0.999, 1e-7)]
+
+    total = sum(int(torch.Size(s).numel()) for s in shapes)
+    yield [Component("adam_f32_25.6M", adam_set(), 28 * n, n, "tfma_adam_flat", make=adam_set),
+           Component("adam_mixed_bf16grad_25.6M", mixed_set(), 26 * n, n, "tfma_adam_flat",
+                     make=mixed_set),
+           Component("grouped_adam_f32_resnet50_161", grouped_set(), 28 * total, total,
+                     "tfma_adam_grouped", make=grouped_set)]
+
+    # cfg5: 1.31B parameters in 145 tensors, 21 GB of state resident (one
+    # step streams 36.7 GB, so the sustained rate reuses the one set).
     shapes5 = cfg5_shapes()
     tv = [0.02 * torch.randn(s, generator=gen, device=dev) for s in shapes5]
     tm = [(1e-4 * torch.randn(s, generator=gen, device=dev)).abs_() for s in shapes5]
@@ -295,54 +361,60 @@ def component_groups(torch, ops, dev):
     grouped5 = ops.bind(ops.MusaGroupedResourceApplyAdam, tv, tm, tvv, tg, 0.9, 0.999, 1e-3,
                         0.9, 0.999, 1e-7)
     yield [Component("grouped_adam_f32_cfg5_145", [grouped5], 28 * total5, total5,
-                     "tfma_adam_grouped", reps=10)]
+                     "tfma_adam_grouped", make=lambda: [grouped5])]
     del tv, tm, tvv, tg, grouped5
     torch.cuda.empty_cache()
 
     for dt, name in ((torch.float32, "f32"), (torch.float16, "f16")):
         s = torch.tensor([], dtype=dt).element_size()
-        x = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
-        b = torch.randn(4096, generator=gen, device=dev).to(dt)
-        E = x.numel()
-        a_full = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
-        b_full = torch.randn(8192, 4096, generator=gen, device=dev).to(dt)
-        xo = torch.randn(8191, 4095, generator=gen, device=dev).to(dt)
-        bo = torch.randn(4095, generator=gen, device=dev).to(dt)
-        yield [
-            Component(f"bias_add_relu_{name}_8192x4096", [ops.bind(ops.MusaBiasAddRelu, x, b)],
-                      2 * s * E + s * 4096, E, "tfma_ew_add_relu"),
-            Component(f"add_v2_relu_{name}_8192x4096", [ops.bind(ops.MusaAddV2Relu, x, b)],
-                      2 * s * E + s * 4096, E, "tfma_ew_add_relu"),
-            Component(f"mul_add_full_{name}_8192x4096",
-                      [ops.bind(ops.MusaShiftedAffineMap, x, a_full, b_full)], 4 * s * E, E,
-                      "tfma_ew_mul_add"),
-            Component(f"mul_add_row_{name}_8192x4096",
-                      [ops.bind(ops.MusaShiftedAffineMap, x, b, b)], 2 * s * E + 2 * s * 4096,
-                      E, "tfma_ew_mul_add"),
-            Component(f"bias_add_relu_{name}_8191x4095",
-                      [ops.bind(ops.MusaBiasAddRelu, xo, bo)], 2 * s * xo.numel() + s * 4095,
-                      xo.numel(), "tfma_ew_add_relu"),
+
+        def rnd(*shape, dt=dt):
+            return torch.randn(*shape, generator=gen, device=dev).to(dt)
+
+        E = 8192 * 4096
+        Eo = 8191 * 4095
+        chains = [
+            (f"bias_add_relu_{name}_8192x4096", 2 * s * E + s * 4096, E, "tfma_ew_add_relu",
+             lambda rnd=rnd: [ops.bind(ops.MusaBiasAddRelu, rnd(8192, 4096), rnd(4096))]),
+            (f"add_v2_relu_{name}_8192x4096", 2 * s * E + s * 4096, E, "tfma_ew_add_relu",
+             lambda rnd=rnd: [ops.bind(ops.MusaAddV2Relu, rnd(8192, 4096), rnd(4096))]),
+            (f"mul_add_full_{name}_8192x4096", 4 * s * E, E, "tfma_ew_mul_add",
+             lambda rnd=rnd: [ops.bind(ops.MusaShiftedAffineMap, rnd(8192, 4096), rnd(8192, 4096),
+                               rnd(8192, 4096))]),
+            (f"mul_add_row_{name}_8192x4096", 2 * s * E + 2 * s * 4096, E, "tfma_ew_mul_add",
+             lambda rnd=rnd: [ops.bind(ops.MusaShiftedAffineMap, rnd(8192, 4096), rnd(4096),
+                               rnd(4096))]),
+            (f"bias_add_relu_{name}_8191x4095", 2 * s * Eo + s * 4095, Eo, "tfma_ew_add_relu",
+             lambda rnd=rnd: [ops.bind(ops.MusaBiasAddRelu, rnd(8191, 4095), rnd(4095))]),
             # The backward side of the chains: ReluGrad (2 reads, 1 write)
             # and BiasAddGrad (one read of the gradient).
-            Component(f"relu_grad_{name}_8192x4096", [ops.bind(ops.ReluGrad, a_full, x)],
-                      3 * s * E, E, "tfma_ew_relu_grad"),
-            Component(f"bias_add_grad_{name}_8192x4096", [ops.bind(ops.BiasAddGrad, a_full)],
-                      s * E + s * 4096, E, "tfma_bias_add_grad"),
+            (f"relu_grad_{name}_8192x4096", 3 * s * E, E, "tfma_ew_relu_grad",
+             lambda rnd=rnd: [ops.bind(ops.ReluGrad, rnd(8192, 4096), rnd(8192, 4096))]),
+            (f"bias_add_grad_{name}_8192x4096", s * E + s * 4096, E, "tfma_bias_add_grad",
+             lambda rnd=rnd: [ops.bind(ops.BiasAddGrad, rnd(8192, 4096))]),
         ]
-        del x, b, a_full, b_full, xo, bo
+        # One group per chain: its buffer sets are freed before the next.
+        for cname, nbytes, elems, kernel, make in chains:
+            yield [Component(cname, make(), nbytes, elems, kernel, make=make)]
 
 
-def components(torch, ops, dev):
+def components(torch, ops, dev, copy_ceiling=None):
     """Every component at its config shape: wall time per rep (HIP events
     around it, dispatch included) after a 1 GiB read that evicts the
-    Infinity Cache, then the kernel time from events on the library's own
-    dispatches in a second pass."""
+    Infinity Cache - median, min and max over the reps - then the kernel
+    time from events on the library's own dispatches in a second pass
+    (mean), and, for the cfg3 / cfg4 / cfg5 components, the sustained rate
+    over rotating buffer sets (time_sustained: median, min, max).  A flushed
+    figure above the measured copy ceiling (`copy_ceiling`, GB/s) is flagged:
+    the op's output was still in the Infinity Cache, not yet written to HBM,
+    when the timing stopped."""
     out = {}
     warm = 3
     flush = torch.ones(1 << 28, device=dev)  # 1 GiB, read between reps
     for group in component_groups(torch, ops, dev):
         for c in group:
-            ms = time_calls(torch, c.calls, c.reps, warm, flush=flush)
+            reps = time_calls(torch, c.calls, c.reps, warm, flush=flush)
+            ms = median(reps)
             gbps = c.nbytes / (ms / 1e3) / 1e9
             ops.trace_enable(c.kernel)
             time_calls(torch, c.calls, c.reps, 0, flush=flush)
@@ -350,12 +422,24 @@ def components(torch, ops, dev):
             ops.trace_enable(None)
             kms = kms / c.reps
             kgbps = c.nbytes / (kms / 1e3) / 1e9 if kms else None
-            r = {"ms": round(ms, 4), "GB/s": round(gbps, 1),
+            r = {"ms": round(ms, 4), "ms_min": round(reps[0], 4), "ms_max": round(reps[-1], 4),
+                 "reps": len(reps), "GB/s": round(gbps, 1),
                  "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
                  "Gelem/s": round(c.elems / (ms / 1e3) / 1e9, 2),
                  "kernel_ms": round(kms, 4) if kms else None,
                  "kernel_GB/s": round(kgbps, 1) if kgbps else None,
                  "kernel_pct_peak": round(100 * kgbps / PEAK_GBPS, 1) if kgbps else None}
+            if c.make is not None:
+                sms, nsets, k = time_sustained(torch, c)
+                smed = median(sms)
+                sg = c.nbytes / (smed / 1e3) / 1e9
+                r["sustained"] = {
+                    "ms": round(smed, 4), "ms_min": round(sms[0], 4),
+                    "ms_max": round(sms[-1], 4), "reps": len(sms),
+                    "GB/s": round(sg, 1), "pct_peak": round(100 * sg / PEAK_GBPS, 1),
+                    "buffer_sets": nsets, "calls_per_rep": k}
+            if copy_ceiling and gbps > copy_ceiling:
+                r["above_copy_ceiling"] = True
             traffic = read_traffic(c.name, "pmc_traffic_components.txt")
             if traffic:
                 r["traffic_ratio"] = round(traffic / c.nbytes, 3)
@@ -703,7 +787,8 @@ def main():
         calibrate(torch, dev)
     if not args.no_components:
         result["stream_copy_ceiling"] = stream_copy_ceiling(torch, ops, dev)
-        result["components"] = components(torch, ops, dev)
+        result["components"] = components(
+            torch, ops, dev, copy_ceiling=max(result["stream_copy_ceiling"]["GB/s"].values()))
         result["host_path"] = host_path(torch, tfma, dev)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, dev)

@@ -61,6 +61,7 @@ typedef enum TFMA_DataType {
   TFMA_FLOAT = 1,
   TFMA_DOUBLE = 2,
   TFMA_INT32 = 3,
+  TFMA_UINT8 = 4,
   TFMA_INT64 = 9,
   TFMA_BFLOAT16 = 14,
   TFMA_HALF = 19
@@ -228,6 +229,15 @@ int TFMA_GroupedResourceApplyAdam(
  * MusaMultiplyOp (musa_ext/kernels/math/musa_multiply_op.cc:248-324).
  * Binary ops follow TF broadcasting (BCast); `z`/`output` must have the
  * broadcast shape.
+ *
+ * dtypes, as the reference registers them: every op takes FLOAT, HALF,
+ * BFLOAT16 and DOUBLE.  TFMA_AddV2 (which also serves TF's legacy `Add`,
+ * musa_add_op.cc:455-470) takes INT32, INT64 and UINT8; TFMA_Mul INT32 and
+ * INT64 (musa_multiply_op.cc:315-325); TFMA_BiasAdd (which also serves
+ * `BiasAddV1` with data_format NULL = "NHWC", musa_biasadd_op.cc:67-80) INT32
+ * and INT64.  Integer add and multiply wrap modulo 2^bits (two's
+ * complement), as TF's CPU kernels do.  The reference's bool Add is not
+ * provided (its semantics are muDNN's, unpinned).
  * ------------------------------------------------------------------------- */
 int TFMA_BiasAdd(void* stream, const TFMA_Tensor* value,
                  const TFMA_Tensor* bias, const char* data_format,
@@ -426,6 +436,36 @@ int TFMA_FusedBatchNormLastPlan(TFMA_FusedBatchNormPlan* plan, TFMA_Status* stat
 /* Name of the last kernel this library launched on the calling thread (for
  * tests that check which path an op took). */
 const char* TFMA_LastKernelName(void);
+
+/* Plan and cache-mode overrides, for tests and measurements (no reference
+ * counterpart).  `value` -1 restores the library's own choice.
+ *   "ew_nt"             elementwise cache mode: 0 plain loads and stores,
+ *                       1 non-temporal loads of full-size operands, 2 also
+ *                       non-temporal row operands and stores (default: by
+ *                       size).
+ *   "bn_slice_tw"       fused BatchNorm gradients: 0 never sliced; 4, 8, 16
+ *                       or 32 sliced (where such a plan exists, at most 8
+ *                       slices) in tiles of that many channel vectors.
+ *   "bn_sliced_overlap" 0: sliced gradients run the plain sliced pass
+ *                       instead of hiding each slice's hand-off.
+ *   "bn_nchw_owned"     0: NCHW training keeps the split kernels instead of
+ *                       one workgroup per channel.
+ * Each starts from the environment variable TFMA_<NAME in upper case>,
+ * read once, at the library's first query of any override; after that the
+ * launch paths read one atomic value (no getenv on the hot path).  An
+ * unknown name is INVALID_ARGUMENT.
+ *
+ * Environment variables read once by the library (diagnostics; not needed
+ * in normal use): TFMA_BN_FORCE_GIVE_UP=1 makes every eager fused BatchNorm
+ * launch give up its grid-wide waits after a short spin (exercises the
+ * co-residency error path: NaN outputs, then INTERNAL, see
+ * TFMA_FusedBatchNormBarrierTimedOut); TFMA_BN_EPOCH_START=<n> starts the
+ * fused launches' epoch counter at n (runs launches across its wrap);
+ * TFMA_BN_FUSED=0 disables the fused BatchNorm kernels; TFMA_BN_DYN_PCT,
+ * TFMA_BN_DYN_CHUNK, TFMA_BN_TARGET_WGS and TFMA_EW_BLOCKS_PER_CU change
+ * launch shapes for measurements; TFMA_COPY_THREADS sizes the host copy
+ * pool. */
+int TFMA_SetTuningOverride(const char* name, int32_t value, TFMA_Status* status);
 
 /* ---------------------------------------------------------------------------
  * Host data path of the stream executor: what the SP_StreamExecutor copy,

@@ -21,7 +21,8 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liboracle.so")
-DT = {"float32": 1, "float64": 2, "bfloat16": 14, "float16": 19}
+DT = {"float32": 1, "float64": 2, "bfloat16": 14, "float16": 19, "int32": 3, "uint8": 4,
+      "int64": 9}
 EW_OPS = {"add": 0, "add_relu": 1, "mul": 2, "mul_add": 3, "relu": 4, "relu_grad": 5}
 
 _lib = None
@@ -271,7 +272,10 @@ def bias_add_grad(x, data_format="NHWC", dtype="float32"):
 def eltwise(op, inputs, dtype="float32"):
     """TF-CPU elementwise op with broadcasting: add, add_relu, mul, mul_add
     (inputs[0]*inputs[1] rounded, + inputs[2]), relu, or relu_grad
-    (inputs[0] = gradients, inputs[1] = features)."""
+    (inputs[0] = gradients, inputs[1] = features).  int32 / int64 / uint8
+    take add and mul, wrapping modulo 2^bits."""
+    if dtype in ("int32", "int64", "uint8") and op not in ("add", "mul"):
+        raise ValueError(f"{op} is not defined for {dtype}")
     lib = load()
     ins = [_c(a) for a in inputs]
     out_shape = np.broadcast_shapes(*[a.shape for a in ins])

@@ -28,7 +28,8 @@
  * oracle is closer to the exact value than TF; the rest rounds exactly where
  * TF does.  Build with -ffp-contract=off (see Makefile).
  *
- * dtype codes are TF_DataType values: 1 float, 2 double, 14 bfloat16, 19 half.
+ * dtype codes are TF_DataType values: 1 float, 2 double, 3 int32, 4 uint8,
+ * 9 int64, 14 bfloat16, 19 half.
  */
 #include <math.h>
 #include <stdint.h>
@@ -38,7 +39,8 @@
 #include <omp.h>
 #endif
 
-enum { DT_FLOAT = 1, DT_DOUBLE = 2, DT_BFLOAT16 = 14, DT_HALF = 19 };
+enum { DT_FLOAT = 1, DT_DOUBLE = 2, DT_INT32 = 3, DT_UINT8 = 4, DT_INT64 = 9,
+       DT_BFLOAT16 = 14, DT_HALF = 19 };
 
 /* ------------------------------------------------------------------------ */
 /* half / bfloat16 <-> float, round to nearest even                          */
@@ -348,7 +350,8 @@ void oracle_adam(int dt, void* var, void* m, void* v, const void* grad, int64_t 
   }
 }
 
-/* Elementwise ops with TF broadcasting.  op: 0 add, 1 add+relu, 2 mul,
+/* Elementwise ops with TF broadcasting (integer dtypes: add and mul only).
+ * op: 0 add, 1 add+relu, 2 mul,
  * 3 mul+add (in0*in1 rounded, + in2), 4 relu, 5 relu grad (in0 = gradients,
  * in1 = features: gradients * (features > 0), TF's ReluGrad as a multiply,
  * so a NaN or infinite gradient at features <= 0 gives NaN and a negative
@@ -378,6 +381,27 @@ void oracle_eltwise(int dt, int op, int nin, const void* const* ins, const int64
       int64_t coord = rem % out_dims[d];
       rem /= out_dims[d];
       for (int k = 0; k < nin; ++k) off[k] += coord * strides[k][d];
+    }
+    if (dt == DT_INT32 || dt == DT_INT64 || dt == DT_UINT8) {
+      /* Integer add / mul wrap modulo 2^bits (two's complement), as TF's CPU
+       * kernels' int32 / int64 / uint8 arithmetic does: computed in uint64,
+       * the low bits kept. */
+      uint64_t x, y;
+      if (dt == DT_INT32) {
+        x = (uint64_t)(int64_t)((const int32_t*)ins[0])[off[0]];
+        y = (uint64_t)(int64_t)((const int32_t*)ins[1])[off[1]];
+      } else if (dt == DT_INT64) {
+        x = (uint64_t)((const int64_t*)ins[0])[off[0]];
+        y = (uint64_t)((const int64_t*)ins[1])[off[1]];
+      } else {
+        x = ((const uint8_t*)ins[0])[off[0]];
+        y = ((const uint8_t*)ins[1])[off[1]];
+      }
+      const uint64_t z = op == 2 ? x * y : x + y;
+      if (dt == DT_INT32) ((int32_t*)out)[i] = (int32_t)(uint32_t)z;
+      else if (dt == DT_INT64) ((int64_t*)out)[i] = (int64_t)z;
+      else ((uint8_t*)out)[i] = (uint8_t)z;
+      continue;
     }
     float a = ld(dt, ins[0], off[0]);
     float r;

@@ -2,21 +2,33 @@
 MooreThreads/tensorflow_musa_extension's hot path.
 
     import tensorflow_musa_extension_amd as tfma
-    out = tfma.raw_ops.FusedBatchNormV3(x, scale, offset, mean, var, ...)
+    tfma.tf_plugin.load_plugin()        # TensorFlow: device "AMDGPU" + kernels
+    out = tfma.raw_ops.FusedBatchNormV3(x, scale, offset, mean, var, ...)  # torch tensors
 
-torch is imported first so that the HIP runtime it bundles is the one
-libtfma.so binds to (both carry the soname libamdhip64.so.7).
+Importing the package (and its TensorFlow loader, `tf_plugin`) needs neither
+torch nor TensorFlow, as the reference's loader needs only TensorFlow
+(python/__init__.py:66-75).  `raw_ops` and `stream_executor`, which take
+torch tensors as device buffers, import torch when first used; libtfma.so is
+loaded (after torch, when torch is installed, so that both bind the same HIP
+runtime) on the first call into it.
 """
-import torch  # noqa: F401  (loads the process's HIP runtime)
+import importlib
 
-from . import _lib, errors, graph_rewrite, raw_ops, stream_executor, tf_plugin  # noqa: F401
+from . import _lib, errors, graph_rewrite, tf_plugin  # noqa: F401
 from .errors import (FailedPreconditionError, InternalError,  # noqa: F401
                      InvalidArgumentError, OpError, UnimplementedError)
 
-__all__ = ["raw_ops", "errors", "graph_rewrite", "stream_executor", "load_library", "device_count",
-           "LIB_PATH"]
+__all__ = ["raw_ops", "errors", "graph_rewrite", "stream_executor", "tf_plugin",
+           "load_library", "device_count", "LIB_PATH"]
 
 LIB_PATH = _lib.LIB_PATH
+_LAZY = ("raw_ops", "stream_executor")
+
+
+def __getattr__(name):
+    if name in _LAZY:
+        return importlib.import_module(f".{name}", __name__)
+    raise AttributeError(f"module {__name__!r} has no attribute {name!r}")
 
 
 def load_library():

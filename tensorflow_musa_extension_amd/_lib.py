@@ -26,6 +26,7 @@ UNAVAILABLE = 14
 DT_FLOAT = 1
 DT_DOUBLE = 2
 DT_INT32 = 3
+DT_UINT8 = 4
 DT_INT64 = 9
 DT_BFLOAT16 = 14
 DT_HALF = 19
@@ -110,6 +111,7 @@ SIGNATURES = {
     "TFMA_CreateStreamDependency": [_vp, _vp, _S],
     "TFMA_HostCallback": [_vp, _vp, _vp, _S],
     "TFMA_StagingPoolStats": [ctypes.POINTER(ctypes.c_uint64)] * 4 + [_S],
+    "TFMA_SetTuningOverride": [_cs, ctypes.c_int32, _S],
 }
 _RESTYPES = {"TFMA_Version": ctypes.c_char_p, "TFMA_LastKernelName": ctypes.c_char_p,
              "TFMA_FreeBuffer": None}
@@ -129,6 +131,13 @@ def load():
         _load_error = (f"{LIB_PATH} is not built; run "
                        "`python -c 'import __graft_entry__ as g; g.build()'`")
         raise ImportError(_load_error)
+    # torch bundles its own HIP runtime with the same soname
+    # (libamdhip64.so.7): when torch is installed it is loaded first, so that
+    # libtfma.so binds that one rather than a second copy.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     try:
         lib = ctypes.CDLL(LIB_PATH)
     except OSError as e:  # pragma: no cover - depends on the machine

@@ -376,6 +376,7 @@ hipError_t LaunchGroupedApplyAdamArgs(DType t, DType tg, const AdamTensorEntry* 
     case DType::kF16: TFMA_GADAM_ARGS(TF16, TF16)
     case DType::kBF16: TFMA_GADAM_ARGS(TBF16, TBF16)
     case DType::kF64: TFMA_GADAM_ARGS(TF64, TF64)
+    default: break;  // integer state: LaunchApplyAdamInt
   }
 #undef TFMA_GADAM_ARGS
   return hipErrorInvalidValue;
@@ -401,6 +402,7 @@ hipError_t LaunchApplyAdam(DType t, DType tg, void* var, void* m, void* v,
     case DType::kF16: TFMA_ADAM_CASE(TF16, TF16)
     case DType::kBF16: TFMA_ADAM_CASE(TBF16, TBF16)
     case DType::kF64: TFMA_ADAM_CASE(TF64, TF64)
+    default: break;  // integer state: LaunchApplyAdamInt
   }
 #undef TFMA_ADAM_CASE
   return hipErrorInvalidValue;
@@ -446,6 +448,7 @@ hipError_t LaunchGroupedApplyAdam(DType t, DType tg, const AdamTensorEntry* dev_
     case DType::kF16: TFMA_GADAM_CASE(TF16, TF16)
     case DType::kBF16: TFMA_GADAM_CASE(TBF16, TBF16)
     case DType::kF64: TFMA_GADAM_CASE(TF64, TF64)
+    default: break;  // integer state: LaunchApplyAdamInt
   }
 #undef TFMA_GADAM_CASE
   return hipErrorInvalidValue;

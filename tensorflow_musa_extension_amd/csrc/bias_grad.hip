@@ -246,9 +246,13 @@ BagPlan make_bag_plan(int64_t outer, int64_t c, int64_t inner, int esize, bool a
   return p;
 }
 
+// chain_end (the allocation-free path): in, an event the finalize dispatch
+// ends with (hipExtLaunchKernelGGL's own stop event: no marker packet between
+// kernels); out, the event that marks its end (a trace event instead when
+// tracing is on for the finalize kernel).
 template <class B>
 hipError_t launch_bag(const void* x, int64_t outer, int64_t c, int64_t inner, void* out,
-                      void* workspace, hipStream_t stream) {
+                      void* workspace, hipStream_t stream, hipEvent_t* chain_end = nullptr) {
   using S = typename B::S;
   using A = typename B::A;
   const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
@@ -282,9 +286,20 @@ hipError_t launch_bag(const void* x, int64_t outer, int64_t c, int64_t inner, vo
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  TFMA_LAUNCH("tfma_bias_add_grad_finalize", (bag_finalize_kernel<B>), dim3((c + 63) / 64),
-                     dim3(kThreads), 0, stream, partial, p.groups, static_cast<int>(c),
-                     static_cast<S*>(out));
+  constexpr const char* kFinalize = "tfma_bias_add_grad_finalize";
+  if (!chain_end) {
+    TFMA_LAUNCH(kFinalize, (bag_finalize_kernel<B>), dim3((c + 63) / 64), dim3(kThreads), 0,
+                stream, partial, p.groups, static_cast<int>(c), static_cast<S*>(out));
+    return hipGetLastError();
+  }
+  SetLastKernel(kFinalize);
+  const TraceEvents tev = TraceTake(kFinalize);
+  hipEvent_t end = tev.end ? tev.end : *chain_end;
+  hipExtLaunchKernelGGL((bag_finalize_kernel<B>), dim3((c + 63) / 64), dim3(kThreads), 0, stream,
+                        tev.start, end, 0, partial, p.groups, static_cast<int>(c),
+                        static_cast<S*>(out));
+  TraceCommit(tev);
+  *chain_end = end;
   return hipGetLastError();
 }
 
@@ -327,17 +342,74 @@ size_t BiasAddGradWorkspaceBytes(int dt, int64_t outer, int64_t c, int64_t inner
   return (static_cast<size_t>(g) * c * acc_bytes(dt) + 255) & ~size_t(255);
 }
 
-hipError_t LaunchBiasAddGrad(int dt, const void* x, int64_t outer, int64_t c, int64_t inner,
-                             void* out, void* workspace, hipStream_t stream) {
+namespace {
+hipError_t dispatch_bag(int dt, const void* x, int64_t outer, int64_t c, int64_t inner,
+                        void* out, void* ws, hipStream_t stream, hipEvent_t* chain_end) {
   switch (dt) {
-    case TFMA_FLOAT: return launch_bag<BagF32>(x, outer, c, inner, out, workspace, stream);
-    case TFMA_HALF: return launch_bag<BagF16>(x, outer, c, inner, out, workspace, stream);
-    case TFMA_BFLOAT16: return launch_bag<BagBF16>(x, outer, c, inner, out, workspace, stream);
-    case TFMA_DOUBLE: return launch_bag<BagF64>(x, outer, c, inner, out, workspace, stream);
-    case TFMA_INT32: return launch_bag<BagI32>(x, outer, c, inner, out, workspace, stream);
-    case TFMA_INT64: return launch_bag<BagI64>(x, outer, c, inner, out, workspace, stream);
+    case TFMA_FLOAT: return launch_bag<BagF32>(x, outer, c, inner, out, ws, stream, chain_end);
+    case TFMA_HALF: return launch_bag<BagF16>(x, outer, c, inner, out, ws, stream, chain_end);
+    case TFMA_BFLOAT16:
+      return launch_bag<BagBF16>(x, outer, c, inner, out, ws, stream, chain_end);
+    case TFMA_DOUBLE: return launch_bag<BagF64>(x, outer, c, inner, out, ws, stream, chain_end);
+    case TFMA_INT32: return launch_bag<BagI32>(x, outer, c, inner, out, ws, stream, chain_end);
+    case TFMA_INT64: return launch_bag<BagI64>(x, outer, c, inner, out, ws, stream, chain_end);
   }
   return hipErrorInvalidValue;
+}
+
+// Per device: the allocation-free calls share one scratch, so a call on
+// another stream than the previous call's first waits for that call's
+// finalize to end (its end event); calls on one stream are ordered by the
+// stream.  The mutex keeps the wait, the launches and the bookkeeping of one
+// call together.
+struct NoAllocChain {
+  std::mutex mu;
+  hipEvent_t own = nullptr;    // the finalize's end event when not traced
+  hipEvent_t chain = nullptr;  // end of the last call (`own` or a trace event)
+  hipStream_t last_stream = nullptr;
+  bool used = false;
+};
+}  // namespace
+
+hipError_t LaunchBiasAddGrad(int dt, const void* x, int64_t outer, int64_t c, int64_t inner,
+                             void* out, void* workspace, hipStream_t stream) {
+  return dispatch_bag(dt, x, outer, c, inner, out, workspace, stream, nullptr);
+}
+
+hipError_t LaunchBiasAddGradNoAlloc(int dt, const void* x, int64_t outer, int64_t c,
+                                    int64_t inner, void* out, hipStream_t stream) {
+  void* scratch = nullptr;
+  hipError_t e = BiasAddGradScratch(&scratch);
+  if (e != hipSuccess) return e;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(stream, &cap);
+  if (e != hipSuccess) return e;
+  // Under capture the graph orders its nodes; a replay must not overlap
+  // other allocation-free BiasAddGrad work on the device.
+  if (cap != hipStreamCaptureStatusNone)
+    return dispatch_bag(dt, x, outer, c, inner, out, scratch, stream, nullptr);
+  int dev = 0;
+  e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  static NoAllocChain chains[64];
+  NoAllocChain& ch = chains[dev];
+  std::lock_guard<std::mutex> lk(ch.mu);
+  if (!ch.own) {
+    e = hipEventCreateWithFlags(&ch.own, hipEventDisableTiming | hipEventReleaseToDevice);
+    if (e != hipSuccess) return e;
+  }
+  if (ch.used && ch.last_stream != stream) {
+    e = hipStreamWaitEvent(stream, ch.chain, 0);
+    if (e != hipSuccess) return e;
+  }
+  hipEvent_t end = ch.own;
+  e = dispatch_bag(dt, x, outer, c, inner, out, scratch, stream, &end);
+  if (e != hipSuccess) return e;
+  ch.chain = end;
+  ch.last_stream = stream;
+  ch.used = true;
+  return hipSuccess;
 }
 
 namespace {

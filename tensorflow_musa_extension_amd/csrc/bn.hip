@@ -34,6 +34,7 @@
 // workgroup uses the same K.
 #include <hip/hip_ext.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "device_util.h"
@@ -2169,28 +2170,29 @@ const void* sliced_overlap_kernel() {
       &bn_sliced_grad_kernel<Tr, Resident<Tr>::kRegGradOverlap, Resident<Tr>::kLdsGrad>);
 }
 
-// TFMA_BN_SLICED_OVERLAP=0 (read per call, for tests and measurements):
-// sliced grads run the plain sliced kernel.
-bool sliced_overlap_enabled() {
-  const char* e = getenv("TFMA_BN_SLICED_OVERLAP");
-  return !(e && e[0] == '0');
-}
+// The "bn_sliced_overlap" override 0 (tests and measurements): sliced grads
+// run the plain sliced kernel.
+bool sliced_overlap_enabled() { return TuneValue(kTuneBnSlicedOverlap) != 0; }
 
 // Per device: the sliced kernel has the unsliced kernel's occupancy (set by
-// fused_blocks_per_cu).
+// fused_blocks_per_cu before it publishes its count).
 template <class Tr, bool kGrad>
-bool* sliced_ok() {
-  static bool ok[64] = {false};
+std::atomic<bool>* sliced_ok() {
+  static std::atomic<bool> ok[64];
   return ok;
 }
 
 // Co-resident workgroups per CU for the fused kernel (0 if it cannot run).
+// Computed once per device; threads that race to compute it store the same
+// values.
 template <class Tr, bool kGrad>
 int fused_blocks_per_cu() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cached[dev] == 0) {
+  const int known = cached[dev].load(std::memory_order_acquire);
+  if (known != 0) return known;
+  {
     int nb = 0, sliced_ns = 0;
     hipError_t e = hipFuncSetAttribute(fused_kernel<Tr, kGrad>(),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -2222,10 +2224,11 @@ int fused_blocks_per_cu() {
       e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fused_kernel<Tr, kGrad>(),
                                                        kFusedThreads, fused_smem<Tr, kGrad>());
     if (e != hipSuccess || nb < 1) nb = -1;
-    cached[dev] = nb > 2 ? 2 : nb;
-    sliced_ok<Tr, kGrad>()[dev] = nb >= 1 && sliced_ns >= cached[dev];
+    const int count = nb > 2 ? 2 : nb;
+    sliced_ok<Tr, kGrad>()[dev].store(nb >= 1 && sliced_ns >= count, std::memory_order_relaxed);
+    cached[dev].store(count, std::memory_order_release);
+    return count;
   }
-  return cached[dev];
 }
 
 struct FusedPlan {
@@ -2340,19 +2343,19 @@ constexpr int64_t kGradSliceStreamMax = int64_t(128) << 20;
 // lines), 256x28x28x512 in 2 of 32.  Forwards are not sliced (measured
 // slower: a slice's read-only phase 1 and write-only phase 3 stream slower
 // than the unsliced phase 3, which reads and writes at once).
-// TFMA_BN_SLICE_TW (read per call, for tests and measurements): 0 never
-// slices; 4, 8, 16 or 32 slices every grad that has such a plan, with tiles
-// of that many vectors.
+// The "bn_slice_tw" override (tests and measurements): 0 never slices; 4,
+// 8, 16 or 32 slices every grad that has such a plan, with tiles of that
+// many vectors.
 template <class Tr, bool kGrad>
 bool choose_fused_plan(const BnGeometry& g, int vec, FusedPlan* fp) {
   const int bpc = fused_blocks_per_cu<Tr, kGrad>();
   if (!make_fused_plan(g, vec, bpc, fp)) return false;
   if constexpr (kGrad) {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !sliced_ok<Tr, kGrad>()[dev])
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 ||
+        !sliced_ok<Tr, kGrad>()[dev].load(std::memory_order_relaxed))
       return true;
-    const char* o = getenv("TFMA_BN_SLICE_TW");
-    int tw = o ? atoi(o) : -1;
+    const int tw = TuneValue(kTuneBnSliceTw);
     if (tw == 0) return true;
     if (tw == 4 || tw == 8 || tw == 16 || tw == 32) {
       FusedPlan sp;
@@ -2726,11 +2729,10 @@ size_t partial_region_bytes(DType t, const BnGeometry& g) {
 // least one channel per CU (fewer channels leave CUs idle: the split path's
 // reduce spreads every channel over many workgroups), and offsets that fit
 // the kernel's 32-bit buffer offsets (rows up to 16 images past the tensor's
-// end).  TFMA_BN_NCHW_OWNED=0 (read per call) keeps the split path.
+// end).  The "bn_nchw_owned" override 0 keeps the split path.
 bool nchw_owned_ok(const BnGeometry& g, int vec, int elem) {
   if (g.nhwc || vec <= 1 || g.c < DeviceCUs()) return false;
-  const char* e = getenv("TFMA_BN_NCHW_OWNED");
-  if (e && e[0] == '0') return false;
+  if (TuneValue(kTuneBnNchwOwned) == 0) return false;
   const int64_t plane = g.h * g.w;
   return plane % vec == 0 && (g.n + 16) * g.c * plane * elem < (int64_t{1} << 31);
 }
@@ -2742,16 +2744,16 @@ hipError_t launch_nchw_owned(const BnGeometry& g, const void* x, const void* dy,
   constexpr int KL = fused_kl<Tr, kGrad>();
   const auto kern = &bn_nchw_owned_kernel<Tr, kGrad, KR, KL>;
   const size_t smem = static_cast<size_t>(KL) * (kGrad ? 2 : 1) * kFusedThreads * 16;
-  static bool attr_set[64] = {false};
+  static std::atomic<bool> attr_set[64];
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-  if (!attr_set[dev]) {
+  if (!attr_set[dev].load(std::memory_order_acquire)) {
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
     if (e != hipSuccess) return e;
-    attr_set[dev] = true;
+    attr_set[dev].store(true, std::memory_order_release);
   }
   NchwArgs na;
   na.x = x;

@@ -78,6 +78,40 @@ struct TF64 {
   __device__ static inline C rnd(C c) { return c; }
 };
 
+// Integer storage types.  They compute in the unsigned type of the same width
+// (uint8 in 32 bits) so that add and multiply wrap modulo 2^bits, the
+// two's-complement result TF's CPU kernels produce, with no signed overflow
+// in the device code; st() keeps the low bits.
+template <typename SS, typename CC>
+struct TInt {
+  using S = SS;
+  using C = CC;
+  static constexpr bool kInt = true;
+  static constexpr int kVec = 16 / static_cast<int>(sizeof(SS));
+  __device__ static inline C ld(S s) {
+    if constexpr (sizeof(S) == sizeof(C))
+      return __builtin_bit_cast(C, s);
+    else
+      return static_cast<C>(s);
+  }
+  __device__ static inline S st(C c) {
+    if constexpr (sizeof(S) == sizeof(C))
+      return __builtin_bit_cast(S, c);
+    else
+      return static_cast<S>(c);
+  }
+  __device__ static inline C rnd(C c) { return c; }
+};
+using TI32 = TInt<int32_t, uint32_t>;
+using TI64 = TInt<int64_t, uint64_t>;
+using TU8 = TInt<uint8_t, uint32_t>;
+
+// Whether Tr is one of the integer traits (the others have no kInt member).
+template <class Tr, class = void>
+struct IsIntTraits : std::false_type {};
+template <class Tr>
+struct IsIntTraits<Tr, std::void_t<decltype(Tr::kInt)>> : std::true_type {};
+
 // ---------------------------------------------------------------------------
 // Vector access: N consecutive storage elements at p (p aligned to
 // N*sizeof(S) bytes when N*sizeof(S) is 16, 8 or 4).
@@ -89,8 +123,9 @@ struct Raw {
       kBytes == 16, uint4,
       typename std::conditional<
           kBytes == 8, uint2,
-          typename std::conditional<kBytes == 4, uint32_t,
-                                    S>::type>::type>::type;
+          typename std::conditional<
+              kBytes == 4, uint32_t,
+              typename std::conditional<kBytes == 2, uint16_t, S>::type>::type>::type>::type;
 };
 
 template <typename S, int N>

@@ -1,5 +1,7 @@
 // Elementwise kernels for gfx950: BiasAdd, Relu, AddV2, Mul and the fused
 // chains Relu(BiasAdd), Relu(AddV2) and Mul+Add (MusaShiftedAffineMap).
+// Add and Mul also run on int32 / int64 (and add on uint8), wrapping modulo
+// 2^bits: the same kernels over 16-byte vectors of 4, 2 or 16 elements.
 //
 // Numerics follow TensorFlow's CPU kernels: each TF op computes in float and
 // rounds to T once, so a fused chain rounds after every op it replaces
@@ -15,6 +17,8 @@
 // its inner extent is (NCHW bias), and gathered per element otherwise (odd
 // shapes such as [8191, 4095]).  Broadcast operands are tiny and stay in
 // L1/L2, so HBM traffic is the compulsory stream of the full-size tensors.
+#include <atomic>
+
 #include "device_util.h"
 #include "tfma_internal.h"
 
@@ -468,11 +472,11 @@ Operand make_operand(const BcastOperand& o, int elem_bytes, int V,
 // a and b, kernel time: f32 74.8 -> 81.3 %, f16 74.2 -> 78.3 % of 8 TB/s;
 // ReluGrad f32 79.7 -> 80.9 %; at 128 MiB, f16 ReluGrad, plain loads are
 // 2 points faster).  Only the kinds that stream (full, scalar, row,
-// channel) have the non-temporal variants.  TFMA_EW_NT (read per call, for
+// channel) have the non-temporal variants.  The "ew_nt" override (for
 // measurements): 0, 1 or 2 forces the mode.
 int stream_mode(int64_t out_bytes, int64_t full_in_bytes) {
-  const char* e = getenv("TFMA_EW_NT");
-  if (e && e[0] >= '0' && e[0] <= '2' && e[1] == 0) return e[0] - '0';
+  const int forced = TuneValue(kTuneEwNt);
+  if (forced >= 0 && forced <= 2) return forced;
   if (out_bytes >= (int64_t(1) << 30)) return 2;
   if (out_bytes >= (int64_t(1) << 29) || full_in_bytes >= (int64_t(192) << 20)) return 1;
   return 0;
@@ -506,16 +510,18 @@ void launch_vec(const Operand& ob, const Operand& oc, const typename Tr::S* a,
   // Two staged operands may need more than the 64 KB a launch gets by default
   // (a failure here is left for the caller's hipGetLastError).
   if (lds > 65536) {
-    static bool raised[64] = {false};
+    // Set once per device (setting it again from another thread is harmless;
+    // the flag only saves the call).
+    static std::atomic<bool> raised[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
-    if (!raised[dev]) {
+    if (!raised[dev].load(std::memory_order_acquire)) {
       constexpr int kMaxLds = static_cast<int>(round16(kOddStageBytes) + kOddStageBytes);
       if (hipFuncSetAttribute(
               reinterpret_cast<const void*>(&ew_flat_kernel<Tr, OP, V, U, KB, KC, 0>),
               hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds) != hipSuccess)
         return;
-      raised[dev] = true;
+      raised[dev].store(true, std::memory_order_release);
     }
   }
   int64_t blocks = grid_for(n / V, U);
@@ -624,17 +630,24 @@ hipError_t launch_ew_strided(int64_t n, const void* a, const void* b,
   return hipGetLastError();
 }
 
+// Integer types take add and multiply only (the stock ops registered for
+// them); the other ops are not instantiated for them.
 template <class Tr>
 hipError_t dispatch_op(EwOp op, int64_t n, const BcastOperand& a,
                        const BcastOperand& b, const BcastOperand& c, void* out,
                        hipStream_t stream) {
-  switch (op) {
-    case EwOp::kAdd: return launch_ew<Tr, EwOp::kAdd>(n, a, b, c, out, stream);
-    case EwOp::kAddRelu: return launch_ew<Tr, EwOp::kAddRelu>(n, a, b, c, out, stream);
-    case EwOp::kMul: return launch_ew<Tr, EwOp::kMul>(n, a, b, c, out, stream);
-    case EwOp::kMulAdd: return launch_ew<Tr, EwOp::kMulAdd>(n, a, b, c, out, stream);
-    case EwOp::kRelu: return launch_ew<Tr, EwOp::kRelu>(n, a, b, c, out, stream);
-    case EwOp::kReluGrad: return launch_ew<Tr, EwOp::kReluGrad>(n, a, b, c, out, stream);
+  if constexpr (IsIntTraits<Tr>::value) {
+    if (op == EwOp::kAdd) return launch_ew<Tr, EwOp::kAdd>(n, a, b, c, out, stream);
+    if (op == EwOp::kMul) return launch_ew<Tr, EwOp::kMul>(n, a, b, c, out, stream);
+  } else {
+    switch (op) {
+      case EwOp::kAdd: return launch_ew<Tr, EwOp::kAdd>(n, a, b, c, out, stream);
+      case EwOp::kAddRelu: return launch_ew<Tr, EwOp::kAddRelu>(n, a, b, c, out, stream);
+      case EwOp::kMul: return launch_ew<Tr, EwOp::kMul>(n, a, b, c, out, stream);
+      case EwOp::kMulAdd: return launch_ew<Tr, EwOp::kMulAdd>(n, a, b, c, out, stream);
+      case EwOp::kRelu: return launch_ew<Tr, EwOp::kRelu>(n, a, b, c, out, stream);
+      case EwOp::kReluGrad: return launch_ew<Tr, EwOp::kReluGrad>(n, a, b, c, out, stream);
+    }
   }
   return hipErrorInvalidValue;
 }
@@ -643,14 +656,21 @@ template <class Tr>
 hipError_t dispatch_strided(EwOp op, int64_t n, const void* a, const void* b,
                             const void* c, const StridedShape& sh, void* out,
                             hipStream_t stream) {
-  switch (op) {
-    case EwOp::kAdd: return launch_ew_strided<Tr, EwOp::kAdd>(n, a, b, c, sh, out, stream);
-    case EwOp::kAddRelu: return launch_ew_strided<Tr, EwOp::kAddRelu>(n, a, b, c, sh, out, stream);
-    case EwOp::kMul: return launch_ew_strided<Tr, EwOp::kMul>(n, a, b, c, sh, out, stream);
-    case EwOp::kMulAdd: return launch_ew_strided<Tr, EwOp::kMulAdd>(n, a, b, c, sh, out, stream);
-    case EwOp::kRelu: return launch_ew_strided<Tr, EwOp::kRelu>(n, a, b, c, sh, out, stream);
-    case EwOp::kReluGrad:
-      return launch_ew_strided<Tr, EwOp::kReluGrad>(n, a, b, c, sh, out, stream);
+  if constexpr (IsIntTraits<Tr>::value) {
+    if (op == EwOp::kAdd) return launch_ew_strided<Tr, EwOp::kAdd>(n, a, b, c, sh, out, stream);
+    if (op == EwOp::kMul) return launch_ew_strided<Tr, EwOp::kMul>(n, a, b, c, sh, out, stream);
+  } else {
+    switch (op) {
+      case EwOp::kAdd: return launch_ew_strided<Tr, EwOp::kAdd>(n, a, b, c, sh, out, stream);
+      case EwOp::kAddRelu:
+        return launch_ew_strided<Tr, EwOp::kAddRelu>(n, a, b, c, sh, out, stream);
+      case EwOp::kMul: return launch_ew_strided<Tr, EwOp::kMul>(n, a, b, c, sh, out, stream);
+      case EwOp::kMulAdd:
+        return launch_ew_strided<Tr, EwOp::kMulAdd>(n, a, b, c, sh, out, stream);
+      case EwOp::kRelu: return launch_ew_strided<Tr, EwOp::kRelu>(n, a, b, c, sh, out, stream);
+      case EwOp::kReluGrad:
+        return launch_ew_strided<Tr, EwOp::kReluGrad>(n, a, b, c, sh, out, stream);
+    }
   }
   return hipErrorInvalidValue;
 }
@@ -699,6 +719,9 @@ hipError_t dispatch_flat(DType t, EwOp op, int64_t n, const BcastOperand& a,
     case DType::kF16: return dispatch_op<TF16>(op, n, a, b, c, out, stream);
     case DType::kBF16: return dispatch_op<TBF16>(op, n, a, b, c, out, stream);
     case DType::kF64: return dispatch_op<TF64>(op, n, a, b, c, out, stream);
+    case DType::kI32: return dispatch_op<TI32>(op, n, a, b, c, out, stream);
+    case DType::kI64: return dispatch_op<TI64>(op, n, a, b, c, out, stream);
+    case DType::kU8: return dispatch_op<TU8>(op, n, a, b, c, out, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -721,7 +744,7 @@ hipError_t LaunchElementwise(DType t, EwOp op, int64_t n,
   const BcastOperand ops[3] = {a, b, c};
   const int64_t chunk = flat_chunk(ops);
   if (chunk <= 0) return hipErrorInvalidValue;
-  const int esize = t == DType::kF64 ? 8 : (t == DType::kF32 ? 4 : 2);
+  const int esize = DTypeBytes(t);
   for (int64_t off = 0; off < n; off += chunk) {
     const int64_t len = n - off < chunk ? n - off : chunk;
     const hipError_t e =
@@ -742,6 +765,9 @@ hipError_t LaunchElementwiseStrided(DType t, EwOp op, int64_t n,
     case DType::kF16: return dispatch_strided<TF16>(op, n, a, b, c, shape, out, stream);
     case DType::kBF16: return dispatch_strided<TBF16>(op, n, a, b, c, shape, out, stream);
     case DType::kF64: return dispatch_strided<TF64>(op, n, a, b, c, shape, out, stream);
+    case DType::kI32: return dispatch_strided<TI32>(op, n, a, b, c, shape, out, stream);
+    case DType::kI64: return dispatch_strided<TI64>(op, n, a, b, c, shape, out, stream);
+    case DType::kU8: return dispatch_strided<TU8>(op, n, a, b, c, shape, out, stream);
   }
   return hipErrorInvalidValue;
 }

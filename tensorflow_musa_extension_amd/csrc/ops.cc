@@ -86,6 +86,7 @@ const char* dtype_name(int dt) {
     case TFMA_BFLOAT16: return "bfloat16";
     case TFMA_INT32: return "int32";
     case TFMA_INT64: return "int64";
+    case TFMA_UINT8: return "uint8";
   }
   return "unknown";
 }
@@ -96,6 +97,28 @@ bool to_dtype(int dt, DType* out) {
     case TFMA_HALF: *out = DType::kF16; return true;
     case TFMA_BFLOAT16: *out = DType::kBF16; return true;
     case TFMA_DOUBLE: *out = DType::kF64; return true;
+  }
+  return false;
+}
+
+// Integer dtypes an elementwise op takes besides the floating ones: those the
+// reference registers for its stock ops - AddV2 / Add int32, int64 and uint8
+// (musa_add_op.cc:455-468), Mul int32 and int64 (musa_multiply_op.cc:315-323),
+// BiasAdd / BiasAddV1 int32 and int64 (musa_biasadd_op.cc:67-79).  The fused
+// ops, Relu and ReluGrad are floating only.  (The reference's bool Add is
+// not taken: its arithmetic is muDNN's and nothing pins it.)
+enum class IntTypes { kNone, kI32I64, kI32I64U8 };
+
+bool to_ew_dtype(int dt, IntTypes ints, DType* out) {
+  if (to_dtype(dt, out)) return true;
+  if (ints == IntTypes::kNone) return false;
+  switch (dt) {
+    case TFMA_INT32: *out = DType::kI32; return true;
+    case TFMA_INT64: *out = DType::kI64; return true;
+    case TFMA_UINT8:
+      if (ints != IntTypes::kI32I64U8) return false;
+      *out = DType::kU8;
+      return true;
   }
   return false;
 }
@@ -149,6 +172,7 @@ double read_scalar(const TFMA_Tensor* s, DType t) {
     case DType::kF64: return *static_cast<const double*>(s->data);
     case DType::kF16: return host_f16_to_f32(*static_cast<const uint16_t*>(s->data));
     case DType::kBF16: return bf16_to_f32(*static_cast<const uint16_t*>(s->data));
+    default: break;
   }
   return 0.0;
 }
@@ -485,7 +509,7 @@ void strides_for(const TFMA_Tensor* t, int nd, const int64_t* od,
 // for messages; commutative says whether inputs 0 and 1 may be swapped.
 int run_elementwise(void* stream, EwOp op, const char* op_name,
                     const TFMA_Tensor* const* ins, int n_in, TFMA_Tensor* out,
-                    bool commutative01, TFMA_Status* st) {
+                    bool commutative01, TFMA_Status* st, IntTypes ints = IntTypes::kNone) {
   for (int i = 0; i < n_in; ++i)
     if (!valid_tensor(ins[i]))
       return set_status(st, TFMA_INVALID_ARGUMENT, "%s: invalid input %d", op_name, i);
@@ -493,7 +517,7 @@ int run_elementwise(void* stream, EwOp op, const char* op_name,
     return set_status(st, TFMA_INVALID_ARGUMENT, "%s: invalid output", op_name);
   const int dt = ins[0]->dtype;
   DType t;
-  if (!to_dtype(dt, &t))
+  if (!to_ew_dtype(dt, ints, &t))
     return set_status(st, TFMA_UNIMPLEMENTED, "%s: dtype %s is not supported",
                       op_name, dtype_name(dt));
   for (int i = 1; i < n_in; ++i)
@@ -571,7 +595,7 @@ int bias_add_impl(void* stream, const TFMA_Tensor* value, const TFMA_Tensor* bia
     return set_status(st, TFMA_INVALID_ARGUMENT, "Biases must be 1D: %s",
                       shape_str(bias).c_str());
   DType t;
-  if (!to_dtype(value->dtype, &t))
+  if (!to_ew_dtype(value->dtype, relu ? IntTypes::kNone : IntTypes::kI32I64, &t))
     return set_status(st, TFMA_UNIMPLEMENTED, "%s: dtype %s is not supported", name,
                       dtype_name(value->dtype));
   if (bias->dtype != value->dtype || output->dtype != value->dtype)
@@ -707,6 +731,13 @@ int TFMA_StreamCopy(void* stream, void* dst, const void* src, uint64_t bytes,
   return hip_status(status,
                     LaunchStreamCopy(dst, src, static_cast<int64_t>(bytes), as_stream(stream)),
                     "StreamCopy");
+}
+
+int TFMA_SetTuningOverride(const char* name, int32_t value, TFMA_Status* status) {
+  if (!name || !SetTune(name, value))
+    return set_status(status, TFMA_INVALID_ARGUMENT, "SetTuningOverride: unknown name %s",
+                      name ? name : "(null)");
+  return ok(status);
 }
 
 int TFMA_GetDeviceCount(int* count, TFMA_Status* status) {
@@ -1452,27 +1483,24 @@ int TFMA_BiasAddGradNoAlloc(void* stream, const TFMA_Tensor* out_backprop,
                       "BiasAddGradNoAlloc: this input needs %zu bytes of scratch, more than the "
                       "library's static %zu bytes; use TFMA_BiasAddGrad with a workspace",
                       need, kBiasAddGradScratchBytes);
-  void* scratch = nullptr;
-  const hipError_t e = BiasAddGradScratch(&scratch);
-  if (e != hipSuccess)
-    return set_status(status, TFMA_INTERNAL, "BiasAddGradNoAlloc: scratch address: %s",
-                      hipGetErrorString(e));
   return hip_status(status,
-                    LaunchBiasAddGrad(out_backprop->dtype, out_backprop->data, outer, c, inner,
-                                      output->data, scratch, strm),
+                    LaunchBiasAddGradNoAlloc(out_backprop->dtype, out_backprop->data, outer, c,
+                                             inner, output->data, strm),
                     "BiasAddGrad");
 }
 
 int TFMA_AddV2(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* y, TFMA_Tensor* z,
                TFMA_Status* status) {
   const TFMA_Tensor* ins[2] = {x, y};
-  return run_elementwise(stream, EwOp::kAdd, "Add", ins, 2, z, true, status);
+  return run_elementwise(stream, EwOp::kAdd, "Add", ins, 2, z, true, status,
+                         IntTypes::kI32I64U8);
 }
 
 int TFMA_Mul(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* y, TFMA_Tensor* z,
              TFMA_Status* status) {
   const TFMA_Tensor* ins[2] = {x, y};
-  return run_elementwise(stream, EwOp::kMul, "Mul", ins, 2, z, true, status);
+  return run_elementwise(stream, EwOp::kMul, "Mul", ins, 2, z, true, status,
+                         IntTypes::kI32I64);
 }
 
 int TFMA_MusaAddV2Relu(void* stream, const TFMA_Tensor* x, const TFMA_Tensor* y,

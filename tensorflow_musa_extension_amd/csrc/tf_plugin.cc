@@ -709,7 +709,10 @@ class Call {
   bool output(int i, TF_DataType dt, const std::vector<int64_t>& shape, Tensor* t) {
     int64_t n = 1;
     for (int64_t d : shape) n *= d;
-    size_t es = dt == TF_HALF || dt == TF_BFLOAT16 ? 2 : (dt == TF_DOUBLE || dt == TF_INT64 ? 8 : 4);
+    const size_t es = dt == TF_UINT8 ? 1
+                      : dt == TF_HALF || dt == TF_BFLOAT16 ? 2
+                      : dt == TF_DOUBLE || dt == TF_INT64  ? 8
+                                                           : 4;
     t->reset(TF_AllocateOutput(ctx_, i, dt, shape.data(), static_cast<int>(shape.size()),
                                static_cast<size_t>(n) * es, st_));
     return check();
@@ -1393,20 +1396,32 @@ std::vector<KernelSpec> kernel_specs() {
                   delete_kernel<AdamKernel>, {{"T", g}}, adam_host});
   const TF_DataType ew_types[] = {TF_FLOAT, TF_HALF, TF_BFLOAT16, TF_DOUBLE};
   for (TF_DataType t : ew_types) {
-    ks.push_back({"BiasAdd", format_create, bias_add_compute<false>,
-                  delete_kernel<FormatKernel>, {{"T", t}}, {}});
     ks.push_back({"MusaBiasAddRelu", format_create, bias_add_compute<true>,
                   delete_kernel<FormatKernel>, {{"T", t}}, {}});
     ks.push_back({"Relu", plain_create, relu_compute, delete_kernel<FormatKernel>, {{"T", t}}, {}});
     ks.push_back({"ReluGrad", plain_create, relu_grad_compute, delete_kernel<FormatKernel>,
                   {{"T", t}}, {}});
-    ks.push_back({"AddV2", plain_create, binary_compute<TFMA_AddV2>, delete_kernel<FormatKernel>,
-                  {{"T", t}}, {}});
-    ks.push_back({"Mul", plain_create, binary_compute<TFMA_Mul>, delete_kernel<FormatKernel>,
-                  {{"T", t}}, {}});
     ks.push_back({"MusaAddV2Relu", plain_create, binary_compute<TFMA_MusaAddV2Relu>,
                   delete_kernel<FormatKernel>, {{"T", t}}, {}});
     ks.push_back({"MusaShiftedAffineMap", plain_create, shifted_affine_map_compute,
+                  delete_kernel<FormatKernel>, {{"T", t}}, {}});
+  }
+  // The stock ops with the reference's dtype lists: AddV2 and the legacy Add
+  // (musa_add_op.cc:455-468; bool, whose arithmetic is muDNN's, is left out),
+  // Mul (musa_multiply_op.cc:315-323), BiasAdd and BiasAddV1 - BiasAdd
+  // without the data_format attr, always NHWC (musa_biasadd_op.cc:67-79).
+  for (TF_DataType t : {TF_FLOAT, TF_INT32, TF_INT64, TF_HALF, TF_BFLOAT16, TF_DOUBLE, TF_UINT8}) {
+    ks.push_back({"AddV2", plain_create, binary_compute<TFMA_AddV2>, delete_kernel<FormatKernel>,
+                  {{"T", t}}, {}});
+    ks.push_back({"Add", plain_create, binary_compute<TFMA_AddV2>, delete_kernel<FormatKernel>,
+                  {{"T", t}}, {}});
+  }
+  for (TF_DataType t : {TF_FLOAT, TF_DOUBLE, TF_HALF, TF_BFLOAT16, TF_INT32, TF_INT64}) {
+    ks.push_back({"Mul", plain_create, binary_compute<TFMA_Mul>, delete_kernel<FormatKernel>,
+                  {{"T", t}}, {}});
+    ks.push_back({"BiasAdd", format_create, bias_add_compute<false>,
+                  delete_kernel<FormatKernel>, {{"T", t}}, {}});
+    ks.push_back({"BiasAddV1", plain_create, bias_add_compute<false>,
                   delete_kernel<FormatKernel>, {{"T", t}}, {}});
   }
   const TF_DataType bag_types[] = {TF_FLOAT, TF_HALF, TF_BFLOAT16, TF_DOUBLE, TF_INT32, TF_INT64};

@@ -14,7 +14,18 @@
 
 namespace tfma {
 
-enum class DType { kF32, kF16, kBF16, kF64 };
+// kI32, kI64, kU8: integer storage for the stock elementwise ops (add and
+// multiply, wrapping); no other kernel family takes them.
+enum class DType { kF32, kF16, kBF16, kF64, kI32, kI64, kU8 };
+
+inline int DTypeBytes(DType t) {
+  switch (t) {
+    case DType::kF64: case DType::kI64: return 8;
+    case DType::kF32: case DType::kI32: return 4;
+    case DType::kU8: return 1;
+    default: return 2;
+  }
+}
 
 // ---------------------------------------------------------------------------
 // Kernel launch tracing (TFMA_TraceEnable / TFMA_TraceRead).
@@ -46,6 +57,16 @@ void TraceCommit(const TraceEvents& ev);
                           0, __VA_ARGS__);                                             \
     ::tfma::TraceCommit(tfma_ev_);                                                     \
   } while (0)
+
+// Plan and cache-mode overrides (TFMA_SetTuningOverride); -1 = not set.
+//   kTuneEwNt: elementwise cache mode 0, 1 or 2 instead of the size rule.
+//   kTuneBnSliceTw: 0 = fused BN grads unsliced; 4, 8, 16, 32 = sliced in
+//     tiles of that many channel vectors.
+//   kTuneBnSlicedOverlap: 0 = sliced grads run the plain sliced pass.
+//   kTuneBnNchwOwned: 0 = NCHW training keeps the split kernels.
+enum Tune { kTuneEwNt, kTuneBnSliceTw, kTuneBnSlicedOverlap, kTuneBnNchwOwned, kTuneCount };
+int TuneValue(Tune k);
+bool SetTune(const char* name, int value);
 
 // Number of compute units of the current device (cached per device).
 int DeviceCUs();
@@ -117,6 +138,11 @@ hipError_t LaunchBiasAddGrad(int dt, const void* x, int64_t outer, int64_t c, in
 // hipGetSymbolAddress on the device's first call, then cached per device).
 constexpr size_t kBiasAddGradScratchBytes = size_t(4) << 20;
 hipError_t BiasAddGradScratch(void** ptr);
+// BiasAddGrad with the partials in that scratch.  Eager calls on one device
+// are chained: a call on another stream than the previous call waits for the
+// previous call's end, so overlapping calls do not share the scratch.
+hipError_t LaunchBiasAddGradNoAlloc(int dt, const void* x, int64_t outer, int64_t c,
+                                    int64_t inner, void* out, hipStream_t stream);
 // Zero-fills n bytes with a kernel (capturable, unlike a memset node).
 hipError_t LaunchZeroBytes(void* p, int64_t n, hipStream_t stream);
 // 16-byte non-temporal streaming copy (bytes a multiple of 16, both pointers

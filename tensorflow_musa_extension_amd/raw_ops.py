@@ -14,7 +14,8 @@ Reference ops mirrored:
       musa_ext/kernels/training/musa_applygradientdescent_op.cc:305-448)
   BiasAdd              musa_ext/kernels/nn/musa_biasadd_op.cc:10-82
   Relu                 musa_ext/kernels/nn/musa_relu_op.cc:10-60
-  AddV2                musa_ext/kernels/math/musa_add_op.cc:379-470
+  AddV2, Add           musa_ext/kernels/math/musa_add_op.cc:379-470
+  BiasAddV1            musa_ext/kernels/nn/musa_biasadd_op.cc:71-73
   Mul                  musa_ext/kernels/math/musa_multiply_op.cc:248-324
   MusaShiftedAffineMap musa_ext/kernels/fusion/musa_shifted_affine_map_op.cc:108-262
   MusaBiasAddRelu, MusaAddV2Relu: fused chains with no reference op.
@@ -35,6 +36,7 @@ _TORCH_TO_TF = {
     torch.float64: _lib.DT_DOUBLE,
     torch.int32: _lib.DT_INT32,
     torch.int64: _lib.DT_INT64,
+    torch.uint8: _lib.DT_UINT8,
 }
 
 FusedBatchNormV3Result = collections.namedtuple(
@@ -305,6 +307,13 @@ def BiasAdd(value, bias, data_format="NHWC", out=None):
     return out
 
 
+def BiasAddV1(value, bias, out=None):
+    """tf.raw_ops.BiasAddV1: BiasAdd over the last dimension (no data_format
+    attr; the reference registers it with BiasAdd's compute,
+    musa_biasadd_op.cc:71-73)."""
+    return BiasAdd(value, bias, "NHWC", out)
+
+
 def MusaBiasAddRelu(value, bias, data_format="NHWC", out=None):
     out = torch.empty_like(value) if out is None else out
     dv, db, do = _desc(value, "value"), _desc(bias, "bias"), _desc(out, "output")
@@ -366,6 +375,12 @@ def bias_add_grad_no_alloc(out_backprop, out, data_format="NHWC"):
 
 
 def AddV2(x, y, out=None):
+    return _binary("TFMA_AddV2", x, y, out)
+
+
+def Add(x, y, out=None):
+    """tf.raw_ops.Add: the legacy name, AddV2's compute (the reference
+    registers both on MusaAddOp, musa_add_op.cc:455-460)."""
     return _binary("TFMA_AddV2", x, y, out)
 
 
@@ -446,6 +461,16 @@ def fused_batch_norm_barrier_timed_out(reset=False):
                                            ctypes.byref(status))
     raise_for_status(status)
     return bool(flag.value)
+
+
+def set_tuning_override(name, value):
+    """Plan / cache-mode override (TFMA_SetTuningOverride): "ew_nt",
+    "bn_slice_tw", "bn_sliced_overlap" or "bn_nchw_owned"; value None or -1
+    restores the library's own choice.  For tests and measurements."""
+    st = _lib.TFMA_Status()
+    _lib.load().TFMA_SetTuningOverride(name.encode(), -1 if value is None else int(value),
+                                       ctypes.byref(st))
+    raise_for_status(st)
 
 
 def last_kernel_name():

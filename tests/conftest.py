@@ -26,3 +26,19 @@ def _oracle_threads():
     from oracle import oracle
     oracle.set_threads(min(16, os.cpu_count() or 1))
     yield
+
+
+@pytest.fixture
+def tune():
+    """set(name, value) for the library's plan / cache-mode overrides
+    (TFMA_SetTuningOverride); every override set is restored at teardown."""
+    import tensorflow_musa_extension_amd as tfma
+    touched = set()
+
+    def set_(name, value):
+        touched.add(name)
+        tfma.raw_ops.set_tuning_override(name, value)
+
+    yield set_
+    for name in touched:
+        tfma.raw_ops.set_tuning_override(name, None)

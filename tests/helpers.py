@@ -26,6 +26,10 @@ def to_np(t, dtype):
 
 
 def gen(rng, shape, dtype, kind="normal", scale=1.0, loc=0.0):
+    if dtype in ("int32", "int64", "uint8"):
+        # the whole range of the type (sums and products wrap)
+        info = np.iinfo(dtype)
+        return rng.integers(info.min, info.max, size=shape, dtype=dtype, endpoint=True)
     if kind == "normal":
         a = loc + scale * rng.standard_normal(shape)
     elif kind == "uniform":
@@ -53,7 +57,7 @@ def assert_bitwise(got, ref, name=""):
     g = np.ascontiguousarray(got)
     r = np.ascontiguousarray(ref)
     assert g.shape == r.shape, f"{name}: shape {g.shape} != {r.shape}"
-    bits = {2: np.uint16, 4: np.uint32, 8: np.uint64}[g.dtype.itemsize]
+    bits = {1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}[g.dtype.itemsize]
     gb, rb = g.view(bits), r.view(bits)
     bad = np.flatnonzero(gb != rb)
     assert bad.size == 0, (f"{name}: {bad.size} of {g.size} elements differ, first at "
@@ -101,6 +105,25 @@ def bn_max_ulp(got, ref_fn, rows, c, rows_per=1 << 20, atol=BN16_ATOL):
         ref = ref32.to(got.dtype)
         d = (_ord16(g2[r:r1]) - _ord16(ref)).abs()
         d[(g2[r:r1].float() - ref32).abs() <= atol] = 0
+        worst = max(worst, int(d.max()))
+    return worst
+
+
+def max_ulp_vs(got, ref, dtype, atol=BN16_ATOL, chunk=1 << 24):
+    """Largest distance in units of the last place between a float16 /
+    bfloat16 device tensor `got` and a reference numpy storage array `ref`
+    (float16, or bfloat16 as uint16 bits) of the same element count, over
+    every element whose absolute difference exceeds atol (the BN16_ATOL
+    floor above); computed on the device in chunks."""
+    g = got.reshape(-1)
+    r = np.ascontiguousarray(ref).reshape(-1)
+    assert g.numel() == r.size
+    worst = 0
+    for i in range(0, r.size, chunk):
+        rc = to_dev(r[i:i + chunk], dtype, got.device)
+        gc = g[i:i + chunk]
+        d = (_ord16(gc) - _ord16(rc)).abs()
+        d[(gc.float() - rc.float()).abs() <= atol] = 0
         worst = max(worst, int(d.max()))
     return worst
 

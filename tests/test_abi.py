@@ -351,3 +351,64 @@ def test_host_path_validation_without_device():
     assert b"null stream in create_stream_dependency" in st.message
     assert lib.TFMA_HostCallback(ctypes.c_void_p(1), None, None,
                                  ctypes.byref(st)) == _lib.INVALID_ARGUMENT
+
+
+def test_elementwise_integer_dtype_validation():
+    """The integer dtypes each stock op takes (uint8: Add only; the fused
+    ops, Relu and ReluGrad none), checked before any device access."""
+    u8, i32 = _lib.DT_UINT8, _lib.DT_INT32
+    # uint8 Mul and BiasAdd, int32 Relu / fused ops: not registered
+    code, msg = call("TFMA_Mul", None, ref(T((4,), u8)), ref(T((4,), u8)), ref(T((4,), u8)))
+    assert code == _lib.UNIMPLEMENTED and "uint8" in msg
+    code, _ = call("TFMA_BiasAdd", None, ref(T((2, 4), u8)), ref(T((4,), u8)), b"NHWC",
+                   ref(T((2, 4), u8)))
+    assert code == _lib.UNIMPLEMENTED
+    code, _ = call("TFMA_MusaAddV2Relu", None, ref(T((4,), i32)), ref(T((4,), i32)),
+                   ref(T((4,), i32)))
+    assert code == _lib.UNIMPLEMENTED
+    code, _ = call("TFMA_Relu", None, ref(T((4,), i32)), ref(T((4,), i32)))
+    assert code == _lib.UNIMPLEMENTED
+    # mixed integer dtypes and bad shapes are still INVALID_ARGUMENT
+    code, msg = call("TFMA_AddV2", None, ref(T((4,), i32)), ref(T((4,), _lib.DT_INT64)),
+                     ref(T((4,), i32)))
+    assert code == _lib.INVALID_ARGUMENT and "int64" in msg
+    code, msg = call("TFMA_AddV2", None, ref(T((4, 5), u8)), ref(T((3,), u8)),
+                     ref(T((4, 5), u8)))
+    assert msg == "Incompatible shapes for Add: [4,5] and [3]"
+    # empty integer outputs succeed without a launch
+    for dt in (u8, i32, _lib.DT_INT64):
+        code, _ = call("TFMA_AddV2", None, ref(T((0, 4), dt, None)), ref(T((4,), dt)),
+                       ref(T((0, 4), dt, None)))
+        assert code == _lib.OK
+
+
+def test_tuning_overrides():
+    """TFMA_SetTuningOverride takes the four documented names (-1 restores
+    the default) and rejects others; host only."""
+    for name in (b"ew_nt", b"bn_slice_tw", b"bn_sliced_overlap", b"bn_nchw_owned"):
+        assert call("TFMA_SetTuningOverride", name, 0)[0] == _lib.OK
+        assert call("TFMA_SetTuningOverride", name, -1)[0] == _lib.OK
+    code, msg = call("TFMA_SetTuningOverride", b"bn_slices", 4)
+    assert code == _lib.INVALID_ARGUMENT and "bn_slices" in msg
+    assert call("TFMA_SetTuningOverride", None, 4)[0] == _lib.INVALID_ARGUMENT
+
+
+def test_package_and_tf_loader_import_without_torch():
+    """Importing the package and its TensorFlow loader needs neither torch
+    nor TensorFlow (the reference's loader needs only TensorFlow,
+    python/__init__.py:66-75); raw_ops, which takes torch tensors, does."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.modules['torch'] = None\n"
+            "import tensorflow_musa_extension_amd as tfma\n"
+            "from tensorflow_musa_extension_amd import tf_plugin\n"
+            "assert tf_plugin.find_plugin_library().endswith('libtfma_tf.so')\n"
+            "assert 'torch' not in [m for m in sys.modules if sys.modules[m] is not None]\n"
+            "try:\n"
+            "    tfma.raw_ops\n"
+            "except ImportError:\n"
+            "    print('raw_ops needs torch')\n")
+    r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.strip() == "raw_ops needs torch"

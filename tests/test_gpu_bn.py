@@ -14,7 +14,7 @@ import torch
 import tensorflow_musa_extension_amd as tfma
 from oracle import oracle
 from tests.helpers import (assert_close, bn_fwd_ref32, bn_grad_ref32, bn_max_ulp,
-                           bn_scale_backprop_ref64, gen, to_dev, to_np)
+                           bn_scale_backprop_ref64, gen, max_ulp_vs, to_dev, to_np)
 
 pytestmark = pytest.mark.gpu
 ops = tfma.raw_ops
@@ -118,11 +118,11 @@ SLICED_CASES = [
 @pytest.mark.parametrize("tw", [4, 8, 16, 32])
 @pytest.mark.parametrize("is_training", [True, False])
 @pytest.mark.parametrize("shape,dtype", SLICED_CASES)
-def test_sliced_grad_matches_oracle(dev, monkeypatch, shape, dtype, tw, is_training):
+def test_sliced_grad_matches_oracle(dev, tune, shape, dtype, tw, is_training):
     """The sliced fused gradient (each workgroup runs the whole two-phase pass
     once per channel tile of tw vectors), forced at small shapes, against the
     oracle; the plan query shows how many slices ran."""
-    monkeypatch.setenv("TFMA_BN_SLICE_TW", str(tw))
+    tune("bn_slice_tw", tw)
     rng = np.random.default_rng(zlib.crc32(repr((shape, dtype, tw)).encode()))
     eps = 1e-3
     c = shape[-1]
@@ -156,21 +156,21 @@ def test_sliced_grad_matches_oracle(dev, monkeypatch, shape, dtype, tw, is_train
                                             ((6, 5, 7, 200), "float16", 8),
                                             ((64, 28, 28, 512), "bfloat16", 32),
                                             ((16, 28, 28, 512), "float32", 16)])
-def test_sliced_overlap_equals_plain_sliced(dev, monkeypatch, shape, dtype, tw):
+def test_sliced_overlap_equals_plain_sliced(dev, tune, shape, dtype, tw):
     """The sliced gradient that reads the next slice's streamed rows while a
     slice's coefficients are pending, against the plain sliced pass
-    (TFMA_BN_SLICED_OVERLAP=0), both forced to tw-vector tiles: the same
+    (override bn_sliced_overlap 0), both forced to tw-vector tiles: the same
     slices, so scale_backprop and offset_backprop within 1e-5 of their
     largest value (the streamed rows' sums are added in a different order)
     and x_backprop within one ulp of its largest value; both against the
     oracle as well."""
-    monkeypatch.setenv("TFMA_BN_SLICE_TW", str(tw))
+    tune("bn_slice_tw", tw)
     rng = np.random.default_rng(zlib.crc32(repr((shape, dtype, tw, "overlap")).encode()))
     eps = 1e-3
     x, scale, offset, dy = _inputs(rng, shape, dtype, "NHWC", loc=0.5)
     outs = {}
     for mode in ("1", "0"):
-        monkeypatch.setenv("TFMA_BN_SLICED_OVERLAP", mode)
+        tune("bn_sliced_overlap", int(mode))
         fwd, grad = _run_fwd_grad(dev, x, scale, offset, dy, dtype, "NHWC", eps)
         plan = ops.fused_batch_norm_last_plan()
         vec = 4 if dtype == "float32" else 8
@@ -232,9 +232,9 @@ def test_nchw_owned_matches_oracle(dev, shape, dtype):
     assert torch.all(grad.reserve_space_4 == 0) and torch.all(grad.reserve_space_5 == 0)
 
 
-def test_nchw_owned_equals_split_path(dev, monkeypatch):
+def test_nchw_owned_equals_split_path(dev, tune):
     """The channel-per-workgroup kernel and the split path (forced with
-    TFMA_BN_NCHW_OWNED=0) agree: statistics to 1e-5 of their largest value
+    override bn_nchw_owned 0) agree: statistics to 1e-5 of their largest value
     (the float32 partial sums of the two are taken in different orders, and
     sums such as offset_backprop cancel), outputs within one ulp of their
     largest value."""
@@ -243,7 +243,7 @@ def test_nchw_owned_equals_split_path(dev, monkeypatch):
     x, scale, offset, dy = _inputs(rng, shape, dtype, "NCHW")
     f1, g1 = _run_fwd_grad(dev, x, scale, offset, dy, dtype, "NCHW", 1e-3)
     assert ops.fused_batch_norm_last_plan()["fused"] == 2
-    monkeypatch.setenv("TFMA_BN_NCHW_OWNED", "0")
+    tune("bn_nchw_owned", 0)
     f2, g2 = _run_fwd_grad(dev, x, scale, offset, dy, dtype, "NCHW", 1e-3)
     assert ops.fused_batch_norm_last_plan()["fused"] == 0
     for name, a, b in (("mean", f1.reserve_space_1, f2.reserve_space_1),
@@ -352,7 +352,8 @@ CFG2_SHAPES = [(256, 56, 56, 256), (256, 28, 28, 512), (256, 14, 14, 1024), (256
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_cfg2_full_size(dev, shape, dtype):
     """BASELINE cfg2 at full size, every shape in both dtypes, against the
-    oracle (eps=1.001e-5): y and x_backprop to 1e-2, every statistic
+    oracle (eps=1.001e-5): y and x_backprop to 1e-2 normwise and within 1
+    ulp at every element (BN16_ATOL floor), every statistic
     (batch_mean, batch_variance, reserve spaces, scale_backprop,
     offset_backprop) to 1e-5 - the outputs the reference's own test checks,
     test/ops/fused_batchnorm_op_test.py:358-448.  The 56x56 gradient runs
@@ -384,6 +385,10 @@ def test_cfg2_full_size(dev, shape, dtype):
     del tx, tdy
     ry, rbm, rbv, rsm, rsv = oracle.bn_fwd(x, scale, offset, epsilon=eps, dtype=dtype)
     assert_close(to_np(fwd.y, dtype), ry, dtype, 1e-2, "y")
+    # Element by element: every y within 1 ulp of the oracle's (or BN16_ATOL
+    # where the float32 terms cancel to near zero).
+    uy = max_ulp_vs(fwd.y, ry, dtype)
+    assert uy <= 1, f"y: {uy} ulp from the oracle"
     del ry
     for name, got, want in (("batch_mean", fwd.batch_mean, rbm),
                             ("batch_variance", fwd.batch_variance, rbv),
@@ -394,6 +399,8 @@ def test_cfg2_full_size(dev, shape, dtype):
     # scale_backprop are checked against values that share nothing with it.
     rdx, rsb, rob = oracle.bn_grad(dy, x, scale, rsm, rsv, epsilon=eps, dtype=dtype)
     assert_close(to_np(grad.x_backprop, dtype), rdx, dtype, 1e-2, "x_backprop")
+    udx = max_ulp_vs(grad.x_backprop, rdx, dtype)
+    assert udx <= 1, f"x_backprop: {udx} ulp from the oracle"
     assert_close(grad.scale_backprop.cpu().numpy(), rsb, "float32", STAT_TOL, "scale_backprop")
     assert_close(grad.offset_backprop.cpu().numpy(), rob, "float32", STAT_TOL, "offset_backprop")
 
@@ -646,8 +653,7 @@ assert torch.isnan(g.x_backprop.float()).all() and torch.isnan(g.scale_backprop)
 expect_internal(fwd, "forward after grad")
 # A sliced gradient (forced: 4 slices of 64 channels, two waits per slice)
 # gives up the same way.
-import os
-os.environ["TFMA_BN_SLICE_TW"] = "8"
+ops.set_tuning_override("bn_slice_tw", 8)
 gs = ops.FusedBatchNormGradV3(dy, x, scale, f.reserve_space_1, f.reserve_space_2,
                               f.reserve_space_3, epsilon=1e-3)
 assert ops.fused_batch_norm_last_plan()["slices"] == 4

@@ -76,6 +76,68 @@ def test_binary_broadcast(dev, dtype, xs, ys, op):
     assert_bitwise(to_np(out, dtype), oracle.eltwise(op, [x, y], dtype), op)
 
 
+INT_DTYPES = ["int32", "int64", "uint8"]
+# cfg4's shapes, and a broadcast case of every operand kind per dtype (row,
+# odd row period staged in LDS, inner-extent walk, scalar, strided).
+INT_BCAST = [
+    ((8192, 4096), (4096,)),
+    ((8192, 4096), (8192, 4096)),
+    ((8191, 4095), (4095,)),
+    ((8191, 4095), (8191, 4095)),
+    ((2048, 33), (33,)),
+    ((64, 37, 33), (37, 1)),
+    ((64, 33), ()),
+    ((4, 1, 5), (1, 3, 1)),
+    ((3, 9001), (9001,)),
+    ((0, 4), (4,)),
+]
+
+
+@pytest.mark.parametrize("dtype", INT_DTYPES)
+@pytest.mark.parametrize("xs,ys", INT_BCAST)
+def test_integer_add_mul(dev, dtype, xs, ys):
+    """The reference's integer registrations of AddV2 / Add (int32, int64,
+    uint8) and Mul (int32, int64): wrapping arithmetic, bitwise against the
+    oracle over the types' whole range."""
+    rng = np.random.default_rng(8)
+    x, y = gen(rng, xs, dtype), gen(rng, ys, dtype)
+    xd, yd = to_dev(x, dtype, dev), to_dev(y, dtype, dev)
+    for name, fn, op in (("AddV2", ops.AddV2, "add"), ("Add", ops.Add, "add"),
+                         ("Mul", ops.Mul, "mul")):
+        if op == "mul" and dtype == "uint8":
+            with pytest.raises(tfma.UnimplementedError):
+                ops.Mul(xd, yd)
+            continue
+        out = fn(xd, yd)
+        torch.cuda.synchronize()
+        assert_bitwise(to_np(out, dtype), oracle.eltwise(op, [x, y], dtype), name)
+
+
+@pytest.mark.parametrize("dtype", ["int32", "int64"])
+@pytest.mark.parametrize("shape,fmt", [((8192, 4096), "NHWC"), ((8191, 4095), "NHWC"),
+                                       ((4, 16, 7, 7), "NCHW"), ((2, 5, 3), "NCHW")])
+def test_integer_bias_add(dev, dtype, shape, fmt):
+    """BiasAdd / BiasAddV1 for int32 and int64 (musa_biasadd_op.cc:67-79)."""
+    rng = np.random.default_rng(9)
+    x = gen(rng, shape, dtype)
+    b = gen(rng, shape[1:2] if fmt == "NCHW" else shape[-1:], dtype)
+    xd, bd = to_dev(x, dtype, dev), to_dev(b, dtype, dev)
+    out = ops.BiasAdd(xd, bd, data_format=fmt)
+    torch.cuda.synchronize()
+    ref = oracle.bias_add(x, b, data_format=fmt, dtype=dtype)
+    assert_bitwise(to_np(out, dtype), ref, "BiasAdd")
+    if fmt == "NHWC":
+        assert_bitwise(to_np(ops.BiasAddV1(xd, bd), dtype), ref, "BiasAddV1")
+    with pytest.raises(tfma.UnimplementedError):
+        ops.MusaBiasAddRelu(xd, bd, data_format=fmt)
+
+
+def test_uint8_bias_add_is_unregistered(dev):
+    x = torch.zeros(4, 8, dtype=torch.uint8, device=dev)
+    with pytest.raises(tfma.UnimplementedError):
+        ops.BiasAdd(x, torch.zeros(8, dtype=torch.uint8, device=dev))
+
+
 MULADD = [
     ((8192, 4096), (8192, 4096), (8192, 4096)),   # a, b full
     ((8192, 4096), (4096,), (4096,)),             # a, b row broadcast

@@ -50,7 +50,7 @@ def _state(d):
 
 
 # (16,14,14,256): every row resident, no dynamic chunks.  (128,56,56,256)
-# unsliced (TFMA_BN_SLICE_TW=0): the grad hands out phase-3 chunks, so the
+# unsliced (override bn_slice_tw 0): the grad hands out phase-3 chunks, so the
 # recorded launch zeroes the chunk counters as well as the barrier counters
 # at exit; left to the host, the grad runs in 2 slices of 128 channels
 # (hand-offs hidden); with slice_tw 8 in 4 slices of 64 channels.
@@ -58,9 +58,9 @@ def _state(d):
                                                    ((128, 56, 56, 256), 0, 1),
                                                    ((128, 56, 56, 256), None, 2),
                                                    ((128, 56, 56, 256), 8, 4)])
-def test_recorded_training_step_replays(dev, monkeypatch, shape, slice_tw, slices):
+def test_recorded_training_step_replays(dev, tune, shape, slice_tw, slices):
     if slice_tw is not None:
-        monkeypatch.setenv("TFMA_BN_SLICE_TW", str(slice_tw))
+        tune("bn_slice_tw", slice_tw)
     d = _inputs(dev, shape, seed=31)
     other = _inputs(dev, (8, 7, 7, 512), seed=32)
     e = torch.empty(0, device=dev)

@@ -59,18 +59,18 @@ def _bn_case(seed):
     if fmt == "NHWC":
         tw = rng.choice(["", "8", "16", "32"], p=[0.55, 0.15, 0.15, 0.15])
         if tw:
-            env["TFMA_BN_SLICE_TW"] = str(tw)
+            env["bn_slice_tw"] = int(tw)
             if rng.random() < 0.5:
-                env["TFMA_BN_SLICED_OVERLAP"] = "0"
+                env["bn_sliced_overlap"] = 0
     return dict(dtype=dtype, fmt=fmt, shape=shape, training=training, factor=factor, loc=loc,
                 env=env, rng=rng)
 
 
 @pytest.mark.parametrize("seed", range(100, 160))
-def test_bn_sweep(dev, monkeypatch, seed):
+def test_bn_sweep(dev, tune, seed):
     k = _bn_case(seed)
     for name, value in k["env"].items():
-        monkeypatch.setenv(name, value)
+        tune(name, value)
     rng, dtype, fmt, shape = k["rng"], k["dtype"], k["fmt"], k["shape"]
     print(f"seed {seed}: {shape} {dtype} {fmt} training={k['training']} "
           f"factor={k['factor']} loc={k['loc']} env={k['env']}", flush=True)

@@ -21,7 +21,7 @@ from tests.helpers import assert_bitwise, assert_close, gen, to_dev, to_np
 pytestmark = pytest.mark.gpu
 ops = tfma.raw_ops
 NP = {"float": np.float32, "half": np.float16, "bfloat16": np.uint16, "double": np.float64,
-      "int32": np.int32, "int64": np.int64}
+      "int32": np.int32, "int64": np.int64, "uint8": np.uint8}
 ORACLE_DT = {"float": "float32", "half": "float16", "bfloat16": "bfloat16",
              "double": "float64"}
 
@@ -86,7 +86,8 @@ def plugin(dev):
 def T(t, kind="dev"):
     """A device (or host) torch tensor as a kernel input."""
     name = {torch.float32: "float", torch.float16: "half", torch.bfloat16: "bfloat16",
-            torch.float64: "double", torch.int32: "int32", torch.int64: "int64"}[t.dtype]
+            torch.float64: "double", torch.int32: "int32", torch.int64: "int64",
+            torch.uint8: "uint8"}[t.dtype]
     return (ctypes.c_void_p(t.data_ptr()), name, tuple(t.shape), kind)
 
 
@@ -390,6 +391,44 @@ def test_elementwise_kernels(plugin, dtype):
     k = p.run("MusaBiasAddRelu", ty, [T(xf, "fwd"), T(b)], dict(data_format="NHWC"))
     assert k.output(0)[3] == 0 and k.output(0)[0] == xf.data_ptr()
     check(k, oracle.bias_add(xs, bs, relu=True, dtype=odt), "forwarded MusaBiasAddRelu")
+
+
+@pytest.mark.parametrize("tname", ["int32", "int64", "uint8", "float"])
+def test_stock_op_registrations_integer_and_legacy_names(plugin, tname):
+    """Add (the legacy name), AddV2, Mul, BiasAdd and BiasAddV1 through their
+    registrations for the reference's integer dtypes (musa_add_op.cc:455-468,
+    musa_multiply_op.cc:315-323, musa_biasadd_op.cc:67-79), bitwise against
+    the oracle's wrapping arithmetic; float for the legacy names."""
+    p = plugin
+    npdt = NP[tname]
+    rng = np.random.default_rng(7)
+    if tname == "float":
+        xs = rng.standard_normal((64, 96)).astype(np.float32)
+        bs = rng.standard_normal(96).astype(np.float32)
+    else:
+        info = np.iinfo(npdt)
+        xs = rng.integers(info.min, info.max, (64, 96), dtype=npdt, endpoint=True)
+        bs = rng.integers(info.min, info.max, 96, dtype=npdt, endpoint=True)
+    odt = ORACLE_DT.get(tname, tname)
+    x, b = torch.from_numpy(xs).cuda(), torch.from_numpy(bs).cuda()
+    ty = {"T": tname}
+
+    def check(kr, want, name):
+        ptr, _, shape, _ = kr.output(0)
+        assert_bitwise(p.to_host(ptr, tname, shape), np.ascontiguousarray(want), name)
+        kr.free()
+
+    for op in ("AddV2", "Add"):
+        check(p.run(op, ty, [T(x), T(b)]), oracle.eltwise("add", [xs, bs], odt), op)
+    if tname == "uint8":
+        for op in ("Mul", "BiasAdd", "BiasAddV1"):  # not registered for uint8
+            with pytest.raises(KeyError):
+                p.h.kernel_index(op, **ty)
+        return
+    check(p.run("Mul", ty, [T(b), T(x)]), oracle.eltwise("mul", [bs, xs], odt), "Mul")
+    check(p.run("BiasAdd", ty, [T(x), T(b)], dict(data_format="NHWC")),
+          oracle.bias_add(xs, bs, dtype=odt), "BiasAdd")
+    check(p.run("BiasAddV1", ty, [T(x), T(b)]), oracle.bias_add(xs, bs, dtype=odt), "BiasAddV1")
 
 
 def test_elementwise_errors(plugin):

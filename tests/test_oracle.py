@@ -488,6 +488,53 @@ def test_eltwise_bf16_matches_torch_bf16_arithmetic():
                                   bits(torch.relu(xt + yt)))
 
 
+INT_EDGES = {"int32": [0, 1, -1, 2**31 - 1, -2**31, 2**30, -2**30 - 7, 46341, -46341],
+             "int64": [0, 1, -1, 2**63 - 1, -2**63, 2**62, 3037000500, -3037000500, 2**32 + 1],
+             "uint8": [0, 1, 2, 127, 128, 200, 255, 16, 17]}
+
+
+def _int_inputs(rng, dtype, shape):
+    info = np.iinfo(dtype)
+    x = rng.integers(info.min, info.max, size=shape, dtype=dtype, endpoint=True)
+    flat = x.reshape(-1)
+    e = np.array(INT_EDGES[dtype], dtype=dtype)
+    flat[:min(e.size, flat.size)] = e[:flat.size]
+    return x
+
+
+@pytest.mark.parametrize("dtype", ["int32", "int64", "uint8"])
+@pytest.mark.parametrize("xs,ys", [((64, 33), (33,)), ((64, 33), (64, 1)), ((4, 1, 5), (3, 1)),
+                                   ((9,), ()), ((9, 9), (9, 9))])
+def test_eltwise_integers_wrap_like_numpy_and_python_ints(dtype, xs, ys):
+    """Integer add / mul wrap modulo 2^bits: against numpy's integer array
+    arithmetic (which wraps silently) and against Python's unbounded
+    integers reduced modulo 2^bits into the type's range, including the
+    extremes (INT_MIN + -1, INT_MAX * 2, 255 + 1 ...)."""
+    rng = np.random.default_rng(53)
+    x, y = _int_inputs(rng, dtype, xs), _int_inputs(rng, dtype, ys)
+    bits = np.iinfo(dtype).bits
+    signed = np.iinfo(dtype).min < 0
+
+    def wrap(v):
+        v %= 1 << bits
+        return v - (1 << bits) if signed and v >= 1 << (bits - 1) else v
+
+    xb, yb = np.broadcast_arrays(x, y)
+    ops = {"add": (np.add, lambda a, b: a + b)}
+    if dtype != "uint8":
+        ops["mul"] = (np.multiply, lambda a, b: a * b)
+    for op, (npf, pyf) in ops.items():
+        got = oracle.eltwise(op, [x, y], dtype)
+        assert got.dtype == np.dtype(dtype) and got.shape == xb.shape
+        with np.errstate(over="ignore"):
+            np.testing.assert_array_equal(got, npf(x, y))
+        want = np.array([wrap(pyf(int(a), int(b))) for a, b in zip(xb.ravel(), yb.ravel())],
+                        dtype=object)
+        np.testing.assert_array_equal(got.ravel().astype(object), want)
+    with pytest.raises(ValueError):
+        oracle.eltwise("add_relu", [x, y], dtype)
+
+
 def test_bias_add_nchw_channel_dim():
     """NCHW bias runs along dim 1 (musa_biasadd_op.cc:31-52)."""
     x = np.zeros((2, 3, 2, 2), np.float32)

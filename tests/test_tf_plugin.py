@@ -161,12 +161,22 @@ def test_adam_registrations_host_memory(h):
 
 
 def test_elementwise_registrations(h):
+    """Every (op, T) pair the reference registers for these ops: AddV2 and
+    Add (musa_add_op.cc:455-468, less bool), Mul (musa_multiply_op.cc:315-323),
+    BiasAdd and BiasAddV1 (musa_biasadd_op.cc:67-79), Relu (musa_relu_op.cc:
+    45-57), BiasAddGrad (musa_biasadd_grad_op.cc:112-123); ReluGrad takes
+    double besides the reference's three; the fused ops are floating only."""
     fp = {th.DT[t] for t in ("float", "half", "bfloat16", "double")}
-    for op in ("BiasAdd", "Relu", "ReluGrad", "AddV2", "Mul", "MusaBiasAddRelu", "MusaAddV2Relu",
-               "MusaShiftedAffineMap"):
-        assert {_types(k)["T"] for k in _reg(h, op)} == fp, op
-    assert {_types(k)["T"] for k in _reg(h, "BiasAddGrad")} == fp | {th.DT["int32"],
-                                                                    th.DT["int64"]}
+    i3264 = {th.DT["int32"], th.DT["int64"]}
+    want = {"Relu": fp, "ReluGrad": fp, "MusaBiasAddRelu": fp, "MusaAddV2Relu": fp,
+            "MusaShiftedAffineMap": fp,
+            "AddV2": fp | i3264 | {th.DT["uint8"]}, "Add": fp | i3264 | {th.DT["uint8"]},
+            "Mul": fp | i3264, "BiasAdd": fp | i3264, "BiasAddV1": fp | i3264,
+            "BiasAddGrad": fp | i3264}
+    for op, types in want.items():
+        regs = _reg(h, op)
+        assert len(regs) == len(types), op  # one registration per type
+        assert {_types(k)["T"] for k in regs} == types, op
 
 
 def test_op_definitions(h):

@@ -48,6 +48,30 @@ def test_no_alloc_matches_workspace_entry_point(dev, dtype, shapes, fmt):
         assert_bitwise(_bits(got), _bits(want), f"{shape} {dtype} {fmt}")
 
 
+def test_no_alloc_calls_on_two_streams_are_ordered(dev):
+    """Allocation-free calls issued alternately on two streams with no
+    synchronization between them share the static scratch: the library
+    chains each call to the previous call's end on the other stream, so
+    every result equals TFMA_BiasAddGrad's bit for bit (a large reduction
+    then a small one, so an unordered small call would read or overwrite the
+    large one's partials mid-flight)."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(23)
+    shapes = [(8192, 4096), (64, 96), (4096, 2048), (257, 33)] * 3
+    xs = [torch.randn(s, generator=gen, device=dev).half() for s in shapes]
+    wants = [ops.BiasAddGrad(x) for x in xs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [torch.full((s[-1],), 7, dtype=torch.half, device=dev) for s in shapes]
+    torch.cuda.synchronize()
+    for i, (x, o) in enumerate(zip(xs, outs)):
+        with torch.cuda.stream(streams[i % 2]):
+            ops.bias_add_grad_no_alloc(x, o)
+    torch.cuda.synchronize()
+    for i, (o, w) in enumerate(zip(outs, wants)):
+        assert_bitwise(_bits(o), _bits(w), f"call {i} {shapes[i]}")
+
+
 def test_no_alloc_refuses_inputs_beyond_the_scratch(dev):
     """1.5M float channels need 6 MB of partials: more than the 4 MiB static
     scratch, so the call is refused before any launch."""
