@@ -43,6 +43,14 @@ components: cfg1 (FusedBatchNormV3 forward, f32 [32,56,56,64]), BN on the
         flushed rate above the measured stream-copy ceiling.
         traffic_ratio = counter-measured HBM bytes per rep (committed
         profiles/pmc_traffic_components.txt) / algorithmic bytes.
+--bn-stamps LIB: with LIB a measurement build of the library
+        (make -C tensorflow_musa_extension_amd/csrc EXTRA=-DTFMA_BN_STAMPS
+        OBJDIR=../../_build/stamps OUT=../../_build/stamps/libtfma.so
+        ../../_build/stamps/libtfma.so), runs the fused BatchNorm kernel at
+        cfg1 and the cfg2 shapes (f16; forward, and the grads that run
+        unsliced) after a cache flush and prints, per op, when its waves reach
+        each phase (mean / slowest wave, microseconds from the first wave's
+        start, median of 5 runs); no JSON line.
 --profile-components: each component once, then 3 times after a cache
         flush, printing a PROFILE_MANIFEST line that attributes a rocprofv3
         --pmc run's dispatches to components (no JSON line).
@@ -110,6 +118,9 @@ def parse():
     p.add_argument("--trace-steps", type=int, default=4,
                    help="timed steps (the last ones) whose launches of --trace carry timing "
                         "events; each such launch costs ~5 us of idle GPU between kernels")
+    p.add_argument("--bn-stamps", metavar="LIB", default=None,
+                   help="phase timestamps of the fused BatchNorm kernel from a library built "
+                        "with EXTRA=-DTFMA_BN_STAMPS (prints a table, no JSON)")
     p.add_argument("--profile-components", action="store_true",
                    help="run each component 1 + 3 times (cache flushed before each) and print "
                         "a PROFILE_MANIFEST line for attributing rocprofv3 counters; no JSON")
@@ -696,6 +707,70 @@ def calibrate(torch, dev):
     del src, dst
 
 
+STAMP_POINTS = ["entry", "phase1", "published", "finals", "coefs", "phase3", "tail"]
+
+
+def bn_stamps(torch, tfma, dev, reps=5):
+    """Per-phase timing of the fused BatchNorm kernel (--bn-stamps): for each
+    op, every wave's stamps relative to the launch's first wave; mean and
+    slowest wave per point, median over `reps` flushed runs."""
+    import ctypes
+
+    import numpy as np
+    from tensorflow_musa_extension_amd import _lib
+    ops = tfma.raw_ops
+    lib = _lib.load()
+    flush = torch.ones(1 << 28, device=dev)
+    buf = (ctypes.c_uint64 * (1024 * 64))()
+
+    def read(blocks):
+        st = _lib.TFMA_Status()
+        lib.TFMA_FusedBatchNormStamps(buf, len(buf), ctypes.byref(st))
+        if st.code:
+            raise RuntimeError(st.message.decode())
+        a = np.frombuffer(buf, dtype=np.uint64)[:blocks * 64].reshape(blocks, 8, 8)
+        a = a.astype(np.int64)
+        t0 = a[:, :, 0].min()
+        return [((a[:, :, i] - t0).mean() / 100.0, (a[:, :, i] - t0).max() / 100.0)
+                for i in range(len(STAMP_POINTS))]
+
+    cases = [((32, 56, 56, 64), torch.float32, 1e-3, "cfg1")] + [
+        (s, torch.float16, EPS, "cfg2") for s in SHAPES]
+    print("op | " + " | ".join(STAMP_POINTS) + "   (us, mean / slowest wave)", flush=True)
+    for shape, dt, eps, cfg in cases:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(0)
+        c = shape[-1]
+        x = torch.randn(shape, generator=gen, device=dev).to(dt)
+        dy = torch.randn(shape, generator=gen, device=dev).to(dt)
+        sc = torch.rand(c, generator=gen, device=dev) + 0.5
+        of = 0.1 * torch.randn(c, generator=gen, device=dev)
+        e = torch.empty(0, device=dev)
+        f = ops.FusedBatchNormV3(x, sc, of, e, e, epsilon=eps)
+        for which in ("fwd", "grad"):
+            runs, plan = [], None
+            for _ in range(reps):
+                torch.cuda.synchronize()
+                flush.sum()
+                if which == "fwd":
+                    ops.FusedBatchNormV3(x, sc, of, e, e, epsilon=eps)
+                else:
+                    ops.FusedBatchNormGradV3(dy, x, sc, f.reserve_space_1, f.reserve_space_2,
+                                             f.reserve_space_3, epsilon=eps)
+                plan = ops.fused_batch_norm_last_plan()
+                runs.append(read(min(plan["workgroups"], 1024)))
+            name = (f"{cfg} {which} {'x'.join(map(str, shape))} {str(dt).split('.')[-1]} "
+                    f"(workgroups {plan['workgroups']}, slices {plan['slices']}, "
+                    f"dynamic rows {plan['dynamic_rows']})")
+            if plan["slices"] > 1:
+                print(f"{name} | sliced: the hand-off-hiding kernel records no stamps",
+                      flush=True)
+                continue
+            med = [(float(np.median([r[i][0] for r in runs])),
+                    float(np.median([r[i][1] for r in runs]))) for i in range(len(STAMP_POINTS))]
+            print(name + " | " + " | ".join(f"{m:.1f} / {x_:.1f}" for m, x_ in med), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -704,12 +779,18 @@ def main():
         sys.exit(2)
     import torch
     sys.path.insert(0, ROOT)
+    if args.bn_stamps:
+        import tensorflow_musa_extension_amd._lib as _lib_mod
+        _lib_mod.LIB_PATH = os.path.abspath(args.bn_stamps)
     import tensorflow_musa_extension_amd as tfma
     ops = tfma.raw_ops
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.bn_stamps:
+        bn_stamps(torch, tfma, dev)
+        return
     if args.profile_components:
         if args.calibrate:
             calibrate(torch, dev)

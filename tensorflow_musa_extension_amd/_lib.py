@@ -112,6 +112,7 @@ SIGNATURES = {
     "TFMA_HostCallback": [_vp, _vp, _vp, _S],
     "TFMA_StagingPoolStats": [ctypes.POINTER(ctypes.c_uint64)] * 4 + [_S],
     "TFMA_SetTuningOverride": [_cs, ctypes.c_int32, _S],
+    "TFMA_FusedBatchNormStamps": [ctypes.POINTER(ctypes.c_uint64), ctypes.c_uint64, _S],
 }
 _RESTYPES = {"TFMA_Version": ctypes.c_char_p, "TFMA_LastKernelName": ctypes.c_char_p,
              "TFMA_FreeBuffer": None}

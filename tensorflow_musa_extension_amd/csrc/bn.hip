@@ -771,7 +771,7 @@ template <class Tr> struct Resident {
   static constexpr bool kOpaqueFwd = false, kOpaqueGrad = true;
   static constexpr int kRegFwd = 29, kRegGrad = 13, kLdsFwd = 18, kLdsGrad = 9;
   static constexpr int kRegGradSliced = 11;
-  static constexpr int kRegGradOverlap = 14;
+  static constexpr int kRegGradOverlap = 17;
   static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 0, kPbFwd = 0, kPaGrad = 0, kPbGrad = 0;
 };
@@ -779,7 +779,7 @@ template <> struct Resident<TF16> {
   static constexpr bool kOpaqueFwd = true, kOpaqueGrad = true;
   static constexpr int kRegFwd = 32, kRegGrad = 13, kLdsFwd = 18, kLdsGrad = 9;
   static constexpr int kRegGradSliced = 12;
-  static constexpr int kRegGradOverlap = 12;
+  static constexpr int kRegGradOverlap = 15;
   static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 0, kPbFwd = 0, kPaGrad = 0, kPbGrad = 0;
 };
@@ -787,7 +787,7 @@ template <> struct Resident<TBF16> {
   static constexpr bool kOpaqueFwd = false, kOpaqueGrad = true;
   static constexpr int kRegFwd = 32, kRegGrad = 11, kLdsFwd = 18, kLdsGrad = 9;
   static constexpr int kRegGradSliced = 9;
-  static constexpr int kRegGradOverlap = 11;
+  static constexpr int kRegGradOverlap = 14;
   static constexpr int kRegFwdSmall = 8;
   static constexpr int kPaFwd = 0, kPbFwd = 0, kPaGrad = 0, kPbGrad = 0;
 };
@@ -831,6 +831,27 @@ struct FusedArgs {
   unsigned* epoch_dev;
   FinArgs fin;
 };
+
+// Per-wave phase timestamps of the fused NHWC kernel, compiled in only with
+// -DTFMA_BN_STAMPS (a measurement build: make EXTRA=-DTFMA_BN_STAMPS).  Lane
+// 0 of each wave stores s_memrealtime (a 100 MHz clock) at kStampCount
+// points into bn_stamps[(blockIdx.x * 8 + wave) * kStampCount + point]; the
+// host reads them with TFMA_FusedBatchNormStamps.  Points: 0 entry, 1 phase
+// 1 summed, 2 partials published, 3 finals done, 4 coefficients in, 5 static
+// phase-3 rows written, 6 dynamic tail done.  A sliced launch keeps its last
+// slice's stamps.
+#ifdef TFMA_BN_STAMPS
+constexpr int kStampCount = 8;
+constexpr int kStampBlocks = 1024;
+__device__ unsigned long long bn_stamps[kStampBlocks * 8 * kStampCount];
+__device__ inline void stamp(int point) {
+  if ((threadIdx.x & 63) == 0 && blockIdx.x < kStampBlocks)
+    bn_stamps[(blockIdx.x * 8 + (threadIdx.x >> 6)) * kStampCount + point] =
+        __builtin_amdgcn_s_memrealtime();
+}
+#else
+__device__ inline void stamp(int) {}
+#endif
 
 __device__ inline double2 wave_sum(double a, double b) {
 #pragma unroll
@@ -1159,6 +1180,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   const int nslices = kSliced ? a.slices : 1;
   const int width = (1 << a.tx_shift) * VEC;  // channels of a tile
 
+  stamp(0);
   // This launch's epoch, in the upper half of the tag word (recorded
   // launches: 2^31 + 1 + (device word mod 2^31 - 1)).
   const unsigned epoch =
@@ -1315,7 +1337,9 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     for (int u = 0; u < U; ++u)
       if (q + u < nk) accum_words<Tr, kGrad>(xw[u], dw[u], k, s1, s2);
   }
+  stamp(1);
   publish_partials<VEC>(a, red, s1, s2, tid, width, ct, g, etag);
+  stamp(2);
 
   // Phase-3 prefetch, part A: the last streamed rows (phase 3 runs
   // last-to-first), loaded by the waves that have no phase-2 channel so the
@@ -1338,6 +1362,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   // ---- phase 2: per-channel finals ---------------------------------------
   finish_channels<Tr, kGrad>(a, cs0, cs1, wave, lane, wtag, etag, epoch);
   if (sl == 0) zero_side_outputs<kGrad>(a.fin);
+  stamp(3);
 
   // Prefetch part B: the next rows, in flight while the tile's coefficients
   // are polled.
@@ -1360,6 +1385,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   }
   float4 cf[VEC];
   tile_coefs<Tr>(a, red, tid, tx, ct, width, active, wtag, epoch, cf);
+  stamp(4);
   // Prefetched rows first, then the remaining streamed rows last-to-first.
   if (pre_a) {
 #pragma unroll
@@ -1413,6 +1439,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
 #pragma unroll
   for (int r = 0; r < KR; ++r)
     if (r < nk) st16(po + base + r * rstride, apply_words<Tr, kGrad>(xr[r], dr[kGrad ? r : 0], cf));
+  stamp(5);
 
   // Dynamic tail: chunk j of group g' covers the owner rows q in
   // [KR+KL + j*B, KR+KL + (j+1)*B) below the owner's static rows.  Wave w of
@@ -1479,6 +1506,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       }
     }
   }
+  stamp(6);
 
   }  // slices
   const int wave = threadIdx.x >> 6;
@@ -1559,7 +1587,11 @@ __global__ __launch_bounds__(kFusedThreads) void bn_sliced_grad_kernel(FusedArgs
   using S = typename Tr::S;
   constexpr int VEC = Tr::kVec;
   constexpr int U = 4;   // streamed vectors per tensor in flight, phase 1
-  constexpr int U3 = 6;  // and phase 3
+  // Phase 3: 4 rows in flight, which leaves the registers for 3 more
+  // resident rows per thread than 6 in flight (f16 15 against 12, bf16 14
+  // against 11, f32 17 against 14; cfg2 16-op step 1.778 -> 1.770 ms, the
+  // 28x28 bf16 grad 159 -> 155 us).
+  constexpr int U3 = 4;
   extern __shared__ uint4 lds_rows[];  // [KL][2][kFusedThreads]
   __shared__ float2 red[(kFusedThreads / 64) * 32 * VEC];
   const int nslices = a.slices;
@@ -2681,6 +2713,19 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
 }
 
 }  // namespace
+
+hipError_t BnStamps(void* host, size_t bytes) {
+#ifdef TFMA_BN_STAMPS
+  if (bytes > sizeof(bn_stamps)) bytes = sizeof(bn_stamps);
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return e;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(bn_stamps), bytes, 0, hipMemcpyDeviceToHost);
+#else
+  (void)host;
+  (void)bytes;
+  return hipErrorNotSupported;
+#endif
+}
 
 hipError_t BnBarrierTimedOut(bool reset, bool* timed_out) {
   *timed_out = false;

@@ -733,6 +733,16 @@ int TFMA_StreamCopy(void* stream, void* dst, const void* src, uint64_t bytes,
                     "StreamCopy");
 }
 
+int TFMA_FusedBatchNormStamps(uint64_t* stamps, uint64_t count, TFMA_Status* status) {
+  if (!stamps && count)
+    return set_status(status, TFMA_INVALID_ARGUMENT, "FusedBatchNormStamps: null buffer");
+  const hipError_t e = BnStamps(stamps, count * sizeof(uint64_t));
+  if (e == hipErrorNotSupported)
+    return set_status(status, TFMA_UNIMPLEMENTED,
+                      "FusedBatchNormStamps: the library was built without TFMA_BN_STAMPS");
+  return hip_status(status, e, "FusedBatchNormStamps");
+}
+
 int TFMA_SetTuningOverride(const char* name, int32_t value, TFMA_Status* status) {
   if (!name || !SetTune(name, value))
     return set_status(status, TFMA_INVALID_ARGUMENT, "SetTuningOverride: unknown name %s",

@@ -252,5 +252,8 @@ hipError_t BnBarrierTimedOut(bool reset, bool* timed_out);
 bool BnPendingGiveUp(unsigned* epoch);
 // Plan of the calling thread's last FusedBatchNorm launch.
 TFMA_FusedBatchNormPlan BnLastPlan();
+// Copies the fused kernel's phase stamps to host memory after a device
+// synchronize (hipErrorNotSupported unless built with -DTFMA_BN_STAMPS).
+hipError_t BnStamps(void* host, size_t bytes);
 
 }  // namespace tfma
