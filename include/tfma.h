@@ -470,13 +470,13 @@ int TFMA_SetTuningOverride(const char* name, int32_t value, TFMA_Status* status)
 /* Phase timestamps of the fused NHWC BatchNorm kernel, for measurement
  * builds only (no reference counterpart): with the library built with
  * -DTFMA_BN_STAMPS, lane 0 of every wave of the last fused launches records
- * a 100 MHz clock (s_memrealtime) at 8 points; this call synchronizes the
- * device and copies `count` values, laid out [workgroup][wave 0..7][point
- * 0..7] for workgroups below 1024.  Points: 0 entry, 1 phase-1 sums done,
+ * a 100 MHz clock (s_memrealtime) at 7 points; this call synchronizes the
+ * device and copies `count` values, laid out [workgroup][wave 0..7][slot
+ * 0..7] for workgroups below 1024.  Slots: 0 entry, 1 phase-1 sums done,
  * 2 partials published, 3 finals done, 4 coefficients in, 5 static phase-3
- * rows written, 6 dynamic tail done (7 unused).  A workgroup's values are
- * those of the last launch that ran it (a sliced launch: its last slice).
- * UNIMPLEMENTED in a normal build. */
+ * rows written, 6 dynamic tail done, 7 the XCD the wave ran on.  A
+ * workgroup's values are those of the last launch that ran it (a sliced
+ * launch: its last slice).  UNIMPLEMENTED in a normal build. */
 int TFMA_FusedBatchNormStamps(uint64_t* stamps, uint64_t count, TFMA_Status* status);
 
 /* ---------------------------------------------------------------------------

@@ -838,16 +838,19 @@ struct FusedArgs {
 // points into bn_stamps[(blockIdx.x * 8 + wave) * kStampCount + point]; the
 // host reads them with TFMA_FusedBatchNormStamps.  Points: 0 entry, 1 phase
 // 1 summed, 2 partials published, 3 finals done, 4 coefficients in, 5 static
-// phase-3 rows written, 6 dynamic tail done.  A sliced launch keeps its last
-// slice's stamps.
+// phase-3 rows written, 6 dynamic tail done; slot 7 holds the wave's XCD.  A
+// sliced launch keeps its last slice's stamps.
 #ifdef TFMA_BN_STAMPS
 constexpr int kStampCount = 8;
 constexpr int kStampBlocks = 1024;
 __device__ unsigned long long bn_stamps[kStampBlocks * 8 * kStampCount];
 __device__ inline void stamp(int point) {
-  if ((threadIdx.x & 63) == 0 && blockIdx.x < kStampBlocks)
-    bn_stamps[(blockIdx.x * 8 + (threadIdx.x >> 6)) * kStampCount + point] =
-        __builtin_amdgcn_s_memrealtime();
+  if ((threadIdx.x & 63) == 0 && blockIdx.x < kStampBlocks) {
+    unsigned long long* p = bn_stamps + (blockIdx.x * 8 + (threadIdx.x >> 6)) * kStampCount;
+    p[point] = __builtin_amdgcn_s_memrealtime();
+    // Point 7: the XCD the wave runs on (HW_REG_XCC_ID bits 3:0).
+    if (point == 0) p[7] = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 15;
+  }
 }
 #else
 __device__ inline void stamp(int) {}
