@@ -265,9 +265,15 @@ int TFMA_ReluGrad(void* stream, const TFMA_Tensor* gradients, const TFMA_Tensor*
  * registered :112-123) for T in {FLOAT, HALF, BFLOAT16, DOUBLE, INT32,
  * INT64}: rank 1 is returned as is (:50-58), an empty reduction gives zeros
  * (:64-69).  Half and bfloat16 accumulate in float (as TF's CPU kernel);
- * integers wrap.  The sum runs in a fixed order (deterministic) in two
- * kernels; `workspace` holds the per-group partials
- * (TFMA_BiasAddGradWorkspaceBytes). */
+ * integers wrap.  The sum runs in a fixed order (deterministic): per-group
+ * partials, then per-channel finals over them in group order.  Eager float,
+ * half and bfloat16 calls run both in one launch whose last workgroups take
+ * the finals, with the partials in library-owned device memory (4 MiB per
+ * device, allocated and zeroed on the device's first such call; calls on one
+ * device are chained across streams); the other dtypes, launches under
+ * stream capture and inputs with more partials than that memory holds run
+ * two kernels with the partials in `workspace`
+ * (TFMA_BiasAddGradWorkspaceBytes).  Both forms give the same bits. */
 int TFMA_BiasAddGradWorkspaceBytes(const TFMA_Tensor* out_backprop, const char* data_format,
                                    size_t* bytes, TFMA_Status* status);
 int TFMA_BiasAddGrad(void* stream, const TFMA_Tensor* out_backprop, const char* data_format,
@@ -450,6 +456,8 @@ const char* TFMA_LastKernelName(void);
  *                       instead of hiding each slice's hand-off.
  *   "bn_nchw_owned"     0: NCHW training keeps the split kernels instead of
  *                       one workgroup per channel.
+ *   "bag_fused"         0: BiasAddGrad runs as two kernels (partials, then
+ *                       per-channel finals) instead of one launch.
  * Each starts from the environment variable TFMA_<NAME in upper case>,
  * read once, at the library's first query of any override; after that the
  * launch paths read one atomic value (no getenv on the hot path).  An

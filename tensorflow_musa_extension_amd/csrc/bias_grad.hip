@@ -16,6 +16,7 @@
 // Every sum runs in a fixed order, so results are deterministic.  Memory:
 // one read of x (s*E bytes), partials of G*C accumulators.
 #include <mutex>
+#include <type_traits>
 
 #include "device_util.h"
 #include "tfma_internal.h"
@@ -49,14 +50,61 @@ struct Narrow {  // half / bfloat16, accumulated in float
 using BagF16 = Narrow<TF16>;
 using BagBF16 = Narrow<TBF16>;
 
-template <class B, int VEC>
+// The one-launch form (kTag): a 1-D grid of ct * groups reducing workgroups
+// (workgroup b: tile b % ct, group b / ct) followed by the finalizing ones;
+// partials are stored as epoch-tagged words (TagArgs).  Otherwise a 2-D grid
+// (tile, group) writing plain partials for bag_finalize_kernel.
+struct TagArgs {
+  unsigned long long* slots;  // [groups][c] {partial bits, epoch}
+  unsigned epoch;
+  int ct;                     // tiles (rows) or channels (planes) per group
+  int64_t groups;
+  unsigned spin_limit;
+};
+
+// Tagged partial words: {value bits (low 32), epoch (high 32)}, written and
+// read with relaxed agent-scope atomics (coherent across the XCDs' L2s; one
+// single-copy-atomic word, so a word validates itself).  Float accumulators
+// only (f32, f16, bf16).
+__device__ inline uint32_t acc_bits(float v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ inline float acc_from(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ inline void store_tagged(const TagArgs& tg, int64_t slot, float v) {
+  __hip_atomic_store(tg.slots + slot,
+                     (static_cast<unsigned long long>(tg.epoch) << 32) | acc_bits(v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <class B, int VEC, bool kTag = false>
 __global__ __launch_bounds__(kThreads) void bag_rows_kernel(
     const typename B::S* __restrict__ x, int64_t rows, int c, int64_t cv, int tx_shift,
-    int64_t rows_per_g, typename B::A* __restrict__ partial) {
+    int64_t rows_per_g, typename B::A* __restrict__ partial, TagArgs tg,
+    typename B::S* __restrict__ out);
+
+template <class B, bool kTag>
+__device__ void bag_finalize_block(const typename B::A* __restrict__ partial, int64_t groups,
+                                   int c, int fb, typename B::S* __restrict__ out,
+                                   const TagArgs& tg);
+
+template <class B, int VEC, bool kTag>
+__global__ __launch_bounds__(kThreads) void bag_rows_kernel(
+    const typename B::S* __restrict__ x, int64_t rows, int c, int64_t cv, int tx_shift,
+    int64_t rows_per_g, typename B::A* __restrict__ partial, TagArgs tg,
+    typename B::S* __restrict__ out) {
   using S = typename B::S;
   using A = typename B::A;
   extern __shared__ unsigned char bag_lds[];
   A* red = reinterpret_cast<A*>(bag_lds);  // [ry][tx * VEC]
+  int64_t bx = blockIdx.x, by = blockIdx.y;
+  if constexpr (kTag) {
+    const int64_t b = blockIdx.x;
+    if (b >= tg.ct * tg.groups) {
+      bag_finalize_block<B, true>(nullptr, tg.groups, c, static_cast<int>(b - tg.ct * tg.groups),
+                                  out, tg);
+      return;
+    }
+    bx = b % tg.ct;
+    by = b / tg.ct;
+  }
   const int tx = threadIdx.x & ((1 << tx_shift) - 1);
   const int ty = threadIdx.x >> tx_shift;
   const int ry = kThreads >> tx_shift;
@@ -64,8 +112,8 @@ __global__ __launch_bounds__(kThreads) void bag_rows_kernel(
   // Channel tiles vary fastest across workgroups, so the workgroups running
   // together read adjacent segments of the same rows instead of one column
   // of many rows (which concentrates on few memory channels).
-  const int64_t cvi = static_cast<int64_t>(blockIdx.x) * (1 << tx_shift) + tx;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * rows_per_g;
+  const int64_t cvi = bx * (1 << tx_shift) + tx;
+  const int64_t r0 = by * rows_per_g;
   int64_t r1 = r0 + rows_per_g;
   if (r1 > rows) r1 = rows;
   A acc[VEC];
@@ -93,26 +141,41 @@ __global__ __launch_bounds__(kThreads) void bag_rows_kernel(
 #pragma unroll
   for (int j = 0; j < VEC; ++j) red[ty * width + tx * VEC + j] = acc[j];
   __syncthreads();
-  const int64_t ch = static_cast<int64_t>(blockIdx.x) * width + threadIdx.x;
+  const int64_t ch = bx * width + threadIdx.x;
   if (static_cast<int>(threadIdx.x) < width && ch < c) {
     A s = A(0);
     for (int k = 0; k < ry; ++k) s += red[k * width + threadIdx.x];
-    partial[static_cast<int64_t>(blockIdx.y) * c + ch] = s;
+    if constexpr (kTag)
+      store_tagged(tg, by * c + ch, s);
+    else
+      partial[by * c + ch] = s;
   }
 }
 
 // VEC > 1 when every plane is a whole number of aligned 16-byte vectors
 // (inner % VEC == 0 and x aligned): `inner` and the flat index then count
 // vectors.
-template <class B, int VEC>
+template <class B, int VEC, bool kTag = false>
 __global__ __launch_bounds__(kThreads) void bag_planes_kernel(
     const typename B::S* __restrict__ x, int64_t outer, int c, int64_t inner,
-    int64_t outer_per_g, FastDiv div_inner, typename B::A* __restrict__ partial) {
+    int64_t outer_per_g, FastDiv div_inner, typename B::A* __restrict__ partial,
+    TagArgs tg, typename B::S* __restrict__ out) {
   using S = typename B::S;
   using A = typename B::A;
   __shared__ A red[kThreads / 64];
-  const int ch = blockIdx.x;
-  const int64_t o0 = static_cast<int64_t>(blockIdx.y) * outer_per_g;
+  int64_t bx = blockIdx.x, by = blockIdx.y;
+  if constexpr (kTag) {
+    const int64_t b = blockIdx.x;
+    if (b >= tg.ct * tg.groups) {
+      bag_finalize_block<B, true>(nullptr, tg.groups, c, static_cast<int>(b - tg.ct * tg.groups),
+                                  out, tg);
+      return;
+    }
+    bx = b % tg.ct;
+    by = b / tg.ct;
+  }
+  const int ch = static_cast<int>(bx);
+  const int64_t o0 = by * outer_per_g;
   int64_t o1 = o0 + outer_per_g;
   if (o1 > outer) o1 = outer;
   const int64_t count = (o1 - o0) * inner;  // < 2^31 (checked by the host)
@@ -147,47 +210,103 @@ __global__ __launch_bounds__(kThreads) void bag_planes_kernel(
   if (threadIdx.x == 0) {
     A s = A(0);
     for (int w = 0; w < kThreads / 64; ++w) s += red[w];
-    partial[static_cast<int64_t>(blockIdx.y) * c + ch] = s;
+    if constexpr (kTag)
+      store_tagged(tg, by * c + ch, s);
+    else
+      partial[by * c + ch] = s;
   }
 }
 
-// Workgroup b finishes channels [64 b, 64 b + 64): lane l of wave w sums
-// channel 64 b + l over groups w, w + 4, w + 8, ... in order (kFinLoads
-// loads in flight, each wave reading 64 consecutive partials of a group),
-// then wave 0 adds the four waves' sums in order.  (One wave per channel,
-// its lanes reading one partial each C elements apart, took 4.1 us for
-// 64 groups x 4096 channels.)
+// kFinLoads partial loads in flight per lane, each wave reading 64
+// consecutive partials of a group.  (One wave per channel, its lanes reading
+// one partial each C elements apart, took 4.1 us for 64 groups x 4096
+// channels.)
 constexpr int kFinLoads = 16;
+
+// Workgroup fb finishes channels [64 fb, 64 fb + 64): lane l of wave w sums
+// channel 64 fb + l over groups w, w + 4, w + 8, ... in order, then wave 0
+// adds the four waves' sums in order - the same additions in the same order
+// in both forms, so both give the same bits.  kTag: the partials are the
+// epoch-tagged words, polled until every one carries this launch's epoch
+// (the reducing workgroups precede this one in dispatch order and wait for
+// nothing, so they all run; the spin is bounded all the same, and a partial
+// that never arrives is taken as NaN).
+template <class B, bool kTag>
+__device__ void bag_finalize_block(const typename B::A* __restrict__ partial, int64_t groups,
+                                   int c, int fb, typename B::S* __restrict__ out,
+                                   const TagArgs& tg) {
+  using A = typename B::A;
+  constexpr int kWaves = kThreads / 64;
+  __shared__ A fred[kWaves][64];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t ch = static_cast<int64_t>(fb) * 64 + lane;
+  const bool active = ch < c;
+  const int64_t c0 = active ? ch : 0;
+  A s = A(0);
+  int64_t g = w;
+  if constexpr (kTag) {
+    const unsigned long long want = static_cast<unsigned long long>(tg.epoch);
+    for (; g < groups; g += kFinLoads * kWaves) {
+      unsigned long long v[kFinLoads];
+#pragma unroll
+      for (int u = 0; u < kFinLoads; ++u) {
+        const int64_t gg = g + u * kWaves;
+        v[u] = gg < groups ? __hip_atomic_load(tg.slots + gg * c + c0, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT)
+                           : (want << 32);
+      }
+      unsigned spins = 0;
+      while (true) {
+        bool ready = true;
+#pragma unroll
+        for (int u = 0; u < kFinLoads; ++u) ready = ready && (v[u] >> 32) == want;
+        if (ready) break;
+        if (++spins > tg.spin_limit) {
+#pragma unroll
+          for (int u = 0; u < kFinLoads; ++u)
+            if ((v[u] >> 32) != want) v[u] = (want << 32) | 0x7fc00000u;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int u = 0; u < kFinLoads; ++u) {
+          const int64_t gg = g + u * kWaves;
+          if ((v[u] >> 32) != want)
+            v[u] = __hip_atomic_load(tg.slots + gg * c + c0, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kFinLoads; ++u)
+        if (g + u * kWaves < groups) s += acc_from(static_cast<uint32_t>(v[u]));
+    }
+  } else {
+    const A* __restrict__ p = partial + c0;
+    for (; g + (kFinLoads - 1) * kWaves < groups; g += kFinLoads * kWaves) {
+      A v[kFinLoads];
+#pragma unroll
+      for (int u = 0; u < kFinLoads; ++u) v[u] = p[(g + u * kWaves) * c];
+#pragma unroll
+      for (int u = 0; u < kFinLoads; ++u) s += v[u];
+    }
+    for (; g < groups; g += kWaves) s += p[g * c];
+  }
+  fred[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && active) {
+    A t = fred[0][lane];
+#pragma unroll
+    for (int k = 1; k < kWaves; ++k) t += fred[k][lane];
+    out[ch] = B::out(t);
+  }
+}
+
 template <class B>
 __global__ __launch_bounds__(kThreads) void bag_finalize_kernel(
     const typename B::A* __restrict__ partial, int64_t groups, int c,
     typename B::S* __restrict__ out) {
-  using A = typename B::A;
-  constexpr int kWaves = kThreads / 64;
-  __shared__ A red[kWaves][64];
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int64_t ch = static_cast<int64_t>(blockIdx.x) * 64 + lane;
-  const bool active = ch < c;
-  const A* __restrict__ p = partial + (active ? ch : 0);
-  A s = A(0);
-  int64_t g = w;
-  for (; g + (kFinLoads - 1) * kWaves < groups; g += kFinLoads * kWaves) {
-    A v[kFinLoads];
-#pragma unroll
-    for (int u = 0; u < kFinLoads; ++u) v[u] = p[(g + u * kWaves) * c];
-#pragma unroll
-    for (int u = 0; u < kFinLoads; ++u) s += v[u];
-  }
-  for (; g < groups; g += kWaves) s += p[g * c];
-  red[w][lane] = s;
-  __syncthreads();
-  if (w == 0 && active) {
-    A t = red[0][lane];
-#pragma unroll
-    for (int k = 1; k < kWaves; ++k) t += red[k][lane];
-    out[ch] = B::out(t);
-  }
+  bag_finalize_block<B, false>(partial, groups, c, blockIdx.x, out, TagArgs{});
 }
 
 __global__ __launch_bounds__(kThreads) void zero_bytes_kernel(uint8_t* __restrict__ p, int64_t n) {
@@ -206,7 +325,13 @@ struct BagPlan {
   int64_t groups;
 };
 
+// Reducing workgroups aimed for: 1024, and 256 for the rows form with 2-byte
+// elements - longer-lived workgroups and a quarter of the partials.
+// Measured in one launch at [8192,4096] (kernel time, % of 8 TB/s): f16 53.5
+// -> 56.8 % with 256 (1024: 53.5, 512: 55.6); f32 unchanged within noise
+// (256: 63.7, 512: 66.1, 1024: 65.5-66.5, 2048: 65.7-67.3).
 constexpr int64_t kTargetBlocks = 1024;
+constexpr int64_t kTargetBlocksRows16 = 256;
 
 BagPlan make_bag_plan(int64_t outer, int64_t c, int64_t inner, int esize, bool aligned) {
   BagPlan p{};
@@ -220,7 +345,7 @@ BagPlan make_bag_plan(int64_t outer, int64_t c, int64_t inner, int esize, bool a
     p.tx_shift = s;
     const int ry = kThreads >> s;
     p.ct = static_cast<int>((p.cv + (1 << s) - 1) >> s);
-    int64_t gt = kTargetBlocks / p.ct;
+    int64_t gt = (esize == 2 ? kTargetBlocksRows16 : kTargetBlocks) / p.ct;
     if (gt < 1) gt = 1;
     int64_t rpg = (outer + gt - 1) / gt;
     const int64_t min_rows = static_cast<int64_t>(ry) * kUnroll;
@@ -246,6 +371,135 @@ BagPlan make_bag_plan(int64_t outer, int64_t c, int64_t inner, int esize, bool a
   return p;
 }
 
+// ---- one launch: tagged partials and trailing finalizing workgroups ------
+// Per device: the tagged partial slots (library-owned, zeroed once), the
+// last epoch, and the end event and stream of the last launch.  Launches on
+// one device are chained (one on another stream than the previous waits for
+// its end), so two launches never share the slots at once; eager epochs stay
+// below 2^31 and the slots are zeroed again at the wrap.
+constexpr size_t kTagSlots = size_t(1) << 19;  // 4 MiB of tagged partials
+constexpr unsigned kTagSpinLimit = 1u << 20;
+struct TagState {
+  std::mutex mu;
+  unsigned long long* slots = nullptr;
+  unsigned epoch = 0;
+  hipEvent_t own = nullptr;    // the launch's end event when not traced
+  hipEvent_t chain = nullptr;  // end of the last launch (`own` or a trace event)
+  hipStream_t last_stream = nullptr;
+  bool used = false;
+};
+
+TagState* tag_state() {
+  static TagState states[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  return &states[dev];
+}
+
+// Whether the one-launch form applies: float accumulators (f32, f16, bf16),
+// an eager launch (under stream capture the graph would keep this launch's
+// epoch), partials that fit the slots, and not switched off (override
+// "bag_fused" 0).
+template <class B>
+bool tag_applies(const BagPlan& p, int64_t c, hipStream_t stream) {
+  if constexpr (!std::is_same<typename B::A, float>::value) {
+    return false;
+  } else {
+    if (TuneValue(kTuneBagFused) == 0) return false;
+    if (static_cast<size_t>(p.groups) * static_cast<size_t>(c) > kTagSlots) return false;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return false;
+    return cap == hipStreamCaptureStatusNone;
+  }
+}
+
+// One launch: ct * groups (rows) or c * groups (planes) reducing workgroups,
+// then ceil(c / 64) finalizing ones; same plan, partials and summation order
+// as the two-kernel form, so the same bits.  The finalizers come last in the
+// 1-D grid, so they are dispatched after every reducing workgroup.
+template <class B>
+hipError_t launch_bag_tagged(const BagPlan& p, const void* x, int64_t outer, int64_t c,
+                             int64_t inner, void* out, hipStream_t stream) {
+  using S = typename B::S;
+  TagState* ts = tag_state();
+  if (!ts) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(ts->mu);
+  hipError_t e;
+  if (!ts->slots) {
+    void* q = nullptr;
+    e = hipMalloc(&q, kTagSlots * sizeof(unsigned long long));
+    if (e != hipSuccess) return e;
+    e = hipMemset(q, 0, kTagSlots * sizeof(unsigned long long));
+    if (e != hipSuccess) {
+      (void)hipFree(q);
+      return e;
+    }
+    e = hipEventCreateWithFlags(&ts->own, hipEventDisableTiming | hipEventReleaseToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(q);
+      return e;
+    }
+    ts->slots = static_cast<unsigned long long*>(q);
+  }
+  if (ts->used && ts->last_stream != stream) {
+    e = hipStreamWaitEvent(stream, ts->chain, 0);
+    if (e != hipSuccess) return e;
+  }
+  if (ts->epoch + 1 >= (1u << 31)) {  // after the wait above: no launch still reads them
+    e = hipMemsetAsync(ts->slots, 0, kTagSlots * sizeof(unsigned long long), stream);
+    if (e != hipSuccess) return e;
+    ts->epoch = 0;
+  }
+  TagArgs tg;
+  tg.slots = ts->slots;
+  tg.epoch = ++ts->epoch;
+  tg.groups = p.groups;
+  tg.spin_limit = kTagSpinLimit;
+  const int64_t fin = (c + 63) / 64;
+  const S* xs = static_cast<const S*>(x);
+  S* o = static_cast<S*>(out);
+  constexpr const char* kName = "tfma_bias_add_grad_fused";
+  SetLastKernel(kName);
+  const TraceEvents tev = TraceTake(kName);
+  hipEvent_t end = tev.end ? tev.end : ts->own;
+  constexpr int V = 16 / sizeof(S);
+  if (p.rows) {
+    tg.ct = p.ct;
+    const dim3 grid(static_cast<unsigned>(p.ct * p.groups + fin));
+    const size_t smem = static_cast<size_t>(kThreads) * p.vec * sizeof(float);
+    if (p.vec == V)
+      hipExtLaunchKernelGGL((bag_rows_kernel<B, V, true>), grid, dim3(kThreads), smem, stream,
+                            tev.start, end, 0, xs, outer, static_cast<int>(c), p.cv, p.tx_shift,
+                            p.per_g, static_cast<float*>(nullptr), tg, o);
+    else
+      hipExtLaunchKernelGGL((bag_rows_kernel<B, 1, true>), grid, dim3(kThreads), smem, stream,
+                            tev.start, end, 0, xs, outer, static_cast<int>(c), p.cv, p.tx_shift,
+                            p.per_g, static_cast<float*>(nullptr), tg, o);
+  } else {
+    tg.ct = static_cast<int>(c);
+    const dim3 grid(static_cast<unsigned>(c * p.groups + fin));
+    if (p.vec > 1) {
+      const int64_t iv = inner / V;
+      hipExtLaunchKernelGGL((bag_planes_kernel<B, V, true>), grid, dim3(kThreads), 0, stream,
+                            tev.start, end, 0, xs, outer, static_cast<int>(c), iv, p.per_g,
+                            FastDiv(static_cast<uint32_t>(iv)), static_cast<float*>(nullptr), tg,
+                            o);
+    } else {
+      hipExtLaunchKernelGGL((bag_planes_kernel<B, 1, true>), grid, dim3(kThreads), 0, stream,
+                            tev.start, end, 0, xs, outer, static_cast<int>(c), inner, p.per_g,
+                            FastDiv(static_cast<uint32_t>(inner)), static_cast<float*>(nullptr),
+                            tg, o);
+    }
+  }
+  TraceCommit(tev);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  ts->chain = end;
+  ts->last_stream = stream;
+  ts->used = true;
+  return hipSuccess;
+}
+
 // chain_end (the allocation-free path): in, an event the finalize dispatch
 // ends with (hipExtLaunchKernelGGL's own stop event: no marker packet between
 // kernels); out, the event that marks its end (a trace event instead when
@@ -257,6 +511,10 @@ hipError_t launch_bag(const void* x, int64_t outer, int64_t c, int64_t inner, vo
   using A = typename B::A;
   const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
   const BagPlan p = make_bag_plan(outer, c, inner, sizeof(S), aligned);
+  if constexpr (std::is_same<A, float>::value) {
+    if (!chain_end && tag_applies<B>(p, c, stream))
+      return launch_bag_tagged<B>(p, x, outer, c, inner, out, stream);
+  }
   A* partial = static_cast<A*>(workspace);
   const S* xs = static_cast<const S*>(x);
   {
@@ -266,22 +524,24 @@ hipError_t launch_bag(const void* x, int64_t outer, int64_t c, int64_t inner, vo
       if (p.vec == V) {
         TFMA_LAUNCH("tfma_bias_add_grad_reduce", (bag_rows_kernel<B, V>), dim3(p.ct, p.groups), dim3(kThreads), smem,
                            stream, xs, outer, static_cast<int>(c), p.cv, p.tx_shift, p.per_g,
-                           partial);
+                           partial, TagArgs{}, static_cast<S*>(nullptr));
       } else {
         TFMA_LAUNCH("tfma_bias_add_grad_reduce", (bag_rows_kernel<B, 1>), dim3(p.ct, p.groups), dim3(kThreads), smem,
                            stream, xs, outer, static_cast<int>(c), p.cv, p.tx_shift, p.per_g,
-                           partial);
+                           partial, TagArgs{}, static_cast<S*>(nullptr));
       }
     } else if (p.vec > 1) {
       constexpr int V = 16 / sizeof(S);
       const int64_t iv = inner / V;
       TFMA_LAUNCH("tfma_bias_add_grad_reduce", (bag_planes_kernel<B, V>), dim3(c, p.groups), dim3(kThreads), 0, stream,
                          xs, outer, static_cast<int>(c), iv, p.per_g,
-                         FastDiv(static_cast<uint32_t>(iv)), partial);
+                         FastDiv(static_cast<uint32_t>(iv)), partial, TagArgs{},
+                         static_cast<S*>(nullptr));
     } else {
       TFMA_LAUNCH("tfma_bias_add_grad_reduce", (bag_planes_kernel<B, 1>), dim3(c, p.groups), dim3(kThreads), 0, stream,
                          xs, outer, static_cast<int>(c), inner, p.per_g,
-                         FastDiv(static_cast<uint32_t>(inner)), partial);
+                         FastDiv(static_cast<uint32_t>(inner)), partial, TagArgs{},
+                         static_cast<S*>(nullptr));
     }
   }
   hipError_t e = hipGetLastError();

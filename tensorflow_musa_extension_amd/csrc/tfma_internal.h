@@ -64,7 +64,16 @@ void TraceCommit(const TraceEvents& ev);
 //     tiles of that many channel vectors.
 //   kTuneBnSlicedOverlap: 0 = sliced grads run the plain sliced pass.
 //   kTuneBnNchwOwned: 0 = NCHW training keeps the split kernels.
-enum Tune { kTuneEwNt, kTuneBnSliceTw, kTuneBnSlicedOverlap, kTuneBnNchwOwned, kTuneCount };
+//   kTuneBagFused: 0 = BiasAddGrad runs as two kernels (partials, then finals)
+//     instead of one launch.
+enum Tune {
+  kTuneEwNt,
+  kTuneBnSliceTw,
+  kTuneBnSlicedOverlap,
+  kTuneBnNchwOwned,
+  kTuneBagFused,
+  kTuneCount
+};
 int TuneValue(Tune k);
 bool SetTune(const char* name, int value);
 

@@ -24,6 +24,7 @@ constexpr Override kOverrides[kTuneCount] = {
     {"bn_slice_tw", "TFMA_BN_SLICE_TW"},
     {"bn_sliced_overlap", "TFMA_BN_SLICED_OVERLAP"},
     {"bn_nchw_owned", "TFMA_BN_NCHW_OWNED"},
+    {"bag_fused", "TFMA_BAG_FUSED"},
 };
 
 std::atomic<int> g_value[kTuneCount];

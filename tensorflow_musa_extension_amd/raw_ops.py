@@ -465,7 +465,7 @@ def fused_batch_norm_barrier_timed_out(reset=False):
 
 def set_tuning_override(name, value):
     """Plan / cache-mode override (TFMA_SetTuningOverride): "ew_nt",
-    "bn_slice_tw", "bn_sliced_overlap" or "bn_nchw_owned"; value None or -1
+    "bn_slice_tw", "bn_sliced_overlap", "bn_nchw_owned" or "bag_fused"; value None or -1
     restores the library's own choice.  For tests and measurements."""
     st = _lib.TFMA_Status()
     _lib.load().TFMA_SetTuningOverride(name.encode(), -1 if value is None else int(value),

@@ -383,9 +383,10 @@ def test_elementwise_integer_dtype_validation():
 
 
 def test_tuning_overrides():
-    """TFMA_SetTuningOverride takes the four documented names (-1 restores
-    the default) and rejects others; host only."""
-    for name in (b"ew_nt", b"bn_slice_tw", b"bn_sliced_overlap", b"bn_nchw_owned"):
+    """TFMA_SetTuningOverride takes the documented names (-1 restores the
+    default) and rejects others; host only."""
+    for name in (b"ew_nt", b"bn_slice_tw", b"bn_sliced_overlap", b"bn_nchw_owned",
+                 b"bag_fused"):
         assert call("TFMA_SetTuningOverride", name, 0)[0] == _lib.OK
         assert call("TFMA_SetTuningOverride", name, -1)[0] == _lib.OK
     code, msg = call("TFMA_SetTuningOverride", b"bn_slices", 4)

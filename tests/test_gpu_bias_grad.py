@@ -118,3 +118,47 @@ def test_bias_add_grad_captured_equals_eager(dev):
         again = ops.BiasAddGrad(x)
         torch.cuda.synchronize()
         assert torch.equal(again.view(torch.int16), eager.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape,fmt", CASES)
+def test_one_launch_equals_two_kernels(dev, tune, dtype, shape, fmt):
+    """The one-launch form (tagged partials, finalizing workgroups at the end
+    of the same grid) against the two-kernel form (override bag_fused 0):
+    same plan, partials and summation order, so the same bits - including
+    the shapes whose partials exceed the tagged slots and fall back."""
+    gen_ = torch.Generator(device=dev)
+    gen_.manual_seed(31)
+    x = torch.randn(shape, generator=gen_, device=dev).to(dtype)
+    one = ops.BiasAddGrad(x, data_format=fmt)
+    name_one = ops.last_kernel_name()
+    tune("bag_fused", 0)
+    two = ops.BiasAddGrad(x, data_format=fmt)
+    assert ops.last_kernel_name() == "tfma_bias_add_grad_finalize"
+    torch.cuda.synchronize()
+    assert name_one in ("tfma_bias_add_grad_fused", "tfma_bias_add_grad_finalize")
+    if shape == (8192, 4096):
+        assert name_one == "tfma_bias_add_grad_fused"
+    assert torch.equal(one.view(torch.int16 if dtype != torch.float32 else torch.int32),
+                       two.view(torch.int16 if dtype != torch.float32 else torch.int32))
+
+
+def test_one_launch_calls_on_two_streams(dev):
+    """One-launch calls alternating between two streams with no
+    synchronization between them share the library's tagged slots: each is
+    chained to the previous one, so every result equals the same call run
+    alone, bit for bit."""
+    gen_ = torch.Generator(device=dev)
+    gen_.manual_seed(32)
+    shapes = [(8192, 4096), (96, 40), (2048, 1024), (33, 7, 7, 64)] * 3
+    xs = [torch.randn(s, generator=gen_, device=dev).half() for s in shapes]
+    wants = [ops.BiasAddGrad(x) for x in xs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = []
+    for i, x in enumerate(xs):
+        with torch.cuda.stream(streams[i % 2]):
+            outs.append(ops.BiasAddGrad(x))
+    torch.cuda.synchronize()
+    for i, (o, w) in enumerate(zip(outs, wants)):
+        assert torch.equal(o.view(torch.int16), w.view(torch.int16)), f"call {i} {shapes[i]}"
