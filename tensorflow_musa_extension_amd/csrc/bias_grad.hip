@@ -383,10 +383,7 @@ struct TagState {
   std::mutex mu;
   unsigned long long* slots = nullptr;
   unsigned epoch = 0;
-  hipEvent_t own = nullptr;    // the launch's end event when not traced
-  hipEvent_t chain = nullptr;  // end of the last launch (`own` or a trace event)
-  hipStream_t last_stream = nullptr;
-  bool used = false;
+  LaunchChain chain;
 };
 
 TagState* tag_state() {
@@ -434,17 +431,10 @@ hipError_t launch_bag_tagged(const BagPlan& p, const void* x, int64_t outer, int
       (void)hipFree(q);
       return e;
     }
-    e = hipEventCreateWithFlags(&ts->own, hipEventDisableTiming | hipEventReleaseToDevice);
-    if (e != hipSuccess) {
-      (void)hipFree(q);
-      return e;
-    }
     ts->slots = static_cast<unsigned long long*>(q);
   }
-  if (ts->used && ts->last_stream != stream) {
-    e = hipStreamWaitEvent(stream, ts->chain, 0);
-    if (e != hipSuccess) return e;
-  }
+  e = ts->chain.before(stream);
+  if (e != hipSuccess) return e;
   if (ts->epoch + 1 >= (1u << 31)) {  // after the wait above: no launch still reads them
     e = hipMemsetAsync(ts->slots, 0, kTagSlots * sizeof(unsigned long long), stream);
     if (e != hipSuccess) return e;
@@ -461,7 +451,7 @@ hipError_t launch_bag_tagged(const BagPlan& p, const void* x, int64_t outer, int
   constexpr const char* kName = "tfma_bias_add_grad_fused";
   SetLastKernel(kName);
   const TraceEvents tev = TraceTake(kName);
-  hipEvent_t end = tev.end ? tev.end : ts->own;
+  hipEvent_t end = ts->chain.end_event(tev.end);
   constexpr int V = 16 / sizeof(S);
   if (p.rows) {
     tg.ct = p.ct;
@@ -494,16 +484,14 @@ hipError_t launch_bag_tagged(const BagPlan& p, const void* x, int64_t outer, int
   TraceCommit(tev);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  ts->chain = end;
-  ts->last_stream = stream;
-  ts->used = true;
+  ts->chain.after(stream, end);
   return hipSuccess;
 }
 
-// chain_end (the allocation-free path): in, an event the finalize dispatch
-// ends with (hipExtLaunchKernelGGL's own stop event: no marker packet between
-// kernels); out, the event that marks its end (a trace event instead when
-// tracing is on for the finalize kernel).
+// chain_end (the allocation-free path): in, the event the finalize dispatch
+// ends with, or null for none (hipExtLaunchKernelGGL's own stop event: no
+// marker packet between kernels); out, the event that marks its end (a trace
+// event instead when tracing is on for the finalize kernel).
 template <class B>
 hipError_t launch_bag(const void* x, int64_t outer, int64_t c, int64_t inner, void* out,
                       void* workspace, hipStream_t stream, hipEvent_t* chain_end = nullptr) {
@@ -554,7 +542,7 @@ hipError_t launch_bag(const void* x, int64_t outer, int64_t c, int64_t inner, vo
   }
   SetLastKernel(kFinalize);
   const TraceEvents tev = TraceTake(kFinalize);
-  hipEvent_t end = tev.end ? tev.end : *chain_end;
+  hipEvent_t end = tev.end ? tev.end : *chain_end;  // may be null: no end event
   hipExtLaunchKernelGGL((bag_finalize_kernel<B>), dim3((c + 63) / 64), dim3(kThreads), 0, stream,
                         tev.start, end, 0, partial, p.groups, static_cast<int>(c),
                         static_cast<S*>(out));
@@ -619,15 +607,12 @@ hipError_t dispatch_bag(int dt, const void* x, int64_t outer, int64_t c, int64_t
 
 // Per device: the allocation-free calls share one scratch, so a call on
 // another stream than the previous call's first waits for that call's
-// finalize to end (its end event); calls on one stream are ordered by the
+// finalize to end (LaunchChain); calls on one stream are ordered by the
 // stream.  The mutex keeps the wait, the launches and the bookkeeping of one
 // call together.
 struct NoAllocChain {
   std::mutex mu;
-  hipEvent_t own = nullptr;    // the finalize's end event when not traced
-  hipEvent_t chain = nullptr;  // end of the last call (`own` or a trace event)
-  hipStream_t last_stream = nullptr;
-  bool used = false;
+  LaunchChain chain;
 };
 }  // namespace
 
@@ -655,20 +640,12 @@ hipError_t LaunchBiasAddGradNoAlloc(int dt, const void* x, int64_t outer, int64_
   static NoAllocChain chains[64];
   NoAllocChain& ch = chains[dev];
   std::lock_guard<std::mutex> lk(ch.mu);
-  if (!ch.own) {
-    e = hipEventCreateWithFlags(&ch.own, hipEventDisableTiming | hipEventReleaseToDevice);
-    if (e != hipSuccess) return e;
-  }
-  if (ch.used && ch.last_stream != stream) {
-    e = hipStreamWaitEvent(stream, ch.chain, 0);
-    if (e != hipSuccess) return e;
-  }
-  hipEvent_t end = ch.own;
+  e = ch.chain.before(stream);
+  if (e != hipSuccess) return e;
+  hipEvent_t end = ch.chain.end_event(nullptr);
   e = dispatch_bag(dt, x, outer, c, inner, out, scratch, stream, &end);
   if (e != hipSuccess) return e;
-  ch.chain = end;
-  ch.last_stream = stream;
-  ch.used = true;
+  ch.chain.after(stream, end);
   return hipSuccess;
 }
 

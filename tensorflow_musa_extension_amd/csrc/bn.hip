@@ -2443,13 +2443,13 @@ void set_dynamic_share(FusedPlan* fp, int resident, int prefetched, int u) {
 
 // Per-device state of the fused kernels: a monotonic exit-arrival counter in
 // device memory (zeroed once), its value before the next launch, the
-// epoch-tagged value regions and the last epoch, and the event and stream of
-// the last fused launch.  The event is the
-// dispatch's own end event (hipExtLaunchKernelGGL), not a marker after it:
-// a marker between kernels costs microseconds.  Fused launches on one
-// device are chained (a launch on another stream waits for the previous
-// one), so at most one persistent grid is resident at a time and every
-// launch knows the counter's starting value.
+// epoch-tagged value regions and the last epoch, and the launch chain
+// (LaunchChain: a launch on another stream than the previous one waits for
+// it; once a device has seen two streams every launch carries the
+// dispatch's own end event, hipExtLaunchKernelGGL's stop event, not a marker
+// after it - a marker between kernels costs microseconds).  So at most one
+// persistent grid is resident at a time and every launch knows the
+// counter's starting value.
 // The allocation also holds the dynamic-chunk counters (from byte 256),
 // which the last workgroup of each launch zeroes again.  A second, identical
 // region serves launches recorded into a graph (stream capture): they start
@@ -2467,10 +2467,7 @@ struct BarrierState {
   unsigned long long* counter = nullptr;  // [0] arrivals
   unsigned long long base = 0;
   unsigned sub_base[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // class counters (mod 2^32)
-  hipEvent_t last = nullptr;   // end of the last launch when it was not traced
-  hipEvent_t chain = nullptr;  // end of the last launch (`last` or a trace event)
-  hipStream_t last_stream = nullptr;
-  bool used = false;
+  LaunchChain chain;           // orders launches from different streams
   unsigned long long* eslots = nullptr;  // epoch-tagged partials, zeroed at creation
   size_t eslot_bytes = 0;
   unsigned long long* ecoef = nullptr;   // epoch-tagged coefficients, zeroed at creation
@@ -2524,8 +2521,6 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
     hipError_t e = hipMalloc(&p, 2 * kStateBytes);
     if (e != hipSuccess) return e;
     e = hipMemset(p, 0, 2 * kStateBytes);
-    if (e == hipSuccess)
-      e = hipEventCreateWithFlags(&bs->last, hipEventDisableTiming | hipEventReleaseToDevice);
     if (e != hipSuccess) {
       (void)hipFree(p);
       return e;
@@ -2588,8 +2583,8 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
       recorded ? reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(bs->counter) +
                                                        kStateBytes)
                : bs->counter;
-  if (!recorded && bs->used && bs->last_stream != stream) {
-    hipError_t e = hipStreamWaitEvent(stream, bs->chain, 0);
+  if (!recorded) {
+    hipError_t e = bs->chain.before(stream);
     if (e != hipSuccess) return e;
   }
   // The epoch, after the wait above: zeroing the regions at the wrap must
@@ -2693,7 +2688,7 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
     return le != hipSuccess ? le : hipGetLastError();
   }
   const TraceEvents tev = TraceTake(name);
-  hipEvent_t end = tev.end ? tev.end : bs->last;
+  hipEvent_t end = bs->chain.end_event(tev.end);
   {
     hipError_t le = hipExtLaunchKernel(kern, dim3(fp.blocks), dim3(kFusedThreads), kargs, smem,
                                        stream, tev.start, end, 0);
@@ -2709,9 +2704,7 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   for (int r = 0; r < 8; ++r)
     bs->sub_base[r] += rounds * static_cast<unsigned>((fp.blocks + 7 - r) / 8);
   bs->base += rounds * classes;
-  bs->chain = end;
-  bs->last_stream = stream;
-  bs->used = true;
+  bs->chain.after(stream, end);
   return hipSuccess;
 }
 

@@ -77,6 +77,43 @@ enum Tune {
 int TuneValue(Tune k);
 bool SetTune(const char* name, int value);
 
+// Orders launches that share per-device library state (the fused BN
+// kernels' counters and epoch regions, BiasAddGrad's tagged slots and static
+// scratch): a launch on another stream than the previous one waits for it.
+// Launches on one stream are ordered by the stream and carry no event (an
+// event on a dispatch delays the next stream operation by ~3 us when the
+// stream is otherwise idle).  The first switch of streams on a device
+// synchronizes the device once (no event exists yet to wait for, and the
+// previous stream may since have been destroyed); from then on every launch
+// ends with an event (`own`, or the trace event the launch already carries)
+// that the next switch waits for.  The caller holds the state's mutex.
+struct LaunchChain {
+  hipEvent_t own = nullptr;    // created on first use
+  hipEvent_t chain = nullptr;  // end of the last launch once `multi`
+  hipStream_t last_stream = nullptr;
+  bool used = false;
+  bool multi = false;  // launches from two streams seen on this device
+
+  hipError_t before(hipStream_t s) {
+    if (!own) {
+      const hipError_t e =
+          hipEventCreateWithFlags(&own, hipEventDisableTiming | hipEventReleaseToDevice);
+      if (e != hipSuccess) return e;
+    }
+    if (!used || last_stream == s) return hipSuccess;
+    const hipError_t e = multi ? hipStreamWaitEvent(s, chain, 0) : hipDeviceSynchronize();
+    multi = true;
+    return e;
+  }
+  // The end event the launch's dispatch carries (null: none).
+  hipEvent_t end_event(hipEvent_t trace_end) const { return trace_end ? trace_end : (multi ? own : nullptr); }
+  void after(hipStream_t s, hipEvent_t end) {
+    chain = end;
+    last_stream = s;
+    used = true;
+  }
+};
+
 // Number of compute units of the current device (cached per device).
 int DeviceCUs();
 
