@@ -74,6 +74,12 @@ __device__ inline void store_tagged(const TagArgs& tg, int64_t slot, float v) {
                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// LDS bytes of bag_rows_kernel's reduction: ry rows of lanes * (VEC + 1)
+// accumulators (VEC for VEC = 1), i.e. kThreads * stride.
+inline size_t bag_rows_smem(int vec, size_t acc_bytes) {
+  return static_cast<size_t>(kThreads) * (vec > 1 ? vec + 1 : 1) * acc_bytes;
+}
+
 template <class B, int VEC, bool kTag = false>
 __global__ __launch_bounds__(kThreads) void bag_rows_kernel(
     const typename B::S* __restrict__ x, int64_t rows, int c, int64_t cv, int tx_shift,
@@ -93,7 +99,7 @@ __global__ __launch_bounds__(kThreads) void bag_rows_kernel(
   using S = typename B::S;
   using A = typename B::A;
   extern __shared__ unsigned char bag_lds[];
-  A* red = reinterpret_cast<A*>(bag_lds);  // [ry][tx * VEC]
+  A* red = reinterpret_cast<A*>(bag_lds);  // [ry][lanes * (VEC + 1)] (bag_rows_smem)
   int64_t bx = blockIdx.x, by = blockIdx.y;
   if constexpr (kTag) {
     const int64_t b = blockIdx.x;
@@ -138,13 +144,21 @@ __global__ __launch_bounds__(kThreads) void bag_rows_kernel(
       for (int j = 0; j < VEC; ++j) acc[j] += B::ld(v[j]);
     }
   }
+  // The row lanes' sums through LDS, a lane's VEC channels at a stride of
+  // VEC + 1 words (odd for VEC > 1): the writes of one channel slot from
+  // consecutive lanes, and the reads of consecutive channels, fall on
+  // distinct banks (a stride of VEC made the writes 8-way conflicts for
+  // half: 3.4 conflicts per access).  Row ty starts at ty * row_words.
+  constexpr int kStride = VEC > 1 ? VEC + 1 : 1;
+  const int row_words = (1 << tx_shift) * kStride;
 #pragma unroll
-  for (int j = 0; j < VEC; ++j) red[ty * width + tx * VEC + j] = acc[j];
+  for (int j = 0; j < VEC; ++j) red[ty * row_words + tx * kStride + j] = acc[j];
   __syncthreads();
   const int64_t ch = bx * width + threadIdx.x;
   if (static_cast<int>(threadIdx.x) < width && ch < c) {
+    const int slot = static_cast<int>(threadIdx.x) / VEC * kStride + static_cast<int>(threadIdx.x) % VEC;
     A s = A(0);
-    for (int k = 0; k < ry; ++k) s += red[k * width + threadIdx.x];
+    for (int k = 0; k < ry; ++k) s += red[k * row_words + slot];
     if constexpr (kTag)
       store_tagged(tg, by * c + ch, s);
     else
@@ -456,7 +470,7 @@ hipError_t launch_bag_tagged(const BagPlan& p, const void* x, int64_t outer, int
   if (p.rows) {
     tg.ct = p.ct;
     const dim3 grid(static_cast<unsigned>(p.ct * p.groups + fin));
-    const size_t smem = static_cast<size_t>(kThreads) * p.vec * sizeof(float);
+    const size_t smem = bag_rows_smem(p.vec, sizeof(float));
     if (p.vec == V)
       hipExtLaunchKernelGGL((bag_rows_kernel<B, V, true>), grid, dim3(kThreads), smem, stream,
                             tev.start, end, 0, xs, outer, static_cast<int>(c), p.cv, p.tx_shift,
@@ -507,7 +521,7 @@ hipError_t launch_bag(const void* x, int64_t outer, int64_t c, int64_t inner, vo
   const S* xs = static_cast<const S*>(x);
   {
     if (p.rows) {
-      const size_t smem = static_cast<size_t>(kThreads) * p.vec * sizeof(A);
+      const size_t smem = bag_rows_smem(p.vec, sizeof(A));
       constexpr int V = 16 / sizeof(S);
       if (p.vec == V) {
         TFMA_LAUNCH("tfma_bias_add_grad_reduce", (bag_rows_kernel<B, V>), dim3(p.ct, p.groups), dim3(kThreads), smem,
