@@ -575,8 +575,12 @@ def cpu_baseline(torch, dev, min_seconds=10.0, component_seconds=1.5):
     embedding and the first layer's six tensors, 153M parameters - the
     1.31B-parameter state would need 21 GB of host memory per pass), and the
     cfg4 chains at [8192,4096], each for at least `component_seconds`.
-    Inputs are drawn on the GPU and copied to host memory before timing;
-    GB/s counts the same algorithmic bytes as the GPU figures."""
+    The chains run oracle_baseline_rows (row loops, F16C/AVX2 half
+    conversion), which gives the checker's bits on the same inputs; the
+    broadcasting checker walks N-d coordinates per element and would
+    understate the CPU.  Inputs are drawn on the GPU and copied to host
+    memory before timing; GB/s counts the same algorithmic bytes as the GPU
+    figures."""
     import numpy as np
     sys.path.insert(0, ROOT)
     from oracle import oracle
@@ -647,14 +651,16 @@ def cpu_baseline(torch, dev, min_seconds=10.0, component_seconds=1.5):
         a = _host(torch, torch.randn(8192, 4096, generator=gen, device=dev).to(tdt))
         c = _host(torch, torch.randn(8192, 4096, generator=gen, device=dev).to(tdt))
         E = x.size
+        # BiasAdd+Relu and AddV2+Relu with a [C] row are the same row chain.
+        rows = "one call of the vectorized row kernels, repeated"
         rate(f"bias_add_relu_{name}_8192x4096", 2 * es * E + es * 4096,
-             lambda: oracle.bias_add(x, b, relu=True, dtype=odt), "one call, repeated")
+             lambda: oracle.baseline_rows("add_relu", x, b, dtype=odt), rows)
         rate(f"add_v2_relu_{name}_8192x4096", 2 * es * E + es * 4096,
-             lambda: oracle.eltwise("add_relu", [x, b], odt), "one call, repeated")
+             lambda: oracle.baseline_rows("add_relu", x, b, dtype=odt), rows)
         rate(f"mul_add_full_{name}_8192x4096", 4 * es * E,
-             lambda: oracle.eltwise("mul_add", [x, a, c], odt), "one call, repeated")
+             lambda: oracle.baseline_rows("mul_add", x, a, c, dtype=odt), rows)
         rate(f"mul_add_row_{name}_8192x4096", 2 * es * E + 2 * es * 4096,
-             lambda: oracle.eltwise("mul_add", [x, b, b], odt), "one call, repeated")
+             lambda: oracle.baseline_rows("mul_add", x, b, b, dtype=odt), rows)
         del x, b, a, c
     return {"value": round(gbps, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "label": "TF-CPU restatement, not TF (TensorFlow is not installed)",

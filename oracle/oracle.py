@@ -46,6 +46,7 @@ def load():
     lib.oracle_adam.argtypes = [i, vp, vp, vp, vp, i64, d, d, d, d, d, d, i]
     lib.oracle_eltwise.argtypes = [i, i, i, vp, vp, vp, i, vp, vp]
     lib.oracle_bias_add_grad.argtypes = [i, vp, i64, i64, i64, vp]
+    lib.oracle_baseline_rows.argtypes = [i, i, vp, vp, i, vp, i, i64, i64, vp]
     lib.oracle_set_threads.argtypes = [i]
     lib.oracle_get_threads.restype = i
     lib.oracle_f32_to_f16.argtypes = [f]
@@ -57,7 +58,7 @@ def load():
     lib.oracle_bf16_to_f32.argtypes = [ctypes.c_uint16]
     lib.oracle_bf16_to_f32.restype = f
     for fn in ("oracle_bn_fwd", "oracle_bn_grad", "oracle_adam", "oracle_eltwise",
-               "oracle_bias_add_grad",
+               "oracle_bias_add_grad", "oracle_baseline_rows",
                "oracle_set_threads"):
         getattr(lib, fn).restype = None
     _lib = lib
@@ -290,6 +291,22 @@ def eltwise(op, inputs, dtype="float32"):
     od = np.array(out_shape, np.int64)
     lib.oracle_eltwise(DT[dtype], EW_OPS[op], nin, ptrs, _p(dims), _p(nd), len(out_shape),
                        _p(od) if len(out_shape) else None, _p(out))
+    return out
+
+
+def baseline_rows(op, x, b, c=None, dtype="float32"):
+    """CPU baseline of the cfg4 chains (bench.py's cpu_baseline leg, not the
+    checker): x [rows, cols] contiguous; b and c full [rows, cols] or a
+    [cols] row; op "add", "add_relu" or "mul_add" (x*b rounded, + c)."""
+    codes = {"add": 0, "add_relu": 1, "mul_add": 3}
+    x = np.ascontiguousarray(x)
+    rows, cols = x.shape
+    b = np.ascontiguousarray(b)
+    c = None if c is None else np.ascontiguousarray(c)
+    out = np.empty_like(x)
+    lib = load()
+    lib.oracle_baseline_rows(DT[dtype], codes[op], _p(x), _p(b), int(b.ndim == 1), _p(c),
+                             int(c is not None and c.ndim == 1), rows, cols, _p(out))
     return out
 
 

@@ -457,3 +457,119 @@ void oracle_bias_add_grad(int dt, const void* x, int64_t outer, int64_t c, int64
     else st(dt, out, ch, (float)acc);
   }
 }
+
+/* ------------------------------------------------------------------------ */
+/* CPU baseline of the cfg4 chains (bench.py's cpu_baseline leg; the parity  */
+/* checker is oracle_eltwise above).  Contiguous [rows, cols] x with b and c  */
+/* either full or a [cols] row vector, run as TF-CPU's vectorized kernels run */
+/* them: a contiguous inner loop per row (OpenMP over rows, SIMD within),     */
+/* and hardware half conversions (F16C) where the host has them.  Same        */
+/* rounding points as oracle_eltwise, which tests/test_oracle.py checks bit   */
+/* for bit.  op: 0 add, 1 add+relu, 3 mul+add (x*b rounded, + c).             */
+/* ------------------------------------------------------------------------ */
+#if defined(__x86_64__)
+#include <immintrin.h>
+__attribute__((target("avx2,f16c"))) static void rows_f16_hw(int op, const uint16_t* x,
+                                                             const uint16_t* b, int b_row,
+                                                             const uint16_t* c, int c_row,
+                                                             int64_t rows, int64_t cols,
+                                                             uint16_t* out) {
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+#endif
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint16_t* xr = x + r * cols;
+    const uint16_t* br = b ? (b_row ? b : b + r * cols) : NULL;
+    const uint16_t* cr = c ? (c_row ? c : c + r * cols) : NULL;
+    uint16_t* orow = out + r * cols;
+    int64_t j = 0;
+    for (; j + 8 <= cols; j += 8) {
+      const __m256 xv = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(xr + j)));
+      const __m256 bv = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(br + j)));
+      __m256 v;
+      if (op == 3) {
+        const __m128i p = _mm256_cvtps_ph(_mm256_mul_ps(xv, bv), _MM_FROUND_TO_NEAREST_INT);
+        const __m256 cv = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(cr + j)));
+        v = _mm256_add_ps(_mm256_cvtph_ps(p), cv);
+      } else {
+        v = _mm256_add_ps(xv, bv);
+      }
+      __m128i h = _mm256_cvtps_ph(v, _MM_FROUND_TO_NEAREST_INT);
+      if (op == 1) {
+        /* relu on the rounded half: a value below zero - sign bit set,
+         * magnitude nonzero (not -0) and at most infinity's (not NaN) -
+         * becomes +0; everything else keeps its bits. */
+        const __m128i mag = _mm_and_si128(h, _mm_set1_epi16(0x7fff));
+        const __m128i sign = _mm_cmplt_epi16(h, _mm_setzero_si128());
+        const __m128i zero = _mm_cmpeq_epi16(mag, _mm_setzero_si128());
+        const __m128i num = _mm_cmplt_epi16(mag, _mm_set1_epi16(0x7c01));
+        const __m128i neg = _mm_andnot_si128(zero, _mm_and_si128(sign, num));
+        h = _mm_andnot_si128(neg, h);
+      }
+      _mm_storeu_si128((__m128i*)(orow + j), h);
+    }
+    for (; j < cols; ++j) {
+      float v;
+      const float xv = oracle_f16_to_f32(xr[j]), bv = oracle_f16_to_f32(br[j]);
+      if (op == 3) v = oracle_f16_to_f32(oracle_f32_to_f16(xv * bv)) + oracle_f16_to_f32(cr[j]);
+      else v = xv + bv;
+      uint16_t h = oracle_f32_to_f16(v);
+      if (op == 1 && oracle_f16_to_f32(h) < 0.f) h = 0;
+      orow[j] = h;
+    }
+  }
+}
+#endif
+
+void oracle_baseline_rows(int dt, int op, const void* x, const void* b, int b_row, const void* c,
+                          int c_row, int64_t rows, int64_t cols, void* out) {
+#if defined(__x86_64__)
+  if (dt == DT_HALF && __builtin_cpu_supports("f16c") && __builtin_cpu_supports("avx2")) {
+    rows_f16_hw(op, (const uint16_t*)x, (const uint16_t*)b, b_row, (const uint16_t*)c, c_row,
+                rows, cols, (uint16_t*)out);
+    return;
+  }
+#endif
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+#endif
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t o = r * cols;
+    const int64_t ob = b_row ? 0 : o, oc = c_row ? 0 : o;
+    if (dt == DT_FLOAT) {
+      const float* xr = (const float*)x + o;
+      const float* br = (const float*)b + ob;
+      const float* cr = c ? (const float*)c + oc : NULL;
+      float* orow = (float*)out + o;
+      if (op == 3) {
+#ifdef _OPENMP
+#pragma omp simd
+#endif
+        for (int64_t j = 0; j < cols; ++j) orow[j] = xr[j] * br[j] + cr[j];
+      } else if (op == 1) {
+#ifdef _OPENMP
+#pragma omp simd
+#endif
+        for (int64_t j = 0; j < cols; ++j) {
+          const float v = xr[j] + br[j];
+          orow[j] = v < 0.f ? 0.f : v;
+        }
+      } else {
+#ifdef _OPENMP
+#pragma omp simd
+#endif
+        for (int64_t j = 0; j < cols; ++j) orow[j] = xr[j] + br[j];
+      }
+    } else {
+      for (int64_t j = 0; j < cols; ++j) {
+        const float xv = ld(dt, x, o + j), bv = ld(dt, b, ob + j);
+        float v = op == 3 ? rnd(dt, xv * bv) + ld(dt, c, oc + j) : xv + bv;
+        if (op == 1) {
+          v = rnd(dt, v);
+          v = v < 0.f ? 0.f : v;
+        }
+        st(dt, out, o + j, v);
+      }
+    }
+  }
+}

@@ -488,6 +488,53 @@ def test_eltwise_bf16_matches_torch_bf16_arithmetic():
                                   bits(torch.relu(xt + yt)))
 
 
+def _baseline_operand(rng, shape, dtype):
+    """Normal values with planted -0, +0, values whose sum cancels to a
+    signed zero, and large values whose sum or product overflows the half
+    types."""
+    v = rng.standard_normal(shape).astype(np.float32)
+    flat = v.reshape(-1)
+    k = flat.size
+    flat[rng.integers(0, k, k // 16)] = -0.0
+    flat[rng.integers(0, k, k // 16)] = 0.0
+    flat[rng.integers(0, k, k // 32)] = 60000.0
+    flat[rng.integers(0, k, k // 32)] = -3.0e38 if dtype == "bfloat16" else -60000.0
+    if dtype == "float16":
+        return v.astype(np.float16)
+    if dtype == "bfloat16":
+        return oracle.f32_to_bf16_bits(v)
+    return v
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("rows,cols", [(37, 203), (8, 8), (3, 5), (64, 1024)])
+def test_baseline_rows_equals_checker(dtype, rows, cols):
+    """bench.py times the cfg4 chains on the CPU with the vectorized row
+    kernels of oracle_baseline_rows (F16C/AVX2 half conversion, row
+    loops); they must give the checker's bits (oracle_eltwise, pinned
+    against numpy / torch arithmetic above) for every op and operand
+    shape they are timed on, including a column count that leaves a
+    scalar tail after the 8-wide vectors."""
+    rng = np.random.default_rng(54)
+    x = _baseline_operand(rng, (rows, cols), dtype)
+    full = _baseline_operand(rng, (rows, cols), dtype)
+    row = _baseline_operand(rng, (cols,), dtype)
+    c = _baseline_operand(rng, (rows, cols), dtype)
+    c_row = _baseline_operand(rng, (cols,), dtype)
+    cases = [("add", [x, full]), ("add", [x, row]), ("add_relu", [x, full]),
+             ("add_relu", [x, row]), ("mul_add", [x, full, c]), ("mul_add", [x, row, c]),
+             ("mul_add", [x, row, c_row]), ("mul_add", [x, full, c_row])]
+    for op, ins in cases:
+        with np.errstate(over="ignore"):
+            want = oracle.eltwise(op, ins, dtype)
+        got = oracle.baseline_rows(op, *ins, dtype=dtype)
+        assert_bitwise(got, want, f"{op} {dtype} b{ins[1].shape} c{ins[2].shape if len(ins) > 2 else None}")
+    # the planted signed zeros reach the outputs: add_relu keeps -0 and clears negatives
+    z = oracle.baseline_rows("add_relu", x, full, dtype=dtype)
+    zf = z.astype(np.float32) if dtype != "bfloat16" else oracle.bf16_bits_to_f32(z)
+    assert (zf >= 0).all()
+
+
 INT_EDGES = {"int32": [0, 1, -1, 2**31 - 1, -2**31, 2**30, -2**30 - 7, 46341, -46341],
              "int64": [0, 1, -1, 2**63 - 1, -2**63, 2**62, 3037000500, -3037000500, 2**32 + 1],
              "uint8": [0, 1, 2, 127, 128, 200, 255, 16, 17]}
