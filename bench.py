@@ -570,7 +570,9 @@ def cpu_baseline(torch, dev, min_seconds=10.0, component_seconds=1.5):
     """The TF-CPU restatement (oracle/: C + OpenMP, on the GPU box's CPU share
     of at most 16 threads), timed on the host in the same run.  Headline: the
     bench step's BN workload (FusedBatchNormV3 + GradV3 over the four cfg2
-    shapes in float16 and bfloat16) for at least `min_seconds`.  Components:
+    shapes in float16 and bfloat16) for at least `min_seconds`, run by
+    oracle_baseline_bn_fwd / _grad (TF's two passes, vectorized over
+    channels with F16C/AVX2 conversions; within 1 ulp of the checker).  Components:
     Adam cfg3 (25.6M f32, 10 steps), a sample of cfg5 (its [50304,2048]
     embedding and the first layer's six tensors, 153M parameters - the
     1.31B-parameter state would need 21 GB of host memory per pass), and the
@@ -598,8 +600,8 @@ def cpu_baseline(torch, dev, min_seconds=10.0, component_seconds=1.5):
                 scale = np.random.default_rng(0).uniform(0.5, 1.5, c).astype(np.float32)
                 offset = np.zeros(c, np.float32)
                 t = time.perf_counter()
-                _, _, _, sm, sv = oracle.bn_fwd(x, scale, offset, epsilon=EPS, dtype=name)
-                oracle.bn_grad(dy, x, scale, sm, sv, epsilon=EPS, dtype=name)
+                _, sm, sv = oracle.baseline_bn_fwd(x, scale, offset, EPS, dtype=name)
+                oracle.baseline_bn_grad(dy, x, scale, sm, sv, EPS, dtype=name)
                 secs += time.perf_counter() - t
                 total_bytes += 10 * x.size
                 del x, dy
@@ -663,7 +665,8 @@ def cpu_baseline(torch, dev, min_seconds=10.0, component_seconds=1.5):
              lambda: oracle.baseline_rows("mul_add", x, b, b, dtype=odt), rows)
         del x, b, a, c
     return {"value": round(gbps, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "label": "TF-CPU restatement, not TF (TensorFlow is not installed)",
+            "label": "TF-CPU restatement, not TF (TensorFlow is not installed): vectorized "
+                     "two-pass BN and row kernels, checked against the oracle",
             "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
             "seconds": round(secs, 2),
             "sample": f"{passes} pass(es) of FusedBatchNormV3+GradV3 over the 4 cfg2 shapes in "

@@ -47,6 +47,8 @@ def load():
     lib.oracle_eltwise.argtypes = [i, i, i, vp, vp, vp, i, vp, vp]
     lib.oracle_bias_add_grad.argtypes = [i, vp, i64, i64, i64, vp]
     lib.oracle_baseline_rows.argtypes = [i, i, vp, vp, i, vp, i, i64, i64, vp]
+    lib.oracle_baseline_bn_fwd.argtypes = [i, vp, i64, i64, vp, vp, f, vp, vp, vp]
+    lib.oracle_baseline_bn_grad.argtypes = [i, vp, vp, i64, i64, vp, vp, vp, f, vp, vp, vp]
     lib.oracle_set_threads.argtypes = [i]
     lib.oracle_get_threads.restype = i
     lib.oracle_f32_to_f16.argtypes = [f]
@@ -58,7 +60,8 @@ def load():
     lib.oracle_bf16_to_f32.argtypes = [ctypes.c_uint16]
     lib.oracle_bf16_to_f32.restype = f
     for fn in ("oracle_bn_fwd", "oracle_bn_grad", "oracle_adam", "oracle_eltwise",
-               "oracle_bias_add_grad", "oracle_baseline_rows",
+               "oracle_bias_add_grad", "oracle_baseline_rows", "oracle_baseline_bn_fwd",
+               "oracle_baseline_bn_grad",
                "oracle_set_threads"):
         getattr(lib, fn).restype = None
     _lib = lib
@@ -308,6 +311,36 @@ def baseline_rows(op, x, b, c=None, dtype="float32"):
     lib.oracle_baseline_rows(DT[dtype], codes[op], _p(x), _p(b), int(b.ndim == 1), _p(c),
                              int(c is not None and c.ndim == 1), rows, cols, _p(out))
     return out
+
+
+def baseline_bn_fwd(x, scale, offset, epsilon, dtype="float32"):
+    """CPU baseline of the NHWC training forward (bench.py's cpu_baseline leg,
+    not the checker): x [..., C] contiguous; returns y and the population
+    mean and variance."""
+    x = np.ascontiguousarray(x)
+    c = x.shape[-1]
+    rows = x.size // c if c else 0
+    y = np.empty_like(x)
+    mean, var = np.zeros(c, np.float32), np.zeros(c, np.float32)
+    load().oracle_baseline_bn_fwd(DT[dtype], _p(x), rows, c, _p(_c(scale, np.float32)),
+                                  _p(_c(offset, np.float32)), float(epsilon), _p(y), _p(mean),
+                                  _p(var))
+    return y, mean, var
+
+
+def baseline_bn_grad(dy, x, scale, mean, var, epsilon, dtype="float32"):
+    """CPU baseline of the NHWC training gradient (bench.py's cpu_baseline
+    leg): returns x_backprop, scale_backprop, offset_backprop."""
+    x = np.ascontiguousarray(x)
+    dy = np.ascontiguousarray(dy)
+    c = x.shape[-1]
+    rows = x.size // c if c else 0
+    dx = np.empty_like(x)
+    sbp, obp = np.zeros(c, np.float32), np.zeros(c, np.float32)
+    load().oracle_baseline_bn_grad(DT[dtype], _p(dy), _p(x), rows, c, _p(_c(scale, np.float32)),
+                                   _p(_c(mean, np.float32)), _p(_c(var, np.float32)),
+                                   float(epsilon), _p(dx), _p(sbp), _p(obp))
+    return dx, sbp, obp
 
 
 def bias_add(value, bias, data_format="NHWC", relu=False, dtype="float32"):

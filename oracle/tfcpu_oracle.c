@@ -573,3 +573,202 @@ void oracle_baseline_rows(int dt, int op, const void* x, const void* b, int b_ro
     }
   }
 }
+
+/* ------------------------------------------------------------------------ */
+/* CPU baseline of the NHWC training BatchNorm (bench.py's cpu_baseline      */
+/* leg; the checker is oracle_bn_fwd / oracle_bn_grad above).  x is          */
+/* [rows, C] contiguous.  The same two passes as TF's CPU kernel (statistics, */
+/* then the outputs), vectorized over channels: per-thread sums over blocks  */
+/* of 64 rows in float, added into per-thread double sums and combined in    */
+/* thread order; the forward's sums are shifted by the first row (no         */
+/* cancellation when |mean| >> std).  Outputs round to T once (bfloat16:     */
+/* round-to-nearest-even on finite values).                                  */
+/* ------------------------------------------------------------------------ */
+#if defined(__x86_64__)
+#define BL_TARGET __attribute__((target("avx2,f16c")))
+BL_TARGET static inline __m256 bl_ld8(int dt, const void* p, int64_t i) {
+  if (dt == DT_FLOAT) return _mm256_loadu_ps((const float*)p + i);
+  const __m128i h = _mm_loadu_si128((const __m128i*)((const uint16_t*)p + i));
+  if (dt == DT_HALF) return _mm256_cvtph_ps(h);
+  return _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_cvtepu16_epi32(h), 16));
+}
+BL_TARGET static inline void bl_st8(int dt, void* p, int64_t i, __m256 v) {
+  if (dt == DT_FLOAT) {
+    _mm256_storeu_ps((float*)p + i, v);
+    return;
+  }
+  __m128i h;
+  if (dt == DT_HALF) {
+    h = _mm256_cvtps_ph(v, _MM_FROUND_TO_NEAREST_INT);
+  } else {
+    __m256i u = _mm256_castps_si256(v);
+    const __m256i lsb = _mm256_and_si256(_mm256_srli_epi32(u, 16), _mm256_set1_epi32(1));
+    u = _mm256_srli_epi32(_mm256_add_epi32(u, _mm256_add_epi32(_mm256_set1_epi32(0x7fff), lsb)),
+                          16);
+    /* 32 -> 16 bits: packus works within each 128-bit half; keep qwords 0, 2 */
+    const __m256i pk = _mm256_permute4x64_epi64(_mm256_packus_epi32(u, u), 0x08);
+    h = _mm256_castsi256_si128(pk);
+  }
+  _mm_storeu_si128((__m128i*)((uint16_t*)p + i), h);
+}
+#define BL_HW 1
+#else
+#define BL_TARGET
+#define BL_HW 0
+#endif
+
+enum { BL_BLOCK = 64 };
+
+/* Per-channel sums over rows [r0, r1) of thread t's share.  mode 0:
+ * (x - K), (x - K)^2; mode 1: dy, dy * (x - K) (K = the mean). */
+BL_TARGET static void bl_sums(int dt, int mode, const void* x, const void* dy, int64_t r0,
+                              int64_t r1, int64_t C, const float* K, float* a1, float* a2,
+                              double* d1, double* d2) {
+  const int64_t cv = BL_HW ? C / 8 * 8 : 0;
+  for (int64_t r = r0; r < r1; r += BL_BLOCK) {
+    const int64_t re = r + BL_BLOCK < r1 ? r + BL_BLOCK : r1;
+    for (int64_t c = 0; c < C; ++c) a1[c] = a2[c] = 0.f;
+    for (int64_t rr = r; rr < re; ++rr) {
+      const int64_t o = rr * C;
+      int64_t c = 0;
+#if BL_HW
+      for (; c < cv; c += 8) {
+        const __m256 xc = _mm256_sub_ps(bl_ld8(dt, x, o + c), _mm256_loadu_ps(K + c));
+        __m256 s1 = _mm256_loadu_ps(a1 + c), s2 = _mm256_loadu_ps(a2 + c);
+        if (mode == 0) {
+          s1 = _mm256_add_ps(s1, xc);
+          s2 = _mm256_add_ps(s2, _mm256_mul_ps(xc, xc));
+        } else {
+          const __m256 d = bl_ld8(dt, dy, o + c);
+          s1 = _mm256_add_ps(s1, d);
+          s2 = _mm256_add_ps(s2, _mm256_mul_ps(d, xc));
+        }
+        _mm256_storeu_ps(a1 + c, s1);
+        _mm256_storeu_ps(a2 + c, s2);
+      }
+#endif
+      for (; c < C; ++c) {
+        const float xc = ld(dt, x, o + c) - K[c];
+        if (mode == 0) {
+          a1[c] += xc;
+          a2[c] += xc * xc;
+        } else {
+          const float d = ld(dt, dy, o + c);
+          a1[c] += d;
+          a2[c] += d * xc;
+        }
+      }
+    }
+    for (int64_t c = 0; c < C; ++c) {
+      d1[c] += a1[c];
+      d2[c] += a2[c];
+    }
+  }
+}
+
+/* Sums over all rows, per-thread then in thread order: s1, s2 [C]. */
+static void bl_all_sums(int dt, int mode, const void* x, const void* dy, int64_t rows, int64_t C,
+                        const float* K, double* s1, double* s2) {
+  const int nt = g_threads;
+  double* part = (double*)calloc((size_t)nt * 2 * (size_t)C, sizeof(double));
+  float* blk = (float*)malloc((size_t)nt * 2 * (size_t)C * sizeof(float));
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(nt) schedule(static, 1)
+#endif
+  for (int t = 0; t < nt; ++t) {
+    const int64_t r0 = rows * t / nt, r1 = rows * (t + 1) / nt;
+    bl_sums(dt, mode, x, dy, r0, r1, C, K, blk + (size_t)t * 2 * C, blk + (size_t)t * 2 * C + C,
+            part + (size_t)t * 2 * C, part + (size_t)t * 2 * C + C);
+  }
+  for (int64_t c = 0; c < C; ++c) s1[c] = s2[c] = 0.0;
+  for (int t = 0; t < nt; ++t)
+    for (int64_t c = 0; c < C; ++c) {
+      s1[c] += part[(size_t)t * 2 * C + c];
+      s2[c] += part[(size_t)t * 2 * C + C + c];
+    }
+  free(part);
+  free(blk);
+}
+
+/* out[r, c] = (x - m[c]) * a[c] + b[c] (forward), or with dy: a[c] * ((dy -
+ * b[c]) - (x - m[c]) * e[c]) (gradient). */
+BL_TARGET static void bl_apply(int dt, int grad, const void* x, const void* dy, int64_t rows,
+                               int64_t C, const float* m, const float* a, const float* b,
+                               const float* e, void* out) {
+  const int64_t cv = BL_HW ? C / 8 * 8 : 0;
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+#endif
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t o = r * C;
+    int64_t c = 0;
+#if BL_HW
+    for (; c < cv; c += 8) {
+      const __m256 xc = _mm256_sub_ps(bl_ld8(dt, x, o + c), _mm256_loadu_ps(m + c));
+      __m256 v;
+      if (!grad) {
+        v = _mm256_add_ps(_mm256_mul_ps(xc, _mm256_loadu_ps(a + c)), _mm256_loadu_ps(b + c));
+      } else {
+        const __m256 d = _mm256_sub_ps(bl_ld8(dt, dy, o + c), _mm256_loadu_ps(b + c));
+        v = _mm256_mul_ps(_mm256_loadu_ps(a + c),
+                          _mm256_sub_ps(d, _mm256_mul_ps(xc, _mm256_loadu_ps(e + c))));
+      }
+      bl_st8(dt, out, o + c, v);
+    }
+#endif
+    for (; c < C; ++c) {
+      const float xc = ld(dt, x, o + c) - m[c];
+      const float v = grad ? a[c] * ((ld(dt, dy, o + c) - b[c]) - xc * e[c]) : xc * a[c] + b[c];
+      st(dt, out, o + c, v);
+    }
+  }
+}
+
+/* Training forward: y, and the population mean and variance per channel. */
+void oracle_baseline_bn_fwd(int dt, const void* x, int64_t rows, int64_t C, const float* scale,
+                            const float* offset, float eps, void* y, float* mean, float* var) {
+  if (rows <= 0 || C <= 0) return;
+  float* K = (float*)malloc(sizeof(float) * 4 * (size_t)C);
+  float* a = K + C;
+  float* b = a + C;
+  float* m = b + C;
+  double* s = (double*)malloc(sizeof(double) * 2 * (size_t)C);
+  for (int64_t c = 0; c < C; ++c) K[c] = ld(dt, x, c);
+  bl_all_sums(dt, 0, x, NULL, rows, C, K, s, s + C);
+  for (int64_t c = 0; c < C; ++c) {
+    const double d = s[c] / (double)rows;
+    m[c] = (float)((double)K[c] + d);
+    const double v = s[C + c] / (double)rows - d * d;
+    mean[c] = m[c];
+    var[c] = (float)(v > 0.0 ? v : 0.0);
+    a[c] = (1.0f / sqrtf(var[c] + eps)) * scale[c];
+    b[c] = offset[c];
+  }
+  bl_apply(dt, 0, x, NULL, rows, C, m, a, b, NULL, y);
+  free(K);
+  free(s);
+}
+
+/* Training gradient from the forward's mean and population variance. */
+void oracle_baseline_bn_grad(int dt, const void* dy, const void* x, int64_t rows, int64_t C,
+                             const float* scale, const float* mean, const float* var, float eps,
+                             void* dx, float* scale_bp, float* offset_bp) {
+  if (rows <= 0 || C <= 0) return;
+  float* k = (float*)malloc(sizeof(float) * 4 * (size_t)C);
+  float* a = k + C;
+  float* b = a + C;
+  float* e = b + C;
+  double* s = (double*)malloc(sizeof(double) * 2 * (size_t)C);
+  bl_all_sums(dt, 1, x, dy, rows, C, mean, s, s + C);
+  for (int64_t c = 0; c < C; ++c) {
+    k[c] = 1.0f / sqrtf(var[c] + eps);
+    offset_bp[c] = (float)s[c];
+    scale_bp[c] = (float)(s[C + c] * (double)k[c]);
+    a[c] = scale[c] * k[c];
+    b[c] = (float)(s[c] / (double)rows);
+    e[c] = (k[c] * k[c]) * (float)(s[C + c] / (double)rows);
+  }
+  bl_apply(dt, 1, x, dy, rows, C, mean, a, b, e, dx);
+  free(k);
+  free(s);
+}

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import oracle
-from tests.helpers import assert_bitwise
+from tests.helpers import assert_bitwise, ulp_diff_f32
 
 rng_global = np.random.default_rng(1234)
 
@@ -533,6 +533,68 @@ def test_baseline_rows_equals_checker(dtype, rows, cols):
     z = oracle.baseline_rows("add_relu", x, full, dtype=dtype)
     zf = z.astype(np.float32) if dtype != "bfloat16" else oracle.bf16_bits_to_f32(z)
     assert (zf >= 0).all()
+
+
+def _ord16_np(bits):
+    """uint16 half / bfloat16 bits -> integers ordered like the values."""
+    b = bits.astype(np.int32)
+    return np.where(b >= 0x8000, -(b & 0x7FFF), b)
+
+
+def _bn_ulps(got, want, dtype, atol):
+    """Largest ulp distance over elements whose difference exceeds atol."""
+    if dtype == "float32":
+        d = ulp_diff_f32(got, want)
+        d[np.abs(got - want) <= atol] = 0
+        return int(d.max())
+    g = got.view(np.uint16)
+    w = want.view(np.uint16)
+    gv = g.view(np.float16).astype(np.float32) if dtype == "float16" else oracle.bf16_bits_to_f32(g)
+    wv = w.view(np.float16).astype(np.float32) if dtype == "float16" else oracle.bf16_bits_to_f32(w)
+    d = np.abs(_ord16_np(g) - _ord16_np(w))
+    d[np.abs(gv - wv) <= atol] = 0
+    return int(d.max())
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("shape", [(4, 7, 5, 64), (3, 9, 1, 12), (2, 300, 1, 24)])
+@pytest.mark.parametrize("threads", [1, 3])
+def test_baseline_bn_matches_checker(dtype, shape, threads):
+    """bench.py times the BatchNorm CPU baseline with the vectorized two-pass
+    kernels of oracle_baseline_bn_fwd / _grad (float block sums, channel
+    vectors of 8, a scalar tail for C % 8); against the checker
+    (oracle_bn_fwd / oracle_bn_grad, pinned against torch float64 and the
+    reference's known answers above) on data whose mean is far from zero:
+    statistics within float32 rounding, 16-bit outputs within 1 ulp outside
+    a 1e-6 absolute floor, float32 outputs within 1 ulp outside a floor of 4
+    float32 ulps of max|x| (a last-bit difference of the float32 mean moves
+    x - mean by that much)."""
+    rng = np.random.default_rng(55)
+    c = shape[-1]
+    x32 = (2.0 * rng.standard_normal(shape) + 3.0).astype(np.float32)
+    dy32 = rng.standard_normal(shape).astype(np.float32)
+    conv = {"float32": lambda a: a, "float16": lambda a: a.astype(np.float16),
+            "bfloat16": oracle.f32_to_bf16_bits}[dtype]
+    x, dy = conv(x32), conv(dy32)
+    scale = rng.uniform(0.5, 1.5, c).astype(np.float32)
+    offset = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    eps = 1.001e-5
+    old = oracle.get_threads()
+    oracle.set_threads(threads)
+    try:
+        y, m, v = oracle.baseline_bn_fwd(x, scale, offset, eps, dtype)
+        ry, _, _, sm, sv = oracle.bn_fwd(x, scale, offset, epsilon=eps, dtype=dtype)
+        np.testing.assert_allclose(m, sm, rtol=2e-6, atol=1e-6)
+        np.testing.assert_allclose(v, sv, rtol=2e-5)
+        floor = 4 * 1.2e-7 * float(np.abs(x32).max()) if dtype == "float32" else 1e-6
+        assert _bn_ulps(y, ry, dtype, floor) <= 1
+        dx, sbp, obp = oracle.baseline_bn_grad(dy, x, scale, sm, sv, eps, dtype)
+        rdx, rsbp, robp = oracle.bn_grad(dy, x, scale, sm, sv, epsilon=eps, dtype=dtype)
+        np.testing.assert_allclose(obp, robp, rtol=1e-4, atol=1e-4 * np.abs(robp).max())
+        np.testing.assert_allclose(sbp, rsbp, rtol=1e-4, atol=1e-4 * np.abs(rsbp).max())
+        assert _bn_ulps(dx, rdx, dtype, floor) <= 1
+    finally:
+        oracle.set_threads(old)
 
 
 INT_EDGES = {"int32": [0, 1, -1, 2**31 - 1, -2**31, 2**30, -2**30 - 7, 46341, -46341],
