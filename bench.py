@@ -572,7 +572,8 @@ def cpu_baseline(torch, dev, min_seconds=10.0, component_seconds=1.5):
     bench step's BN workload (FusedBatchNormV3 + GradV3 over the four cfg2
     shapes in float16 and bfloat16) for at least `min_seconds`, run by
     oracle_baseline_bn_fwd / _grad (TF's two passes, vectorized over
-    channels with F16C/AVX2 conversions; within 1 ulp of the checker).  Components:
+    channels with F16C/AVX2 conversions; within 1 ulp of the checker).
+    Adam runs oracle_baseline_adam_f32 (8-wide, the checker's bits).  Components:
     Adam cfg3 (25.6M f32, 10 steps), a sample of cfg5 (its [50304,2048]
     embedding and the first layer's six tensors, 153M parameters - the
     1.31B-parameter state would need 21 GB of host memory per pass), and the
@@ -623,8 +624,8 @@ def cpu_baseline(torch, dev, min_seconds=10.0, component_seconds=1.5):
 
     def ten_steps():
         for t_ in range(1, 11):
-            oracle.adam(var, m, v, g, np.float32(0.9) ** t_, np.float32(0.999) ** t_, 1e-3, 0.9,
-                        0.999, 1e-7)
+            oracle.baseline_adam_f32(var, m, v, g, np.float32(0.9) ** t_,
+                                     np.float32(0.999) ** t_, 1e-3, 0.9, 0.999, 1e-7)
 
     rate("adam_f32_25.6M", 10 * 28 * n, ten_steps, "10 steps (t = 1..10) of 25.6M f32")
     del var, m, v, g
@@ -639,7 +640,7 @@ def cpu_baseline(torch, dev, min_seconds=10.0, component_seconds=1.5):
 
     def cfg5_step():
         for a in st:
-            oracle.adam(a[0], a[1], a[2], a[3], 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7)
+            oracle.baseline_adam_f32(a[0], a[1], a[2], a[3], 0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7)
 
     rate("grouped_adam_f32_cfg5_145", 28 * n5, cfg5_step,
          f"one step over {len(sample)} of the 145 tensors ({n5} parameters: the [50304,2048] "

@@ -47,6 +47,7 @@ def load():
     lib.oracle_eltwise.argtypes = [i, i, i, vp, vp, vp, i, vp, vp]
     lib.oracle_bias_add_grad.argtypes = [i, vp, i64, i64, i64, vp]
     lib.oracle_baseline_rows.argtypes = [i, i, vp, vp, i, vp, i, i64, i64, vp]
+    lib.oracle_baseline_adam_f32.argtypes = [vp, vp, vp, vp, i64, d, d, d, d, d, d]
     lib.oracle_baseline_bn_fwd.argtypes = [i, vp, i64, i64, vp, vp, f, vp, vp, vp]
     lib.oracle_baseline_bn_grad.argtypes = [i, vp, vp, i64, i64, vp, vp, vp, f, vp, vp, vp]
     lib.oracle_set_threads.argtypes = [i]
@@ -61,7 +62,7 @@ def load():
     lib.oracle_bf16_to_f32.restype = f
     for fn in ("oracle_bn_fwd", "oracle_bn_grad", "oracle_adam", "oracle_eltwise",
                "oracle_bias_add_grad", "oracle_baseline_rows", "oracle_baseline_bn_fwd",
-               "oracle_baseline_bn_grad",
+               "oracle_baseline_bn_grad", "oracle_baseline_adam_f32",
                "oracle_set_threads"):
         getattr(lib, fn).restype = None
     _lib = lib
@@ -180,6 +181,17 @@ def adam(var, m, v, grad, beta1_power, beta2_power, lr, beta1, beta2, epsilon,
     lib.oracle_adam(DT[dtype], _p(var), _p(m), _p(v), _p(grad), var.size, float(beta1_power),
                     float(beta2_power), float(lr), float(beta1), float(beta2), float(epsilon),
                     int(bool(use_nesterov)))
+
+
+def baseline_adam_f32(var, m, v, grad, beta1_power, beta2_power, lr, beta1, beta2, epsilon):
+    """CPU baseline of float32 ResourceApplyAdam (bench.py's cpu_baseline
+    leg, not the checker): in place, the checker's bits, 8-wide."""
+    for a in (var, m, v, grad):
+        if not a.flags["C_CONTIGUOUS"] or a.dtype != np.float32:
+            raise ValueError("arrays must be contiguous float32")
+    load().oracle_baseline_adam_f32(_p(var), _p(m), _p(v), _p(grad), var.size,
+                                    float(beta1_power), float(beta2_power), float(lr),
+                                    float(beta1), float(beta2), float(epsilon))
 
 
 def adam_mixed(var, m, v, grad, beta1_power, beta2_power, lr, beta1, beta2, epsilon,

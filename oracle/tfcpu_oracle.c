@@ -772,3 +772,45 @@ void oracle_baseline_bn_grad(int dt, const void* dy, const void* x, int64_t rows
   free(k);
   free(s);
 }
+
+/* CPU baseline of float ResourceApplyAdam (bench.py's cpu_baseline leg; the
+ * checker is oracle_adam): the checker's float operations in its order,
+ * without the per-element dtype dispatch, so the loop vectorizes (8-wide
+ * IEEE sqrt and divide give the scalar loop's bits). */
+BL_TARGET void oracle_baseline_adam_f32(float* var, float* m, float* v, const float* grad,
+                                        int64_t n, double b1p_, double b2p_, double lr_,
+                                        double b1_, double b2_, double eps_) {
+  const float b1p = (float)b1p_, b2p = (float)b2p_, lr = (float)lr_;
+  const float b1 = (float)b1_, b2 = (float)b2_, eps = (float)eps_;
+  const float alpha = (lr * sqrtf(1.0f - b2p)) / (1.0f - b1p);
+  const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
+  (void)b1;
+  const int64_t nv = BL_HW ? n / 8 : 0;
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+#endif
+  for (int64_t k = 0; k < nv; ++k) {
+#if BL_HW
+    const int64_t i = 8 * k;
+    const __m256 g = _mm256_loadu_ps(grad + i);
+    const __m256 m0 = _mm256_loadu_ps(m + i), v0 = _mm256_loadu_ps(v + i);
+    const __m256 mm =
+        _mm256_add_ps(m0, _mm256_mul_ps(_mm256_sub_ps(g, m0), _mm256_set1_ps(omb1)));
+    const __m256 vv = _mm256_add_ps(
+        v0, _mm256_mul_ps(_mm256_sub_ps(_mm256_mul_ps(g, g), v0), _mm256_set1_ps(omb2)));
+    _mm256_storeu_ps(m + i, mm);
+    _mm256_storeu_ps(v + i, vv);
+    const __m256 den = _mm256_add_ps(_mm256_sqrt_ps(vv), _mm256_set1_ps(eps));
+    const __m256 step = _mm256_div_ps(_mm256_mul_ps(mm, _mm256_set1_ps(alpha)), den);
+    _mm256_storeu_ps(var + i, _mm256_sub_ps(_mm256_loadu_ps(var + i), step));
+#endif
+  }
+  for (int64_t i = 8 * nv; i < n; ++i) {
+    const float g = grad[i];
+    const float mm = m[i] + (g - m[i]) * omb1;
+    const float vv = v[i] + (g * g - v[i]) * omb2;
+    m[i] = mm;
+    v[i] = vv;
+    var[i] = var[i] - (mm * alpha) / (sqrtf(vv) + eps);
+  }
+}

@@ -597,6 +597,25 @@ def test_baseline_bn_matches_checker(dtype, shape, threads):
         oracle.set_threads(old)
 
 
+@pytest.mark.parametrize("n", [1, 7, 8, 1003, 65536 + 5])
+def test_baseline_adam_equals_checker(n):
+    """bench.py times float32 Adam on the CPU with oracle_baseline_adam_f32
+    (8-wide AVX, no per-element dtype dispatch); ten steps of it give the
+    checker's bits (oracle_adam, pinned against torch.optim.Adam and the
+    closed forms above), including the scalar tail past the last 8."""
+    rng = np.random.default_rng(56)
+    var0 = (0.02 * rng.standard_normal(n)).astype(np.float32)
+    state = [var0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)]
+    ref = [var0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)]
+    for t in range(1, 11):
+        g = (1e-3 * rng.standard_normal(n)).astype(np.float32)
+        b1p, b2p = np.float32(0.9) ** t, np.float32(0.999) ** t
+        oracle.baseline_adam_f32(*state, g, b1p, b2p, 1e-3, 0.9, 0.999, 1e-7)
+        oracle.adam(*ref, g, b1p, b2p, 1e-3, 0.9, 0.999, 1e-7)
+    for got, want, name in zip(state, ref, ("var", "m", "v")):
+        assert_bitwise(got, want, name)
+
+
 INT_EDGES = {"int32": [0, 1, -1, 2**31 - 1, -2**31, 2**30, -2**30 - 7, 46341, -46341],
              "int64": [0, 1, -1, 2**63 - 1, -2**63, 2**62, 3037000500, -3037000500, 2**32 + 1],
              "uint8": [0, 1, 2, 127, 128, 200, 255, 16, 17]}
