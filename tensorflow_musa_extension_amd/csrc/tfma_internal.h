@@ -86,7 +86,10 @@ bool SetTune(const char* name, int value);
 // synchronizes the device once (no event exists yet to wait for, and the
 // previous stream may since have been destroyed); from then on every launch
 // ends with an event (`own`, or the trace event the launch already carries)
-// that the next switch waits for.  The caller holds the state's mutex.
+// that the next switch waits for.  A trace event goes back to the tracer's
+// pool only once its launch has completed, so waiting for it after it was
+// recorded again elsewhere never lets a launch start before the previous
+// one ended.  The caller holds the state's mutex.
 struct LaunchChain {
   hipEvent_t own = nullptr;    // created on first use
   hipEvent_t chain = nullptr;  // end of the last launch once `multi`
