@@ -326,6 +326,44 @@ def component_groups(torch, ops, dev):
                      "tfma_bn_infer", note="NCHW, coefficients from running statistics, one kernel")]
     del xn, dyn, fn_, gn, wsn, xi, wsi, bi, bin_
 
+    # One GPU's share of an 8-way data-parallel job (per-replica statistics,
+    # no exchange): the cfg2 BatchNorms at per-replica batch 32 and cfg3's
+    # Adam on 25.6M / 8 elements; the kernels only, no collective.
+    share = []
+    for shp in ((32, 56, 56, 256), (32, 28, 28, 512), (32, 14, 14, 1024), (32, 7, 7, 2048)):
+        cs = shp[-1]
+        xs_ = torch.randn(*shp, generator=gen, device=dev).half()
+        dys = torch.randn(*shp, generator=gen, device=dev).half()
+        scs = torch.rand(cs, generator=gen, device=dev) + 0.5
+        ofs = 0.1 * torch.randn(cs, generator=gen, device=dev)
+        wss = torch.empty(ops.fused_batch_norm_workspace_bytes(xs_), dtype=torch.uint8,
+                          device=dev)
+        fs = ops.bind(ops.FusedBatchNormV3, xs_, scs, ofs, e1, e1, epsilon=EPS,
+                      data_format="NHWC", is_training=True, workspace=wss)
+        rs = fs.result
+        gs = ops.bind(ops.FusedBatchNormGradV3, dys, xs_, scs, rs.reserve_space_1,
+                      rs.reserve_space_2, rs.reserve_space_3, epsilon=EPS, data_format="NHWC",
+                      is_training=True, workspace=wss)
+        Es = xs_.numel()
+        tag = "x".join(map(str, shp))
+        share += [Component(f"share8_bn_fwd_f16_{tag}", [fs], 4 * Es, Es, "tfma_bn_fwd",
+                            note="one GPU's share of cfg2 at 8-way data parallelism"),
+                  Component(f"share8_bn_grad_f16_{tag}", [gs], 6 * Es, Es, "tfma_bn_grad",
+                            note="one GPU's share of cfg2 at 8-way data parallelism")]
+    ns = 25_600_000 // 8
+
+    def share_adam_set():
+        var = 0.02 * torch.randn(ns, generator=gen, device=dev)
+        return [ops.bind(ops.ResourceApplyAdam, var, torch.zeros_like(var), torch.zeros_like(var),
+                         0.9, 0.999, 1e-3, 0.9, 0.999, 1e-7,
+                         1e-3 * torch.randn(ns, generator=gen, device=dev))]
+
+    share.append(Component("share8_adam_f32_3.2M", share_adam_set(), 28 * ns, ns,
+                           "tfma_adam_flat", make=share_adam_set,
+                           note="one GPU's share of cfg3 at 8-way sharding (ZeRO-1)"))
+    yield share
+    del share, xs_, dys, wss, fs, gs
+
     n = 25_600_000
     shapes = resnet50_shapes()
 
@@ -745,7 +783,8 @@ def bn_stamps(torch, tfma, dev, reps=5):
                 for i in range(len(STAMP_POINTS))]
 
     cases = [((32, 56, 56, 64), torch.float32, 1e-3, "cfg1")] + [
-        (s, torch.float16, EPS, "cfg2") for s in SHAPES]
+        (s, torch.float16, EPS, "cfg2") for s in SHAPES] + [
+        ((32,) + tuple(s[1:]), torch.float16, EPS, "share8") for s in SHAPES]
     print("op | " + " | ".join(STAMP_POINTS) + "   (us, mean / slowest wave)", flush=True)
     for shape, dt, eps, cfg in cases:
         gen = torch.Generator(device=dev)
