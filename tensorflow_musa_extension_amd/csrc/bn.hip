@@ -827,6 +827,11 @@ struct FusedArgs {
   // last workgroup to exit advances it for the next replay.
   unsigned long long* eslots;
   unsigned long long* ecoef;
+  // The forward's shift K of every channel ([c], one word each), published
+  // by the first row group's workgroups with their partials, so the waves
+  // finishing a channel read it with the partials instead of re-reading
+  // five elements of x.
+  unsigned long long* ekey;
   unsigned epoch;
   unsigned* epoch_dev;
   FinArgs fin;
@@ -1037,8 +1042,9 @@ __device__ __forceinline__ void finish_channels(const FusedArgs& a, int cs0, int
     __hip_atomic_store(a.gave_up, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   };
   for (int ch = cs0 + blockIdx.x + wave * gridDim.x; ch < cs1; ch += kWaves * gridDim.x) {
-    // The channel's other inputs, in flight while its partials are polled.
-    const FinIn fin_in = fin_inputs<Tr, kGrad>(a.fin, ch);
+    // The channel's other inputs, in flight while its partials are polled;
+    // the forward's shift K comes with them (lane 0 polls its word).
+    FinIn fin_in = fin_inputs<Tr, kGrad>(a.fin, ch, 0.f);
     double t1 = 0.0, t2 = 0.0;
     {
       // Lane l sums groups l, l + 64, ... (at most kMaxGroups / 64 of them):
@@ -1046,6 +1052,8 @@ __device__ __forceinline__ void finish_channels(const FusedArgs& a, int cs0, int
       // with this launch's epoch are polled again.
       const uint64_t tag = static_cast<uint64_t>(wtag) << 32;
       uint64_t v1[kEpochPerLane], v2[kEpochPerLane];
+      const bool has_key = !kGrad && lane == 0;
+      uint64_t vk = has_key ? load_shared(a.ekey + ch) : tag;
 #pragma unroll
       for (int i = 0; i < kEpochPerLane; ++i) {
         const int64_t gg = lane + 64 * i;
@@ -1058,7 +1066,7 @@ __device__ __forceinline__ void finish_channels(const FusedArgs& a, int cs0, int
       unsigned spins = 0;
       bool lost = false;
       while (true) {
-        bool ready = true;
+        bool ready = (vk >> 32) == (tag >> 32);
 #pragma unroll
         for (int i = 0; i < kEpochPerLane; ++i)
           ready = ready && (v1[i] >> 32) == (tag >> 32) && (v2[i] >> 32) == (tag >> 32);
@@ -1069,6 +1077,7 @@ __device__ __forceinline__ void finish_channels(const FusedArgs& a, int cs0, int
           break;
         }
         __builtin_amdgcn_s_sleep(1);
+        if ((vk >> 32) != (tag >> 32)) vk = load_shared(a.ekey + ch);
 #pragma unroll
         for (int i = 0; i < kEpochPerLane; ++i) {
           const int64_t gg = lane + 64 * i;
@@ -1077,6 +1086,7 @@ __device__ __forceinline__ void finish_channels(const FusedArgs& a, int cs0, int
             v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
         }
       }
+      fin_in.k = __builtin_bit_cast(float, static_cast<uint32_t>(vk));
 #pragma unroll
       for (int i = 0; i < kEpochPerLane; ++i) {
         if (lane + 64 * i < a.groups) {
@@ -1341,6 +1351,13 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       if (q + u < nk) accum_words<Tr, kGrad>(xw[u], dw[u], k, s1, s2);
   }
   stamp(1);
+  if constexpr (!kGrad) {
+    if (g == 0 && ty == 0 && active) {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j)
+        store_shared(a.ekey + c0 + j, etag | __builtin_bit_cast(uint32_t, k[j]));
+    }
+  }
   publish_partials<VEC>(a, red, s1, s2, tid, width, ct, g, etag);
   stamp(2);
 
@@ -2556,7 +2573,7 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   // regions are zeroed again.
   if (!bs->eslots) {
     const size_t slot_bytes = static_cast<size_t>(2 * DeviceCUs()) * 256 * 16;
-    const size_t coef_bytes = static_cast<size_t>(2 * DeviceCUs()) * 256 * 32;
+    const size_t coef_bytes = static_cast<size_t>(2 * DeviceCUs()) * 256 * 40;  // 4 + 1 words
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, slot_bytes + coef_bytes);
     if (e != hipSuccess) return e;
@@ -2577,7 +2594,7 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   }
   if (fp.groups > kMaxEpochGroups ||
       static_cast<size_t>(fp.groups) * g.c * 16 > bs->eslot_bytes ||
-      static_cast<size_t>(g.c) * 32 > bs->ecoef_bytes)
+      static_cast<size_t>(g.c) * 40 > bs->ecoef_bytes)
     return hipErrorInvalidValue;  // excluded by make_fused_plan
   unsigned long long* region =
       recorded ? reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(bs->counter) +
@@ -2627,6 +2644,8 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   fa.reset_at_exit = recorded ? 1 : 0;
   fa.eslots = bs->eslots;
   fa.ecoef = bs->ecoef;
+  // The key words after the largest coefficient array ([C][4] words).
+  fa.ekey = bs->ecoef + bs->ecoef_bytes / 40 * 4;
   fa.epoch = epoch;
   fa.epoch_dev = recorded ? reinterpret_cast<unsigned*>(reinterpret_cast<char*>(region) +
                                                         kEpochOffset)
