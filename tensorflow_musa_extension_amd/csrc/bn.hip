@@ -1110,6 +1110,89 @@ __device__ __forceinline__ void finish_channels(const FusedArgs& a, int cs0, int
   }
 }
 
+// Phase 2 in blocks of B consecutive channels (for kernels with registers
+// to spare): block j of [cs0, cs1) is finished by wave j / gridDim.x of
+// workgroup j % gridDim.x.  Lane l reads channel l % B of groups l / B,
+// l / B + 64 / B, ... - so each group's B channels are one contiguous
+// segment of partial words (B * 16 bytes) instead of B words a line apart
+// - sums them in group order, then across the lanes of its channel; lanes
+// 0 .. B-1 finish one channel each.  B = 16, or smaller where the groups
+// need more than kEpochPerLane words per lane.  Same give-up behaviour as
+// finish_channels.
+template <class Tr, bool kGrad>
+__device__ __forceinline__ void finish_channel_blocks(const FusedArgs& a, int cs0, int cs1,
+                                                      int wave, int lane, uint32_t wtag,
+                                                      uint64_t etag, unsigned epoch) {
+  constexpr int kWaves = kFusedThreads / 64;
+  int B = 16;
+  while (B > 1 && static_cast<int64_t>(64 / B) * kEpochPerLane < a.groups) B >>= 1;
+  const int gpl = 64 / B;
+  const int cl = lane % B, gl = lane / B;
+  const int nb = (cs1 - cs0 + B - 1) / B;
+  const uint64_t tag = static_cast<uint64_t>(wtag) << 32;
+  auto tagged = [&](uint64_t v) { return (v >> 32) == (tag >> 32); };
+  for (int blk = blockIdx.x + wave * gridDim.x; blk < nb; blk += kWaves * gridDim.x) {
+    const int ch = cs0 + blk * B + cl;
+    const bool chv = ch < cs1;
+    FinIn fin_in = fin_inputs<Tr, kGrad>(a.fin, chv ? ch : cs1 - 1, 0.f);
+    uint64_t vk = !kGrad && chv ? load_shared(a.ekey + ch) : tag;
+    uint64_t v1[kEpochPerLane], v2[kEpochPerLane];
+#pragma unroll
+    for (int i = 0; i < kEpochPerLane; ++i) {
+      const int64_t gg = gl + static_cast<int64_t>(gpl) * i;
+      v1[i] = v2[i] = tag;
+      if (chv && gg < a.groups) {
+        v1[i] = load_shared(a.eslots + 2 * (gg * a.c + ch));
+        v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
+      }
+    }
+    unsigned spins = 0;
+    bool lost = false;
+    while (true) {
+      bool ready = tagged(vk);
+#pragma unroll
+      for (int i = 0; i < kEpochPerLane; ++i) ready = ready && tagged(v1[i]) && tagged(v2[i]);
+      if (ready) break;
+      if (++spins > a.spin_limit) {
+        lost = true;
+        __hip_atomic_store(a.gave_up, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      if (!tagged(vk)) vk = load_shared(a.ekey + ch);
+#pragma unroll
+      for (int i = 0; i < kEpochPerLane; ++i) {
+        const int64_t gg = gl + static_cast<int64_t>(gpl) * i;
+        if (!tagged(v1[i])) v1[i] = load_shared(a.eslots + 2 * (gg * a.c + ch));
+        if (!tagged(v2[i])) v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
+      }
+    }
+    fin_in.k = __builtin_bit_cast(float, static_cast<uint32_t>(vk));
+    double t1 = 0.0, t2 = 0.0;
+#pragma unroll
+    for (int i = 0; i < kEpochPerLane; ++i) {
+      if (chv && gl + static_cast<int64_t>(gpl) * i < a.groups) {
+        t1 += __builtin_bit_cast(float, static_cast<uint32_t>(v1[i]));
+        t2 += __builtin_bit_cast(float, static_cast<uint32_t>(v2[i]));
+      }
+    }
+    // A lane whose partials never arrived poisons its channel's sums.
+    if (lost) t1 = t2 = __builtin_nan("");
+    for (int off = 32; off >= B; off >>= 1) {
+      t1 += __shfl_xor(t1, off, 64);
+      t2 += __shfl_xor(t2, off, 64);
+    }
+    if (lane < B && chv) {
+      const float4 cfc = finish_channel<Tr, kGrad>(a.fin, ch, t1, t2, fin_in);
+      const float v4[4] = {cfc.x, cfc.y, cfc.z, cfc.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        store_shared(a.ecoef + 4 * static_cast<int64_t>(ch) + i,
+                     etag | __builtin_bit_cast(uint32_t, v4[i]));
+    }
+  }
+}
+
 // The coefficients of channel tile ct (4 words per channel, at most 1024
 // words: two per thread, consecutive words to consecutive threads, so the
 // cross-XCD loads stay coalesced), polled until tagged with this launch's
@@ -1380,7 +1463,13 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   const int64_t qb = nk - 1 - (pre_a ? PA : 0);  // first row of part B
 
   // ---- phase 2: per-channel finals ---------------------------------------
-  finish_channels<Tr, kGrad>(a, cs0, cs1, wave, lane, wtag, etag, epoch);
+  // In channel blocks where the registers allow it (the small-shape forward
+  // and the unsliced half / bfloat16 grads), else a channel per wave.
+  constexpr bool kBlockFin = kGrad ? (!kSliced && sizeof(S) == 2) : KR <= 8;
+  if constexpr (kBlockFin)
+    finish_channel_blocks<Tr, kGrad>(a, cs0, cs1, wave, lane, wtag, etag, epoch);
+  else
+    finish_channels<Tr, kGrad>(a, cs0, cs1, wave, lane, wtag, etag, epoch);
   if (sl == 0) zero_side_outputs<kGrad>(a.fin);
   stamp(3);
 
