@@ -1110,8 +1110,8 @@ __device__ __forceinline__ void finish_channels(const FusedArgs& a, int cs0, int
   }
 }
 
-// Phase 2 in blocks of B consecutive channels (for kernels with registers
-// to spare): block j of [cs0, cs1) is finished by wave j / gridDim.x of
+// Phase 2 in blocks of B consecutive channels (every fused kernel whose
+// registers allow it): block j of [cs0, cs1) is finished by wave j / gridDim.x of
 // workgroup j % gridDim.x.  Lane l reads channel l % B of groups l / B,
 // l / B + 64 / B, ... - so each group's B channels are one contiguous
 // segment of partial words (B * 16 bytes) instead of B words a line apart
@@ -1463,9 +1463,9 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   const int64_t qb = nk - 1 - (pre_a ? PA : 0);  // first row of part B
 
   // ---- phase 2: per-channel finals ---------------------------------------
-  // In channel blocks where the registers allow it (the small-shape forward
-  // and the unsliced half / bfloat16 grads), else a channel per wave.
-  constexpr bool kBlockFin = kGrad ? (!kSliced && sizeof(S) == 2) : KR <= 8;
+  // In channel blocks where the registers allow it (all but the unsliced
+  // float grad, which would spill), else a channel per wave.
+  constexpr bool kBlockFin = !(kGrad && !kSliced && sizeof(S) == 4);
   if constexpr (kBlockFin)
     finish_channel_blocks<Tr, kGrad>(a, cs0, cs1, wave, lane, wtag, etag, epoch);
   else
@@ -1847,7 +1847,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_sliced_grad_kernel(FusedArgs
     const int cs0 = sl * width;
     const int cs1 = a.c < cs0 + width ? a.c : cs0 + width;
     // ---- phase 2 of slice sl ----
-    finish_channels<Tr, true>(a, cs0, cs1, wave, lane, wtag, etag, epoch);
+    finish_channel_blocks<Tr, true>(a, cs0, cs1, wave, lane, wtag, etag, epoch);
     if (sl == 0) zero_side_outputs<true>(a.fin);
     const bool more = sl + 1 < nslices;
     // ---- while slice sl's coefficients are pending: the streamed rows of
