@@ -75,6 +75,12 @@ CASES = [
     ((16, 7, 7, 33), "float16", "NHWC"),     # odd C: scalar path
     ((5, 3, 3, 520), "bfloat16", "NHWC"),    # C % 256 != 0: partial channel tile
     ((2, 3, 5, 5), "float32", "NCHW"),
+    # The reference's regression shapes (test/ops/fused_batchnorm_op_test.py):
+    # Keras' 2-D BatchNormalization as [N,1,1,C] (:97-141), the NCHW grad
+    # (:178-216) and the NCHW batch / saved variance values (:407-).
+    ((512, 1, 1, 64), "float32", "NHWC"),
+    ((4, 8, 6, 6), "float32", "NCHW"),
+    ((2, 3, 4, 5), "float32", "NCHW"),
     ((4, 16, 7, 7), "float16", "NCHW"),
     ((2, 8, 28, 28), "bfloat16", "NCHW"),
     ((3, 6, 8, 8), "float32", "NCHW"),
@@ -104,6 +110,60 @@ def test_fwd_grad_matches_oracle(dev, shape, dtype, data_format):
     assert_close(grad.scale_backprop.cpu().numpy(), rsb, "float32", STAT_TOL, "scale_backprop")
     assert_close(grad.offset_backprop.cpu().numpy(), rob, "float32", STAT_TOL, "offset_backprop")
     assert torch.all(grad.reserve_space_4 == 0) and torch.all(grad.reserve_space_5 == 0)
+
+
+def test_dense_weight_grad_through_batch_norm(dev):
+    """The reference's testFusedBatchNormGradDX2DWeightGrad
+    (test/ops/fused_batchnorm_op_test.py:143-176): h = x @ w of [4096,128] x
+    [128,256], BatchNormalization over the 256 features as the [N,1,1,C] op
+    Keras runs, loss = sum(y), and the dense layer's weight gradient
+    dW = x^T @ dh compared with the same product of the oracle's dh (float64
+    products, rtol 1e-3 and atol 1e-3 as there)."""
+    rng = np.random.default_rng(61)
+    xin = rng.standard_normal((4096, 128)).astype(np.float32)
+    w = rng.standard_normal((128, 256)).astype(np.float32)
+    h = (xin @ w).astype(np.float32).reshape(4096, 1, 1, 256)
+    scale = np.ones(256, np.float32)
+    offset = np.zeros(256, np.float32)
+    dy = np.ones_like(h)  # d sum(y) / dy
+    eps = 1e-5
+    fwd, grad = _run_fwd_grad(dev, h, scale, offset, dy, "float32", "NHWC", eps)
+    rdx, _, _ = oracle.bn_grad(dy, h, scale, fwd.reserve_space_1.cpu().numpy(),
+                               fwd.reserve_space_2.cpu().numpy(), epsilon=eps)
+    dx = grad.x_backprop.cpu().numpy().reshape(4096, 256).astype(np.float64)
+    dw = xin.astype(np.float64).T @ dx
+    rdw = xin.astype(np.float64).T @ rdx.reshape(4096, 256).astype(np.float64)
+    np.testing.assert_allclose(dw, rdw, rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_layer_norm_grad_large_variance(dev, dtype):
+    """The reference's testLayerNormGradNCHWLargeVariance
+    (test/ops/fused_batchnorm_op_test.py:218-256): Keras' LayerNormalization
+    of [128,1536] runs FusedBatchNormV3 / GradV3 on NCHW [1,128,1536,1]
+    (128 channels of 1536 elements), x = 10 N(0,1) (variance 100), dy =
+    1e-3 N(0,1), epsilon 1e-3; the grad must use the population variance
+    from reserve_space_2 (the reference's bug: a variance passed where the
+    reciprocal standard deviation was expected inflated dx by orders of
+    magnitude).  Against the oracle at this file's bars."""
+    rng = np.random.default_rng(42)
+    x = gen(rng, (1, 128, 1536, 1), dtype, scale=10.0)
+    dy = gen(rng, (1, 128, 1536, 1), dtype, scale=1e-3)
+    scale = np.ones(128, np.float32)
+    offset = np.zeros(128, np.float32)
+    eps = 1e-3
+    fwd, grad = _run_fwd_grad(dev, x, scale, offset, dy, dtype, "NCHW", eps)
+    ry, _, _, rsm, rsv = oracle.bn_fwd(x, scale, offset, epsilon=eps, data_format="NCHW",
+                                       dtype=dtype)
+    assert_close(to_np(fwd.y, dtype), ry, dtype, ACT_TOL[dtype], "y")
+    assert_close(fwd.reserve_space_2.cpu().numpy(), rsv, "float32", STAT_TOL, "reserve_space_2")
+    rdx, rsb, rob = oracle.bn_grad(dy, x, scale, fwd.reserve_space_1.cpu().numpy(),
+                                   fwd.reserve_space_2.cpu().numpy(), epsilon=eps,
+                                   data_format="NCHW", dtype=dtype)
+    assert_close(to_np(grad.x_backprop, dtype), rdx, dtype, ACT_TOL[dtype], "x_backprop")
+    assert_close(grad.scale_backprop.cpu().numpy(), rsb, "float32", STAT_TOL, "scale_backprop")
+    # dx stays at the scale of dy / std (1e-4), not inflated
+    assert float(grad.x_backprop.float().abs().max()) < 1e-2
 
 
 SLICED_CASES = [
