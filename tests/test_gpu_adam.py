@@ -376,3 +376,36 @@ def test_adam_int_matches_oracle(dev, dtype):
         torch.cuda.synchronize()
         for name, got, want in (("var", tv, rv), ("m", tm, rm), ("v", tvv, rvv)):
             np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=f"{name} {sc}")
+
+
+def test_resource_apply_adam_reference_setup(dev):
+    """The setup of the reference's ResourceApplyAdam test
+    (test/ops/apply_resource_op_test.py:12-55): float32 variables, one update
+    with beta1_power 0.9, beta2_power 0.999, lr 0.01, beta1 0.9, beta2 0.999,
+    epsilon 1e-8, use_nesterov False.  Checked bitwise against the oracle and,
+    from m = v = 0, against the closed form of the first step:
+    var - 0.01 * sqrt(0.001) * g / (sqrt(0.001) * |g| + 1e-8)."""
+    rng = np.random.default_rng(21)
+    n = 4099
+    var = rng.standard_normal(n).astype(np.float32)
+    g = (rng.standard_normal(n) * 10.0 ** rng.integers(-6, 2, n)).astype(np.float32)
+    zeros = np.zeros(n, np.float32)
+    tv, tm, tvv = (torch.from_numpy(a.copy()).to(dev) for a in (var, zeros, zeros))
+    ops.ResourceApplyAdam(tv, tm, tvv, 0.9, 0.999, 0.01, 0.9, 0.999, 1e-8,
+                          torch.from_numpy(g).to(dev), use_nesterov=False)
+    torch.cuda.synchronize()
+    rv, rm, rvv = var.copy(), zeros.copy(), zeros.copy()
+    oracle.adam(rv, rm, rvv, g, _t_scalar(0.9, "float32"), _t_scalar(0.999, "float32"),
+                _t_scalar(0.01, "float32"), _t_scalar(0.9, "float32"),
+                _t_scalar(0.999, "float32"), _t_scalar(1e-8, "float32"), dtype="float32")
+    for name, got, ref in (("var", tv, rv), ("m", tm, rm), ("v", tvv, rvv)):
+        assert_bitwise(got.cpu().numpy(), ref, name)
+    g64 = g.astype(np.float64)
+    step = 0.01 * np.sqrt(0.001) * g64 / (np.sqrt(0.001) * np.abs(g64) + 1e-8)
+    got_step = var.astype(np.float64) - tv.cpu().numpy().astype(np.float64)
+    # f32 rounding of var (|var| < 6) and of the update: a few float ulps.
+    assert np.max(np.abs(got_step - step)) < 4e-6
+    # 1 - beta is taken in float32: 1 - f32(0.9) is 0.1 within 2.4e-7 and
+    # 1 - f32(0.999) is 0.001 within 1.3e-5, relative.
+    np.testing.assert_allclose(tm.cpu().numpy(), 0.1 * g64, rtol=5e-7, atol=0)
+    np.testing.assert_allclose(tvv.cpu().numpy(), 0.001 * g64 * g64, rtol=2e-5, atol=0)

@@ -84,6 +84,13 @@ CASES = [
     ((4, 16, 7, 7), "float16", "NCHW"),
     ((2, 8, 28, 28), "bfloat16", "NCHW"),
     ((3, 6, 8, 8), "float32", "NCHW"),
+    # test/ops/fused_batchnorm_hcnw_op_test.py:86-105
+    ((2, 32, 1, 1), "float32", "NCHW"),
+    ((2, 1, 1, 32), "float32", "NHWC"),
+    ((4, 16, 8, 8), "float16", "NCHW"),
+    ((1, 64, 32, 32), "float32", "NCHW"),
+    ((8, 128, 16, 16), "float32", "NCHW"),
+    ((2, 3, 224, 224), "float32", "NCHW"),
 ]
 
 

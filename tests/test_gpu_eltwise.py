@@ -15,7 +15,9 @@ DTYPES = ["float32", "float16", "bfloat16"]
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("shape", [(8192, 4096), (8191, 4095), (3, 5), (1, 1), (7, 9, 33)])
+@pytest.mark.parametrize("shape", [(8192, 4096), (8191, 4095), (3, 5), (1, 1), (7, 9, 33),
+                                   # the reference's shapes (test/ops/biasadd_op_test.py:74-116)
+                                   (10, 5), (2, 3, 4, 5), (2, 3, 4), (100, 50)])
 @pytest.mark.parametrize("relu", [False, True])
 def test_bias_add_nhwc(dev, dtype, shape, relu):
     rng = np.random.default_rng(1)
@@ -28,15 +30,18 @@ def test_bias_add_nhwc(dev, dtype, shape, relu):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("shape", [(4, 16, 7, 7), (2, 3, 5, 8), (2, 5, 3)])
-def test_bias_add_relu_nchw(dev, dtype, shape):
+@pytest.mark.parametrize("shape", [(4, 16, 7, 7), (2, 3, 5, 8), (2, 5, 3),
+                                   (2, 5, 3, 4)])   # biasadd_op_test.py:88-91
+@pytest.mark.parametrize("relu", [False, True])
+def test_bias_add_nchw(dev, dtype, shape, relu):
     rng = np.random.default_rng(2)
     x = gen(rng, shape, dtype)
     b = gen(rng, shape[1:2], dtype)
-    out = ops.MusaBiasAddRelu(to_dev(x, dtype, dev), to_dev(b, dtype, dev), data_format="NCHW")
+    fn = ops.MusaBiasAddRelu if relu else ops.BiasAdd
+    out = fn(to_dev(x, dtype, dev), to_dev(b, dtype, dev), data_format="NCHW")
     torch.cuda.synchronize()
-    ref = oracle.bias_add(x, b, data_format="NCHW", relu=True, dtype=dtype)
-    assert_bitwise(to_np(out, dtype), ref, "bias_add_relu nchw")
+    ref = oracle.bias_add(x, b, data_format="NCHW", relu=relu, dtype=dtype)
+    assert_bitwise(to_np(out, dtype), ref, "bias_add nchw")
 
 
 BCAST = [
@@ -60,6 +65,16 @@ BCAST = [
     ((4, 1, 5), (1, 3, 1)),         # neither operand full: strided path
     ((2, 3, 4, 8), (3, 1, 8)),      # two broadcast runs: strided path
     ((0, 4), (4,)),                 # empty
+    # the reference's hot shapes (test/ops/add_op_test.py:80-107,
+    # multiply_op_test.py:114-126)
+    ((7, 48), (48,)),
+    ((5, 64), (64,)),
+    ((3, 768), (1, 768)),
+    ((2, 8, 160), (160,)),
+    ((), (64,)),
+    ((1024, 1024), (1024, 1024)),
+    ((1024, 1024), ()),
+    ((1024, 1024), (1024,)),
 ]
 
 
@@ -90,6 +105,8 @@ INT_BCAST = [
     ((4, 1, 5), (1, 3, 1)),
     ((3, 9001), (9001,)),
     ((0, 4), (4,)),
+    ((1024, 1024), ()),             # the reference's Mul hot shapes with int32 / int64
+    ((1024, 1024), (1024,)),
 ]
 
 
@@ -115,7 +132,8 @@ def test_integer_add_mul(dev, dtype, xs, ys):
 
 @pytest.mark.parametrize("dtype", ["int32", "int64"])
 @pytest.mark.parametrize("shape,fmt", [((8192, 4096), "NHWC"), ((8191, 4095), "NHWC"),
-                                       ((4, 16, 7, 7), "NCHW"), ((2, 5, 3), "NCHW")])
+                                       ((4, 16, 7, 7), "NCHW"), ((2, 5, 3), "NCHW"),
+                                       ((5, 3), "NHWC")])   # biasadd_op_test.py:98-111
 def test_integer_bias_add(dev, dtype, shape, fmt):
     """BiasAdd / BiasAddV1 for int32 and int64 (musa_biasadd_op.cc:67-79)."""
     rng = np.random.default_rng(9)
@@ -146,6 +164,10 @@ MULADD = [
     ((5, 7), (5, 7), ()),
     ((5, 1, 7), (1, 3, 1), (3, 7)),               # strided path
     ((1024, 1021), (1021,), (1021,)),             # two staged odd-period operands
+    # the reference's cases (test/ops/shifted_affine_map_op_test.py:53-152)
+    ((2, 4, 8), (2, 4, 8), (8,)),
+    ((2, 1, 4, 8), (2, 3, 1, 8), (1, 3, 4, 1)),   # rank expansion, multi-axis broadcast
+    ((0, 8), (0, 8), (8,)),                       # empty
 ]
 
 
@@ -252,3 +274,46 @@ def test_signed_zero_products(dev, dtype):
         assert np.all(np.signbit(oracle.to_f32(w, dtype)[:4]) == [True, True, True, True]) or \
             k == "relu_grad"
         assert_bitwise(to_np(t, dtype), w, f"{dtype} {k}")
+
+
+def test_multiply_zero_values_and_float64(dev):
+    """The reference's testMultiplyZeroValues and testMultiplyFloat64StaysOnMusa
+    (test/ops/multiply_op_test.py:99-112, 128-140): literal operands and
+    results, the float64 product on the device."""
+    x = torch.tensor([[0.0, 1.0], [2.0, 0.0]], device=dev)
+    y = torch.tensor([[1.0, 0.0], [0.0, 3.0]], device=dev)
+    out = ops.Mul(x, y)
+    assert out.device.type == "cuda"
+    assert torch.equal(out.cpu(), torch.zeros(2, 2))
+    d = ops.Mul(torch.tensor([2.0], dtype=torch.float64, device=dev),
+                torch.tensor([3.0], dtype=torch.float64, device=dev))
+    assert d.dtype == torch.float64 and d.device.type == "cuda"
+    assert float(d.cpu()[0]) == 6.0
+
+
+F64_CASES = [
+    ((2, 3, 4), (2, 1, 4), (4,)),       # shifted_affine_map_op_test.py:121-136
+    ((8191, 4095), (4095,), (4095,)),
+    ((64, 37, 33), (37, 1), (33,)),
+    ((4, 1, 5), (1, 3, 1), (3, 5)),     # strided path
+    ((0, 4), (4,), (4,)),
+]
+
+
+@pytest.mark.parametrize("xs,ys,zs", F64_CASES)
+def test_float64_binary_and_mul_add(dev, xs, ys, zs):
+    """The float64 registrations (AddV2, Mul, MusaAddV2Relu,
+    MusaShiftedAffineMap) against numpy's IEEE double arithmetic: every op
+    rounds once per TF op (mul_add rounds the product, then the sum), so the
+    bar is bitwise."""
+    rng = np.random.default_rng(12)
+    x, y, z = (rng.standard_normal(s) for s in (xs, ys, zs))
+    xd, yd, zd = (torch.from_numpy(a).to(dev) for a in (x, y, z))
+    s = x + y
+    for name, got, ref in (
+            ("AddV2", ops.AddV2(xd, yd), s),
+            ("Mul", ops.Mul(xd, yd), x * y),
+            ("MusaAddV2Relu", ops.MusaAddV2Relu(xd, yd), np.where(s < 0, 0.0, s)),
+            ("MusaShiftedAffineMap", ops.MusaShiftedAffineMap(xd, yd, zd), y * x + z)):
+        assert got.dtype == torch.float64
+        assert_bitwise(got.cpu().numpy(), ref, name)
