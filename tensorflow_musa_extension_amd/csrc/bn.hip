@@ -749,6 +749,16 @@ constexpr unsigned kSpinLimit = 1u << 24;
 // Epoch-tagged partials: at most 8 row groups per lane of a finishing wave.
 constexpr int kEpochPerLane = 8;
 constexpr int64_t kMaxEpochGroups = 64 * kEpochPerLane;
+// Copies of the epoch-tagged coefficient words (at most kCoefCopies, one
+// per kPollersPerCopy row groups of a tile): the finishing waves store every
+// channel's coefficients into each copy and the workgroups of row group g
+// poll copy g mod copies, so the polls of a tile's workgroups are spread
+// over as many line sets instead of queueing on the few lines of one.
+#ifndef TFMA_COEF_COPIES
+#define TFMA_COEF_COPIES 8
+#endif
+constexpr int kCoefCopies = TFMA_COEF_COPIES;
+constexpr int kPollersPerCopy = 32;
 // Resident 16-byte vectors per thread and per input tensor: KR in VGPRs (the
 // largest counts that compile without spills at 256 VGPRs), KL in LDS (the
 // LDS budget split over the inputs).  kOpaque*: the register rows are made
@@ -827,6 +837,8 @@ struct FusedArgs {
   // last workgroup to exit advances it for the next replay.
   unsigned long long* eslots;
   unsigned long long* ecoef;
+  int64_t coef_copy;            // words from one copy of `ecoef` to the next
+  int coef_copies;              // copies in use (1 .. kCoefCopies)
   // The forward's shift K of every channel ([c], one word each), published
   // by the first row group's workgroups with their partials, so the waves
   // finishing a channel read it with the partials instead of re-reading
@@ -1028,6 +1040,23 @@ __device__ __forceinline__ void publish_partials(const FusedArgs& a, float2* red
   }
 }
 
+// Stores the coefficients of a finished channel block into every copy:
+// lanes [0, B) hold channels cb .. cb + B - 1 (lane l's channel is ch, the
+// one of lane l mod B; chv: it exists); lane l stores copies l / B,
+// l / B + 64 / B, ...  Every lane of the wave takes part (shuffles).
+__device__ __forceinline__ void store_coefs(const FusedArgs& a, int ch, bool chv, float4 cfc,
+                                            int lane, int B, uint64_t etag) {
+  const int src = lane % B;
+  const float v4[4] = {__shfl(cfc.x, src, 64), __shfl(cfc.y, src, 64), __shfl(cfc.z, src, 64),
+                       __shfl(cfc.w, src, 64)};
+  if (!chv) return;
+  for (int r = lane / B; r < a.coef_copies; r += 64 / B) {
+    unsigned long long* const dst = a.ecoef + r * a.coef_copy + 4 * static_cast<int64_t>(ch);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_shared(dst + i, etag | __builtin_bit_cast(uint32_t, v4[i]));
+  }
+}
+
 // Phase 2 for channels [cs0, cs1): channel ch is finished by wave
 // (ch - cs0) / gridDim.x of workgroup (ch - cs0) % gridDim.x, one channel
 // at a time per wave, so all of a workgroup's partial loads are in flight
@@ -1099,14 +1128,9 @@ __device__ __forceinline__ void finish_channels(const FusedArgs& a, int cs0, int
       if (lost) t1 = t2 = __builtin_nan("");
     }
     const double2 w = wave_sum(t1, t2);
-    if (lane == 0) {
-      const float4 cfc = finish_channel<Tr, kGrad>(a.fin, ch, w.x, w.y, fin_in);
-      const float v4[4] = {cfc.x, cfc.y, cfc.z, cfc.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        store_shared(a.ecoef + 4 * static_cast<int64_t>(ch) + i,
-                     etag | __builtin_bit_cast(uint32_t, v4[i]));
-    }
+    float4 cfc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (lane == 0) cfc = finish_channel<Tr, kGrad>(a.fin, ch, w.x, w.y, fin_in);
+    store_coefs(a, ch, true, cfc, lane, 1, etag);
   }
 }
 
@@ -1182,14 +1206,9 @@ __device__ __forceinline__ void finish_channel_blocks(const FusedArgs& a, int cs
       t1 += __shfl_xor(t1, off, 64);
       t2 += __shfl_xor(t2, off, 64);
     }
-    if (lane < B && chv) {
-      const float4 cfc = finish_channel<Tr, kGrad>(a.fin, ch, t1, t2, fin_in);
-      const float v4[4] = {cfc.x, cfc.y, cfc.z, cfc.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        store_shared(a.ecoef + 4 * static_cast<int64_t>(ch) + i,
-                     etag | __builtin_bit_cast(uint32_t, v4[i]));
-    }
+    float4 cfc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (lane < B && chv) cfc = finish_channel<Tr, kGrad>(a.fin, ch, t1, t2, fin_in);
+    store_coefs(a, ch, chv, cfc, lane, B, etag);
   }
 }
 
@@ -1214,6 +1233,9 @@ __device__ __forceinline__ void tile_coefs(const FusedArgs& a, float2* red, int 
                 "coefficients fit in red");
   float* const cs = reinterpret_cast<float*>(red);
   const uint64_t tag = static_cast<uint64_t>(wtag) << 32;
+  // Row group blockIdx.x / ct_conc polls its copy.
+  const unsigned long long* const ecoef =
+      a.ecoef + ((blockIdx.x / a.ct_conc) % a.coef_copies) * a.coef_copy;
   uint64_t v[2];
   int64_t wi[2];
 #pragma unroll
@@ -1221,7 +1243,7 @@ __device__ __forceinline__ void tile_coefs(const FusedArgs& a, float2* red, int 
     wi[i] = tid + kFusedThreads * i;
     const int64_t chn = static_cast<int64_t>(ct) * width + (wi[i] >> 2);
     const bool need = (wi[i] >> 2) < width && chn < a.c;
-    v[i] = need ? load_shared(a.ecoef + 4 * chn + (wi[i] & 3)) : tag;
+    v[i] = need ? load_shared(ecoef + 4 * chn + (wi[i] & 3)) : tag;
     if (!need) wi[i] = -1;
   }
   unsigned spins = 0;
@@ -1238,7 +1260,7 @@ __device__ __forceinline__ void tile_coefs(const FusedArgs& a, float2* red, int 
     for (int i = 0; i < 2; ++i) {
       if ((v[i] >> 32) != (tag >> 32)) {
         const int64_t chn = static_cast<int64_t>(ct) * width + (wi[i] >> 2);
-        v[i] = load_shared(a.ecoef + 4 * chn + (wi[i] & 3));
+        v[i] = load_shared(ecoef + 4 * chn + (wi[i] & 3));
       }
     }
   }
@@ -2385,6 +2407,13 @@ struct FusedPlan {
   int dyn_chunk;  // rows per thread in one chunk
 };
 
+// Channels of the largest fused plan (at most 2 workgroups per CU, tiles of
+// at most 256 channels), and the words from one copy of the epoch-tagged
+// coefficients ([C][4]) to the next: 4 KiB + 256 B more than a copy holds,
+// so the copies start at different offsets within a page.
+int64_t max_fused_channels() { return static_cast<int64_t>(2 * DeviceCUs()) * 256; }
+size_t coef_copy_words() { return static_cast<size_t>(max_fused_channels()) * 4 + 544; }
+
 // Share of each thread's streamed rows (after the prefetched ones) that is
 // handed out dynamically in phase 3 (percent; TFMA_BN_DYN_PCT, default 20).
 int dyn_pct() {
@@ -2662,7 +2691,9 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   // regions are zeroed again.
   if (!bs->eslots) {
     const size_t slot_bytes = static_cast<size_t>(2 * DeviceCUs()) * 256 * 16;
-    const size_t coef_bytes = static_cast<size_t>(2 * DeviceCUs()) * 256 * 40;  // 4 + 1 words
+    // kCoefCopies copies of 4 words per channel, then 1 key word per channel.
+    const size_t coef_bytes =
+        (kCoefCopies * coef_copy_words() + static_cast<size_t>(max_fused_channels())) * 8;
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, slot_bytes + coef_bytes);
     if (e != hipSuccess) return e;
@@ -2681,9 +2712,9 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
     const unsigned long long start = es ? strtoull(es, nullptr, 10) : 0ull;
     bs->epoch = start < (1ull << 31) ? static_cast<unsigned>(start) : 0u;
   }
-  if (fp.groups > kMaxEpochGroups ||
+  if (fp.groups > kMaxEpochGroups || fp.ct_conc < 1 ||
       static_cast<size_t>(fp.groups) * g.c * 16 > bs->eslot_bytes ||
-      static_cast<size_t>(g.c) * 40 > bs->ecoef_bytes)
+      g.c > max_fused_channels())
     return hipErrorInvalidValue;  // excluded by make_fused_plan
   unsigned long long* region =
       recorded ? reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(bs->counter) +
@@ -2733,8 +2764,11 @@ hipError_t launch_fused(const FusedPlan& fp, const BnGeometry& g, const void* x,
   fa.reset_at_exit = recorded ? 1 : 0;
   fa.eslots = bs->eslots;
   fa.ecoef = bs->ecoef;
-  // The key words after the largest coefficient array ([C][4] words).
-  fa.ekey = bs->ecoef + bs->ecoef_bytes / 40 * 4;
+  fa.coef_copy = static_cast<int64_t>(coef_copy_words());
+  fa.coef_copies = static_cast<int>(std::min<int64_t>(
+      kCoefCopies, std::max<int64_t>(1, fp.groups / kPollersPerCopy)));
+  // The key words after the last copy of the coefficients.
+  fa.ekey = bs->ecoef + kCoefCopies * coef_copy_words();
   fa.epoch = epoch;
   fa.epoch_dev = recorded ? reinterpret_cast<unsigned*>(reinterpret_cast<char*>(region) +
                                                         kEpochOffset)
