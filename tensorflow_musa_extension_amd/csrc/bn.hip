@@ -1300,15 +1300,21 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
 
   stamp(0);
   // This launch's epoch, in the upper half of the tag word (recorded
-  // launches: 2^31 + 1 + (device word mod 2^31 - 1)).
-  const unsigned epoch =
-      a.epoch_dev ? 0x80000001u + __hip_atomic_load(a.epoch_dev, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT) % 0x7fffffffu
-                  : a.epoch;
-  const uint64_t etag = static_cast<uint64_t>(epoch) << 32;
-  // The tag the waits look for: this launch's epoch (wait_xor is 0 except
-  // under the host's forced-give-up test hook).
-  const uint32_t wtag = epoch ^ a.wait_xor;
+  // launches: 2^31 + 1 + (device word mod 2^31 - 1)), and the tag the waits
+  // look for (wait_xor is 0 except under the host's forced-give-up test
+  // hook).  Read once the first phase-1 loads are issued: the branch and
+  // its kernel-argument loads would otherwise stand before them.
+  unsigned epoch = 0;
+  uint64_t etag = 0;
+  uint32_t wtag = 0;
+  auto read_epoch = [&]() {
+    epoch = a.epoch_dev ? 0x80000001u + __hip_atomic_load(a.epoch_dev, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT) %
+                                            0x7fffffffu
+                        : a.epoch;
+    etag = static_cast<uint64_t>(epoch) << 32;
+    wtag = epoch ^ a.wait_xor;
+  };
 
 #pragma clang loop unroll(disable)
   for (int sl = 0; sl < nslices; ++sl) {
@@ -1334,7 +1340,9 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   if (kSliced && sl > 0) __syncthreads();
   const int64_t cvi = static_cast<int64_t>(ct) * (1 << a.tx_shift) + tx;
   const bool active = cvi < a.cv;
-  const int64_t nk = (active && r0 + ty < r1) ? (r1 - r0 - ty + ry - 1) / ry : 0;
+  static_assert(kFusedThreads == 512, "ry = 2^(9 - tx_shift)");
+  const int ry_shift = 9 - a.tx_shift;
+  const int64_t nk = (active && r0 + ty < r1) ? (r1 - r0 - ty + ry - 1) >> ry_shift : 0;
   const int64_t c0 = active ? cvi * VEC : 0;
   const S* __restrict__ px = static_cast<const S*>(a.x) + c0;
   const S* __restrict__ pd = kGrad ? static_cast<const S*>(a.dy) + c0 : nullptr;
@@ -1400,6 +1408,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
     xl[q] = bld16_last(rx, roff(KR + q));
     if constexpr (kGrad) dl[q] = bld16_last(rd, roff(KR + q));
   }
+  if (sl == 0) read_epoch();
   if constexpr (!kGrad) shift_words<Tr>(kw, k);
   // After its phase-1 use a register row is made opaque, so the compiler
   // keeps its packed words to phase 3 rather than the half-width pieces it
@@ -1608,7 +1617,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       const int64_t o0 = go * a.rows_per_g;
       int64_t o1 = o0 + a.rows_per_g;
       if (o1 > a.rows) o1 = a.rows;
-      const int64_t onk = (active && o0 + ty < o1) ? (o1 - o0 - ty + ry - 1) / ry : 0;
+      const int64_t onk = (active && o0 + ty < o1) ? (o1 - o0 - ty + ry - 1) >> ry_shift : 0;
       const bool opre = PA > 0 && static_cast<int>(go * ct_conc + ct - sl * ct_conc) +
                                           wave * static_cast<int>(gridDim.x) >= cs1 - cs0;
       int64_t qhi = onk - 1 - (opre ? PA : 0) - PB;  // owner's last streamed row
