@@ -1343,6 +1343,13 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
   static_assert(kFusedThreads == 512, "ry = 2^(9 - tx_shift)");
   const int ry_shift = 9 - a.tx_shift;
   const int64_t nk = (active && r0 + ty < r1) ? (r1 - r0 - ty + ry - 1) >> ry_shift : 0;
+  // The wave's last LDS row (see the LDS loops below); the large forwards
+  // keep all KL slots (bounded, their phase 1 was scheduled worse: the
+  // 56x56 forward 178 -> 194 us).
+  constexpr bool kWaveLds = kGrad || KR == Resident<Tr>::kRegFwdSmall;
+  const int nk_w = __builtin_amdgcn_readfirstlane(static_cast<int>(nk));
+  const int kl_w =
+      !kWaveLds ? KL : (nk_w - KR < 0 ? 0 : (nk_w - KR < KL ? nk_w - KR : KL));
   const int64_t c0 = active ? cvi * VEC : 0;
   const S* __restrict__ px = static_cast<const S*>(a.x) + c0;
   const S* __restrict__ pd = kGrad ? static_cast<const S*>(a.dy) + c0 : nullptr;
@@ -1422,17 +1429,22 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
         asm volatile("" : "+v"(dr[q].x), "+v"(dr[q].y), "+v"(dr[q].z), "+v"(dr[q].w));
     }
   }
-  // LDS rows: stored as they arrive (rows past nk hold zeros and are never
-  // used), then accumulated from LDS in a loop, not unrolled - the unrolled
-  // per-row code made the kernel about as large as the 64 KB instruction
-  // cache a CU pair shares, which the small shapes (code run once) paid for.
+  // LDS rows: stored as they arrive, then accumulated from LDS in a loop,
+  // not unrolled - the unrolled per-row code made the kernel about as large
+  // as the 64 KB instruction cache a CU pair shares, which the small shapes
+  // (code run once) paid for.  Both loops, and phase 3's, stop at the
+  // wave's last LDS row (kl_w, wave-uniform: lane 0 has the wave's smallest
+  // ty, hence its largest nk) instead of running all KL slots; slots past a
+  // lane's own nk are never read.
 #pragma unroll
   for (int q = 0; q < KL; ++q) {
-    lds(q, 0) = xl[q];
-    if constexpr (kGrad) lds(q, kGrad ? 1 : 0) = dl[kGrad ? q : 0];
+    if (q < kl_w) {
+      lds(q, 0) = xl[q];
+      if constexpr (kGrad) lds(q, kGrad ? 1 : 0) = dl[kGrad ? q : 0];
+    }
   }
 #pragma unroll 2
-  for (int q = 0; q < KL; ++q) {
+  for (int q = 0; q < kl_w; ++q) {
     if (KR + q < nk) {
       const uint4 xw = lds(q, 0);
       const uint4 dw = kGrad ? lds(q, kGrad ? 1 : 0) : xw;
@@ -1569,7 +1581,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_fused_nhwc_kernel(FusedArgs 
       if (q - u >= qlo) st16(po + base + (q - u) * rstride, apply_words<Tr, kGrad>(xw[u], dw[u], cf));
   }
 #pragma unroll 2
-  for (int q2 = 0; q2 < KL; ++q2) {
+  for (int q2 = 0; q2 < kl_w; ++q2) {
     if (KR + q2 < nk) {
       const uint4 xw = lds(q2, 0);
       const uint4 dw = kGrad ? lds(q2, kGrad ? 1 : 0) : xw;
