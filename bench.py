@@ -115,7 +115,7 @@ def parse():
                    help="skip the Adam / elementwise component lines")
     p.add_argument("--trace", default="tfma_bn_grad_fused",
                    help="kernel timed for the roofline object")
-    p.add_argument("--trace-steps", type=int, default=4,
+    p.add_argument("--trace-steps", type=int, default=2,
                    help="timed steps (the last ones) whose launches of --trace carry timing "
                         "events; each such launch costs ~5 us of idle GPU between kernels")
     p.add_argument("--bn-stamps", metavar="LIB", default=None,
