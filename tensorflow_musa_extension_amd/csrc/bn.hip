@@ -626,7 +626,8 @@ __global__ __launch_bounds__(kThreads) void bn_nhwc_apply_kernel(
 #pragma unroll
   for (int j = 0; j < VEC; ++j) cf[j] = kInfer ? infer_coef(fa, c0 + j) : coef[c0 + j];
   if (r0 + ty >= r1) return;
-  const int64_t nr = (r1 - r0 - ty + ry - 1) / ry;  // rows of this thread
+  static_assert((kThreads & (kThreads - 1)) == 0, "ry = kThreads >> tx_shift is a power of two");
+  const int64_t nr = (r1 - r0 - ty + ry - 1) >> (__builtin_ctz(kThreads) - tx_shift);  // rows of this thread
   const S* __restrict__ px = x + c0;
   const S* __restrict__ pd = kGrad ? dy + c0 : nullptr;
   S* __restrict__ po = out + c0;
@@ -1781,7 +1782,7 @@ __global__ __launch_bounds__(kFusedThreads) void bn_sliced_grad_kernel(FusedArgs
     l.ty = tid >> a.tx_shift;
     const int64_t cvi = static_cast<int64_t>(s) * (1 << a.tx_shift) + l.tx;
     l.active = cvi < a.cv;
-    l.nk = l.active && r0 + l.ty < r1 ? (r1 - r0 - l.ty + ry - 1) / ry : 0;
+    l.nk = l.active && r0 + l.ty < r1 ? (r1 - r0 - l.ty + ry - 1) >> (9 - a.tx_shift) : 0;
     l.c0 = l.active ? cvi * VEC : 0;
     l.off = l.active ? static_cast<uint32_t>((l.ty * static_cast<int64_t>(a.c) + l.c0) *
                                              static_cast<int64_t>(sizeof(S)))
