@@ -4,7 +4,12 @@
 //
 //   Relu(BiasAdd(x, b))        -> MusaBiasAddRelu(x, b)          priority 100
 //   Relu(AddV2|Add(x, y))      -> MusaAddV2Relu(x, y)            priority  90
-//   AddV2|Add(Mul(x, a), b)    -> MusaShiftedAffineMap(x, a, b)  priority  80
+//   AddV2(Mul(Const, mask), Const)
+//                              -> MusaShiftedAffineMap           priority  80
+//                                 (mask: Select, SelectV2, Where or Identity;
+//                                 Consts through Identity nodes; the
+//                                 reference's exact topology,
+//                                 shifted_affine_map_fusion.cc:109-233)
 //   ResourceApplyAdam<float>(..., Cast<half|bfloat16 -> float>(g))
 //                              -> MusaResourceApplyAdamMixed(..., g)  priority 40
 //                                 (musa_ext/graph/fusion/adam_mixed_fusion.cc:93-216)
@@ -20,7 +25,8 @@
 // keeps the output node's name, device and control inputs, and the absorbed
 // node goes away (FusionGraphUtils::RemoveNodesIfUnused, .h:189-191).  A
 // producer is absorbed only if the pattern's node is its only consumer and it
-// is not fetched.  Adam grouping follows the reference's grouped-SGD rewrite
+// is not fetched (MusaShiftedAffineMap, as the reference's, fuses whatever
+// else reads the Mul and keeps the Mul then).  Adam grouping follows the reference's grouped-SGD rewrite
 // (musa_graph_optimizer.cc:2014-2120) and additionally refuses to group nodes
 // where one depends on another, which would create a cycle.
 //
@@ -435,26 +441,80 @@ bool apply_add_v2_relu(Graph* g, int i) {
   return true;
 }
 
+// The node an input edge reads, followed through Identity nodes (their
+// first input) as the reference's ResolveIdentityLike does
+// (shifted_affine_map_fusion.cc:62-68).
+const Node* resolve_identity(const Graph& g, const std::string& in) {
+  int port;
+  const Node* p = g.producer(in, &port);
+  for (size_t hops = 0; p && p->op == "Identity" && !p->inputs.empty() &&
+                        !is_control(p->inputs[0]) && hops < g.nodes.size();
+       ++hops)
+    p = g.producer(p->inputs[0], &port);
+  return p;
+}
+
+// AddV2(Mul(data_left, mask), sliced_var_right) -> MusaShiftedAffineMap,
+// matched as the reference matches it (shifted_affine_map_fusion.cc:109-233):
+// an AddV2 with exactly two inputs, one produced by a Mul and the other
+// resolving through Identity nodes to a Const; the Mul with exactly two
+// inputs, one resolving to a Const (data_left) and the other produced by a
+// Select, SelectV2, Where or Identity node (the mask).  The fused node keeps
+// the AddV2's name, device and T (float when absent) and takes the three
+// edges as the Mul and the AddV2 read them (:240-316); the Mul goes away
+// only when nothing else reads it.  Two guards the reference lacks: T must be
+// a type the op is registered for, and a fetched Mul is kept.
 bool apply_mul_add(Graph* g, int i) {
   Node& add = g->nodes[i];
-  if (add.removed || (add.op != "AddV2" && add.op != "Add")) return false;
-  if (add.inputs.size() < 2 || is_control(add.inputs[0]) || is_control(add.inputs[1])) return false;
-  for (int k = 0; k < 2; ++k) {
-    const int m = fusable_producer(*g, add, k, {"Mul"});
-    if (m < 0) continue;
-    const Node& mul = g->nodes[m];
-    if (mul.inputs.size() < 2 || is_control(mul.inputs[1])) continue;
-    int64_t t = 0;
-    attr_varint(add, "T", 6, &t);
-    const std::string other = add.inputs[1 - k];
-    const std::vector<std::string> old = add.inputs;
-    set_inputs(&add, {mul.inputs[0], mul.inputs[1], other}, old);
-    add.op = "MusaShiftedAffineMap";
-    add.attrs = {{"T", attr_of_type(t)}};
-    absorb(g, m, i);
-    return true;
+  if (add.removed || add.op != "AddV2" || !g->on_device(add)) return false;
+  if (add.inputs.size() != 2 || is_control(add.inputs[0]) || is_control(add.inputs[1])) return false;
+  int64_t t = TFMA_FLOAT;
+  attr_varint(add, "T", 6, &t);
+  if (!fusable_type(t) && t != TFMA_DOUBLE) return false;
+  auto produced_by = [&](const std::string& in, std::initializer_list<const char*> ops) {
+    int port;
+    const Node* p = g->producer(in, &port);
+    if (!p) return false;
+    for (const char* op : ops)
+      if (p->op == op) return true;
+    return false;
+  };
+  auto is_const = [&](const std::string& in) {
+    const Node* r = resolve_identity(*g, in);
+    return r && r->op == "Const";
+  };
+  int k;
+  if (produced_by(add.inputs[0], {"Mul"}) && is_const(add.inputs[1]))
+    k = 0;
+  else if (produced_by(add.inputs[1], {"Mul"}) && is_const(add.inputs[0]))
+    k = 1;
+  else
+    return false;
+  int port;
+  const int m = g->index.at(g->producer(add.inputs[k], &port)->name);
+  const Node& mul = g->nodes[m];
+  if (mul.inputs.size() != 2 || is_control(mul.inputs[0]) || is_control(mul.inputs[1]))
+    return false;
+  std::string left, mask;
+  const std::initializer_list<const char*> mask_ops = {"Select", "SelectV2", "Where", "Identity"};
+  if (is_const(mul.inputs[0]) && produced_by(mul.inputs[1], mask_ops)) {
+    left = mul.inputs[0];
+    mask = mul.inputs[1];
+  } else if (is_const(mul.inputs[1]) && produced_by(mul.inputs[0], mask_ops)) {
+    left = mul.inputs[1];
+    mask = mul.inputs[0];
+  } else {
+    return false;
   }
-  return false;
+  const std::string mul_name = mul.name;
+  add.inputs = {left, mask, add.inputs[1 - k]};
+  add.op = "MusaShiftedAffineMap";
+  add.attrs = {{"T", attr_of_type(t)}};
+  if (g->consumers(mul_name).empty() && !g->fetch.count(mul_name)) {
+    g->nodes[m].removed = true;
+    g->reindex();
+  }
+  return true;
 }
 
 // ResourceApplyAdam<float> whose grad is Cast(SrcT = half|bfloat16, DstT =

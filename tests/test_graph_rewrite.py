@@ -166,26 +166,124 @@ def test_add_relu_fused(add_op):
     assert "a" not in nodes(gd) and stats["add_v2_relu"] == 1
 
 
-@pytest.mark.parametrize("mul_at", [0, 1])
-def test_mul_add_fused_either_side(mul_at):
-    g = base().node("m", "Mul", ["x", "b"], T=DT_FLOAT)
-    ins = ["m", "y"] if mul_at == 0 else ["y", "m"]
-    g.node("s", "AddV2", ins + ["^init"], T=DT_FLOAT).node("o", "Identity", ["s"], T=DT_FLOAT)
+# ---------------------------------------------------------------------------
+# AddV2(Mul(Const, mask), Const) -> MusaShiftedAffineMap, the reference's
+# topology (musa_ext/graph/fusion/shifted_affine_map_fusion.cc:109-233; its
+# graphs, test/fusion/shifted_affine_map_fusion_test.py:59-100)
+# ---------------------------------------------------------------------------
+DT_INT32, DT_BOOL = 3, 10
+
+
+def affine_graph(mask_op="Select", identities=True, mul_order=0, add_order=0, t=DT_FLOAT,
+                 sink=True):
+    """mask = Select(cond, ones, zeros); out = AddV2(Mul(left, mask), right),
+    left and right Consts read directly or through Identity nodes (the
+    reference's frozen-graph form)."""
+    g = G()
+    g.node("cond", "Placeholder", dtype=DT_BOOL).node("ones", "Const", dtype=t)
+    g.node("zeros", "Const", dtype=t).node("init", "NoOp")
+    g.node("mask", mask_op, ["cond", "ones", "zeros"], T=t)
+    g.node("left", "Const", dtype=t).node("right", "Const", dtype=t)
+    left, right = "left", "right"
+    if identities:
+        g.node("id_left", "Identity", ["left"], T=t).node("id_right", "Identity", ["right"], T=t)
+        left, right = "id_left", "id_right"
+    g.node("mul", "Mul", [left, "mask"] if mul_order == 0 else ["mask", left], T=t)
+    g.node("out", "AddV2", ["mul", right] if add_order == 0 else [right, "mul"], T=t)
+    if sink:
+        g.node("sink", "Identity", ["out"], T=t)
+    return g, left, right
+
+
+@pytest.mark.parametrize("identities", [True, False])
+@pytest.mark.parametrize("mul_order", [0, 1])
+@pytest.mark.parametrize("add_order", [0, 1])
+@pytest.mark.parametrize("mask_op", ["Select", "SelectV2", "Identity"])
+def test_shifted_affine_map_reference_topology(identities, mul_order, add_order, mask_op):
+    g, left, right = affine_graph(mask_op, identities, mul_order, add_order)
     gd, stats = run(g)
-    s = nodes(gd)["s"]
-    assert s.op == "MusaShiftedAffineMap" and list(s.input) == ["x", "b", "y", "^init"]
-    assert stats["mul_add"] == 1 and "m" not in nodes(gd)
+    check_well_formed(gd)
+    by = nodes(gd)
+    out = by["out"]
+    assert out.op == "MusaShiftedAffineMap" and stats["mul_add"] == 1
+    assert list(out.input) == [left, "mask", right]
+    assert out.device.endswith("MUSA:0") and out.attr["T"].type == DT_FLOAT
+    assert "mul" not in by and list(by["sink"].input) == ["out"]
+
+
+def test_shifted_affine_map_keeps_a_shared_or_fetched_mul():
+    """The reference fuses whatever else reads the Mul and keeps the Mul then
+    (FusionGraphUtils::RemoveNodesIfUnused); a fetched Mul is kept too."""
+    g, left, right = affine_graph()
+    g.node("other", "Identity", ["mul"], T=DT_FLOAT)
+    gd, stats = run(g)
+    by = nodes(gd)
+    assert by["out"].op == "MusaShiftedAffineMap" and by["mul"].op == "Mul"
+    assert list(by["other"].input) == ["mul"] and stats["mul_add"] == 1
+    g, left, right = affine_graph()
+    gd, stats = run(g, fetch=["mul"])
+    by = nodes(gd)
+    assert by["out"].op == "MusaShiftedAffineMap" and by["mul"].op == "Mul"
+
+
+def test_shifted_affine_map_double():
+    g, left, right = affine_graph(t=DT_DOUBLE)
+    gd, stats = run(g)
+    assert nodes(gd)["out"].op == "MusaShiftedAffineMap"
+    assert nodes(gd)["out"].attr["T"].type == DT_DOUBLE
+
+
+def _unfused(g, **kw):
+    before = [(n.name, n.op, list(n.input)) for n in g.gd.node]
+    gd, stats = run(g, **kw)
+    assert stats["mul_add"] == 0
+    assert [(n.name, n.op, list(n.input)) for n in gd.node] == before
+
+
+def test_shifted_affine_map_not_applied_when_pattern_incomplete():
+    """The reference's negative case (shifted_affine_map_fusion_test.py:215-242):
+    a plain Mul of two placeholders plus a constant is not fused; nor is any
+    other graph its matcher rejects."""
+    g = G().node("a", "Placeholder", dtype=DT_FLOAT).node("b", "Placeholder", dtype=DT_FLOAT)
+    g.node("one", "Const", dtype=DT_FLOAT).node("m", "Mul", ["a", "b"], T=DT_FLOAT)
+    g.node("incomplete_output", "AddV2", ["m", "one"], T=DT_FLOAT)
+    _unfused(g)
+    # Add, not AddV2
+    g, _, _ = affine_graph()
+    nodes(g.gd)["out"].op = "Add"
+    _unfused(g)
+    # the AddV2 with a control input (three inputs)
+    g, _, _ = affine_graph()
+    nodes(g.gd)["out"].input.append("^init")
+    _unfused(g)
+    # right operand not a Const
+    g, _, right = affine_graph(identities=False)
+    g.node("p", "Placeholder", dtype=DT_FLOAT)
+    out = nodes(g.gd)["out"]
+    out.input[1] = "p"
+    _unfused(g)
+    # the Mul's non-constant operand not a mask op
+    g, _, _ = affine_graph(mask_op="Relu")
+    _unfused(g)
+    # a type the op is not registered for
+    g, _, _ = affine_graph(t=DT_INT32)
+    _unfused(g)
+    # a Mul of three inputs (a control one)
+    g, _, _ = affine_graph()
+    nodes(g.gd)["mul"].input.append("^init")
+    _unfused(g)
 
 
 def test_priority_bias_relu_before_mul_add():
-    # Relu(AddV2(Mul(x, b), y)): AddV2+Relu (priority 90) wins over Mul+Add (80).
-    g = base().node("m", "Mul", ["x", "b"], T=DT_FLOAT)
-    g.node("a", "AddV2", ["m", "y"], T=DT_FLOAT).node("r", "Relu", ["a"], T=DT_FLOAT)
+    # Relu(AddV2(Mul(left, mask), right)): AddV2+Relu (priority 90) wins over
+    # Mul+Add (80).
+    g, left, right = affine_graph(sink=False)
+    g.node("r", "Relu", ["out"], T=DT_FLOAT)
     gd, stats = run(g)
-    assert nodes(gd)["r"].op == "MusaAddV2Relu" and nodes(gd)["m"].op == "Mul"
+    assert nodes(gd)["r"].op == "MusaAddV2Relu" and nodes(gd)["mul"].op == "Mul"
     assert stats == dict(stats, add_v2_relu=1, mul_add=0)
     gd, stats = run(g, disabled_patterns=["MusaAddV2Relu"])
-    assert nodes(gd)["a"].op == "MusaShiftedAffineMap" and nodes(gd)["r"].op == "Relu"
+    assert nodes(gd)["out"].op == "MusaShiftedAffineMap" and nodes(gd)["r"].op == "Relu"
 
 
 # ---------------------------------------------------------------------------
@@ -335,6 +433,8 @@ def evaluate(gd, feeds):
             vals[name] = a[0] + a[1]
         elif op == "Mul":
             vals[name] = a[0] * a[1]
+        elif op == "Select":
+            vals[name] = np.where(a[0], a[1], a[2])
         elif op == "Relu":
             vals[name] = np.maximum(a[0], 0.0)
         elif op in ("MusaBiasAddRelu", "MusaAddV2Relu"):
@@ -356,16 +456,46 @@ def random_graph(rng, n_ops=60):
     for i in range(2):
         g.node(f"c{i}", "Const", dtype=DT_FLOAT)
         feeds[f"c{i}"] = rng.standard_normal(6)
+    g.node("q", "Placeholder", dtype=DT_BOOL)
+    feeds["q"] = rng.random((4, 6)) < 0.5
     allnames = list(full)
     for k in range(n_ops):
         name = f"n{k}"
-        op = rng.choice(["BiasAdd", "Relu", "Relu", "AddV2", "Add", "Mul", "Identity"])
+        op = rng.choice(["BiasAdd", "Relu", "Relu", "AddV2", "Add", "Mul", "Identity", "Select",
+                         "Affine"])
         recent = full[-6:]
         pick = lambda: str(rng.choice(recent if rng.random() < 0.7 else full))
+        if op == "Affine":
+            # AddV2(Mul(Const, mask), Const) in a random arrangement: operand
+            # order, Identity nodes in front of the Consts, Select or Identity
+            # as the mask; later nodes may read the Mul or the AddV2 too.
+            def const_edge(tag):
+                c = f"c{rng.integers(2)}"
+                if rng.random() < 0.5:
+                    g.node(f"{name}_{tag}", "Identity", [c], T=DT_FLOAT)
+                    return f"{name}_{tag}"
+                return c
+            mask_op = "Select" if rng.random() < 0.7 else "Identity"
+            g.node(f"{name}_mask", mask_op,
+                   ["q", pick(), pick()] if mask_op == "Select" else [pick()], T=DT_FLOAT)
+            left = const_edge("l")
+            mul_in = [left, f"{name}_mask"]
+            g.node(f"{name}_mul", "Mul", mul_in if rng.random() < 0.5 else mul_in[::-1],
+                   T=DT_FLOAT)
+            add_in = [f"{name}_mul", const_edge("r")]
+            g.node(name, "AddV2", add_in if rng.random() < 0.5 else add_in[::-1], T=DT_FLOAT)
+            for extra in (f"{name}_mask", f"{name}_mul"):
+                full.append(extra)
+                allnames.append(extra)
+            full.append(name)
+            allnames.append(name)
+            continue
         if op == "BiasAdd":
             ins = [pick(), f"c{rng.integers(2)}"]
         elif op in ("Relu", "Identity"):
             ins = [pick()]
+        elif op == "Select":
+            ins = ["q", pick(), pick()]
         else:
             ins = [pick(), pick() if rng.random() < 0.8 else f"c{rng.integers(2)}"]
         if rng.random() < 0.5:
@@ -392,8 +522,11 @@ def test_random_graphs_keep_values(seed):
     for name, v in after.items():
         if v is not None:
             np.testing.assert_array_equal(v, before[name], err_msg=name)
+    # Each fusion removes its absorbed node, except that Mul+Add keeps a Mul
+    # something else still reads.
     removed = len(g.gd.node) - len(gd.node)
-    assert removed == stats["bias_add_relu"] + stats["add_v2_relu"] + stats["mul_add"]
+    assert stats["bias_add_relu"] + stats["add_v2_relu"] <= removed
+    assert removed <= stats["bias_add_relu"] + stats["add_v2_relu"] + stats["mul_add"]
     assert optimize_graph_def(gd.SerializeToString(), fetch=fetch)[1]["bias_add_relu"] == 0
 
 
