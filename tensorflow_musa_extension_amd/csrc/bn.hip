@@ -957,6 +957,34 @@ __device__ inline uint4 bld16_last(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2 /* nt */);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
+
+// A channel's two partial words of one row group - {sum 1, epoch} and {sum
+// 2, epoch}, adjacent and 16-byte aligned - moved in one 16-byte access
+// with the cache policy of the agent-scope atomics (sc1: coherent across
+// the XCDs' L2s) instead of two 8-byte ones: half the requests for the
+// finishing waves' polls, which gather one slot per row group.  Each 8-byte
+// half carries its own tag, so a read that saw one half before the other
+// was written looks not yet ready and is polled again.  These are plain
+// loads to the compiler: a poll loop reloads them after a compiler barrier.
+// Their words are read as floats through bits_f32 (by value): this clang's
+// __builtin_bit_cast applied to an element of an ext_vector_type value
+// reads element 0 whatever the index.
+constexpr int kSc1 = 16;  // buffer cache policy bit sc1
+__device__ inline __amdgpu_buffer_rsrc_t slots_rsrc(const void* slots, int64_t groups, int c) {
+  return rows_rsrc(slots, groups * c * 16);
+}
+__device__ inline u32x4 load_pair(__amdgpu_buffer_rsrc_t r, int64_t slot) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<uint32_t>(slot) * 16u, 0, kSc1);
+}
+__device__ inline void store_pair(__amdgpu_buffer_rsrc_t r, int64_t slot, uint32_t epoch,
+                                  float sa, float sb) {
+  const u32x4 w = {__builtin_bit_cast(uint32_t, sa), epoch, __builtin_bit_cast(uint32_t, sb),
+                   epoch};
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, static_cast<uint32_t>(slot) * 16u, 0, kSc1);
+}
+__device__ inline bool pair_tagged(const u32x4& v, uint32_t wtag) {
+  return v[1] == wtag && v[3] == wtag;
+}
 // Outputs are written once and not read again by the op: non-temporal.
 __device__ inline void st16(void* p, const uint4& v) {
   __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(p));
@@ -1036,8 +1064,8 @@ __device__ __forceinline__ void publish_partials(const FusedArgs& a, float2* red
     sa += pend.x;
     sb += pend.y;
     const int64_t slot = g * a.c + static_cast<int64_t>(ct) * width + tid;
-    store_shared(a.eslots + 2 * slot, etag | __builtin_bit_cast(uint32_t, sa));
-    store_shared(a.eslots + 2 * slot + 1, etag | __builtin_bit_cast(uint32_t, sb));
+    store_pair(slots_rsrc(a.eslots, a.groups, a.c), slot, static_cast<uint32_t>(etag >> 32), sa,
+               sb);
   }
 }
 
@@ -1051,10 +1079,14 @@ __device__ __forceinline__ void store_coefs(const FusedArgs& a, int ch, bool chv
   const float v4[4] = {__shfl(cfc.x, src, 64), __shfl(cfc.y, src, 64), __shfl(cfc.z, src, 64),
                        __shfl(cfc.w, src, 64)};
   if (!chv) return;
+  // Two 16-byte pairs per channel and copy (a copy is an even number of
+  // words, so every channel's four words start 16-byte aligned).
+  const auto rc = rows_rsrc(a.ecoef, a.coef_copies * a.coef_copy * 8);
+  const uint32_t e = static_cast<uint32_t>(etag >> 32);
   for (int r = lane / B; r < a.coef_copies; r += 64 / B) {
-    unsigned long long* const dst = a.ecoef + r * a.coef_copy + 4 * static_cast<int64_t>(ch);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) store_shared(dst + i, etag | __builtin_bit_cast(uint32_t, v4[i]));
+    const int64_t pr = (r * a.coef_copy + 4 * static_cast<int64_t>(ch)) / 2;
+    store_pair(rc, pr, e, v4[0], v4[1]);
+    store_pair(rc, pr + 1, e, v4[2], v4[3]);
   }
 }
 
@@ -1081,25 +1113,27 @@ __device__ __forceinline__ void finish_channels(const FusedArgs& a, int cs0, int
       // all their slots are loaded at once, then the ones not yet tagged
       // with this launch's epoch are polled again.
       const uint64_t tag = static_cast<uint64_t>(wtag) << 32;
-      uint64_t v1[kEpochPerLane], v2[kEpochPerLane];
       const bool has_key = !kGrad && lane == 0;
       uint64_t vk = has_key ? load_shared(a.ekey + ch) : tag;
-#pragma unroll
-      for (int i = 0; i < kEpochPerLane; ++i) {
+      // Slots past the groups are out of range: they read as zeros and are
+      // treated as tagged.
+      const auto rs = slots_rsrc(a.eslots, a.groups, a.c);
+      auto pslot = [&](int i) -> int64_t {
         const int64_t gg = lane + 64 * i;
-        v1[i] = v2[i] = tag;
-        if (gg < a.groups) {
-          v1[i] = load_shared(a.eslots + 2 * (gg * a.c + ch));
-          v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
-        }
-      }
+        return gg < a.groups ? gg * a.c + ch : int64_t(kOutOfRange / 16);
+      };
+      auto ok = [&](const u32x4& v, int i) {
+        return lane + 64 * i >= a.groups || pair_tagged(v, wtag);
+      };
+      u32x4 v[kEpochPerLane];
+#pragma unroll
+      for (int i = 0; i < kEpochPerLane; ++i) v[i] = load_pair(rs, pslot(i));
       unsigned spins = 0;
       bool lost = false;
       while (true) {
         bool ready = (vk >> 32) == (tag >> 32);
 #pragma unroll
-        for (int i = 0; i < kEpochPerLane; ++i)
-          ready = ready && (v1[i] >> 32) == (tag >> 32) && (v2[i] >> 32) == (tag >> 32);
+        for (int i = 0; i < kEpochPerLane; ++i) ready = ready && ok(v[i], i);
         if (ready) break;
         if (++spins > a.spin_limit) {
           lost = true;
@@ -1108,20 +1142,17 @@ __device__ __forceinline__ void finish_channels(const FusedArgs& a, int cs0, int
         }
         __builtin_amdgcn_s_sleep(1);
         if ((vk >> 32) != (tag >> 32)) vk = load_shared(a.ekey + ch);
+        asm volatile("" ::: "memory");  // the reloads below are not the loads above
 #pragma unroll
-        for (int i = 0; i < kEpochPerLane; ++i) {
-          const int64_t gg = lane + 64 * i;
-          if ((v1[i] >> 32) != (tag >> 32)) v1[i] = load_shared(a.eslots + 2 * (gg * a.c + ch));
-          if ((v2[i] >> 32) != (tag >> 32))
-            v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
-        }
+        for (int i = 0; i < kEpochPerLane; ++i)
+          if (!ok(v[i], i)) v[i] = load_pair(rs, pslot(i));
       }
       fin_in.k = __builtin_bit_cast(float, static_cast<uint32_t>(vk));
 #pragma unroll
       for (int i = 0; i < kEpochPerLane; ++i) {
         if (lane + 64 * i < a.groups) {
-          t1 += __builtin_bit_cast(float, static_cast<uint32_t>(v1[i]));
-          t2 += __builtin_bit_cast(float, static_cast<uint32_t>(v2[i]));
+          t1 += bits_f32(v[i][0]);
+          t2 += bits_f32(v[i][2]);
         }
       }
       // A lane whose partials never arrived poisons the channel's sums (the
@@ -1161,22 +1192,24 @@ __device__ __forceinline__ void finish_channel_blocks(const FusedArgs& a, int cs
     const bool chv = ch < cs1;
     FinIn fin_in = fin_inputs<Tr, kGrad>(a.fin, chv ? ch : cs1 - 1, 0.f);
     uint64_t vk = !kGrad && chv ? load_shared(a.ekey + ch) : tag;
-    uint64_t v1[kEpochPerLane], v2[kEpochPerLane];
+    // Slots of absent channels or past the groups are out of range: they
+    // read as zeros and are treated as tagged.
+    const auto rs = slots_rsrc(a.eslots, a.groups, a.c);
+    auto has = [&](int i) { return chv && gl + static_cast<int64_t>(gpl) * i < a.groups; };
+    auto pslot = [&](int i) -> int64_t {
+      return has(i) ? (gl + static_cast<int64_t>(gpl) * i) * a.c + ch
+                    : int64_t(kOutOfRange / 16);
+    };
+    u32x4 v[kEpochPerLane];
 #pragma unroll
-    for (int i = 0; i < kEpochPerLane; ++i) {
-      const int64_t gg = gl + static_cast<int64_t>(gpl) * i;
-      v1[i] = v2[i] = tag;
-      if (chv && gg < a.groups) {
-        v1[i] = load_shared(a.eslots + 2 * (gg * a.c + ch));
-        v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
-      }
-    }
+    for (int i = 0; i < kEpochPerLane; ++i) v[i] = load_pair(rs, pslot(i));
     unsigned spins = 0;
     bool lost = false;
     while (true) {
       bool ready = tagged(vk);
 #pragma unroll
-      for (int i = 0; i < kEpochPerLane; ++i) ready = ready && tagged(v1[i]) && tagged(v2[i]);
+      for (int i = 0; i < kEpochPerLane; ++i)
+        ready = ready && (!has(i) || pair_tagged(v[i], wtag));
       if (ready) break;
       if (++spins > a.spin_limit) {
         lost = true;
@@ -1185,20 +1218,18 @@ __device__ __forceinline__ void finish_channel_blocks(const FusedArgs& a, int cs
       }
       __builtin_amdgcn_s_sleep(1);
       if (!tagged(vk)) vk = load_shared(a.ekey + ch);
+      asm volatile("" ::: "memory");  // the reloads below are not the loads above
 #pragma unroll
-      for (int i = 0; i < kEpochPerLane; ++i) {
-        const int64_t gg = gl + static_cast<int64_t>(gpl) * i;
-        if (!tagged(v1[i])) v1[i] = load_shared(a.eslots + 2 * (gg * a.c + ch));
-        if (!tagged(v2[i])) v2[i] = load_shared(a.eslots + 2 * (gg * a.c + ch) + 1);
-      }
+      for (int i = 0; i < kEpochPerLane; ++i)
+        if (has(i) && !pair_tagged(v[i], wtag)) v[i] = load_pair(rs, pslot(i));
     }
     fin_in.k = __builtin_bit_cast(float, static_cast<uint32_t>(vk));
     double t1 = 0.0, t2 = 0.0;
 #pragma unroll
     for (int i = 0; i < kEpochPerLane; ++i) {
       if (chv && gl + static_cast<int64_t>(gpl) * i < a.groups) {
-        t1 += __builtin_bit_cast(float, static_cast<uint32_t>(v1[i]));
-        t2 += __builtin_bit_cast(float, static_cast<uint32_t>(v2[i]));
+        t1 += bits_f32(v[i][0]);
+        t2 += bits_f32(v[i][2]);
       }
     }
     // A lane whose partials never arrived poisons its channel's sums.
@@ -1214,15 +1245,14 @@ __device__ __forceinline__ void finish_channel_blocks(const FusedArgs& a, int cs
 }
 
 // The coefficients of channel tile ct (4 words per channel, at most 1024
-// words: two per thread, consecutive words to consecutive threads, so the
-// cross-XCD loads stay coalesced), polled until tagged with this launch's
-// epoch, then shared through `red`, free since phase 1's reduction (the
-// first __syncthreads below orders those reads before these writes).  LDS:
-// component c of channel cl (= tx * VEC + j) at c * kW + cl + cl / VEC - a
-// stride kW = 8 (mod 32) between components and one pad word per channel
-// vector, so the writes (consecutive words) and the reads (lane tx at
-// tx * (VEC + 1) + j) hit distinct banks.  Coefficients that never arrive
-// are used as NaN.
+// words: one 16-byte pair per thread, consecutive pairs to consecutive
+// threads, so the cross-XCD loads stay coalesced), polled until tagged with
+// this launch's epoch, then shared through `red`, free since phase 1's
+// reduction (the first __syncthreads below orders those reads before these
+// writes).  LDS: component c of channel cl (= tx * VEC + j) at c * kW + cl +
+// cl / VEC - a stride kW = 8 (mod 32) between components and one pad word
+// per channel vector, so the reads (lane tx at tx * (VEC + 1) + j) hit
+// distinct banks.  Coefficients that never arrive are used as NaN.
 template <class Tr>
 __device__ __forceinline__ void tile_coefs(const FusedArgs& a, float2* red, int tid, int tx, int ct,
                                            int width, bool active, uint32_t wtag, unsigned epoch,
@@ -1233,45 +1263,33 @@ __device__ __forceinline__ void tile_coefs(const FusedArgs& a, float2* red, int 
   static_assert(4 * kW * sizeof(float) <= (kFusedThreads / 64) * 32 * VEC * sizeof(float2),
                 "coefficients fit in red");
   float* const cs = reinterpret_cast<float*>(red);
-  const uint64_t tag = static_cast<uint64_t>(wtag) << 32;
-  // Row group blockIdx.x / ct_conc polls its copy.
-  const unsigned long long* const ecoef =
-      a.ecoef + ((blockIdx.x / a.ct_conc) % a.coef_copies) * a.coef_copy;
-  uint64_t v[2];
-  int64_t wi[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    wi[i] = tid + kFusedThreads * i;
-    const int64_t chn = static_cast<int64_t>(ct) * width + (wi[i] >> 2);
-    const bool need = (wi[i] >> 2) < width && chn < a.c;
-    v[i] = need ? load_shared(ecoef + 4 * chn + (wi[i] & 3)) : tag;
-    if (!need) wi[i] = -1;
-  }
+  // Row group blockIdx.x / ct_conc polls its copy.  Thread t polls the pair
+  // of words 2t, 2t + 1: components 2 (t & 1) and 2 (t & 1) + 1 of channel
+  // t / 2; a pair it does not need is out of range and not polled.
+  const int64_t copy0 = ((blockIdx.x / a.ct_conc) % a.coef_copies) * a.coef_copy;
+  const auto rc = rows_rsrc(a.ecoef, a.coef_copies * a.coef_copy * 8);
+  const int cl = tid >> 1;
+  const int64_t chn = static_cast<int64_t>(ct) * width + cl;
+  const bool need = cl < width && chn < a.c;
+  const int64_t pr = need ? (copy0 + 4 * chn) / 2 + (tid & 1) : int64_t(kOutOfRange / 16);
+  u32x4 v = load_pair(rc, pr);
   unsigned spins = 0;
-  while ((v[0] >> 32) != (tag >> 32) || (v[1] >> 32) != (tag >> 32)) {
+  while (need && !pair_tagged(v, wtag)) {
     if (++spins > a.spin_limit) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        if ((v[i] >> 32) != (tag >> 32)) v[i] = 0x7fc00000u;
+      if (v[1] != wtag) v[0] = 0x7fc00000u;
+      if (v[3] != wtag) v[2] = 0x7fc00000u;
       __hip_atomic_store(a.gave_up, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       break;
     }
     __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      if ((v[i] >> 32) != (tag >> 32)) {
-        const int64_t chn = static_cast<int64_t>(ct) * width + (wi[i] >> 2);
-        v[i] = load_shared(ecoef + 4 * chn + (wi[i] & 3));
-      }
-    }
+    asm volatile("" ::: "memory");  // the reload is not the load above
+    v = load_pair(rc, pr);
   }
   __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    if (wi[i] >= 0) {
-      const int cl = static_cast<int>(wi[i] >> 2);
-      cs[(wi[i] & 3) * kW + cl + cl / VEC] = __builtin_bit_cast(float, static_cast<uint32_t>(v[i]));
-    }
+  if (need) {
+    const int c2 = 2 * (tid & 1);
+    cs[c2 * kW + cl + cl / VEC] = bits_f32(v[0]);
+    cs[(c2 + 1) * kW + cl + cl / VEC] = bits_f32(v[2]);
   }
   __syncthreads();
   const int cb = tx * (VEC + 1);
